@@ -1,0 +1,262 @@
+// Dispatch: the stable counting sort of the (token, slot) pairs p = t k + i by expert, deterministic on the GPU
+// (reference csrc/artlite/moe_host.cpp:201-215: histogram, exclusive prefix, scatter in p order), and the chunk plan
+// dealt to the columns (moe_host.cpp:216-234); the C entry point artlite_moe_plan.
+//
+// Two launches over blocks of DISPATCH_BLOCK consecutive pairs:
+//  1. k_count: per-block histograms (LDS atomics: counts are order-free) into table[b][e]; the last block to finish
+//     (a device-scope ticket) sums them into counts, scans them into offsets and per-(block, expert) bases, and
+//     writes the tile list of the expert GEMMs and the plan's chunk prefix.
+//  2. k_scatter: each pair's rank among the earlier pairs of its block with the same expert (wave ballots over the
+//     id bits give the peers and the in-wave rank; a per-wave count table orders the waves) plus its block's base:
+//     its position in the sorted order. Stable by construction: no atomics decide any position.
+#include "route.h"
+
+namespace artlite {
+
+// exclusive prefix of one value per thread of a DISPATCH_BLOCK block; *total the sum (all threads)
+__device__ int block_scan(int v, int* total) {
+  __shared__ int wsum[DISPATCH_BLOCK / WAVE];
+  const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < WAVE; o <<= 1) {
+    const int y = __shfl_up(x, o, WAVE);
+    if (lane >= o) x += y;
+  }
+  if (lane == WAVE - 1) wsum[wv] = x;
+  __syncthreads();
+  if (wv == 0) {
+    int s = lane < DISPATCH_BLOCK / WAVE ? wsum[lane] : 0;
+#pragma unroll
+    for (int o = 1; o < DISPATCH_BLOCK / WAVE; o <<= 1) {
+      const int y = __shfl_up(s, o, WAVE);
+      if (lane >= o) s += y;
+    }
+    if (lane < DISPATCH_BLOCK / WAVE) wsum[lane] = s;  // (inclusive over waves)
+  }
+  __syncthreads();
+  const int before = (wv ? wsum[wv - 1] : 0) + x - v;
+  *total = wsum[DISPATCH_BLOCK / WAVE - 1];
+  __syncthreads();
+  return before;
+}
+
+__global__ __launch_bounds__(DISPATCH_BLOCK) void k_count(DispatchBufs d) {
+  __shared__ int hist[MAX_EXPERTS];
+  __shared__ int last;
+  const int tid = threadIdx.x;
+  const int64_t nb = gridDim.x;
+  for (int e = tid; e < d.E; e += DISPATCH_BLOCK) hist[e] = 0;
+  __syncthreads();
+  const int64_t p = int64_t(blockIdx.x) * DISPATCH_BLOCK + tid;
+  if (p < d.P) {
+    const int id = d.ids[p];
+    if (id < 0 || id >= d.E) {
+      atomicOr(&d.ctrl[CTRL_BAD], 1);
+      atomicMax(&d.ctrl[CTRL_BAD_FIRST], int(d.P - p));
+    } else {
+      atomicAdd(&hist[id], 1);
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < d.E; e += DISPATCH_BLOCK) d.table[int64_t(blockIdx.x) * d.E + e] = hist[e];
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) last = atomicAdd(&d.ctrl[CTRL_DONE], 1) == int(nb - 1);
+  __syncthreads();
+  if (!last) return;
+  __threadfence();  // (acquire: the other blocks' tables)
+  // counts, offsets, per-block bases (one expert per thread: E <= MAX_EXPERTS == DISPATCH_BLOCK)
+  const int e = tid;
+  int c = 0;
+  if (e < d.E)
+    for (int64_t b = 0; b < nb; b++) c += __builtin_nontemporal_load(&d.table[b * d.E + e]);
+  int total;
+  const int start = block_scan(c, &total);
+  if (e < d.E) {
+    d.counts[e] = c;
+    d.offsets[e] = start;
+    int run = start;
+    for (int64_t b = 0; b < nb; b++) {
+      int* cell = &d.table[b * d.E + e];
+      const int v = __builtin_nontemporal_load(cell);
+      *cell = run;
+      run += v;
+    }
+  }
+  if (e == 0) d.offsets[d.E] = total;
+  if (d.BM > 0) {  // the expert GEMMs' tiles: experts ascending, BM sorted rows each
+    const int nt = e < d.E ? (c + d.BM - 1) / d.BM : 0;
+    int nt_total;
+    const int t0 = block_scan(nt, &nt_total);
+    for (int m = 0; m < nt; m++) {
+      d.tiles[2 * (t0 + m)] = e;
+      d.tiles[2 * (t0 + m) + 1] = start + m * d.BM;
+    }
+    if (e == 0) d.ctrl[CTRL_TILES] = nt_total;
+  }
+  if (d.chunk > 0) {  // the plan's chunks per expert
+    const int nc = e < d.E ? (c + d.chunk - 1) / d.chunk : 0;
+    int nc_total;
+    const int c0 = block_scan(nc, &nc_total);
+    if (e < d.E) d.cstart[e] = c0;
+    if (e == 0) {
+      d.cstart[d.E] = nc_total;
+      d.ctrl[CTRL_CHUNKS] = nc_total;
+    }
+  }
+  if (e == 0) d.ctrl[CTRL_DONE] = 0;  // (ready for the next dispatch)
+}
+
+__global__ __launch_bounds__(DISPATCH_BLOCK) void k_scatter(DispatchBufs d, PlanBufs pl) {
+  __shared__ uint16_t wcnt[DISPATCH_BLOCK / WAVE][MAX_EXPERTS];
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), wv = tid / WAVE;
+  for (int i = tid; i < (DISPATCH_BLOCK / WAVE) * d.E; i += DISPATCH_BLOCK) wcnt[i / d.E][i % d.E] = 0;
+  __syncthreads();
+  const int64_t p = int64_t(blockIdx.x) * DISPATCH_BLOCK + tid;
+  const int id = p < d.P ? d.ids[p] : -1;
+  const bool valid = id >= 0 && id < d.E;
+  // the lanes of this wave with the same expert (ballots over the id bits)
+  uint64_t peers = __ballot(valid);
+  for (int bit = 0; (1 << bit) < d.E; bit++) {
+    const bool set = (id >> bit) & 1;
+    const uint64_t b = __ballot(set);
+    peers &= set ? b : ~b;
+  }
+  const uint64_t below = (uint64_t(1) << lane) - 1;
+  int rank = __popcll(peers & below);
+  if (valid && !(peers & below)) wcnt[wv][id] = uint16_t(__popcll(peers));
+  __syncthreads();
+  if (!valid) return;
+  for (int w = 0; w < wv; w++) rank += wcnt[w][id];
+  const int dest = d.table[int64_t(blockIdx.x) * d.E + id] + rank;
+  d.order[dest] = int32_t(p);
+  d.slot[p] = dest;
+  if (pl.pos) {  // the plan's row of this pair
+    const int o = dest - d.offsets[id];
+    const int j = d.cstart[id] + o / d.chunk, i = o % d.chunk;
+    const int c = j % pl.cols, kk = j / pl.cols;
+    if (kk < pl.cap) {
+      const int64_t g = (int64_t(c) * pl.cap + kk) * d.chunk + i;
+      pl.pos[p] = g;
+      pl.rows[g] = int32_t(p / d.k);
+    }
+  }
+}
+
+// per chunk j: its column's expert and size, the padding rows (the chunk's first token); the columns' counts
+__global__ void k_plan_fill(DispatchBufs d, PlanBufs pl) {
+  const int total = d.ctrl[CTRL_CHUNKS];
+  const int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (j == 0 && total > int64_t(pl.cols) * pl.cap) d.ctrl[CTRL_OVER_CAP] = 1;
+  if (j < pl.cols) pl.ccounts[j] = total > j ? int32_t((total - 1 - j) / pl.cols + 1) : 0;
+  if (j >= total) return;
+  const int c = int(j % pl.cols), kk = int(j / pl.cols);
+  if (kk >= pl.cap) return;
+  int lo = 0, hi = d.E;  // the expert e with cstart[e] <= j < cstart[e + 1]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) / 2;
+    if (d.cstart[mid] <= j)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  const int e = lo, q = int(j) - d.cstart[e];
+  const int size = min(d.chunk, d.counts[e] - q * d.chunk);
+  pl.experts[int64_t(c) * pl.cap + kk] = e;
+  pl.sizes[int64_t(c) * pl.cap + kk] = size;
+  const int32_t first = d.order[d.offsets[e] + q * d.chunk] / d.k;
+  int32_t* r = pl.rows + (int64_t(c) * pl.cap + kk) * d.chunk;
+  for (int i = size; i < d.chunk; i++) r[i] = first;
+}
+
+int launch_dispatch_count(const DispatchBufs& d, int64_t nb, hipStream_t s) {
+  if (d.E < 1 || d.E > MAX_EXPERTS) return fail(ARTLITE_EINVAL, "dispatch: E %d outside [1, %d]", d.E, MAX_EXPERTS);
+  k_count<<<unsigned(nb), DISPATCH_BLOCK, 0, s>>>(d);
+  ART_HIP(hipGetLastError());
+  return ARTLITE_OK;
+}
+
+int launch_dispatch_scatter(const DispatchBufs& d, int64_t nb, hipStream_t s) {
+  k_scatter<<<unsigned(nb), DISPATCH_BLOCK, 0, s>>>(d, PlanBufs{0, 0, nullptr, nullptr, nullptr, nullptr, nullptr});
+  ART_HIP(hipGetLastError());
+  return ARTLITE_OK;
+}
+
+int launch_dispatch(const DispatchBufs& d, hipStream_t s) {
+  const int64_t nb = dispatch_blocks(d.P);
+  ART_TRY(launch_dispatch_count(d, nb, s));
+  return launch_dispatch_scatter(d, nb, s);
+}
+
+int launch_plan(const DispatchBufs& d, const PlanBufs& pl, hipStream_t s) {
+  if (d.E < 1 || d.E > MAX_EXPERTS) return fail(ARTLITE_EINVAL, "dispatch: E %d outside [1, %d]", d.E, MAX_EXPERTS);
+  const int64_t nb = dispatch_blocks(d.P);
+  k_count<<<unsigned(nb), DISPATCH_BLOCK, 0, s>>>(d);
+  ART_HIP(hipGetLastError());
+  k_scatter<<<unsigned(nb), DISPATCH_BLOCK, 0, s>>>(d, pl);
+  ART_HIP(hipGetLastError());
+  const int64_t bound = d.E + (d.P + d.chunk - 1) / d.chunk;
+  const int64_t threads = bound > pl.cols ? bound : pl.cols;
+  k_plan_fill<<<unsigned((threads + 255) / 256), 256, 0, s>>>(d, pl);
+  ART_HIP(hipGetLastError());
+  return ARTLITE_OK;
+}
+
+}  // namespace artlite
+
+using namespace artlite;
+
+extern "C" int artlite_moe_plan(const int32_t* ids, int64_t n, int k, int E, int cols, int cap, int chunk,
+                                int32_t* experts, int32_t* counts, int32_t* sizes, int32_t* rows, int64_t* pos) {
+  if (n < 0 || k < 1 || E < 1 || cols < 1 || cap < 0 || chunk < 1)
+    return fail(ARTLITE_EINVAL, "moe_plan: n %lld, k %d, E %d, cols %d, cap %d, chunk %d", (long long)n, k, E, cols,
+                cap, chunk);
+  if (E > MAX_EXPERTS) return fail(ARTLITE_EINVAL, "moe_plan: E %d beyond this build's %d", E, MAX_EXPERTS);
+  if (!counts || (n && (!ids || !pos)) || (cap && (!experts || !sizes || !rows)))
+    return fail(ARTLITE_EINVAL, "moe_plan: null array");
+  const int64_t P = n * k;
+  HostCtx* c;
+  ART_TRY(host_ctx(&c));
+  const int64_t nb = dispatch_blocks(P);
+  const size_t slots = size_t(cols) * cap;
+  // in: ids | out: table | out2: counts, offsets, cstart | out3: order, slot | out4: pos | out5: rows, experts, sizes,
+  // column counts | flag: ctrl
+  ART_TRY(c->in.reserve(size_t(P) * 4));
+  ART_TRY(c->out.reserve(size_t(nb) * E * 4));
+  ART_TRY(c->out2.reserve(size_t(3 * E + 3) * 4));
+  ART_TRY(c->out3.reserve(size_t(2 * P) * 4));
+  ART_TRY(c->out4.reserve(size_t(P) * 8));
+  ART_TRY(c->out5.reserve((slots * chunk + 2 * slots + cols) * 4));
+  ART_TRY(c->flag.reserve(CTRL_WORDS * 4));
+  if (P) ART_HIP(hipMemcpyAsync(c->in.p, ids, size_t(P) * 4, hipMemcpyHostToDevice, c->stream));
+  ART_HIP(hipMemsetAsync(c->flag.p, 0, CTRL_WORDS * 4, c->stream));
+  int32_t* o2 = c->out2.as<int32_t>();
+  int32_t* o5 = c->out5.as<int32_t>();
+  DispatchBufs d{c->in.as<int32_t>(), P, E, k, c->out.as<int32_t>(), c->flag.as<int32_t>(), o2, o2 + E,
+                 c->out3.as<int32_t>(), c->out3.as<int32_t>() + P, nullptr, 0, o2 + 2 * E + 1, chunk};
+  PlanBufs pl{cols, cap, o5 + slots * chunk, o5 + slots * chunk + 2 * slots, o5 + slots * chunk + slots, o5,
+              c->out4.as<int64_t>()};
+  ART_TRY(launch_plan(d, pl, c->stream));
+  int32_t ctrl[CTRL_WORDS];
+  ART_HIP(hipMemcpyAsync(ctrl, c->flag.p, sizeof ctrl, hipMemcpyDeviceToHost, c->stream));
+  ART_HIP(hipStreamSynchronize(c->stream));
+  if (ctrl[CTRL_BAD]) return fail(ARTLITE_EINVAL, "moe_plan: expert id %d of %d", ids[P - ctrl[CTRL_BAD_FIRST]], E);
+  if (ctrl[CTRL_OVER_CAP]) return fail(ARTLITE_EINVAL, "moe_plan: more than %d chunks in a column", cap);
+  const int total = ctrl[CTRL_CHUNKS];
+  ART_HIP(hipMemcpyAsync(counts, pl.ccounts, size_t(cols) * 4, hipMemcpyDeviceToHost, c->stream));
+  // (only the dealt slots are written: the reference's arrays keep their other entries)
+  for (int col = 0; col < cols; col++) {
+    const int m = total > col ? (total - 1 - col) / cols + 1 : 0;
+    if (!m) continue;
+    ART_HIP(hipMemcpyAsync(experts + size_t(col) * cap, pl.experts + size_t(col) * cap, size_t(m) * 4,
+                           hipMemcpyDeviceToHost, c->stream));
+    ART_HIP(hipMemcpyAsync(sizes + size_t(col) * cap, pl.sizes + size_t(col) * cap, size_t(m) * 4,
+                           hipMemcpyDeviceToHost, c->stream));
+    ART_HIP(hipMemcpyAsync(rows + size_t(col) * cap * chunk, pl.rows + size_t(col) * cap * chunk,
+                           size_t(m) * chunk * 4, hipMemcpyDeviceToHost, c->stream));
+  }
+  if (P) ART_HIP(hipMemcpyAsync(pos, pl.pos, size_t(P) * 8, hipMemcpyDeviceToHost, c->stream));
+  ART_HIP(hipStreamSynchronize(c->stream));
+  return ARTLITE_OK;
+}

@@ -1,0 +1,483 @@
+// The MoE layer object: its weights in HBM as the GGUF file lays them out (no repacking), its activations, and the
+// forward pass on one HIP stream: router -> top k -> dispatch -> gate / up (SwiGLU) -> down -> combine, plus the
+// shared expert. The semantics are the reference's oracle (tests/moe/ref.py:43-60) with its routing
+// (csrc/artlite/moe_host.cpp:45-73) and combine (src/artlite/moe/gather.py:12-18).
+#include <string>
+#include <vector>
+
+#include "experts.h"
+#include "route.h"
+
+using namespace artlite;
+
+struct artlite_moe_layer {
+  artlite_moe_desc d{};
+  int device = 0;
+  hipStream_t stream = nullptr;
+  const QType *gq = nullptr, *dq = nullptr, *sq = nullptr;
+  size_t gate_row = 0, down_row = 0, sgate_row = 0, sdown_row = 0;  // row bytes
+  DevBuf router, gate, up, down, sgate, sup, sdown, sinp;
+  bool have[8] = {};
+  // activations of the staged input
+  int x_dtype = ARTLITE_X_BF16;
+  int64_t staged = -1;  // tokens staged, -1: none
+  DevBuf x, xhi, xlo;
+  DevBuf logits, ids, w, sg;
+  DevBuf table, ctrl, counts, offsets, order, slot, tiles;
+  DevBuf hhi, hlo, ypairs, shhi, shlo, ys, y;
+  int64_t last_T = -1;
+};
+
+namespace {
+
+size_t tensor_bytes(const artlite_moe_layer* L, int t) {
+  const artlite_moe_desc& d = L->d;
+  switch (t) {
+    case ARTLITE_ROUTER: return size_t(d.n_experts) * d.hidden * 4;
+    case ARTLITE_GATE_EXPS:
+    case ARTLITE_UP_EXPS: return size_t(d.n_experts) * d.expert_ffn * L->gate_row;
+    case ARTLITE_DOWN_EXPS: return size_t(d.n_experts) * d.hidden * L->down_row;
+    case ARTLITE_GATE_SHEXP:
+    case ARTLITE_UP_SHEXP: return size_t(d.shared_ffn) * L->sgate_row;
+    case ARTLITE_DOWN_SHEXP: return size_t(d.hidden) * L->sdown_row;
+    case ARTLITE_GATE_INP_SHEXP: return size_t(d.hidden) * 4;
+    default: return 0;
+  }
+}
+
+DevBuf* tensor_buf(artlite_moe_layer* L, int t) {
+  switch (t) {
+    case ARTLITE_ROUTER: return &L->router;
+    case ARTLITE_GATE_EXPS: return &L->gate;
+    case ARTLITE_UP_EXPS: return &L->up;
+    case ARTLITE_DOWN_EXPS: return &L->down;
+    case ARTLITE_GATE_SHEXP: return &L->sgate;
+    case ARTLITE_UP_SHEXP: return &L->sup;
+    case ARTLITE_DOWN_SHEXP: return &L->sdown;
+    case ARTLITE_GATE_INP_SHEXP: return &L->sinp;
+    default: return nullptr;
+  }
+}
+
+bool is_expert_type(const QType* q) {
+  return q && (q->id == ARTLITE_Q4_0 || q->id == ARTLITE_Q8_0 || q->id == ARTLITE_Q4_K);
+}
+
+int check_ready(const artlite_moe_layer* L) {
+  for (int t = ARTLITE_ROUTER; t <= ARTLITE_DOWN_EXPS; t++)
+    if (!L->have[t]) return fail(ARTLITE_EINVAL, "moe layer: tensor %d not uploaded", t);
+  if (L->d.shared_ffn) {
+    for (int t = ARTLITE_GATE_SHEXP; t <= ARTLITE_DOWN_SHEXP; t++)
+      if (!L->have[t]) return fail(ARTLITE_EINVAL, "moe layer: shared tensor %d not uploaded", t);
+    if (L->d.shared_gated && !L->have[ARTLITE_GATE_INP_SHEXP])
+      return fail(ARTLITE_EINVAL, "moe layer: shared gate not uploaded");
+  }
+  return ARTLITE_OK;
+}
+
+// the named kernels of a forward pass, in launch order
+std::vector<std::string> kernel_list(const artlite_moe_layer* L) {
+  std::vector<std::string> k;
+  if (L->x_dtype == ARTLITE_X_F32) k.push_back("split");
+  k.push_back("router");
+  if (L->d.shared_ffn && L->d.shared_gated) k.push_back("shared_gate");
+  k.push_back("topk");
+  k.push_back("dispatch_count");
+  k.push_back("dispatch_scatter");
+  k.push_back("gate_up");
+  k.push_back("down");
+  if (L->d.shared_ffn) {
+    k.push_back("shared_gate_up");
+    k.push_back("shared_down");
+  }
+  k.push_back("combine");
+  return k;
+}
+
+// The forward pass of the staged T tokens. ev (optional): an event recorded before each kernel and one after the
+// last (kernel_list order).
+int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
+  const artlite_moe_desc& d = L->d;
+  hipStream_t s = L->stream;
+  const int H = d.hidden, E = d.n_experts, k = d.top_k, F = d.expert_ffn;
+  const int64_t P = T * k;
+  int ei = 0;
+  auto mark = [&]() -> int {
+    if (ev) ART_HIP(hipEventRecord(ev[ei++], s));
+    return ARTLITE_OK;
+  };
+  const uint16_t *ahi, *alo = nullptr;
+  if (L->x_dtype == ARTLITE_X_F32) {
+    ART_TRY(mark());
+    ART_TRY(launch_split(L->x.as<float>(), T * H, L->xhi.as<uint16_t>(), L->xlo.as<uint16_t>(), s));
+    ahi = L->xhi.as<uint16_t>();
+    alo = L->xlo.as<uint16_t>();
+  } else {
+    ahi = L->x.as<uint16_t>();
+  }
+  ART_TRY(mark());
+  ART_TRY(launch_router(L->x.p, L->x_dtype, L->router.as<float>(), H, E, T, L->logits.as<float>(), E, s));
+  if (d.shared_ffn && d.shared_gated) {
+    ART_TRY(mark());
+    ART_TRY(launch_router(L->x.p, L->x_dtype, L->sinp.as<float>(), H, 1, T, L->sg.as<float>(), 1, s));
+  }
+  ART_TRY(mark());
+  ART_TRY(launch_topk(L->logits.as<float>(), T, E, E, 0, E, k, d.gating, L->ids.as<int32_t>(), L->w.as<float>(),
+                      nullptr, s));
+  const int BM = DECODE_BM;
+  DispatchBufs db{L->ids.as<int32_t>(), P, E, k, L->table.as<int32_t>(), L->ctrl.as<int32_t>(),
+                  L->counts.as<int32_t>(), L->offsets.as<int32_t>(), L->order.as<int32_t>(), L->slot.as<int32_t>(),
+                  L->tiles.as<int32_t>(), BM, nullptr, 0};
+  {
+    const int64_t nb = dispatch_blocks(P);
+    ART_TRY(mark());
+    ART_TRY(launch_dispatch_count(db, nb, s));
+    ART_TRY(mark());
+    ART_TRY(launch_dispatch_scatter(db, nb, s));
+  }
+  GemmArgs g{};
+  g.w[0] = L->gate.as<uint8_t>();
+  g.w[1] = L->up.as<uint8_t>();
+  g.expert_bytes = int64_t(F) * L->gate_row;
+  g.row_bytes = int(L->gate_row);
+  g.N = F;
+  g.K = H;
+  g.qtype = d.gate_type;
+  g.a_hi = ahi;
+  g.a_lo = alo;
+  g.a_gather = 1;
+  g.order = L->order.as<int32_t>();
+  g.topk = k;
+  g.tiles = L->tiles.as<int32_t>();
+  g.n_tiles = L->ctrl.as<int32_t>() + CTRL_TILES;
+  g.offsets = L->offsets.as<int32_t>();
+  g.max_tiles = tile_bound(P, E, BM);
+  g.h_hi = L->hhi.as<uint16_t>();
+  g.h_lo = L->hlo.as<uint16_t>();
+  ART_TRY(mark());
+  ART_TRY(launch_expert_gemm(g, s));
+  GemmArgs dn = g;
+  dn.w[0] = L->down.as<uint8_t>();
+  dn.w[1] = nullptr;
+  dn.expert_bytes = int64_t(H) * L->down_row;
+  dn.row_bytes = int(L->down_row);
+  dn.N = H;
+  dn.K = F;
+  dn.qtype = d.down_type;
+  dn.a_hi = L->hhi.as<uint16_t>();
+  dn.a_lo = L->hlo.as<uint16_t>();
+  dn.a_gather = 0;
+  dn.y = L->ypairs.as<float>();
+  ART_TRY(mark());
+  ART_TRY(launch_expert_gemm(dn, s));
+  const float* ys = nullptr;
+  if (d.shared_ffn) {
+    GemmArgs sg{};
+    sg.w[0] = L->sgate.as<uint8_t>();
+    sg.w[1] = L->sup.as<uint8_t>();
+    sg.expert_bytes = 0;
+    sg.row_bytes = int(L->sgate_row);
+    sg.N = d.shared_ffn;
+    sg.K = H;
+    sg.qtype = d.shared_type;
+    sg.a_hi = ahi;
+    sg.a_lo = alo;
+    sg.dense_rows = int(T);
+    sg.h_hi = L->shhi.as<uint16_t>();
+    sg.h_lo = L->shlo.as<uint16_t>();
+    ART_TRY(mark());
+    ART_TRY(launch_expert_gemm(sg, s));
+    GemmArgs sd = sg;
+    sd.w[0] = L->sdown.as<uint8_t>();
+    sd.w[1] = nullptr;
+    sd.row_bytes = int(L->sdown_row);
+    sd.N = H;
+    sd.K = d.shared_ffn;
+    sd.a_hi = L->shhi.as<uint16_t>();
+    sd.a_lo = L->shlo.as<uint16_t>();
+    sd.y = L->ys.as<float>();
+    ART_TRY(mark());
+    ART_TRY(launch_expert_gemm(sd, s));
+    ys = L->ys.as<float>();
+  }
+  ART_TRY(mark());
+  ART_TRY(launch_combine(L->ypairs.as<float>(), L->slot.as<int32_t>(), L->w.as<float>(), k, ys,
+                         d.shared_gated ? L->sg.as<float>() : nullptr, 1, T, H, L->y.as<float>(), s));
+  ART_TRY(mark());
+  L->last_T = T;
+  return ARTLITE_OK;
+}
+
+}  // namespace
+
+extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_moe_layer** out) {
+  if (!desc || !out) return fail(ARTLITE_EINVAL, "moe layer: null argument");
+  *out = nullptr;
+  const artlite_moe_desc& d = *desc;
+  if (d.hidden <= 0 || d.n_experts <= 0 || d.expert_ffn <= 0 || d.max_tokens <= 0)
+    return fail(ARTLITE_EINVAL, "moe layer: H %d, E %d, F %d, max tokens %d", d.hidden, d.n_experts, d.expert_ffn,
+                d.max_tokens);
+  ART_TRY(check_route_args(1, d.n_experts, d.n_experts, d.top_k));
+  const QType *gq = qtype_by_id(d.gate_type), *dq = qtype_by_id(d.down_type);
+  if (!is_expert_type(gq) || !is_expert_type(dq))
+    return fail(ARTLITE_EINVAL, "moe layer: expert types %d / %d (Q4_0, Q8_0, Q4_K)", d.gate_type, d.down_type);
+  if (d.hidden % gq->per || d.expert_ffn % dq->per)
+    return fail(ARTLITE_EINVAL, "moe layer: H %d / F %d not multiples of the blocks (%d / %d)", d.hidden,
+                d.expert_ffn, gq->per, dq->per);
+  if (d.hidden % 4) return fail(ARTLITE_EINVAL, "moe layer: H %d not a multiple of 4", d.hidden);
+  const QType* sq = nullptr;
+  if (d.shared_ffn) {
+    sq = qtype_by_id(d.shared_type);
+    if (!is_expert_type(sq) || d.hidden % sq->per || d.shared_ffn % sq->per)
+      return fail(ARTLITE_EINVAL, "moe layer: shared expert type %d / width %d", d.shared_type, d.shared_ffn);
+  }
+  if (d.gating != 0 && d.gating != 1) return fail(ARTLITE_EINVAL, "moe layer: gating %d", d.gating);
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(ARTLITE_EHIP, "moe layer: no HIP device");
+  auto* L = new artlite_moe_layer();
+  L->d = d;
+  L->gq = gq;
+  L->dq = dq;
+  L->sq = sq;
+  L->gate_row = size_t(d.hidden) / gq->per * gq->bytes;
+  L->down_row = size_t(d.expert_ffn) / dq->per * dq->bytes;
+  if (sq) {
+    L->sgate_row = size_t(d.hidden) / sq->per * sq->bytes;
+    L->sdown_row = size_t(d.shared_ffn) / sq->per * sq->bytes;
+  }
+  hipError_t e = hipGetDevice(&L->device);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&L->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete L;
+    return fail(ARTLITE_EHIP, "moe layer: %s", hipGetErrorString(e));
+  }
+  // activation buffers for max_tokens
+  const int64_t T = d.max_tokens, P = T * d.top_k, H = d.hidden, F = d.expert_ffn, E = d.n_experts;
+  int rc = ARTLITE_OK;
+  auto res = [&](DevBuf& b, size_t bytes) {
+    if (rc == ARTLITE_OK) rc = b.reserve(bytes);
+  };
+  res(L->x, size_t(T * H) * 4);
+  res(L->xhi, size_t(T * H) * 2);
+  res(L->xlo, size_t(T * H) * 2);
+  res(L->logits, size_t(T * E) * 4);
+  res(L->ids, size_t(P) * 4);
+  res(L->w, size_t(P) * 4);
+  res(L->sg, size_t(T) * 4);
+  res(L->table, size_t(dispatch_blocks(P) * E) * 4);
+  res(L->ctrl, CTRL_WORDS * 4);
+  res(L->counts, size_t(E) * 4);
+  res(L->offsets, size_t(E + 1) * 4);
+  res(L->order, size_t(P) * 4);
+  res(L->slot, size_t(P) * 4);
+  res(L->tiles, size_t(2 * tile_bound(P, int(E), 1)) * 4);
+  res(L->hhi, size_t(P * F) * 2);
+  res(L->hlo, size_t(P * F) * 2);
+  res(L->ypairs, size_t(P * H) * 4);
+  res(L->y, size_t(T * H) * 4);
+  if (d.shared_ffn) {
+    res(L->shhi, size_t(T) * d.shared_ffn * 2);
+    res(L->shlo, size_t(T) * d.shared_ffn * 2);
+    res(L->ys, size_t(T * H) * 4);
+  }
+  if (rc == ARTLITE_OK && hipMemset(L->ctrl.p, 0, CTRL_WORDS * 4) != hipSuccess)
+    rc = fail(ARTLITE_EHIP, "moe layer: memset");
+  if (rc != ARTLITE_OK) {
+    artlite_moe_layer_destroy(L);
+    return rc;
+  }
+  *out = L;
+  return ARTLITE_OK;
+}
+
+extern "C" int artlite_moe_layer_destroy(artlite_moe_layer* L) {
+  if (!L) return ARTLITE_OK;
+  if (L->stream) {
+    (void)hipStreamSynchronize(L->stream);
+    (void)hipStreamDestroy(L->stream);
+  }
+  delete L;
+  return ARTLITE_OK;
+}
+
+extern "C" int artlite_moe_layer_upload(artlite_moe_layer* L, int t, const void* data, size_t nbytes) {
+  if (!L || !data) return fail(ARTLITE_EINVAL, "moe layer upload: null argument");
+  DevBuf* b = tensor_buf(L, t);
+  const size_t want = tensor_bytes(L, t);
+  if (!b || !want) return fail(ARTLITE_EINVAL, "moe layer upload: tensor %d not in this layer", t);
+  if (nbytes != want) return fail(ARTLITE_EINVAL, "moe layer upload: tensor %d is %zu bytes, not %zu", t, nbytes, want);
+  ART_TRY(b->reserve(want));
+  ART_HIP(hipMemcpyAsync(b->p, data, want, hipMemcpyHostToDevice, L->stream));
+  ART_HIP(hipMemsetAsync(static_cast<uint8_t*>(b->p) + want, 0, 256, L->stream));  // (the tail the loaders touch)
+  ART_HIP(hipStreamSynchronize(L->stream));
+  L->have[t] = true;
+  return ARTLITE_OK;
+}
+
+extern "C" int artlite_moe_layer_stage(artlite_moe_layer* L, const void* x, int x_dtype, int64_t T) {
+  if (!L || (!x && T)) return fail(ARTLITE_EINVAL, "moe layer stage: null argument");
+  if (T < 0 || T > L->d.max_tokens) return fail(ARTLITE_EINVAL, "moe layer: %lld tokens of at most %d", (long long)T,
+                                                L->d.max_tokens);
+  if (x_dtype != ARTLITE_X_F32 && x_dtype != ARTLITE_X_BF16) return fail(ARTLITE_EINVAL, "moe layer: x dtype %d", x_dtype);
+  const size_t bytes = size_t(T) * L->d.hidden * (x_dtype == ARTLITE_X_F32 ? 4 : 2);
+  if (bytes) ART_HIP(hipMemcpyAsync(L->x.p, x, bytes, hipMemcpyHostToDevice, L->stream));
+  ART_HIP(hipStreamSynchronize(L->stream));
+  L->x_dtype = x_dtype;
+  L->staged = T;
+  return ARTLITE_OK;
+}
+
+extern "C" int artlite_moe_layer_run(artlite_moe_layer* L, int64_t T) {
+  if (!L) return fail(ARTLITE_EINVAL, "moe layer run: null layer");
+  if (T != L->staged) return fail(ARTLITE_EINVAL, "moe layer run: %lld tokens, %lld staged", (long long)T,
+                                  (long long)L->staged);
+  ART_TRY(check_ready(L));
+  if (T == 0) return ARTLITE_OK;
+  return run(L, T, nullptr);
+}
+
+extern "C" int artlite_moe_layer_sync(artlite_moe_layer* L) {
+  if (!L) return fail(ARTLITE_EINVAL, "moe layer sync: null layer");
+  ART_HIP(hipStreamSynchronize(L->stream));
+  return ARTLITE_OK;
+}
+
+extern "C" int artlite_moe_layer_output(artlite_moe_layer* L, float* y, int64_t T) {
+  if (!L || (!y && T)) return fail(ARTLITE_EINVAL, "moe layer output: null argument");
+  if (T != L->last_T && T) return fail(ARTLITE_EINVAL, "moe layer output: %lld tokens, the last run had %lld",
+                                       (long long)T, (long long)L->last_T);
+  if (T) ART_HIP(hipMemcpyAsync(y, L->y.p, size_t(T) * L->d.hidden * 4, hipMemcpyDeviceToHost, L->stream));
+  ART_HIP(hipStreamSynchronize(L->stream));
+  return ARTLITE_OK;
+}
+
+extern "C" int artlite_moe_layer_forward(artlite_moe_layer* L, const void* x, int x_dtype, int64_t T, float* y) {
+  ART_TRY(artlite_moe_layer_stage(L, x, x_dtype, T));
+  ART_TRY(artlite_moe_layer_run(L, T));
+  if (T == 0) {
+    L->last_T = 0;
+    return ARTLITE_OK;
+  }
+  ART_TRY(artlite_moe_layer_output(L, y, T));
+  int32_t ctrl[CTRL_WORDS];
+  ART_HIP(hipMemcpy(ctrl, L->ctrl.p, sizeof ctrl, hipMemcpyDeviceToHost));
+  if (ctrl[CTRL_BAD]) return fail(ARTLITE_EHIP, "moe layer: the dispatch saw an invalid expert id");
+  return ARTLITE_OK;
+}
+
+extern "C" int artlite_moe_layer_tap(artlite_moe_layer* L, int tap, void* out, size_t nbytes) {
+  if (!L || !out) return fail(ARTLITE_EINVAL, "moe layer tap: null argument");
+  const int64_t T = L->last_T;
+  if (T < 0) return fail(ARTLITE_EINVAL, "moe layer tap: no run yet");
+  const int64_t P = T * L->d.top_k, E = L->d.n_experts;
+  const void* src = nullptr;
+  size_t bytes = 0;
+  switch (tap) {
+    case ARTLITE_TAP_LOGITS: src = L->logits.p, bytes = size_t(T * E) * 4; break;
+    case ARTLITE_TAP_IDS: src = L->ids.p, bytes = size_t(P) * 4; break;
+    case ARTLITE_TAP_WEIGHTS: src = L->w.p, bytes = size_t(P) * 4; break;
+    case ARTLITE_TAP_COUNTS: src = L->counts.p, bytes = size_t(E) * 4; break;
+    case ARTLITE_TAP_OFFSETS: src = L->offsets.p, bytes = size_t(E + 1) * 4; break;
+    case ARTLITE_TAP_ORDER: src = L->order.p, bytes = size_t(P) * 4; break;
+    case ARTLITE_TAP_SLOT: src = L->slot.p, bytes = size_t(P) * 4; break;
+    case ARTLITE_TAP_Y: src = L->ypairs.p, bytes = size_t(P) * L->d.hidden * 4; break;
+    case ARTLITE_TAP_H: {
+      const size_t n = size_t(P) * L->d.expert_ffn;
+      if (nbytes < n * 4) return fail(ARTLITE_EINVAL, "moe layer tap: %zu bytes, need %zu", nbytes, n * 4);
+      std::vector<uint16_t> hi(n), lo(n);
+      ART_HIP(hipMemcpy(hi.data(), L->hhi.p, n * 2, hipMemcpyDeviceToHost));
+      ART_HIP(hipMemcpy(lo.data(), L->hlo.p, n * 2, hipMemcpyDeviceToHost));
+      float* o = static_cast<float*>(out);
+      for (size_t i = 0; i < n; i++) {
+        uint32_t a = uint32_t(hi[i]) << 16, b = uint32_t(lo[i]) << 16;
+        float fa, fb;
+        std::memcpy(&fa, &a, 4);
+        std::memcpy(&fb, &b, 4);
+        o[i] = fa + fb;
+      }
+      return ARTLITE_OK;
+    }
+    default: return fail(ARTLITE_EINVAL, "moe layer tap: unknown tap %d", tap);
+  }
+  if (nbytes < bytes) return fail(ARTLITE_EINVAL, "moe layer tap: %zu bytes, need %zu", nbytes, bytes);
+  ART_HIP(hipStreamSynchronize(L->stream));
+  if (bytes) ART_HIP(hipMemcpy(out, src, bytes, hipMemcpyDeviceToHost));
+  return ARTLITE_OK;
+}
+
+extern "C" int artlite_moe_kernel_names(artlite_moe_layer* L, int64_t T, char* buf, size_t cap) {
+  if (!L || !buf || !cap) return fail(ARTLITE_EINVAL, "kernel names: null argument");
+  (void)T;
+  std::string s;
+  for (const std::string& k : kernel_list(L)) s += (s.empty() ? "" : ";") + k;
+  const size_t n = s.size() < cap - 1 ? s.size() : cap - 1;
+  std::memcpy(buf, s.data(), n);
+  buf[n] = 0;
+  return ARTLITE_OK;
+}
+
+extern "C" int artlite_moe_layer_time(artlite_moe_layer** layers, int n, int64_t T, int warmup, int iters,
+                                      double* ms_per_run, double* kernel_ms, int kernel_cap, int* n_kernels) {
+  if (!layers || n < 1 || iters < 1 || warmup < 0 || !ms_per_run) return fail(ARTLITE_EINVAL, "layer time: arguments");
+  artlite_moe_layer* L0 = layers[0];
+  for (int i = 0; i < n; i++) {
+    if (!layers[i]) return fail(ARTLITE_EINVAL, "layer time: null layer");
+    if (layers[i]->staged != T) return fail(ARTLITE_EINVAL, "layer time: layer %d has %lld tokens staged", i,
+                                            (long long)layers[i]->staged);
+    if (layers[i]->stream != L0->stream && layers[i]->device != L0->device)
+      return fail(ARTLITE_EINVAL, "layer time: layers on different devices");
+    ART_TRY(check_ready(layers[i]));
+  }
+  // every layer runs on the first layer's stream (one ordered sequence)
+  std::vector<hipStream_t> own(n);
+  for (int i = 0; i < n; i++) {
+    own[i] = layers[i]->stream;
+    layers[i]->stream = L0->stream;
+  }
+  int rc = ARTLITE_OK;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  std::vector<hipEvent_t> ev;
+  const std::vector<std::string> names = kernel_list(L0);
+  const int nk = int(names.size());
+  auto done = [&](int code) {
+    for (int i = 0; i < n; i++) layers[i]->stream = own[i];
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    for (hipEvent_t x : ev) (void)hipEventDestroy(x);
+    return code;
+  };
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+    return done(fail(ARTLITE_EHIP, "layer time: events"));
+  hipStream_t s = L0->stream;
+  for (int i = 0; i < warmup; i++)
+    if ((rc = run(layers[i % n], T, nullptr)) != ARTLITE_OK) return done(rc);
+  if (hipStreamSynchronize(s) != hipSuccess) return done(fail(ARTLITE_EHIP, "layer time: sync"));
+  if (hipEventRecord(e0, s) != hipSuccess) return done(fail(ARTLITE_EHIP, "layer time: record"));
+  for (int i = 0; i < iters; i++)
+    if ((rc = run(layers[i % n], T, nullptr)) != ARTLITE_OK) return done(rc);
+  if (hipEventRecord(e1, s) != hipSuccess || hipEventSynchronize(e1) != hipSuccess)
+    return done(fail(ARTLITE_EHIP, "layer time: record"));
+  float ms = 0;
+  if (hipEventElapsedTime(&ms, e0, e1) != hipSuccess) return done(fail(ARTLITE_EHIP, "layer time: elapsed"));
+  *ms_per_run = double(ms) / iters;
+  if (n_kernels) *n_kernels = nk;
+  if (kernel_ms) {
+    // a second timed region with an event before each kernel and after the last
+    ev.resize(size_t(iters) * (nk + 1), nullptr);
+    for (hipEvent_t& x : ev)
+      if (hipEventCreate(&x) != hipSuccess) return done(fail(ARTLITE_EHIP, "layer time: events"));
+    for (int i = 0; i < iters; i++)
+      if ((rc = run(layers[i % n], T, ev.data() + size_t(i) * (nk + 1))) != ARTLITE_OK) return done(rc);
+    if (hipStreamSynchronize(s) != hipSuccess) return done(fail(ARTLITE_EHIP, "layer time: sync"));
+    std::vector<double> sum(nk, 0.0);
+    for (int i = 0; i < iters; i++)
+      for (int j = 0; j < nk; j++) {
+        float t = 0;
+        if (hipEventElapsedTime(&t, ev[size_t(i) * (nk + 1) + j], ev[size_t(i) * (nk + 1) + j + 1]) != hipSuccess)
+          return done(fail(ARTLITE_EHIP, "layer time: elapsed"));
+        sum[j] += t;
+      }
+    for (int j = 0; j < nk && j < kernel_cap; j++) kernel_ms[j] = sum[j] / iters;
+  }
+  return done(ARTLITE_OK);
+}

@@ -1,0 +1,107 @@
+"""The GPU MoE layer against the oracle, stage by stage through its taps, on every benchmark configuration:
+
+- router logits: float64 accumulation on both sides, so bit-exact fp32 logits (a rounding-boundary tie may differ by
+  one ulp);
+- routing: ids bit-exact against the C++ host routing's restatement applied to the GPU's logits, weights within one
+  fp32 ulp; ids equal to the layer oracle's (by probability, on its own logits) except where a near-tie leaves the
+  order to rounding;
+- dispatch: counts, offsets, sorted order and slots bit-exact against the stable counting sort of the GPU's ids;
+- experts: h = silu(x G^T) (x U^T) of each sorted pair and each pair's expert output against float64 math;
+- output: within 1e-3 relative L2 of the fp32 oracle (``moe_ffn`` + ``shared_expert``) and of float64 math for the
+  same routing; bitwise identical on a second run (deterministic kernels, no float atomics).
+Config sizes are reduced where the oracle would take long; the full sizes follow in test_layer_full_gpu.py."""
+
+import numpy as np
+import pytest
+
+from oracle import host_ref, layers, moe_ref
+
+from .helpers import gpu_input, gpu_layer, rel_l2, ulp_diff
+
+pytestmark = pytest.mark.gpu
+
+CASES = [("cpu", 16), ("decode", 1), ("decode", 4), ("decode", 16), ("decode", 64), ("prefill", 256),
+         ("deepseek", 64), ("skewed", 192)]
+
+
+def check_layer(name: str, T: int, seed: int = 0) -> None:
+    spec = layers.CONFIGS[name]
+    layer = layers.make_layer(spec, seed)
+    x = layers.make_x(spec, T, seed)
+    with gpu_layer(layer, max_tokens=T) as g:
+        y = g(gpu_input(spec, x))
+        lg = g.tap("logits")
+        ids, w = g.tap("ids"), g.tap("weights")
+        # logits
+        lg_ref = layers.logits(layer, x)
+        d = ulp_diff(lg, lg_ref)
+        assert d.max() <= 1 and (d == 0).mean() > 0.999, (name, T, d.max(), (d == 0).mean())
+        # routing of the GPU's logits: the host step's semantics, bit for bit
+        hids, hw = layers.route_host(layer, lg)
+        assert np.array_equal(ids, hids), name
+        assert ulp_diff(w, hw).max() <= 1
+        # the layer oracle's own routing: equal but where a near-tie leaves it to rounding
+        rids, rw = moe_ref.moe_route(lg_ref, spec.k)
+        srt = np.sort(lg_ref, axis=1)[:, ::-1]
+        gap = srt[:, :spec.k] - srt[:, 1:spec.k + 1]
+        near = (gap < 1e-5 * np.abs(srt[:, :spec.k]).max(1, keepdims=True)).any(1) | layers.tie_collapsed(lg_ref,
+                                                                                                       spec.k)
+        assert np.array_equal(ids[~near], rids[~near]), name
+        # dispatch
+        dref = host_ref.dispatch(ids, spec.E)
+        for tap in ("counts", "offsets", "order", "slot"):
+            assert np.array_equal(g.tap(tap), dref[tap]), tap
+        # experts: per sorted pair, h and the expert output against float64 math
+        get = layers.expert(layer)
+        order = dref["order"]
+        h, yp = g.tap("h"), g.tap("y_pairs")
+        x64 = x.astype(np.float64)
+        for e in np.unique(ids)[:6]:
+            s0, s1 = dref["offsets"][e], dref["offsets"][e + 1]
+            gw, uw, dw = (m.astype(np.float64) for m in get(int(e)))
+            xt = x64[order[s0:s1] // spec.k]
+            a = xt @ gw.T
+            h64 = a / (1 + np.exp(-a)) * (xt @ uw.T)
+            assert rel_l2(h[s0:s1], h64) < 1e-5, (name, e)
+            assert rel_l2(yp[s0:s1], h64 @ dw.T) < 1e-4, (name, e)
+        # output: the fp32 oracle and float64 math for the GPU's routing
+        want = moe_ref.moe_ffn(x, ids, w, get) + layers.shared_out(layer, x)
+        assert rel_l2(y, want) < 1e-3, (name, T, rel_l2(y, want))
+        y64 = layers.forward_f64(layer, x, ids, w)
+        assert rel_l2(y, y64) < 1e-3, (name, T, rel_l2(y, y64))
+        # determinism
+        assert np.array_equal(g(gpu_input(spec, x)).view(np.uint32), y.view(np.uint32))
+
+
+@pytest.mark.parametrize(("name", "T"), CASES)
+def test_layer(name: str, T: int) -> None:
+    check_layer(name, T)
+
+
+def test_layer_token_counts() -> None:
+    """One layer object for several token counts in turn (buffers sized for the largest), zero tokens included."""
+    spec = layers.CONFIGS["decode"]
+    layer = layers.make_layer(spec, 3)
+    with gpu_layer(layer, max_tokens=40) as g:
+        assert g(np.zeros((0, spec.H), np.uint16)).shape == (0, spec.H)
+        for T in (40, 3, 17):
+            x = layers.make_x(spec, T, T)
+            y = g(gpu_input(spec, x))
+            ids, w = g.tap("ids"), g.tap("weights")
+            assert rel_l2(y, layers.forward_f64(layer, x, ids, w)) < 1e-3
+
+
+def test_layer_errors() -> None:
+    from artlite_amd import Error
+    from artlite_amd.moe.layer import MoELayer
+
+    with pytest.raises(Error, match="K of E|of E"):
+        MoELayer(hidden=64, n_experts=4, top_k=5, expert_ffn=32, gate_type="Q4_0", down_type="Q4_0", max_tokens=4)
+    g = MoELayer(hidden=64, n_experts=4, top_k=2, expert_ffn=32, gate_type="Q4_0", down_type="Q4_0", max_tokens=4)
+    with pytest.raises(Error, match="not uploaded"):
+        g(np.zeros((2, 64), np.float32))
+    with pytest.raises(Error, match="is 10 bytes, not 1024"):
+        g.upload("ffn_gate_inp", np.zeros(10, np.uint8))
+    with pytest.raises(Error, match="5 tokens of at most 4"):
+        g.stage(np.zeros((5, 64), np.float32))
+    g.close()
