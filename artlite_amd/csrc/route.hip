@@ -76,7 +76,7 @@ __global__ __launch_bounds__(TOPK_WAVES * WAVE) void k_topk(const float* __restr
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   if (lane == 0) {
     double s = row_sum(ev[wv], k);
-    if (sigmoid) s = s > 6.103515625e-5 ? s : 6.103515625e-5;
+    if (sigmoid) s = s < 6.103515625e-5 ? 6.103515625e-5 : s;  // (std::max(s, 2^-14): a NaN sum stays NaN)
     sum[wv] = s;
   }
   __builtin_amdgcn_wave_barrier();
