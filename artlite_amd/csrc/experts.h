@@ -30,7 +30,9 @@ struct GemmArgs {
 };
 
 // rows of A (tokens / pairs) per tile of the decode (GEMV-like) kernel
-constexpr int DECODE_BM = 16;
+constexpr int DECODE_BM = 8;
+// the most 32-value groups of a row (K <= 32 MAX_GROUPS)
+constexpr int MAX_GROUPS = 128;
 
 int launch_expert_gemm(const GemmArgs& a, hipStream_t s);
 

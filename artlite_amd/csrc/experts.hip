@@ -59,77 +59,122 @@ __device__ __forceinline__ u32x4 byte8(uint32_t v0, uint32_t v1) {
   return u32x4{byte2(v0, 0), byte2(v0, 1), byte2(v1, 0), byte2(v1, 1)};
 }
 
+// Per format: bytes per 32-value group (in a run of whole blocks), the 32-value groups of one K-range (a stage:
+// ~560 bytes of each row, so a 16-row stage is 16 long runs; a straddled cache line is read again by the next range
+// of the same wave, from L2), the offset of the codes' bf16 encoding.
 template <int QT>
 struct Fmt;
 template <>
 struct Fmt<ARTLITE_Q4_0> {
-  static constexpr int GROUPS = 8;         // 32-value groups per stage
-  static constexpr int STAGE_BYTES = 144;  // a stage's bytes of a row
-  static constexpr float OFF = 136.0f;     // (128 + q) - (q - 8)
+  static constexpr int GROUP_BYTES = 18;
+  static constexpr int KR = 32;
+  static constexpr float OFF = 136.0f;  // (128 + q) - (q - 8)
 };
 template <>
 struct Fmt<ARTLITE_Q8_0> {
-  static constexpr int GROUPS = 4;
-  static constexpr int STAGE_BYTES = 136;
+  static constexpr int GROUP_BYTES = 34;
+  static constexpr int KR = 16;
   static constexpr float OFF = 128.0f;
 };
 template <>
 struct Fmt<ARTLITE_Q4_K> {
-  static constexpr int GROUPS = 8;  // (one super-block)
-  static constexpr int STAGE_BYTES = 144;
+  static constexpr int GROUP_BYTES = 18;  // (144 bytes per super-block of 8 groups)
+  static constexpr int KR = 32;
   static constexpr float OFF = 128.0f;
 };
 
-constexpr int CPR = 10;                 // 16-byte chunks per row and stage (the cover of <= 144 bytes at any offset)
-constexpr int SLOT = CPR * 16 + 16;     // a row's LDS bytes (padded: rows' groups fall in different banks)
-constexpr uint32_t ONES = 0x3F803F80u;  // bf16 1.0 pair
+// the 16-byte chunks of a 16-row stage: the aligned cover of each row's run; a row's LDS slot is an odd number of
+// 16-byte units, so the 16 rows' same-offset dwords fall in 16 different banks
+template <int QT>
+struct Stage {
+  static constexpr int BYTES = Fmt<QT>::KR * Fmt<QT>::GROUP_BYTES;
+  static constexpr int CPR = (BYTES + 15 + 15) / 16;
+  static constexpr int SLOT = 16 * (CPR | 1);
+  static constexpr int LOADS = (16 * CPR + WAVE - 1) / WAVE;  // per lane
+};
 
-// a stage's weight chunks (the 16-byte-aligned cover of each row's run) and A groups into registers
-template <class F, int LOADS, int AP>
-__device__ __forceinline__ void load_stage(int s, u32x4 (&wreg)[LOADS], u32x4 (&areg)[F::GROUPS][AP],
-                                           const int64_t (&roff)[LOADS], uint32_t second, const uint8_t* w0,
-                                           const uint8_t* w1, int lane, int lg, const uint16_t* ah,
-                                           const uint16_t* al, bool arow_ok, int ng) {
-  const int64_t off = int64_t(s) * F::STAGE_BYTES;
-#pragma unroll
-  for (int i = 0; i < LOADS; i++) {
-    const int64_t o = ((roff[i] + off) & ~int64_t(15)) + 16 * ((lane + WAVE * i) % CPR);
-    wreg[i] = *reinterpret_cast<const u32x4*>(((second >> i) & 1 ? w1 : w0) + o);
-  }
-  const int g0 = s * F::GROUPS;
-#pragma unroll
-  for (int g = 0; g < F::GROUPS; g++) {
-    const int k = min(g0 + g, ng - 1) * 32 + 8 * lg;
-    const bool ok = arow_ok && g0 + g < ng;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(ah + k);
-    areg[g][0] = ok ? v : u32x4{0, 0, 0, 0};
-    if (AP == 2) {
-      const u32x4 u = *reinterpret_cast<const u32x4*>(al + k);
-      areg[g][AP - 1] = ok ? u : u32x4{0, 0, 0, 0};
-    }
+// B operand of group gl of a row's run (row: its first byte in LDS) for lane group lg: 8 codes as 4 dwords of bf16,
+// and the scale (Q4_K: d sc, with dmin mn in mn)
+template <int QT>
+__device__ __forceinline__ u32x4 b_operand(const uint8_t* row, int gl, int lg, float& sc, float& mn) {
+  if (QT == ARTLITE_Q4_0) {
+    const uint8_t* blk = row + 18 * gl;
+    sc = h2f(lds_u16(blk));
+    const int sh = 4 * (lg >> 1);
+    const uint32_t u0 = (lds_u32(blk + 2 + 8 * (lg & 1)) >> sh) & 0x0F0F0F0Fu;
+    const uint32_t u1 = (lds_u32(blk + 6 + 8 * (lg & 1)) >> sh) & 0x0F0F0F0Fu;
+    return nib8(u0, u1);
+  } else if (QT == ARTLITE_Q8_0) {
+    const uint8_t* blk = row + 34 * gl;
+    sc = h2f(lds_u16(blk));
+    return byte8(lds_u32(blk + 2 + 8 * lg) ^ 0x80808080u, lds_u32(blk + 6 + 8 * lg) ^ 0x80808080u);
+  } else {  // Q4_K: group gl % 8 of the super-block at gl / 8
+    const uint8_t* sb = row + 144 * (gl >> 3);
+    const int g = gl & 7;
+    const float d = h2f(lds_u16(sb)), dmin = h2f(lds_u16(sb + 2));
+    const uint8_t* s6 = sb + 4;
+    const int q6 = g < 4 ? s6[g] & 63 : (s6[8 + g - 4] & 15) | ((s6[g - 4] >> 6) << 4);
+    const int m6 = g < 4 ? s6[4 + g] & 63 : (s6[8 + g - 4] >> 4) | ((s6[4 + g - 4] >> 6) << 4);
+    sc = __fmul_rn(d, float(q6));
+    mn = __fmul_rn(dmin, float(m6));
+    const uint8_t* qs = sb + 16 + 32 * (g >> 1) + 8 * lg;
+    const int sh = 4 * (g & 1);
+    return nib8((lds_u32(qs) >> sh) & 0x0F0F0F0Fu, (lds_u32(qs + 4) >> sh) & 0x0F0F0F0Fu);
   }
 }
 
-template <int LOADS>
-__device__ __forceinline__ void store_stage(const u32x4 (&wreg)[LOADS], uint8_t* my, int lane) {
+// One 16-row block's products over groups [0, gn) of its K-range (rows at rowp in LDS; this lane's A row at arow
+// in LDS; cin: -OFF group sums), ni scale FMAs per group (the lane's output rows that hold tokens).
+template <int QT, int AP, int KR, bool FULL>
+__device__ __forceinline__ f32x4 block_products(f32x4 acc, const uint8_t* rowp, const uint8_t* arow, int a_plane,
+                                                const float (*gsum)[16], int g0, int gn, int lg, int ni) {
+#pragma unroll 8
+  for (int gl = 0; gl < (FULL ? KR : gn); gl++) {
+    const int g = g0 + gl;
+    const u32x4 ahi = *reinterpret_cast<const u32x4*>(arow + 64 * g);
+    const f32x4 cin = *reinterpret_cast<const f32x4*>(&gsum[g][4 * lg]);
+    float sc, mn = 0.0f;
+    const u32x4 b = b_operand<QT>(rowp, gl, lg, sc, mn);
+    f32x4 p = mfma(ahi, b, cin);
+    if (AP == 2) p = mfma(*reinterpret_cast<const u32x4*>(arow + a_plane + 64 * g), b, p);
 #pragma unroll
-  for (int i = 0; i < LOADS; i++) {
-    const int q = lane + WAVE * i;
-    *reinterpret_cast<u32x4*>(my + (q / CPR) * SLOT + 16 * (q % CPR)) = wreg[i];
+    for (int i = 0; i < 4; i++)
+      if (i < ni) {
+        acc[i] = __builtin_fmaf(sc, p[i], acc[i]);
+        if (QT == ARTLITE_Q4_K) acc[i] = __builtin_fmaf(mn, cin[i] * (1.0f / Fmt<QT>::OFF), acc[i]);
+      }
   }
+  return acc;
 }
 
-template <int QT, int NMAT, int CB, int AP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gemm_decode(const GemmArgs a) {
+// MFMA row of tile token t (and back): token t in row 4 (t % 4) + t / 4, so a lane's output i = 0 holds tokens
+// 0 .. 3 across its four lane groups and output i = 1 tokens 4 .. 7: ceil(tokens / 4) scale FMAs per group
+__device__ __forceinline__ int token_of_row(int m) { return 4 * (m % 4) + m / 4; }
+
+// Decode kernel: a workgroup is one tile of DECODE_BM sorted rows of one expert (tokens for gate / up, pairs for
+// down) times RB weight rows per matrix. The tile's A rows (its valid ones, all of K; both planes when A is split)
+// are staged in LDS once, with the group sums that correct the codes' offset. SwiGLU: waves 0, 1 stream gate rows,
+// waves 2, 3 the same up rows (h is formed after an exchange through LDS); plain: 4 different 16-row blocks. A wave
+// takes BLK 16-row blocks, each in K-ranges of Fmt::KR groups (units); two units' chunks are in flight in registers
+// while the current one computes from the wave's LDS slot, and no other load is issued during the products.
+template <int QT, bool SWIGLU, int AP, int BLK>
+__global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs a) {
   using F = Fmt<QT>;
-  constexpr int RW = 16 * CB;      // rows per matrix per wave
-  constexpr int ROWS = NMAT * RW;  // rows per wave
-  constexpr int LOADS = ROWS * CPR / WAVE;
-  static_assert(ROWS * CPR % WAVE == 0, "loads per lane");
-  __shared__ __attribute__((aligned(16))) uint8_t lds[4][ROWS * SLOT];
+  using S = Stage<QT>;
+  constexpr int WPM = SWIGLU ? 2 : 4;  // waves per matrix
+  constexpr int RB = 16 * WPM * BLK;   // rows per matrix per workgroup
+  static_assert(BLK == 1 || BLK == 2, "blocks per wave");
+  static_assert(DECODE_BM <= 16, "tile rows");
+  const int ng = a.K / 32;
+  const int a_plane = a.K * 2;               // bytes of one plane of a staged A row
+  const int arow_bytes = a_plane * AP + 16;  // (padded: the 16 lanes' rows fall in 16 bank groups)
+  // LDS: the waves' slots (4 x 16 rows) | the tile's A rows | group sums [ng][16] (by MFMA row) | up accumulators
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  uint8_t* as = lds + 4 * 16 * S::SLOT;
+  float(*gsum)[16] = reinterpret_cast<float(*)[16]>(as + DECODE_BM * arow_bytes);
+  f32x4* xch = reinterpret_cast<f32x4*>(as + DECODE_BM * arow_bytes + ng * 16 * 4);
 
   const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE, lg = lane >> 4, lr = lane & 15;
-  // the tile
   int e = 0, s0, m_valid;
   if (a.tiles) {
     if (int64_t(blockIdx.x) >= *a.n_tiles) return;
@@ -140,141 +185,146 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     s0 = blockIdx.x * DECODE_BM;
     m_valid = min(DECODE_BM, a.dense_rows - s0);
   }
-  const int n0 = (blockIdx.y * 4 + wv) * RW;  // the wave's first row of each matrix
-  uint8_t* my = lds[wv];
+  const int mtx = SWIGLU ? wv / 2 : 0;
+  const uint8_t* wbase = (mtx ? a.w[1] : a.w[0]) + e * a.expert_bytes;
+  const int ns = (ng + F::KR - 1) / F::KR;  // K-ranges per block
+  const int sub = SWIGLU ? wv % 2 : wv;
+  const int n0 = blockIdx.y * RB;
+  const int units = BLK * ns;
+  uint8_t* my = lds + wv * 16 * S::SLOT;
 
-  // A row of this lane (row lr of the tile; lanes past the tile read row s0 and are zeroed)
-  const bool arow_ok = lr < m_valid;
-  const int64_t arow = a.a_gather ? a.order[s0 + (arow_ok ? lr : 0)] / a.topk : s0 + (arow_ok ? lr : 0);
-  const uint16_t* ah = a.a_hi + arow * a.K;
-  const uint16_t* al = a.a_lo + (AP == 2 ? arow * a.K : 0);
-
-  // the loader's chunks: chunk q = lane + 64 i -> (row q / CPR, chunk q % CPR); rows past N read row N - 1
-  int64_t roff[LOADS];
-  uint32_t second = 0;  // bit i: chunk i is of the second matrix
+  u32x4 wa[S::LOADS], wb[S::LOADS];  // (two units in flight)
+  auto load_unit = [&](int u, u32x4(&w)[S::LOADS]) {
+    const int j = u / ns, kr = u % ns;
+    const int r0 = n0 + 16 * (sub + WPM * j);
+    const int64_t koff = int64_t(kr) * F::KR * F::GROUP_BYTES;
 #pragma unroll
-  for (int i = 0; i < LOADS; i++) {
-    const int q = lane + WAVE * i, r = q / CPR;
-    const int m = r / RW, rr = min(n0 + r % RW, a.N - 1);
-    second |= uint32_t(m) << i;
-    roff[i] = e * a.expert_bytes + int64_t(rr) * a.row_bytes;
+    for (int i = 0; i < S::LOADS; i++) {
+      const int q = min(lane + WAVE * i, 16 * S::CPR - 1);
+      const int r = min(r0 + q / S::CPR, a.N - 1);
+      const int64_t o = ((int64_t(r) * a.row_bytes + koff) & ~int64_t(15)) + 16 * (q % S::CPR);
+      w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wbase + o));
+    }
+  };
+  auto store_unit = [&](const u32x4(&w)[S::LOADS]) {
+#pragma unroll
+    for (int i = 0; i < S::LOADS; i++) {
+      const int q = min(lane + WAVE * i, 16 * S::CPR - 1);
+      *reinterpret_cast<u32x4*>(my + (q / S::CPR) * S::SLOT + 16 * (q % S::CPR)) = w[i];
+    }
+  };
+  load_unit(0, wa);
+  if (units > 1) load_unit(1, wb);
+
+  // stage the tile's valid A rows: row t = [hi plane (K bf16) | lo plane | pad]
+  {
+    const int per_row = a.K / 8;  // 16-byte pieces per plane
+    for (int i = threadIdx.x; i < m_valid * AP * per_row; i += 256) {
+      const int t = i / (AP * per_row), rest = i % (AP * per_row), pl = rest / per_row, c = rest % per_row;
+      const int64_t r = a.a_gather ? int64_t(a.order[s0 + t]) / a.topk : int64_t(s0 + t);
+      const uint16_t* src = (pl ? a.a_lo : a.a_hi) + r * a.K + 8 * c;
+      *reinterpret_cast<u32x4*>(as + t * arow_bytes + pl * a_plane + 16 * c) = *reinterpret_cast<const u32x4*>(src);
+    }
   }
-  const uint8_t* w0 = a.w[0];
-  const uint8_t* w1 = a.w[NMAT - 1];
-  // the lane's rows' address low bits (matrix m, column block c)
-  int mis0[CB];
+  __syncthreads();
+  // group sums by MFMA row m: gsum[g][m] = -OFF sum over group g of A[token_of_row(m)] (zero past the tile)
+  for (int i = threadIdx.x; i < ng * 16; i += 256) {
+    const int g = i / 16, m = i % 16, t = token_of_row(m);
+    float sum = 0.0f;
+    if (t < m_valid)
 #pragma unroll
-  for (int c = 0; c < CB; c++) mis0[c] = int((e * a.expert_bytes + int64_t(n0 + 16 * c + lr) * a.row_bytes) & 15);
-
-  const int ng = a.K / 32;  // groups per row
-  const int ns = (ng + F::GROUPS - 1) / F::GROUPS;
-
-  u32x4 wreg[LOADS];
-  u32x4 acur[F::GROUPS][AP], anext[F::GROUPS][AP];
-  load_stage<F, LOADS, AP>(0, wreg, acur, roff, second, w0, w1, lane, lg, ah, al, arow_ok, ng);
-  store_stage<LOADS>(wreg, my, lane);
-
-  f32x4 acc[NMAT][CB];
+      for (int pl = 0; pl < AP; pl++) {
+        const u32x4* p = reinterpret_cast<const u32x4*>(as + t * arow_bytes + pl * a_plane + 64 * g);
 #pragma unroll
-  for (int m = 0; m < NMAT; m++)
+        for (int j = 0; j < 4; j++) {
+          const u32x4 v = p[j];
 #pragma unroll
-    for (int c = 0; c < CB; c++) acc[m][c] = f32x4{0, 0, 0, 0};
-
-  for (int s = 0; s < ns; s++) {
-    if (s + 1 < ns) load_stage<F, LOADS, AP>(s + 1, wreg, anext, roff, second, w0, w1, lane, lg, ah, al, arow_ok, ng);
-    __builtin_amdgcn_wave_barrier();
-    const int gn = min(F::GROUPS, ng - s * F::GROUPS);
-    const int64_t off = int64_t(s) * F::STAGE_BYTES;
-#pragma unroll
-    for (int g = 0; g < F::GROUPS; g++) {
-      if (g < gn) {
-        // sum x of the lane's four outputs' tokens: the C input of the group's products
-        f32x4 sx = mfma(acur[g][0], u32x4{ONES, ONES, ONES, ONES}, f32x4{0, 0, 0, 0});
-        if (AP == 2) sx = mfma(acur[g][AP - 1], u32x4{ONES, ONES, ONES, ONES}, sx);
-        const f32x4 cin = sx * (-F::OFF);
-#pragma unroll
-        for (int m = 0; m < NMAT; m++)
-#pragma unroll
-          for (int c = 0; c < CB; c++) {
-            const uint8_t* row = my + (m * RW + 16 * c + lr) * SLOT + ((mis0[c] + off) & 15);
-            u32x4 b;
-            float sc;
-            float mn = 0.0f;
-            if (QT == ARTLITE_Q4_0) {
-              const uint8_t* blk = row + 18 * g;
-              sc = h2f(lds_u16(blk));
-              const int sh = 4 * (lg >> 1);
-              const uint32_t u0 = (lds_u32(blk + 2 + 8 * (lg & 1)) >> sh) & 0x0F0F0F0Fu;
-              const uint32_t u1 = (lds_u32(blk + 6 + 8 * (lg & 1)) >> sh) & 0x0F0F0F0Fu;
-              b = nib8(u0, u1);
-            } else if (QT == ARTLITE_Q8_0) {
-              const uint8_t* blk = row + 34 * g;
-              sc = h2f(lds_u16(blk));
-              const uint32_t u0 = lds_u32(blk + 2 + 8 * lg) ^ 0x80808080u;
-              const uint32_t u1 = lds_u32(blk + 6 + 8 * lg) ^ 0x80808080u;
-              b = byte8(u0, u1);
-            } else {  // Q4_K: group g of the stage's super-block
-              const float d = h2f(lds_u16(row)), dmin = h2f(lds_u16(row + 2));
-              const uint8_t* s6 = row + 4;
-              const int q6 = g < 4 ? s6[g] & 63 : (s6[8 + g - 4] & 15) | ((s6[g - 4] >> 6) << 4);
-              const int m6 = g < 4 ? s6[4 + g] & 63 : (s6[8 + g - 4] >> 4) | ((s6[4 + g - 4] >> 6) << 4);
-              sc = __fmul_rn(d, float(q6));
-              mn = __fmul_rn(dmin, float(m6));
-              const uint8_t* qs = row + 16 + 32 * (g >> 1) + 8 * lg;
-              const int sh = 4 * (g & 1);
-              b = nib8((lds_u32(qs) >> sh) & 0x0F0F0F0Fu, (lds_u32(qs + 4) >> sh) & 0x0F0F0F0Fu);
-            }
-            f32x4 p = mfma(acur[g][0], b, cin);
-            if (AP == 2) p = mfma(acur[g][AP - 1], b, p);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-              acc[m][c][i] = __builtin_fmaf(sc, p[i], acc[m][c][i]);
-              if (QT == ARTLITE_Q4_K) acc[m][c][i] = __builtin_fmaf(-mn, sx[i], acc[m][c][i]);
-            }
-          }
+          for (int q = 0; q < 4; q++) sum += bf16_to_f32(v[q] & 0xFFFFu) + bf16_to_f32(v[q] >> 16);
+        }
       }
-    }
-    if (s + 1 < ns) {
-      __builtin_amdgcn_wave_barrier();
-      store_stage<LOADS>(wreg, my, lane);
+    gsum[g][m] = -F::OFF * sum;
+  }
+  __syncthreads();
+
+  // this lane's A row: the token of MFMA row lr (rows without a token repeat token 0: they only feed outputs that
+  // are never stored, since MFMA output row m depends on A row m alone)
+  const int tl = token_of_row(lr);
+  const uint8_t* arow = as + (tl < m_valid ? tl : 0) * arow_bytes + 16 * lg;
+  const int ni = (m_valid + 3) / 4;  // outputs per lane that hold tokens
+
+  f32x4 acc[BLK];
 #pragma unroll
-      for (int g = 0; g < F::GROUPS; g++)
-#pragma unroll
-        for (int p = 0; p < AP; p++) acur[g][p] = anext[g][p];
+  for (int j = 0; j < BLK; j++) acc[j] = f32x4{0, 0, 0, 0};
+  for (int u = 0; u < units; u++) {
+    const int j = u / ns, kr = u % ns;
+    // this unit's chunks: wa (even units) or wb (odd); then the unit two ahead into the freed registers
+    __builtin_amdgcn_wave_barrier();
+    if (u & 1) {
+      store_unit(wb);
+      if (u + 2 < units) load_unit(u + 2, wb);
+    } else {
+      store_unit(wa);
+      if (u + 2 < units) load_unit(u + 2, wa);
     }
+    __builtin_amdgcn_wave_barrier();
+    const int r = min(n0 + 16 * (sub + WPM * j) + lr, a.N - 1);
+    const uint8_t* rowp =
+        my + lr * S::SLOT + ((int64_t(r) * a.row_bytes + int64_t(kr) * F::KR * F::GROUP_BYTES) & 15);
+    const int g0 = kr * F::KR, gn = min(F::KR, ng - g0);
+    f32x4 accj = (BLK > 1 && j) ? acc[BLK - 1] : acc[0];
+    if (gn == F::KR)
+      accj = block_products<QT, AP, F::KR, true>(accj, rowp, arow, a_plane, gsum, g0, gn, lg, ni);
+    else
+      accj = block_products<QT, AP, F::KR, false>(accj, rowp, arow, a_plane, gsum, g0, gn, lg, ni);
+    if (BLK > 1 && j)
+      acc[BLK - 1] = accj;
+    else
+      acc[0] = accj;
   }
 
-  // epilogue: lane holds rows (tokens / pairs) 4 lg + i of output column n0 + 16 c + lr
+  // epilogue: lane output i of block j holds token 4 i + lg of the tile, column n0 + 16 (sub + WPM j) + lr
+  if (SWIGLU) {
+    if (mtx == 1)
 #pragma unroll
-  for (int c = 0; c < CB; c++) {
-    const int n = n0 + 16 * c + lr;
+      for (int j = 0; j < BLK; j++) xch[(sub * BLK + j) * WAVE + lane] = acc[j];
+    __syncthreads();
+    if (mtx == 1) return;
+  }
+#pragma unroll
+  for (int j = 0; j < BLK; j++) {
+    const int n = n0 + 16 * (sub + WPM * j) + lr;
     if (n >= a.N) continue;
+    f32x4 up = acc[j];
+    if (SWIGLU) up = xch[(sub * BLK + j) * WAVE + lane];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const int m = 4 * lg + i;
-      if (m >= m_valid) continue;
-      const int64_t o = int64_t(s0 + m) * a.N + n;
-      if (NMAT == 2) {
-        const float g = acc[0][c][i], u = acc[1][c][i];
-        const float h = g / (1.0f + expf(-g)) * u;
+      const int t = 4 * i + lg;
+      if (t >= m_valid) continue;
+      const int64_t o = int64_t(s0 + t) * a.N + n;
+      if (SWIGLU) {
+        const float g = acc[j][i];
+        const float h = g / (1.0f + expf(-g)) * up[i];
         const uint32_t hi = f32_to_bf16(h);
         a.h_hi[o] = uint16_t(hi);
         a.h_lo[o] = uint16_t(f32_to_bf16(h - bf16_to_f32(hi)));
       } else {
-        a.y[o] = acc[0][c][i];
+        a.y[o] = acc[j][i];
       }
     }
   }
 }
 
-template <int QT, int NMAT, int CB>
+template <int QT, bool SWIGLU, int BLK>
 int launch_decode(const GemmArgs& a, hipStream_t s) {
+  constexpr int RB = 16 * (SWIGLU ? 2 : 4) * BLK;
   const int64_t tiles = a.tiles ? a.max_tiles : (a.dense_rows + DECODE_BM - 1) / DECODE_BM;
-  const dim3 grid(unsigned(tiles), unsigned((a.N + 4 * 16 * CB - 1) / (4 * 16 * CB))), block(256);
+  const dim3 grid(unsigned(tiles), unsigned((a.N + RB - 1) / RB)), block(256);
+  const size_t lds = 4 * 16 * Stage<QT>::SLOT + size_t(DECODE_BM) * (size_t(a.K) * 2 * (a.a_lo ? 2 : 1) + 16) +
+                     size_t(a.K / 32) * 16 * 4 + (SWIGLU ? 2 * BLK * WAVE * 16 : 0);
   if (a.a_lo)
-    k_gemm_decode<QT, NMAT, CB, 2><<<grid, block, 0, s>>>(a);
+    k_gemm_decode<QT, SWIGLU, 2, BLK><<<grid, block, lds, s>>>(a);
   else
-    k_gemm_decode<QT, NMAT, CB, 1><<<grid, block, 0, s>>>(a);
+    k_gemm_decode<QT, SWIGLU, 1, BLK><<<grid, block, lds, s>>>(a);
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
 }
@@ -282,11 +332,11 @@ int launch_decode(const GemmArgs& a, hipStream_t s) {
 int launch_expert_gemm(const GemmArgs& a, hipStream_t s) {
   if (a.K % 32 || (a.qtype == ARTLITE_Q4_K && a.K % 256))
     return fail(ARTLITE_EINVAL, "expert GEMM: K %d is not a multiple of the format's block", a.K);
+  if (a.K / 32 > MAX_GROUPS) return fail(ARTLITE_EINVAL, "expert GEMM: K %d beyond %d", a.K, 32 * MAX_GROUPS);
   const int64_t tiles = a.tiles ? a.max_tiles : (a.dense_rows + DECODE_BM - 1) / DECODE_BM;
   if (tiles <= 0) return ARTLITE_OK;
   const bool swiglu = a.w[1] != nullptr;
-#define ART_DISPATCH(QT) \
-  return swiglu ? launch_decode<QT, 2, 2>(a, s) : launch_decode<QT, 1, 4>(a, s)
+#define ART_DISPATCH(QT) return swiglu ? launch_decode<QT, true, 2>(a, s) : launch_decode<QT, false, 2>(a, s)
   switch (a.qtype) {
     case ARTLITE_Q4_0: ART_DISPATCH(ARTLITE_Q4_0);
     case ARTLITE_Q8_0: ART_DISPATCH(ARTLITE_Q8_0);

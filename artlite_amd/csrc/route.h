@@ -7,7 +7,9 @@ namespace artlite {
 
 constexpr int MAX_EXPERTS = 1024;  // (keys per lane: 16)
 constexpr int MAX_TOPK = 64;       // (one lane per chosen expert)
-constexpr int ROUTER_TG = 16;      // tokens per router wave
+constexpr int ROUTER_TG = 16;      // tokens per router block (at most)
+constexpr int ROUTER_EW = 8;       // experts (waves) per router block
+constexpr int ROUTER_LDS = 64 * 1024;  // bytes of staged token rows per router block
 
 int check_route_args(int64_t n, int per_col, int E, int k);
 

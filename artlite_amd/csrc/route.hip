@@ -7,6 +7,8 @@
 // order (moe_host.cpp:25-39), e / sum rounded to fp32.
 #include "route.h"
 
+#include <algorithm>
+
 namespace artlite {
 
 __device__ __forceinline__ uint64_t logit_key(float l, int e) {
@@ -110,42 +112,74 @@ int launch_topk(const float* logits, int64_t n, int64_t row, int per_col, int64_
   return ARTLITE_OK;
 }
 
-// Router logits: one wave per (expert e, group of ROUTER_TG tokens); lane partial sums over h = lane + 64 j in
-// float64 (exact products of fp32 / bf16 values), a fixed shuffle tree, rounded to fp32.
+// Router logits: a block of ROUTER_EW waves (one expert each) over a tile of up to ROUTER_TG tokens whose rows are
+// staged in LDS; each lane accumulates float64 partial dot products (exact products of fp32 / bf16 values) over
+// h = 4 lane + 256 j, then a fixed shuffle tree; the sum is rounded once to fp32.
 template <int XT>
-__global__ __launch_bounds__(4 * WAVE) void k_router(const void* __restrict__ xv, const float* __restrict__ W, int H,
-                                                     int E, int64_t T, float* __restrict__ out, int64_t out_row) {
-  const int lane = threadIdx.x & (WAVE - 1);
-  const int64_t wid = int64_t(blockIdx.x) * 4 + threadIdx.x / WAVE;
-  const int64_t groups = (T + ROUTER_TG - 1) / ROUTER_TG;
-  if (wid >= int64_t(E) * groups) return;
-  const int e = int(wid % E);
-  const int64_t t0 = (wid / E) * ROUTER_TG;
+__global__ __launch_bounds__(ROUTER_EW * WAVE) void k_router(const void* __restrict__ xv, const float* __restrict__ W,
+                                                            int H, int E, int64_t T, int tt, float* __restrict__ out,
+                                                            int64_t out_row) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t xs[];  // tt rows of H values (x's own dtype)
+  constexpr int XB = XT == ARTLITE_X_F32 ? 4 : 2;
+  const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE;
+  const int64_t t0 = int64_t(blockIdx.y) * tt;
+  const int nt = int(min(int64_t(tt), T - t0));
+  {  // stage the tile's rows (16-byte pieces)
+    const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(xv) + t0 * H * XB);
+    uint4* dst = reinterpret_cast<uint4*>(xs);
+    const int n16 = nt * H * XB / 16;
+    for (int i = threadIdx.x; i < n16; i += blockDim.x) dst[i] = src[i];
+  }
+  __syncthreads();
+  const int e = blockIdx.x * ROUTER_EW + wv;
+  if (e >= E) return;
   const float* w = W + int64_t(e) * H;
-  for (int64_t t = t0; t < t0 + ROUTER_TG && t < T; t++) {
-    double acc = 0;
-    if (XT == ARTLITE_X_F32) {
-      const float* x = static_cast<const float*>(xv) + t * H;
-      for (int h = lane; h < H; h += WAVE) acc += double(x[h]) * double(w[h]);
-    } else {
-      const uint16_t* x = static_cast<const uint16_t*>(xv) + t * H;
-      for (int h = lane; h < H; h += WAVE) acc += double(bf16_to_f32(x[h])) * double(w[h]);
-    }
+  double acc[ROUTER_TG];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, WAVE);
-    if (lane == 0) out[t * out_row + e] = float(acc);
+  for (int t = 0; t < ROUTER_TG; t++) acc[t] = 0.0;
+  for (int h = 4 * lane; h < H; h += 4 * WAVE) {
+    const float4 wq = *reinterpret_cast<const float4*>(w + h);
+#pragma unroll
+    for (int t = 0; t < ROUTER_TG; t++) {
+      if (t < nt) {
+        float x0, x1, x2, x3;
+        if (XT == ARTLITE_X_F32) {
+          const float4 v = *reinterpret_cast<const float4*>(xs + (int64_t(t) * H + h) * 4);
+          x0 = v.x, x1 = v.y, x2 = v.z, x3 = v.w;
+        } else {
+          const uint2 v = *reinterpret_cast<const uint2*>(xs + (int64_t(t) * H + h) * 2);
+          x0 = bf16_to_f32(v.x & 0xFFFFu), x1 = bf16_to_f32(v.x >> 16);
+          x2 = bf16_to_f32(v.y & 0xFFFFu), x3 = bf16_to_f32(v.y >> 16);
+        }
+        acc[t] += double(x0) * double(wq.x);
+        acc[t] += double(x1) * double(wq.y);
+        acc[t] += double(x2) * double(wq.z);
+        acc[t] += double(x3) * double(wq.w);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < ROUTER_TG; t++) {
+    double v = acc[t];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    if (lane == 0 && t < nt) out[(t0 + t) * out_row + e] = float(v);
   }
 }
 
 int launch_router(const void* x, int x_dtype, const float* W, int H, int E, int64_t T, float* out, int64_t out_row,
                   hipStream_t s) {
   if (T <= 0) return ARTLITE_OK;
-  const int64_t waves = int64_t(E) * ((T + ROUTER_TG - 1) / ROUTER_TG);
-  const dim3 grid(unsigned((waves + 3) / 4)), block(4 * WAVE);
+  if (H % 8) return fail(ARTLITE_EINVAL, "router: H %d not a multiple of 8", H);
+  const int xb = x_dtype == ARTLITE_X_F32 ? 4 : 2;
+  const int tt = int(std::min<int64_t>(ROUTER_TG, std::max<int64_t>(1, ROUTER_LDS / (int64_t(H) * xb))));
+  if (int64_t(H) * xb > ROUTER_LDS) return fail(ARTLITE_EINVAL, "router: H %d too wide", H);
+  const dim3 grid(unsigned((E + ROUTER_EW - 1) / ROUTER_EW), unsigned((T + tt - 1) / tt)), block(ROUTER_EW * WAVE);
+  const size_t lds = size_t(tt) * H * xb;
   if (x_dtype == ARTLITE_X_F32)
-    k_router<ARTLITE_X_F32><<<grid, block, 0, s>>>(x, W, H, E, T, out, out_row);
+    k_router<ARTLITE_X_F32><<<grid, block, lds, s>>>(x, W, H, E, T, tt, out, out_row);
   else
-    k_router<ARTLITE_X_BF16><<<grid, block, 0, s>>>(x, W, H, E, T, out, out_row);
+    k_router<ARTLITE_X_BF16><<<grid, block, lds, s>>>(x, W, H, E, T, tt, out, out_row);
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
 }
