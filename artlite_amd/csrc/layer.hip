@@ -6,6 +6,7 @@
 #include <vector>
 
 #include "experts.h"
+#include "gemv.h"
 #include "route.h"
 
 using namespace artlite;
@@ -25,7 +26,10 @@ struct artlite_moe_layer {
   DevBuf logits, ids, w, sg;
   DevBuf table, ctrl, counts, offsets, order, slot, tiles;
   DevBuf hhi, hlo, ypairs, shhi, shlo, ys, y;
+  DevBuf xq, hq, shq;  // the decode path's XQ activations
+  bool gemv_ok = false, shared_gemv_ok = false;
   int64_t last_T = -1;
+  bool last_gemv = false;
 };
 
 namespace {
@@ -75,10 +79,31 @@ int check_ready(const artlite_moe_layer* L) {
   return ARTLITE_OK;
 }
 
+// The kernels a forward pass of T tokens takes. Decode-sized passes (at most GEMV_BM pairs per expert on
+// average) run the experts on the VALU GEMV over XQ activations; larger ones on the MFMA tiles over bf16 planes.
+struct Path {
+  bool gemv;         // routed experts on the GEMV
+  bool shared_gemv;  // the shared expert on the GEMV
+  bool split;        // bf16 hi / lo planes of fp32 x needed
+  bool quant;        // XQ of x needed
+};
+
+Path path_of(const artlite_moe_layer* L, int64_t T) {
+  Path p{};
+  p.gemv = L->gemv_ok && T * L->d.top_k <= int64_t(GEMV_BM) * L->d.n_experts;
+  p.shared_gemv = L->d.shared_ffn && p.gemv && L->shared_gemv_ok;
+  const bool mfma_x = !p.gemv || (L->d.shared_ffn && !p.shared_gemv);
+  p.split = mfma_x && L->x_dtype == ARTLITE_X_F32;
+  p.quant = p.gemv;
+  return p;
+}
+
 // the named kernels of a forward pass, in launch order
-std::vector<std::string> kernel_list(const artlite_moe_layer* L) {
+std::vector<std::string> kernel_list(const artlite_moe_layer* L, int64_t T) {
+  const Path p = path_of(L, T);
   std::vector<std::string> k;
-  if (L->x_dtype == ARTLITE_X_F32) k.push_back("split");
+  if (p.quant) k.push_back("quant");
+  if (p.split) k.push_back("split");
   k.push_back("router");
   if (L->d.shared_ffn && L->d.shared_gated) k.push_back("shared_gate");
   k.push_back("topk");
@@ -106,14 +131,17 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     if (ev) ART_HIP(hipEventRecord(ev[ei++], s));
     return ARTLITE_OK;
   };
-  const uint16_t *ahi, *alo = nullptr;
-  if (L->x_dtype == ARTLITE_X_F32) {
+  const Path path = path_of(L, T);
+  if (path.quant) {
+    ART_TRY(mark());
+    ART_TRY(launch_quant(L->x.p, L->x_dtype, T, H, L->xq.as<uint32_t>(), s));
+  }
+  const uint16_t *ahi = L->x.as<uint16_t>(), *alo = nullptr;
+  if (path.split) {
     ART_TRY(mark());
     ART_TRY(launch_split(L->x.as<float>(), T * H, L->xhi.as<uint16_t>(), L->xlo.as<uint16_t>(), s));
     ahi = L->xhi.as<uint16_t>();
     alo = L->xlo.as<uint16_t>();
-  } else {
-    ahi = L->x.as<uint16_t>();
   }
   ART_TRY(mark());
   ART_TRY(launch_router(L->x.p, L->x_dtype, L->router.as<float>(), H, E, T, L->logits.as<float>(), E, s));
@@ -124,7 +152,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
   ART_TRY(mark());
   ART_TRY(launch_topk(L->logits.as<float>(), T, E, E, 0, E, k, d.gating, L->ids.as<int32_t>(), L->w.as<float>(),
                       nullptr, s));
-  const int BM = DECODE_BM;
+  const int BM = path.gemv ? GEMV_BM : DECODE_BM;
   DispatchBufs db{L->ids.as<int32_t>(), P, E, k, L->table.as<int32_t>(), L->ctrl.as<int32_t>(),
                   L->counts.as<int32_t>(), L->offsets.as<int32_t>(), L->order.as<int32_t>(), L->slot.as<int32_t>(),
                   L->tiles.as<int32_t>(), BM, nullptr, 0};
@@ -135,43 +163,104 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     ART_TRY(mark());
     ART_TRY(launch_dispatch_scatter(db, nb, s));
   }
-  GemmArgs g{};
-  g.w[0] = L->gate.as<uint8_t>();
-  g.w[1] = L->up.as<uint8_t>();
-  g.expert_bytes = int64_t(F) * L->gate_row;
-  g.row_bytes = int(L->gate_row);
-  g.N = F;
-  g.K = H;
-  g.qtype = d.gate_type;
-  g.a_hi = ahi;
-  g.a_lo = alo;
-  g.a_gather = 1;
-  g.order = L->order.as<int32_t>();
-  g.topk = k;
-  g.tiles = L->tiles.as<int32_t>();
-  g.n_tiles = L->ctrl.as<int32_t>() + CTRL_TILES;
-  g.offsets = L->offsets.as<int32_t>();
-  g.max_tiles = tile_bound(P, E, BM);
-  g.h_hi = L->hhi.as<uint16_t>();
-  g.h_lo = L->hlo.as<uint16_t>();
-  ART_TRY(mark());
-  ART_TRY(launch_expert_gemm(g, s));
-  GemmArgs dn = g;
-  dn.w[0] = L->down.as<uint8_t>();
-  dn.w[1] = nullptr;
-  dn.expert_bytes = int64_t(H) * L->down_row;
-  dn.row_bytes = int(L->down_row);
-  dn.N = H;
-  dn.K = F;
-  dn.qtype = d.down_type;
-  dn.a_hi = L->hhi.as<uint16_t>();
-  dn.a_lo = L->hlo.as<uint16_t>();
-  dn.a_gather = 0;
-  dn.y = L->ypairs.as<float>();
-  ART_TRY(mark());
-  ART_TRY(launch_expert_gemm(dn, s));
+  if (path.gemv) {
+    GemvArgs g{};
+    g.w[0] = L->gate.as<uint8_t>();
+    g.w[1] = L->up.as<uint8_t>();
+    g.expert_bytes = int64_t(F) * L->gate_row;
+    g.row_bytes = int(L->gate_row);
+    g.N = F;
+    g.K = H;
+    g.qtype = d.gate_type;
+    g.xq = L->xq.as<uint32_t>();
+    g.a_gather = 1;
+    g.order = L->order.as<int32_t>();
+    g.topk = k;
+    g.tiles = L->tiles.as<int32_t>();
+    g.n_tiles = L->ctrl.as<int32_t>() + CTRL_TILES;
+    g.offsets = L->offsets.as<int32_t>();
+    g.max_tiles = tile_bound(P, E, BM);
+    g.hq = L->hq.as<uint32_t>();
+    ART_TRY(mark());
+    ART_TRY(launch_gemv(g, s));
+    GemvArgs dn = g;
+    dn.w[0] = L->down.as<uint8_t>();
+    dn.w[1] = nullptr;
+    dn.expert_bytes = int64_t(H) * L->down_row;
+    dn.row_bytes = int(L->down_row);
+    dn.N = H;
+    dn.K = F;
+    dn.qtype = d.down_type;
+    dn.xq = L->hq.as<uint32_t>();
+    dn.a_gather = 0;
+    dn.hq = nullptr;
+    dn.y = L->ypairs.as<float>();
+    ART_TRY(mark());
+    ART_TRY(launch_gemv(dn, s));
+  } else {
+    GemmArgs g{};
+    g.w[0] = L->gate.as<uint8_t>();
+    g.w[1] = L->up.as<uint8_t>();
+    g.expert_bytes = int64_t(F) * L->gate_row;
+    g.row_bytes = int(L->gate_row);
+    g.N = F;
+    g.K = H;
+    g.qtype = d.gate_type;
+    g.a_hi = ahi;
+    g.a_lo = alo;
+    g.a_gather = 1;
+    g.order = L->order.as<int32_t>();
+    g.topk = k;
+    g.tiles = L->tiles.as<int32_t>();
+    g.n_tiles = L->ctrl.as<int32_t>() + CTRL_TILES;
+    g.offsets = L->offsets.as<int32_t>();
+    g.max_tiles = tile_bound(P, E, BM);
+    g.h_hi = L->hhi.as<uint16_t>();
+    g.h_lo = L->hlo.as<uint16_t>();
+    ART_TRY(mark());
+    ART_TRY(launch_expert_gemm(g, s));
+    GemmArgs dn = g;
+    dn.w[0] = L->down.as<uint8_t>();
+    dn.w[1] = nullptr;
+    dn.expert_bytes = int64_t(H) * L->down_row;
+    dn.row_bytes = int(L->down_row);
+    dn.N = H;
+    dn.K = F;
+    dn.qtype = d.down_type;
+    dn.a_hi = L->hhi.as<uint16_t>();
+    dn.a_lo = L->hlo.as<uint16_t>();
+    dn.a_gather = 0;
+    dn.y = L->ypairs.as<float>();
+    ART_TRY(mark());
+    ART_TRY(launch_expert_gemm(dn, s));
+  }
   const float* ys = nullptr;
-  if (d.shared_ffn) {
+  if (d.shared_ffn && path.shared_gemv) {
+    GemvArgs sg{};
+    sg.w[0] = L->sgate.as<uint8_t>();
+    sg.w[1] = L->sup.as<uint8_t>();
+    sg.row_bytes = int(L->sgate_row);
+    sg.N = d.shared_ffn;
+    sg.K = H;
+    sg.qtype = d.shared_type;
+    sg.xq = L->xq.as<uint32_t>();
+    sg.dense_rows = int(T);
+    sg.hq = L->shq.as<uint32_t>();
+    ART_TRY(mark());
+    ART_TRY(launch_gemv(sg, s));
+    GemvArgs sd = sg;
+    sd.w[0] = L->sdown.as<uint8_t>();
+    sd.w[1] = nullptr;
+    sd.row_bytes = int(L->sdown_row);
+    sd.N = H;
+    sd.K = d.shared_ffn;
+    sd.xq = L->shq.as<uint32_t>();
+    sd.hq = nullptr;
+    sd.y = L->ys.as<float>();
+    ART_TRY(mark());
+    ART_TRY(launch_gemv(sd, s));
+    ys = L->ys.as<float>();
+  } else if (d.shared_ffn) {
     GemmArgs sg{};
     sg.w[0] = L->sgate.as<uint8_t>();
     sg.w[1] = L->sup.as<uint8_t>();
@@ -205,6 +294,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
                          d.shared_gated ? L->sg.as<float>() : nullptr, 1, T, H, L->y.as<float>(), s));
   ART_TRY(mark());
   L->last_T = T;
+  L->last_gemv = path.gemv;
   return ARTLITE_OK;
 }
 
@@ -245,6 +335,8 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
     L->sgate_row = size_t(d.hidden) / sq->per * sq->bytes;
     L->sdown_row = size_t(d.shared_ffn) / sq->per * sq->bytes;
   }
+  L->gemv_ok = gemv_supported(d.gate_type, d.hidden) && gemv_supported(d.down_type, d.expert_ffn);
+  L->shared_gemv_ok = sq && gemv_supported(d.shared_type, d.hidden) && gemv_supported(d.shared_type, d.shared_ffn);
   hipError_t e = hipGetDevice(&L->device);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&L->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
@@ -275,6 +367,11 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
   res(L->hlo, size_t(P * F) * 2);
   res(L->ypairs, size_t(P * H) * 4);
   res(L->y, size_t(T * H) * 4);
+  if (L->gemv_ok) {
+    res(L->xq, size_t(T * xq_row_dwords(d.hidden)) * 4);
+    res(L->hq, size_t(P * xq_row_dwords(d.expert_ffn)) * 4);
+    if (L->shared_gemv_ok) res(L->shq, size_t(T * xq_row_dwords(d.shared_ffn)) * 4);
+  }
   if (d.shared_ffn) {
     res(L->shhi, size_t(T) * d.shared_ffn * 2);
     res(L->shlo, size_t(T) * d.shared_ffn * 2);
@@ -384,10 +481,18 @@ extern "C" int artlite_moe_layer_tap(artlite_moe_layer* L, int tap, void* out, s
     case ARTLITE_TAP_H: {
       const size_t n = size_t(P) * L->d.expert_ffn;
       if (nbytes < n * 4) return fail(ARTLITE_EINVAL, "moe layer tap: %zu bytes, need %zu", nbytes, n * 4);
+      ART_HIP(hipStreamSynchronize(L->stream));
+      float* o = static_cast<float*>(out);
+      if (L->last_gemv) {
+        const int64_t rw = xq_row_dwords(L->d.expert_ffn);
+        std::vector<uint32_t> q(size_t(P * rw));
+        if (P) ART_HIP(hipMemcpy(q.data(), L->hq.p, q.size() * 4, hipMemcpyDeviceToHost));
+        for (int64_t r = 0; r < P; r++) xq_dequant_row(q.data() + r * rw, L->d.expert_ffn, o + r * L->d.expert_ffn);
+        return ARTLITE_OK;
+      }
       std::vector<uint16_t> hi(n), lo(n);
       ART_HIP(hipMemcpy(hi.data(), L->hhi.p, n * 2, hipMemcpyDeviceToHost));
       ART_HIP(hipMemcpy(lo.data(), L->hlo.p, n * 2, hipMemcpyDeviceToHost));
-      float* o = static_cast<float*>(out);
       for (size_t i = 0; i < n; i++) {
         uint32_t a = uint32_t(hi[i]) << 16, b = uint32_t(lo[i]) << 16;
         float fa, fb;
@@ -407,9 +512,8 @@ extern "C" int artlite_moe_layer_tap(artlite_moe_layer* L, int tap, void* out, s
 
 extern "C" int artlite_moe_kernel_names(artlite_moe_layer* L, int64_t T, char* buf, size_t cap) {
   if (!L || !buf || !cap) return fail(ARTLITE_EINVAL, "kernel names: null argument");
-  (void)T;
   std::string s;
-  for (const std::string& k : kernel_list(L)) s += (s.empty() ? "" : ";") + k;
+  for (const std::string& k : kernel_list(L, T)) s += (s.empty() ? "" : ";") + k;
   const size_t n = s.size() < cap - 1 ? s.size() : cap - 1;
   std::memcpy(buf, s.data(), n);
   buf[n] = 0;
@@ -437,7 +541,7 @@ extern "C" int artlite_moe_layer_time(artlite_moe_layer** layers, int n, int64_t
   int rc = ARTLITE_OK;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   std::vector<hipEvent_t> ev;
-  const std::vector<std::string> names = kernel_list(L0);
+  const std::vector<std::string> names = kernel_list(L0, T);
   const int nk = int(names.size());
   auto done = [&](int code) {
     for (int i = 0; i < n; i++) layers[i]->stream = own[i];

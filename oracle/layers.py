@@ -48,6 +48,12 @@ CONFIGS = {
                      dmin_scale=1.5e-3, shared_F=2816, shared_type="Q4_K", tokens=(512,)),
     "skewed": Spec("skewed", H=2880, E=32, k=4, F=2880, gate_type="Q8_0", down_type="Q8_0", scale=0.01,
                    router="zipf", tokens=(2048,)),
+    # test-only mixes of the block types at decode sizes (every product on the decode GEMV)
+    "mix_q8k": Spec("mix_q8k", H=1024, E=32, k=4, F=512, gate_type="Q8_0", down_type="Q4_K", scale=0.01,
+                    dmin_scale=1.5e-3, x_dtype="f32", shared_F=512, shared_type="Q4_K", shared_gated=True,
+                    tokens=(16,)),
+    "mix_k8": Spec("mix_k8", H=1536, E=16, k=2, F=768, gate_type="Q4_K", down_type="Q8_0", scale=2e-4,
+                   dmin_scale=1.5e-3, shared_F=256, shared_type="Q8_0", tokens=(24,)),
 }
 
 ZIPF_S, ZIPF_ACTIVE, ZIPF_BETA = 1.2, 26, 0.7
