@@ -10,14 +10,14 @@ namespace artlite {
 constexpr int GEMV_BM = 4;
 
 // XQ, the decode activations: each row of K values (K a multiple of 256) as units of 256 values, a unit as 8
-// groups of 32 and each group as two int8 planes, x ~ s (a + b / 256) with s = max |x| / 127 over the group. A unit
-// is 16 records of XQ_REC dwords, record i: [dword i of group 0's 16-dword block, ..., of group 7's,
-// list word i, sum word i, 0, 0], where a group's block is its plane a (8 dwords of 4 int8 in value order) then
-// plane b, list word 2 g = s_g / 256 (fp32), list word 2 g + 1 = sum over the group of (256 a + b) (int32), and sum
-// word g = s_g / 256 times that sum (fp32: the group's dequantised sum). A group with a non-finite value has
-// s = NaN; a group of zeros has s = 0.
-constexpr int XQ_REC = 12;
-constexpr int XQ_UNIT = 16 * XQ_REC;  // dwords per unit
+// groups of 32 and each group as two int8 planes, x ~ s (a + b / 256) with s = max |x| / 127 over the group. A
+// group's block is 16 dwords: plane a (8 dwords of 4 int8 in value order), then plane b. Per group three words:
+// s / 256 (fp32), the sum over the group of 256 a + b (int32), and s / 256 times that sum (fp32: the group's
+// dequantised sum). A group with a non-finite value has s = NaN; a group of zeros has s = 0.
+// A unit is 64 chunks of 4 dwords, chunk 16 p + r (p < 4, r < 16) = [dword r of group 2 p's block, dword r of group
+// 2 p + 1's block, L, S], with L = (s / 256 of group 2 p, its sum, s / 256 of group 2 p + 1, its sum)[r % 4] and
+// S = (dequantised sum of group 2 p, of group 2 p + 1)[r % 2]: chunk i is exactly what lane i of the GEMV needs.
+constexpr int XQ_UNIT = 256;  // dwords per unit
 
 __host__ __device__ inline int64_t xq_row_dwords(int K) { return int64_t(K / 256) * XQ_UNIT; }
 

@@ -1,13 +1,14 @@
 // Decode expert products on the VALU, and the XQ activations they read.
 //
-// A workgroup is one wave: one tile of at most GEMV_BM sorted rows of A (tokens for gate / up, pairs for down) of
-// one expert, times 64 weight rows, one per lane (SwiGLU: the lane's gate row and its up row). The wave streams its
-// rows in units of 8 groups of 32 values (Q4_0 / Q4_K: 144 bytes of a row, Q8_0: 272), 64 rows per unit, with
-// global_load_lds_dwordx4 straight into one of D LDS slots (consecutive lanes load consecutive 16-byte chunks, so
-// each load instruction reads whole runs of rows). A row occupies an odd number of 16-byte chunks of its slot, so
-// the lanes' own-row ds_read_b128 fall in distinct banks. The tile's XQ records of the unit come with it (three
-// dwordx4 per row of A, one record per lane of each 16-lane row), and DPP row_newbcast:j hands dword j of a group's
-// block to every lane as the broadcast operand of v_dot4c_i32_i8: the activations cost no LDS traffic.
+// A workgroup is one tile of at most GEMV_BM sorted rows of A (tokens for gate / up, pairs for down) of one expert,
+// times 64 weight rows (SwiGLU: those rows of gate and of up), as 4 independent waves of 16 rows. A wave streams its
+// rows in units of 8 groups of 32 values (Q4_0 / Q4_K: 144 bytes of a row, Q8_0: 272) with global_load_lds_dwordx4
+// into one of D LDS slots of its own (consecutive lanes load consecutive 16-byte chunks), D - 1 units ahead. Lane
+// (p, r) -- 16-lane row p, lane r in it -- takes row r and groups 2 p, 2 p + 1 of each unit, so four lanes share a
+// row and a unit's products of 64 rows are spread over four waves (one wave per SIMD issues VALU at well under half
+// rate). The activations come straight into registers, one 16-byte XQ chunk per lane per row of A: DPP
+// row_newbcast:j hands every lane of 16-lane row p dword j of its groups' blocks as the broadcast operand of
+// v_dot4c_i32_i8, and the per-group words the same way. The four lanes of a row are summed at the end.
 //
 // Arithmetic of one (row of A, group): A = sum_j dot4(a_j, q_j) and B = C + sum_j dot4(b_j, q_j), exactly in int32,
 // with q_j the group's codes as int8 (Q4_0 / Q4_K: nibbles 0..15, Q8_0: the signed bytes) and C the code offset's
@@ -21,25 +22,28 @@
 
 namespace artlite {
 
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
 __device__ __forceinline__ float h2f(uint32_t h) { return float(__builtin_bit_cast(_Float16, uint16_t(h))); }
 
+// per format: bytes of a row's unit, dwords a lane reads of it (Q4_0 / Q8_0: its two groups; Q4_K: the super-block
+// header and the 32-byte run holding its two groups)
 template <int QT>
 struct Unit;
 template <>
 struct Unit<ARTLITE_Q4_0> {
-  static constexpr int BYTES = 144;
+  static constexpr int BYTES = 144, LW = 9;
 };
 template <>
 struct Unit<ARTLITE_Q8_0> {
-  static constexpr int BYTES = 272;
+  static constexpr int BYTES = 272, LW = 17;
 };
 template <>
 struct Unit<ARTLITE_Q4_K> {
-  static constexpr int BYTES = 144;
+  static constexpr int BYTES = 144, LW = 12;
 };
 
 template <typename F, int... I>
@@ -52,122 +56,138 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// dword i of a unit held as 16-byte chunks (i a constant after unrolling)
-template <int CH>
-__device__ __forceinline__ uint32_t dw(const u32x4 (&w)[CH], int i) {
-  return w[i >> 2][i & 3];
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
 }
 
-// After vmcnt(N), the lane's row of a unit and the tile's XQ records of it from the unit's LDS slot, and their
-// completion, in one asm block: the compiler would otherwise wait for every load in flight before reading LDS (it
-// takes the slots' global_load_lds writes for possible producers), and it must not touch the outputs before the
-// final wait. pw: the lane's row; px: record (lane % 16) of the tile's first row of A (rows 768 bytes apart).
-#define ART_RW(I) "ds_read_b128 %[w" #I "], %[pw] offset:" #I "*16\n\t"
-#define ART_RX(T, C) "ds_read_b128 %[x" #T #C "], %[px] offset:" #T "*768+" #C "*16\n\t"
-#define ART_W9 ART_RW(0) ART_RW(1) ART_RW(2) ART_RW(3) ART_RW(4) ART_RW(5) ART_RW(6) ART_RW(7) ART_RW(8)
-#define ART_W17 ART_W9 ART_RW(9) ART_RW(10) ART_RW(11) ART_RW(12) ART_RW(13) ART_RW(14) ART_RW(15) ART_RW(16)
-#define ART_OW(I) [w##I] "=&v"(w[I])
-#define ART_OW9 ART_OW(0), ART_OW(1), ART_OW(2), ART_OW(3), ART_OW(4), ART_OW(5), ART_OW(6), ART_OW(7), ART_OW(8)
+// After vmcnt(N), the lane's dwords of a unit (at pw; Q4_K: header at pw, its run at pr) and its XQ chunk of each
+// of the M rows of A (at px, 1024 bytes apart), and their completion, in one asm block: the compiler would otherwise
+// wait for every load in flight before reading LDS (it takes the slots' global_load_lds writes for possible
+// producers), and it must not touch the outputs before the final wait.
+#define ART_R2(I, J) "ds_read2_b32 %[w" #I "], %[pw] offset0:" #J " offset1:" #J "+1\n\t"
+#define ART_R1(I, J) "ds_read_b32 %[w" #I "], %[pw] offset:" #J "*4\n\t"
+#define ART_OW2(I) [w##I] "=&v"(w2[I])
+#define ART_OW1(I) [w##I] "=&v"(w1)
+#define ART_W9 ART_R2(0, 0) ART_R2(1, 2) ART_R2(2, 4) ART_R2(3, 6) ART_R1(4, 8)
+#define ART_OW9 ART_OW2(0), ART_OW2(1), ART_OW2(2), ART_OW2(3), ART_OW1(4)
+#define ART_W17 \
+  ART_R2(0, 0) ART_R2(1, 2) ART_R2(2, 4) ART_R2(3, 6) ART_R2(4, 8) ART_R2(5, 10) ART_R2(6, 12) ART_R2(7, 14) ART_R1(8, 16)
 #define ART_OW17 \
-  ART_OW9, ART_OW(9), ART_OW(10), ART_OW(11), ART_OW(12), ART_OW(13), ART_OW(14), ART_OW(15), ART_OW(16)
-#define ART_X1 ART_RX(0, 0) ART_RX(0, 1) ART_RX(0, 2)
-#define ART_X2 ART_X1 ART_RX(1, 0) ART_RX(1, 1) ART_RX(1, 2)
-#define ART_X3 ART_X2 ART_RX(2, 0) ART_RX(2, 1) ART_RX(2, 2)
-#define ART_X4 ART_X3 ART_RX(3, 0) ART_RX(3, 1) ART_RX(3, 2)
-#define ART_OX(T) [x##T##0] "=&v"(x[T][0]), [x##T##1] "=&v"(x[T][1]), [x##T##2] "=&v"(x[T][2])
-#define ART_OX1 ART_OX(0)
-#define ART_OX2 ART_OX1, ART_OX(1)
-#define ART_OX3 ART_OX2, ART_OX(2)
-#define ART_OX4 ART_OX3, ART_OX(3)
-#define ART_READ(CHN, MN)                                                                                      \
-  asm volatile("s_waitcnt vmcnt(%[n])\n\t" ART_W##CHN ART_X##MN "s_waitcnt lgkmcnt(0)"                      \
-               : ART_OW##CHN, ART_OX##MN                                                                      \
-               : [pw] "v"(pw), [px] "v"(px), [n] "i"(N))
-template <int N, int CH, int M>
-__device__ __forceinline__ void read_unit(u32x4 (&w)[CH], u32x4 (&x)[M][3], uint32_t pw, uint32_t px) {
+  ART_OW2(0), ART_OW2(1), ART_OW2(2), ART_OW2(3), ART_OW2(4), ART_OW2(5), ART_OW2(6), ART_OW2(7), ART_OW1(8)
+#define ART_W12                    \
+  "ds_read_b128 %[w0], %[pw]\n\t"  \
+  "ds_read_b128 %[w1], %[pr]\n\t"  \
+  "ds_read_b128 %[w2], %[pr] offset:16\n\t"
+#define ART_OW12 [w0] "=&v"(w4[0]), [w1] "=&v"(w4[1]), [w2] "=&v"(w4[2])
+#define ART_RX(T) "ds_read_b128 %[x" #T "], %[px] offset:" #T "*1024\n\t"
+#define ART_X1 ART_RX(0)
+#define ART_X2 ART_X1 ART_RX(1)
+#define ART_X3 ART_X2 ART_RX(2)
+#define ART_X4 ART_X3 ART_RX(3)
+#define ART_OX1 [x0] "=&v"(x[0])
+#define ART_OX2 ART_OX1, [x1] "=&v"(x[1])
+#define ART_OX3 ART_OX2, [x2] "=&v"(x[2])
+#define ART_OX4 ART_OX3, [x3] "=&v"(x[3])
+#define ART_READ(WN, MN)                                                                             \
+  asm volatile("s_waitcnt vmcnt(%[n])\n\t" ART_W##WN ART_X##MN "s_waitcnt lgkmcnt(0)"              \
+               : ART_OW##WN, ART_OX##MN                                                             \
+               : [pw] "v"(pw), [pr] "v"(pr), [px] "v"(px), [n] "i"(N))
+#define ART_READ_M(WN)         \
+  if constexpr (M == 1) ART_READ(WN, 1); \
+  if constexpr (M == 2) ART_READ(WN, 2); \
+  if constexpr (M == 3) ART_READ(WN, 3); \
+  if constexpr (M == 4) ART_READ(WN, 4);
+template <int N, int QT, int M>
+__device__ __forceinline__ void read_unit(uint32_t (&w)[Unit<QT>::LW], u32x4 (&x)[M], uint32_t pw, uint32_t pr,
+                                          uint32_t px) {
   static_assert(N >= 0 && N < 64, "vmcnt");
-  static_assert(CH == 9 || CH == 17, "unit chunks");
-  if constexpr (CH == 9 && M == 1) ART_READ(9, 1);
-  if constexpr (CH == 9 && M == 2) ART_READ(9, 2);
-  if constexpr (CH == 9 && M == 3) ART_READ(9, 3);
-  if constexpr (CH == 9 && M == 4) ART_READ(9, 4);
-  if constexpr (CH == 17 && M == 1) ART_READ(17, 1);
-  if constexpr (CH == 17 && M == 2) ART_READ(17, 2);
-  if constexpr (CH == 17 && M == 3) ART_READ(17, 3);
-  if constexpr (CH == 17 && M == 4) ART_READ(17, 4);
+  constexpr int LW = Unit<QT>::LW;
+  if constexpr (LW == 12) {
+    u32x4 w4[3];
+    ART_READ_M(12)
+#pragma unroll
+    for (int i = 0; i < 12; i++) w[i] = w4[i >> 2][i & 3];
+  } else {
+    u32x2 w2[LW / 2];
+    uint32_t w1;
+    if constexpr (LW == 9) {
+      ART_READ_M(9)
+    } else {
+      ART_READ_M(17)
+    }
+#pragma unroll
+    for (int i = 0; i < LW / 2; i++) w[2 * i] = w2[i][0], w[2 * i + 1] = w2[i][1];
+    w[LW - 1] = w1;
+  }
 }
+#undef ART_READ_M
 #undef ART_READ
 #undef ART_OX4
 #undef ART_OX3
 #undef ART_OX2
 #undef ART_OX1
-#undef ART_OX
 #undef ART_X4
 #undef ART_X3
 #undef ART_X2
 #undef ART_X1
-#undef ART_OW17
-#undef ART_OW9
-#undef ART_OW
-#undef ART_W17
-#undef ART_W9
 #undef ART_RX
-#undef ART_RW
+#undef ART_OW12
+#undef ART_W12
+#undef ART_OW17
+#undef ART_W17
+#undef ART_OW9
+#undef ART_W9
+#undef ART_OW1
+#undef ART_OW2
+#undef ART_R1
+#undef ART_R2
 
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N));
 }
 
-// codes of group G of a unit as 8 dwords of int8 (q[j]: values 4 j .. 4 j + 3 of the group), its scale d
-// (Q4_K: d sc) and Q4_K's dmin mn
-template <int QT, int G>
-__device__ __forceinline__ void codes(const u32x4 (&w)[Unit<QT>::BYTES / 16], uint32_t (&q)[8], float& d, float& mn) {
-  if constexpr (QT == ARTLITE_Q4_0) {
-    // 18 bytes at 18 G: fp16 d, then 16 bytes whose low nibbles are values 0..15 and high nibbles 16..31
-    constexpr int o = 18 * G;
+// Codes of the lane's group H (0, 1) as 8 dwords of int8 (q[j]: values 4 j .. 4 j + 3 of the group), its scale d
+// (Q4_K: d sc) and Q4_K's dmin mn. g: the group's index in the unit (Q4_K's scales).
+template <int QT, int H>
+__device__ __forceinline__ void codes(const uint32_t (&w)[Unit<QT>::LW], int g, uint32_t (&q)[8], float& d,
+                                      float& mn) {
+  if constexpr (QT == ARTLITE_Q4_0 || QT == ARTLITE_Q8_0) {
+    // Q4_0: 18 bytes at 18 H: fp16 d, then 16 bytes whose low nibbles are values 0..15, high nibbles 16..31;
+    // Q8_0: 34 bytes at 34 H: fp16 d, then 32 signed bytes in value order
+    constexpr int o = (QT == ARTLITE_Q4_0 ? 18 : 34) * H;
+    constexpr int NQ = QT == ARTLITE_Q4_0 ? 4 : 8;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int j = 0; j < NQ; j++) {
       uint32_t v;
       if constexpr (o % 4 == 0)
-        v = __builtin_amdgcn_alignbit(dw(w, o / 4 + j + 1), dw(w, o / 4 + j), 16);
+        v = __builtin_amdgcn_alignbit(w[o / 4 + j + 1], w[o / 4 + j], 16);
       else
-        v = dw(w, (o + 2) / 4 + j);
-      q[j] = v & 0x0F0F0F0Fu;
-      q[4 + j] = (v >> 4) & 0x0F0F0F0Fu;
+        v = w[(o + 2) / 4 + j];
+      if constexpr (QT == ARTLITE_Q4_0) {
+        q[j] = v & 0x0F0F0F0Fu;
+        q[4 + j] = (v >> 4) & 0x0F0F0F0Fu;
+      } else {
+        q[j] = v;
+      }
     }
-    d = o % 4 == 0 ? h2f(dw(w, o / 4) & 0xFFFFu) : h2f(dw(w, (o - 2) / 4) >> 16);
-    mn = 0.0f;
-  } else if constexpr (QT == ARTLITE_Q8_0) {
-    // 34 bytes at 34 G: fp16 d, then 32 signed bytes in value order
-    constexpr int o = 34 * G;
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-      if constexpr (o % 4 == 0)
-        q[j] = __builtin_amdgcn_alignbit(dw(w, o / 4 + j + 1), dw(w, o / 4 + j), 16);
-      else
-        q[j] = dw(w, (o + 2) / 4 + j);
-    }
-    d = o % 4 == 0 ? h2f(dw(w, o / 4) & 0xFFFFu) : h2f(dw(w, (o - 2) / 4) >> 16);
+    d = o % 4 == 0 ? h2f(w[o / 4] & 0xFFFFu) : h2f(w[(o - 2) / 4] >> 16);
     mn = 0.0f;
   } else {
-    // a super-block: fp16 d, dmin; 12 bytes of 6-bit scales / mins; 4 runs of 32 bytes, run c holding group 2 c in
-    // its low nibbles and group 2 c + 1 in its high nibbles (value order)
-    auto sb = [&](int k) { return (dw(w, 1 + k / 4) >> (8 * (k % 4))) & 0xFFu; };
-    uint32_t sc, m;
-    if constexpr (G < 4) {
-      sc = sb(G) & 63u;
-      m = sb(G + 4) & 63u;
-    } else {
-      sc = (sb(G + 4) & 15u) | ((sb(G - 4) >> 6) << 4);
-      m = (sb(G + 4) >> 4) | ((sb(G) >> 6) << 4);
-    }
-    d = h2f(dw(w, 0) & 0xFFFFu) * float(sc);  // (exact: 11 x 6 significant bits)
-    mn = h2f(dw(w, 0) >> 16) * float(m);
+    // a super-block: fp16 d, dmin; 12 bytes of 6-bit scales / mins (w[1..3]); the lane's 32-byte run (w[4..11]),
+    // its group 2 p in the low nibbles and 2 p + 1 in the high nibbles (value order)
+    // (bytes g, g + 4 and g - 4 of the scales by a runtime byte select)
+    const uint32_t sel = 0x0C0C0C00u | uint32_t(g);
+    const uint32_t b0 = __builtin_amdgcn_perm(w[2], w[1], sel);
+    const uint32_t b4 = __builtin_amdgcn_perm(w[3], w[2], sel);
+    const uint32_t bm = __builtin_amdgcn_perm(w[2], w[1], 0x0C0C0C00u | uint32_t((g - 4) & 7));
+    const uint32_t sc = g < 4 ? b0 & 63u : (b4 & 15u) | ((bm >> 6) << 4);
+    const uint32_t m = g < 4 ? b4 & 63u : (b4 >> 4) | ((b0 >> 6) << 4);
+    d = h2f(w[0] & 0xFFFFu) * float(sc);  // (exact: 11 x 6 significant bits)
+    mn = h2f(w[0] >> 16) * float(m);
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const uint32_t v = dw(w, 4 + 8 * (G / 2) + j);
-      q[j] = G % 2 ? (v >> 4) & 0x0F0F0F0Fu : v & 0x0F0F0F0Fu;
-    }
+    for (int j = 0; j < 8; j++) q[j] = H ? (w[4 + j] >> 4) & 0x0F0F0F0Fu : w[4 + j] & 0x0F0F0F0Fu;
   }
 }
 
@@ -190,9 +210,9 @@ __device__ __forceinline__ void codes(const u32x4 (&w)[Unit<QT>::BYTES / 16], ui
       [q6] "v"(q[6]), [q7] "v"(q[7])
 #define ART_ACC [a0] "=&v"(a0), [a1] "=&v"(a1), [b0] "=&v"(b0), [b1] "=&v"(b1), [c] "=&v"(coef)
 
-// acc += the group's term for one row of A. x: its block dword; l: the record's list word (lane 2 G: s / 256,
-// lane 2 G + 1: the sum of 256 a + b); xs: the record's sum word (lane G: the dequantised sum).
-template <int QT, int G>
+// acc += the term of the lane's group H for one row of A. x: the group's block dword; l: the list word (16-lane row
+// lanes 2 H: s / 256, 2 H + 1: the sum of 256 a + b); xs: the sum word (lane H: the dequantised sum).
+template <int QT, int H>
 __device__ __forceinline__ float group_term(float acc, uint32_t x, uint32_t l, uint32_t xs, const uint32_t (&q)[8],
                                             float d, float mn) {
   int a0, a1, b0, b1;
@@ -206,7 +226,7 @@ __device__ __forceinline__ float group_term(float acc, uint32_t x, uint32_t l, u
         "v_mul_f32_dpp %[c], %[l], %[d] row_newbcast:%[l0] row_mask:0xf bank_mask:0xf\n\t"
         "s_nop 1"
         : ART_ACC
-        : [x] "v"(x), [l] "v"(l), [d] "v"(d), [m8] "v"(-8), ART_QIN, [l0] "i"(2 * G), [l1] "i"(2 * G + 1));
+        : [x] "v"(x), [l] "v"(l), [d] "v"(d), [m8] "v"(-8), ART_QIN, [l0] "i"(2 * H), [l1] "i"(2 * H + 1));
   } else if constexpr (QT == ARTLITE_Q8_0) {
     asm("s_nop 1\n\t"
         "v_mov_b32 %[a0], 0\n\t"
@@ -216,7 +236,7 @@ __device__ __forceinline__ float group_term(float acc, uint32_t x, uint32_t l, u
         "v_mul_f32_dpp %[c], %[l], %[d] row_newbcast:%[l0] row_mask:0xf bank_mask:0xf\n\t"
         "s_nop 1"
         : ART_ACC
-        : [x] "v"(x), [l] "v"(l), [d] "v"(d), ART_QIN, [l0] "i"(2 * G));
+        : [x] "v"(x), [l] "v"(l), [d] "v"(d), ART_QIN, [l0] "i"(2 * H));
   } else {
     float mterm;
     asm("s_nop 1\n\t"
@@ -225,10 +245,10 @@ __device__ __forceinline__ float group_term(float acc, uint32_t x, uint32_t l, u
         "v_mov_b32 %[a1], 0\n\t"
         "v_mov_b32 %[b1], 0\n\t" ART_DOTS
         "v_mul_f32_dpp %[c], %[l], %[d] row_newbcast:%[l0] row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %[t], %[xs], %[nm] row_newbcast:%[g] row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t], %[xs], %[nm] row_newbcast:%[h] row_mask:0xf bank_mask:0xf\n\t"
         "s_nop 0"
         : ART_ACC, [t] "=&v"(mterm)
-        : [x] "v"(x), [l] "v"(l), [xs] "v"(xs), [d] "v"(d), [nm] "v"(-mn), ART_QIN, [l0] "i"(2 * G), [g] "i"(G));
+        : [x] "v"(x), [l] "v"(l), [xs] "v"(xs), [d] "v"(d), [nm] "v"(-mn), ART_QIN, [l0] "i"(2 * H), [h] "i"(H));
     return __builtin_fmaf(coef, float((a0 + a1) * 256 + (b0 + b1)), acc) + mterm;
   }
   return __builtin_fmaf(coef, float((a0 + a1) * 256 + (b0 + b1)), acc);
@@ -274,114 +294,185 @@ __device__ __forceinline__ void quant_group(const float (&x)[V], int (&qa)[V], i
   xsum = s256 * float(sum);
 }
 
-// the group's three per-group words into unit ub (group g)
-__device__ __forceinline__ void put_group_words(uint32_t* ub, int g, float s256, int sum, float xsum) {
-  ub[(2 * g) * XQ_REC + 8] = __float_as_uint(s256);
-  ub[(2 * g + 1) * XQ_REC + 8] = uint32_t(sum);
-  ub[g * XQ_REC + 9] = __float_as_uint(xsum);
+// dword of an XQ unit holding block dword i (< 16) of group g
+__host__ __device__ inline int xq_block(int g, int i) { return 4 * (16 * (g >> 1) + i) + (g & 1); }
+
+// word k (< 16) of the 16 copies of group g's three words in an XQ unit: k < 4: s / 256, k < 8: the sum, else the
+// dequantised sum
+__device__ __forceinline__ void xq_put_word(uint32_t* ub, int g, int k, float s256, int sum, float xsum) {
+  const int c = 16 * (g >> 1), h = g & 1;
+  if (k < 4)
+    ub[4 * (c + 2 * h + 4 * k) + 2] = __float_as_uint(s256);
+  else if (k < 8)
+    ub[4 * (c + 2 * h + 1 + 4 * (k - 4)) + 2] = uint32_t(sum);
+  else
+    ub[4 * (c + h + 2 * (k - 8)) + 3] = __float_as_uint(xsum);
 }
 
-// LDS slot of a unit: 64 rows x CH chunks, then the tile's XQ records (up to GEMV_BM rows of 48 chunks)
-template <int QT>
-constexpr int slot_chunks() {
-  return 64 * (Unit<QT>::BYTES / 16) + 48 * GEMV_BM;
+// LDS of a workgroup: each wave's D slots of 16 rows x BYTES, two record slots (GEMV_BM x 1 KB), then h of the
+// tile (GEMV_BM x 64 fp32)
+template <int QT, int D>
+constexpr size_t gemv_lds() {
+  return size_t(4) * D * 16 * Unit<QT>::BYTES + 2 * GEMV_BM * 1024 + GEMV_BM * 64 * 4;
+}
+
+// choose among waits vmcnt(N0), (N0 + NI), ... by a small runtime count c (< 4)
+template <int N0, int NI, int CMAX>
+__device__ __forceinline__ void wait_vm_c(int c) {
+  if (c <= 0)
+    wait_vm<N0>();
+  else if (c == 1 || CMAX < 2)
+    wait_vm<(CMAX >= 1 ? N0 + NI : N0)>();
+  else if (c == 2 || CMAX < 3)
+    wait_vm<(CMAX >= 2 ? N0 + 2 * NI : N0)>();
+  else
+    wait_vm<(CMAX >= 3 ? N0 + 3 * NI : N0)>();
 }
 
 template <int QT, bool SWIGLU, int D, int M>
 __device__ __forceinline__ void gemv_tile(const GemvArgs& a, int e, int s0) {
-  constexpr int BY = Unit<QT>::BYTES, CH = BY / 16, NM = SWIGLU ? 2 : 1;
-  constexpr int XI = (48 * M + 63) / 64;  // load instructions of the records of a unit
-  constexpr int LPU = CH + XI, SLOT = slot_chunks<QT>();
-  static_assert((D - 1) * LPU <= 63, "loads in flight beyond vmcnt");
-  static_assert(D % NM == 0, "a slot's matrix is fixed");
-  static_assert(48 * GEMV_BM % 64 == 0, "record loads fill the slot's record area");
-  extern __shared__ u32x4 slab[];  // D slots
-  const int lane = threadIdx.x;
-  const int n0 = blockIdx.y * 64;
+  constexpr int BY = Unit<QT>::BYTES, CH = BY / 16, LW = Unit<QT>::LW, NM = SWIGLU ? 2 : 1;
+  constexpr int WCH = 16 * CH;               // chunks of a wave's unit
+  constexpr int NI = (WCH + 63) / 64;         // its load instructions (the last for LAST lanes)
+  constexpr int LAST = WCH - 64 * (NI - 1);
+  static_assert((D - 1) * NI + D * M < 64, "loads in flight beyond vmcnt");
+  static_assert(D % NM == 0, "slots per matrix");
+  extern __shared__ u32x4 slab[];
+  // (wv through readfirstlane: wave-uniform to the compiler, so the branches on it are scalar)
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, p = lane >> 4, r = lane & 15;
+  u32x4* my = slab + wv * D * WCH;
+  u32x4* xslot = slab + 4 * D * WCH;  // 2 x GEMV_BM x 64 chunks
+  float* hbuf = reinterpret_cast<float*>(xslot + 2 * GEMV_BM * 64);
+  const int n0 = blockIdx.y * 64, nw = n0 + 16 * wv;
   const int U = a.K / 256, NV = U * NM;
 
-  // this lane's chunk of each load instruction of a unit: weight chunk 64 i + lane of the 64 x CH, record chunk
-  // 64 i + lane of the M x 48 (past the last: the last again, landing in the slot's spare record area)
-  int32_t off[CH];
+  // the lane's chunk of each load instruction of a unit (chunk 64 i + lane of the wave's 16 x CH)
+  int32_t off[NI];
 #pragma unroll
-  for (int i = 0; i < CH; i++) {
-    const int q = 64 * i + lane, r = q / CH;
-    off[i] = min(n0 + r, a.N - 1) * a.row_bytes + 16 * (q - r * CH);
-  }
-  const uint8_t* xs[XI];
-#pragma unroll
-  for (int i = 0; i < XI; i++) {
-    const int q = min(64 * i + lane, 48 * M - 1), t = q / 48;
-    const int64_t r = a.a_gather ? a.order[s0 + t] / a.topk : s0 + t;
-    xs[i] = reinterpret_cast<const uint8_t*>(a.xq + r * xq_row_dwords(a.K)) + 16 * (q - 48 * t);
+  for (int i = 0; i < NI; i++) {
+    const int q = min(64 * i + lane, WCH - 1), row = q / CH;
+    off[i] = min(nw + row, a.N - 1) * a.row_bytes + 16 * (q - row * CH);
   }
   const uint8_t* wb[NM];
 #pragma unroll
-  for (int mtx = 0; mtx < NM; mtx++) wb[mtx] = a.w[mtx] + int64_t(e) * a.expert_bytes;
-  float acc[NM][M];
+  for (int mx = 0; mx < NM; mx++) wb[mx] = a.w[mx] + int64_t(e) * a.expert_bytes;
+  // wave 0 loads the tile's record chunks of each K-unit (row t: one instruction, lane i -> chunk i)
+  const uint8_t* xr[M];
+  if (wv == 0)
 #pragma unroll
-  for (int mtx = 0; mtx < NM; mtx++)
+    for (int t = 0; t < M; t++) {
+      const int64_t ar = a.a_gather ? a.order[s0 + t] / a.topk : s0 + t;
+      xr[t] = reinterpret_cast<const uint8_t*>(a.xq + ar * xq_row_dwords(a.K)) + 16 * lane;
+    }
+  auto issue_x = [&](int ku) {  // (wave 0; ku past the last: the last again, into the idle slot)
+    u32x4* dst = xslot + (ku & 1) * GEMV_BM * 64;
+    ku = min(ku, U - 1);
 #pragma unroll
-    for (int t = 0; t < M; t++) acc[mtx][t] = 0.0f;
-
-  // unit v (K-range v / NM of matrix v % NM) and its records into slot J = v % D
-  auto issue = [&](int v, auto jc) {
-    constexpr int J = decltype(jc)::value;
-    const int ku = v / NM;
-    const uint8_t* src = wb[J % NM] + int64_t(ku) * BY;
-    u32x4* dst = slab + J * SLOT;
+    for (int t = 0; t < M; t++)
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(xr[t] + ku * (XQ_UNIT * 4)),
+                                       (__attribute__((address_space(3))) void*)(dst + 64 * t), 16, 0, 0);
+  };
+  // the weights of unit v (K-range v / NM of matrix v % NM) into this wave's slot v % D
+  auto issue_w = [&](int v, auto mtx_c) {
+    constexpr int MX = decltype(mtx_c)::value;
+    const uint8_t* src = wb[MX] + int64_t(v / NM) * BY;
+    u32x4* dst = my + (v % D) * WCH;
 #pragma unroll
-    for (int i = 0; i < CH; i++)
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src + off[i]),
-                                       (__attribute__((address_space(3))) void*)(dst + 64 * i), 16, 0, 0);
-#pragma unroll
-    for (int i = 0; i < XI; i++)
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(xs[i] + ku * (XQ_UNIT * 4)),
-                                       (__attribute__((address_space(3))) void*)(dst + 64 * CH + 64 * i), 16, 0, 0);
+    for (int i = 0; i < NI; i++)
+      if (i < NI - 1 || lane < LAST)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src + off[i]),
+                                         (__attribute__((address_space(3))) void*)(dst + 64 * i), 16, 0, 0);
   };
 
-  static_for<D - 1>([&](auto jc) {
-    if (jc.value < NV) issue(jc.value, jc);
-  });
-  for (int v0 = 0; v0 < NV; v0 += D) {
-    static_for<D>([&](auto jc) {
-      constexpr int J = decltype(jc)::value;
-      const int v = v0 + J;
+  // the lane's read addresses
+  const uint32_t wbase = lds_addr(my), xbase = lds_addr(xslot) + 16 * lane;
+  const uint32_t o_w = r * BY + (QT == ARTLITE_Q4_K ? 0 : (QT == ARTLITE_Q4_0 ? 36 : 68) * p);
+  const uint32_t o_r = r * BY + 16 + 32 * p;  // (Q4_K)
+
+  float acc[NM][M];
+#pragma unroll
+  for (int mx = 0; mx < NM; mx++)
+#pragma unroll
+    for (int t = 0; t < M; t++) acc[mx][t] = 0.0f;
+
+  // Weights D - 1 units ahead in each wave's own slots (a slot refilled right after the step that read it); the
+  // records of K-unit ku + 1 issued by wave 0 at ku's first step, right after the barrier that opens it: every wave is
+  // then past K-unit ku - 1, whose record slot it takes, and sees K-unit ku's records, which wave 0 waited for just
+  // before. The loop is unrolled by NM, which fixes each step's matrix.
+  if (wv == 0) issue_x(0);
+  for (int v = 0; v < D - 1 && v < NV; v++) {
+    if (NM == 1 || v % NM == 0)
+      issue_w(v, std::integral_constant<int, 0>{});
+    else
+      issue_w(v, std::integral_constant<int, NM - 1>{});
+  }
+  for (int v0 = 0; v0 < NV; v0 += NM) {
+    static_for<NM>([&](auto jc) {
+      constexpr int MX = decltype(jc)::value;
+      const int v = v0 + MX, ku = v0 / NM;
       if (v >= NV) return;
-      if (v + D - 1 < NV) issue(v + D - 1, std::integral_constant<int, (J + D - 1) % D>{});
-      // unit v has landed once only the units issued after it are outstanding
-      u32x4 w[CH], x[M][3];
-      const uint32_t pw = lds_addr(slab + J * SLOT + lane * CH);
-      const uint32_t px = lds_addr(slab + J * SLOT + 64 * CH + (lane & 15) * 3);
+      if (MX == 0) {
+        // wave 0: K-unit ku's records (issued before the weights of the units since its issue that were issued)
+        if (wv == 0) {
+          if (ku == 0)
+            wait_vm_c<0, NI, 3>(min(D - 1, NV));
+          else
+            wait_vm_c<0, NI, NM>(min(NM, max(0, NV - D + 1 - (ku - 1) * NM)));
+        }
+        __builtin_amdgcn_s_barrier();
+        if (wv == 0) issue_x(ku + 1);
+      }
+      if (v + D - 1 < NV) issue_w(v + D - 1, std::integral_constant<int, (MX + D - 1) % NM>{});
+      // unit v's weights have landed once only the loads issued after them are outstanding: the weights of the
+      // `ahead` units after it, and (wave 0) the records issued at the K-unit starts among steps v - D + 2 .. v
       const int ahead = min(D - 1, NV - 1 - v);
-      if (ahead == 0)
-        read_unit<0>(w, x, pw, px);
-      else if (D > 1 && ahead == 1)
-        read_unit<(D > 1 ? LPU : 0)>(w, x, pw, px);
-      else if (D > 2 && ahead == 2)
-        read_unit<(D > 2 ? 2 * LPU : 0)>(w, x, pw, px);
-      else if (D > 3)
-        read_unit<(D > 3 ? 3 * LPU : 0)>(w, x, pw, px);
-      static_for<8>([&](auto gc) {
-        constexpr int G = decltype(gc)::value;
+      int nx = 0;
+      if (wv == 0)
+        for (int j = max(0, v - D + 2); j <= v; j++) nx += j % NM == 0;
+      uint32_t w[LW];
+      u32x4 x[M];
+      const uint32_t sw = wbase + (v % D) * WCH * 16, px = xbase + (ku & 1) * GEMV_BM * 1024;
+      // (the count in one immediate: nx rows of M records plus ahead x NI)
+      const int n = ahead * NI + nx * M;
+      static_for<(D - 1) * NI + D * M + 1>([&](auto nc) {
+        constexpr int NN = decltype(nc)::value;
+        if (n == NN) read_unit<NN, QT, M>(w, x, sw + o_w, sw + o_r, px);
+      });
+      static_for<2>([&](auto hc) {
+        constexpr int H = decltype(hc)::value;
         uint32_t q[8];
         float d, mn;
-        codes<QT, G>(w, q, d, mn);
+        codes<QT, H>(w, 2 * p + H, q, d, mn);
 #pragma unroll
-        for (int t = 0; t < M; t++)
-          acc[J % NM][t] = group_term<QT, G>(acc[J % NM][t], x[t][G >> 2][G & 3], x[t][2][0], x[t][2][1], q, d, mn);
+        for (int t = 0; t < M; t++) acc[MX][t] = group_term<QT, H>(acc[MX][t], x[t][H], x[t][2], x[t][3], q, d, mn);
       });
     });
   }
 
-  if constexpr (SWIGLU) {
-    // h = silu(gate) up, quantised to XQ rows of N values (lanes 0..31: one group, 32..63: the next)
-    const int UH = a.N / 256;
-    const int g = ((n0 & 255) >> 5) + (lane >> 5), j = (lane & 31) >> 2;
+  // the four lanes of a row: their groups' sums
+#pragma unroll
+  for (int mx = 0; mx < NM; mx++)
 #pragma unroll
     for (int t = 0; t < M; t++) {
-      const float gv = acc[0][t];
-      const float hv[1] = {gv / (1.0f + expf(-gv)) * acc[1][t]};
+      acc[mx][t] += __shfl_xor(acc[mx][t], 16);
+      acc[mx][t] += __shfl_xor(acc[mx][t], 32);
+    }
+  if constexpr (SWIGLU) {
+    // h = silu(gate) up of the 64 rows, then quantised by wave 0 into XQ rows of N values (lanes 0..31: one group,
+    // 32..63: the next)
+    if (p == 0)
+#pragma unroll
+      for (int t = 0; t < M; t++) {
+        const float gv = acc[0][t];
+        hbuf[t * 64 + 16 * wv + r] = gv / (1.0f + expf(-gv)) * acc[1][t];
+      }
+    __syncthreads();
+    if (wv) return;
+    const int UH = a.N / 256;
+    const int g = ((n0 & 255) >> 5) + (lane >> 5), v = lane & 31;
+#pragma unroll
+    for (int t = 0; t < M; t++) {
+      const float hv[1] = {hbuf[t * 64 + lane]};
       int qa[1], qb[1], sum;
       float s256, xsum;
       quant_group<1>(hv, qa, qb, s256, sum, xsum);
@@ -392,22 +483,22 @@ __device__ __forceinline__ void gemv_tile(const GemvArgs& a, int e, int s0) {
       pa |= __shfl_xor(pa, 2);
       pb |= __shfl_xor(pb, 2);
       uint32_t* ub = a.hq + int64_t(s0 + t) * UH * XQ_UNIT + (n0 >> 8) * XQ_UNIT;
-      if ((lane & 3) == 0) {
-        ub[j * XQ_REC + g] = pa;
-        ub[(8 + j) * XQ_REC + g] = pb;
+      if ((v & 3) == 0) {
+        ub[xq_block(g, v >> 2)] = pa;
+        ub[xq_block(g, 8 + (v >> 2))] = pb;
       }
-      if ((lane & 31) == 0) put_group_words(ub, g, s256, sum, xsum);
+      if (v < 16) xq_put_word(ub, g, v, s256, sum, xsum);
     }
   } else {
-    const int n = n0 + lane;
-    if (n < a.N)
+    const int n = nw + r;
+    if (p == 0 && n < a.N)
 #pragma unroll
       for (int t = 0; t < M; t++) a.y[int64_t(s0 + t) * a.N + n] = acc[0][t];
   }
 }
 
 template <int QT, bool SWIGLU, int D>
-__global__ __launch_bounds__(64) void k_gemv(const GemvArgs a) {
+__global__ __launch_bounds__(256) void k_gemv(const GemvArgs a) {
   int e = 0, s0, m;
   if (a.tiles) {
     if (int64_t(blockIdx.x) >= *a.n_tiles) return;
@@ -458,9 +549,10 @@ __global__ __launch_bounds__(256) void k_quant(const void* __restrict__ x, int64
   }
   uint32_t* ub = xq + row * (int64_t(U) * XQ_UNIT) + int64_t(u) * XQ_UNIT;
   const int g = lane >> 3, j = lane & 7;
-  ub[j * XQ_REC + g] = pa;
-  ub[(8 + j) * XQ_REC + g] = pb;
-  if (j == 0) put_group_words(ub, g, s256, sum, xsum);
+  ub[xq_block(g, j)] = pa;
+  ub[xq_block(g, 8 + j)] = pb;
+  xq_put_word(ub, g, j, s256, sum, xsum);
+  xq_put_word(ub, g, 8 + j, s256, sum, xsum);
 }
 
 template <int QT, bool SWIGLU>
@@ -468,9 +560,8 @@ int launch_t(const GemvArgs& a, hipStream_t s) {
   constexpr int D = 2;
   const int64_t tiles = a.tiles ? a.max_tiles : (a.dense_rows + GEMV_BM - 1) / GEMV_BM;
   if (tiles <= 0) return ARTLITE_OK;
-  const dim3 grid(unsigned(tiles), unsigned((a.N + 63) / 64)), block(64);
-  const size_t lds = size_t(D) * slot_chunks<QT>() * 16;
-  k_gemv<QT, SWIGLU, D><<<grid, block, lds, s>>>(a);
+  const dim3 grid(unsigned(tiles), unsigned((a.N + 63) / 64)), block(256);
+  k_gemv<QT, SWIGLU, D><<<grid, block, gemv_lds<QT, D>(), s>>>(a);
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
 }
@@ -518,11 +609,11 @@ void xq_dequant_row(const uint32_t* row, int K, float* out) {
     const uint32_t* ub = row + int64_t(u) * XQ_UNIT;
     for (int g = 0; g < 8; g++) {
       float s;
-      std::memcpy(&s, &ub[(2 * g) * XQ_REC + 8], 4);
+      std::memcpy(&s, &ub[4 * (16 * (g >> 1) + 2 * (g & 1)) + 2], 4);
       for (int v = 0; v < 32; v++) {
         const int j = v / 4, sh = 8 * (v % 4);
-        const int qa = int8_t((ub[j * XQ_REC + g] >> sh) & 0xFFu);
-        const int qb = int8_t((ub[(8 + j) * XQ_REC + g] >> sh) & 0xFFu);
+        const int qa = int8_t((ub[xq_block(g, j)] >> sh) & 0xFFu);
+        const int qb = int8_t((ub[xq_block(g, 8 + j)] >> sh) & 0xFFu);
         out[u * 256 + 32 * g + v] = s * float(256 * qa + qb);
       }
     }
