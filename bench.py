@@ -112,6 +112,19 @@ def cpu_baseline(shape: dict, T: int, budget_s: float) -> dict:
                       f"{med * 1e3:.0f} ms; host {os.cpu_count()} logical CPUs"}
 
 
+def traffic_bytes(path: str) -> float | None:
+    """HBM bytes per launch of the decode gate / up kernel from its counter summary (the line
+    ``traffic_bytes_per_launch: N``: FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the copy calibration), or
+    None without one."""
+    try:
+        for line in Path(path).read_text().splitlines():
+            if line.strip().startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -123,6 +136,10 @@ def main() -> None:
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="also run a plain device copy of MIB MiB (the calibration kernel of counter profiles)")
+    ap.add_argument("--traffic", default=str(ROOT / "profiles" / "gemv_gate_up_decode_b16_traffic.md"),
+                    help="the counter summary giving the decode gate / up kernel's HBM bytes per launch")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU (asked for {args.gpus}); the path is single-GPU by design",
@@ -137,6 +154,10 @@ def main() -> None:
     T = args.tokens
     log(f"decode: T={T}, {args.weight_sets} weight sets")
     dec = measure(shape, T, args.weight_sets, args.steps, args.warmup)
+    if args.copy_probe:
+        from artlite_amd.moe.layer import hbm_copy_ms
+
+        log(f"copy probe: {args.copy_probe} MiB, {hbm_copy_ms(args.copy_probe << 20, 1):.3f} ms")
     ms = dec["ms"]
     U = dec["U"]
     # algorithmic bytes: the layer (weights of the experts touched, router, x in, y out) and the dominant kernel
@@ -153,7 +174,7 @@ def main() -> None:
                    "experts": E, "top_k": k, "expert_ffn": F, "weights": shape["qtype"], "activations": "bf16",
                    "weight_sets": args.weight_sets, "experts_touched": U},
         "roofline": {"bound": "hbm", "kernel": "gate_up", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel_ms": gu_ms,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_bytes(args.traffic), "kernel_ms": gu_ms,
                      "algorithmic_bytes": gu_bytes},
         "layer_roofline": {"bound": "hbm", "achieved": layer_bytes / (ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS,
                            "unit": "GB/s", "frac": layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
