@@ -13,34 +13,6 @@
 
 namespace artlite {
 
-// exclusive prefix of one value per thread of a DISPATCH_BLOCK block; *total the sum (all threads)
-__device__ int block_scan(int v, int* total) {
-  __shared__ int wsum[DISPATCH_BLOCK / WAVE];
-  const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE;
-  int x = v;
-#pragma unroll
-  for (int o = 1; o < WAVE; o <<= 1) {
-    const int y = __shfl_up(x, o, WAVE);
-    if (lane >= o) x += y;
-  }
-  if (lane == WAVE - 1) wsum[wv] = x;
-  __syncthreads();
-  if (wv == 0) {
-    int s = lane < DISPATCH_BLOCK / WAVE ? wsum[lane] : 0;
-#pragma unroll
-    for (int o = 1; o < DISPATCH_BLOCK / WAVE; o <<= 1) {
-      const int y = __shfl_up(s, o, WAVE);
-      if (lane >= o) s += y;
-    }
-    if (lane < DISPATCH_BLOCK / WAVE) wsum[lane] = s;  // (inclusive over waves)
-  }
-  __syncthreads();
-  const int before = (wv ? wsum[wv - 1] : 0) + x - v;
-  *total = wsum[DISPATCH_BLOCK / WAVE - 1];
-  __syncthreads();
-  return before;
-}
-
 __global__ __launch_bounds__(DISPATCH_BLOCK) void k_count(DispatchBufs d) {
   __shared__ int hist[MAX_EXPERTS];
   __shared__ int last;

@@ -85,7 +85,8 @@ struct Path {
   bool gemv;         // routed experts on the GEMV
   bool shared_gemv;  // the shared expert on the GEMV
   bool split;        // bf16 hi / lo planes of fp32 x needed
-  bool quant;        // XQ of x needed
+  bool quant;        // XQ of x needed (made by the router's launch)
+  bool small;        // top k and dispatch in one workgroup
 };
 
 Path path_of(const artlite_moe_layer* L, int64_t T) {
@@ -95,6 +96,7 @@ Path path_of(const artlite_moe_layer* L, int64_t T) {
   const bool mfma_x = !p.gemv || (L->d.shared_ffn && !p.shared_gemv);
   p.split = mfma_x && L->x_dtype == ARTLITE_X_F32;
   p.quant = p.gemv;
+  p.small = p.gemv && T * L->d.top_k <= DISPATCH_BLOCK && L->d.n_experts <= MAX_EXPERTS;
   return p;
 }
 
@@ -102,13 +104,16 @@ Path path_of(const artlite_moe_layer* L, int64_t T) {
 std::vector<std::string> kernel_list(const artlite_moe_layer* L, int64_t T) {
   const Path p = path_of(L, T);
   std::vector<std::string> k;
-  if (p.quant) k.push_back("quant");
   if (p.split) k.push_back("split");
-  k.push_back("router");
+  k.push_back(p.quant ? "router_quant" : "router");
   if (L->d.shared_ffn && L->d.shared_gated) k.push_back("shared_gate");
-  k.push_back("topk");
-  k.push_back("dispatch_count");
-  k.push_back("dispatch_scatter");
+  if (p.small) {
+    k.push_back("route");
+  } else {
+    k.push_back("topk");
+    k.push_back("dispatch_count");
+    k.push_back("dispatch_scatter");
+  }
   k.push_back("gate_up");
   k.push_back("down");
   if (L->d.shared_ffn) {
@@ -132,10 +137,6 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     return ARTLITE_OK;
   };
   const Path path = path_of(L, T);
-  if (path.quant) {
-    ART_TRY(mark());
-    ART_TRY(launch_quant(L->x.p, L->x_dtype, T, H, L->xq.as<uint32_t>(), s));
-  }
   const uint16_t *ahi = L->x.as<uint16_t>(), *alo = nullptr;
   if (path.split) {
     ART_TRY(mark());
@@ -144,19 +145,24 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     alo = L->xlo.as<uint16_t>();
   }
   ART_TRY(mark());
-  ART_TRY(launch_router(L->x.p, L->x_dtype, L->router.as<float>(), H, E, T, L->logits.as<float>(), E, s));
+  ART_TRY(launch_router(L->x.p, L->x_dtype, L->router.as<float>(), H, E, T, L->logits.as<float>(), E,
+                        path.quant ? L->xq.as<uint32_t>() : nullptr, s));
   if (d.shared_ffn && d.shared_gated) {
     ART_TRY(mark());
-    ART_TRY(launch_router(L->x.p, L->x_dtype, L->sinp.as<float>(), H, 1, T, L->sg.as<float>(), 1, s));
+    ART_TRY(launch_router(L->x.p, L->x_dtype, L->sinp.as<float>(), H, 1, T, L->sg.as<float>(), 1, nullptr, s));
   }
-  ART_TRY(mark());
-  ART_TRY(launch_topk(L->logits.as<float>(), T, E, E, 0, E, k, d.gating, L->ids.as<int32_t>(), L->w.as<float>(),
-                      nullptr, s));
   const int BM = path.gemv ? GEMV_BM : DECODE_BM;
   DispatchBufs db{L->ids.as<int32_t>(), P, E, k, L->table.as<int32_t>(), L->ctrl.as<int32_t>(),
                   L->counts.as<int32_t>(), L->offsets.as<int32_t>(), L->order.as<int32_t>(), L->slot.as<int32_t>(),
                   L->tiles.as<int32_t>(), BM, nullptr, 0};
-  {
+  if (path.small) {
+    ART_TRY(mark());
+    ART_TRY(launch_route_small(L->logits.as<float>(), T, E, k, d.gating, L->ids.as<int32_t>(), L->w.as<float>(), db,
+                               s));
+  } else {
+    ART_TRY(mark());
+    ART_TRY(launch_topk(L->logits.as<float>(), T, E, E, 0, E, k, d.gating, L->ids.as<int32_t>(), L->w.as<float>(),
+                        nullptr, s));
     const int64_t nb = dispatch_blocks(P);
     ART_TRY(mark());
     ART_TRY(launch_dispatch_count(db, nb, s));

@@ -11,13 +11,96 @@ constexpr int ROUTER_TG = 16;      // tokens per router block (at most)
 constexpr int ROUTER_EW = 8;       // experts (waves) per router block
 constexpr int ROUTER_LDS = 64 * 1024;  // bytes of staged token rows per router block
 
+// ---- the top k of one token's logits, one wave (shared by k_topk and the small-batch routing)
+//
+// Ranking follows the reference's host step (csrc/artlite/moe_host.cpp:45-73): a logit's 64-bit key is its ordered
+// fp32 bits (after l + 0, so -0 ranks as +0) above ~id, so larger logits win and equal logits go to the lower id.
+// The weights follow moe_host.cpp:62-72: e^(l - l_max) (or sigmoid(l)) in double, their sum in numpy's pairwise
+// order (moe_host.cpp:25-39), e / sum rounded to fp32.
+__device__ __forceinline__ uint64_t logit_key(float l, int e) {
+  uint32_t u = __float_as_uint(l);
+  if (u == 0x80000000u) u = 0;  // (-0 ranks as +0)
+  const uint32_t ord = (u >> 31) ? ~u : (u | 0x80000000u);
+  return (uint64_t(ord) << 32) | uint32_t(~uint32_t(e));
+}
+
+// numpy's pairwise sum of n <= 128 doubles (moe_host.cpp:25-39)
+__device__ __forceinline__ double row_sum(const double* a, int n) {
+  if (n < 8) {
+    double s = 0;
+    for (int i = 0; i < n; i++) s += a[i];
+    return s;
+  }
+  double r[8];
+  for (int j = 0; j < 8; j++) r[j] = a[j];
+  int i = 8;
+  for (; i + 8 <= n; i += 8)
+    for (int j = 0; j < 8; j++) r[j] += a[i + j];
+  double s = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+  for (; i < n; i++) s += a[i];
+  return s;
+}
+
+// One token's top k by one wave: R keys per lane (expert e = lane + 64 r of the logits p, expert e at
+// (e / per_col) pitch + e % per_col), k rounds of a wave maximum (the winner's key cleared), lane j keeping the j-th;
+// then the weights. ev (64 doubles) and sum (1): the wave's LDS scratch. Lane j < k writes ids[j] and the weights
+// (w32 / w64 when given) and returns its id; other lanes return -1.
+template <int R>
+__device__ __forceinline__ int topk_wave(const float* __restrict__ p, int per_col, int64_t pitch, int E, int k,
+                                         int sigmoid, double* ev, double* sum, int lane, int32_t* __restrict__ ids,
+                                         float* __restrict__ w32, double* __restrict__ w64) {
+  uint64_t key[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int e = lane + WAVE * r;
+    key[r] = e < E ? logit_key(p[int64_t(e / per_col) * pitch + e % per_col], e) : 0;
+  }
+  uint64_t mine = 0;
+  for (int j = 0; j < k; j++) {
+    uint64_t m = 0;
+#pragma unroll
+    for (int r = 0; r < R; r++) m = key[r] > m ? key[r] : m;
+    m = wave_max_u64(m);
+#pragma unroll
+    for (int r = 0; r < R; r++)
+      if (key[r] == m) key[r] = 0;
+    if (lane == j) mine = m;
+  }
+  const int id = int(~uint32_t(mine));
+  const bool on = lane < k;
+  const float l = on ? p[int64_t(id / per_col) * pitch + id % per_col] : 0.0f;
+  const double l0 = __shfl(double(l), 0, WAVE);
+  double e = 0;
+  if (on) e = sigmoid ? 1.0 / (1.0 + exp(-double(l))) : exp(double(l) - l0);
+  ev[lane] = e;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  if (lane == 0) {
+    double s = row_sum(ev, k);
+    if (sigmoid) s = s < 6.103515625e-5 ? 6.103515625e-5 : s;  // (std::max(s, 2^-14): a NaN sum stays NaN)
+    *sum = s;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  const double s = *sum;
+  __builtin_amdgcn_wave_barrier();  // (the scratch is free again once every lane has read the sum)
+  if (!on) return -1;
+  ids[lane] = id;
+  const double w = e / s;
+  if (w32) w32[lane] = float(w);
+  if (w64) w64[lane] = w;
+  return id;
+}
+
 int check_route_args(int64_t n, int per_col, int E, int k);
 
 int launch_topk(const float* logits, int64_t n, int64_t row, int per_col, int64_t pitch, int E, int k, int sigmoid,
                 int32_t* ids, float* w32, double* w64, hipStream_t s);
 
+// Router logits out[t out_row + e] = x[t] . W[e] (float64 accumulation, rounded once). xq: when given, x is also
+// quantised into XQ rows (gemv.h) by extra workgroups of the same launch (H a multiple of 256).
 int launch_router(const void* x, int x_dtype, const float* W, int H, int E, int64_t T, float* out, int64_t out_row,
-                  hipStream_t s);
+                  uint32_t* xq, hipStream_t s);
 
 // ---- dispatch: the stable counting sort of the (token, slot) pairs by expert
 constexpr int DISPATCH_BLOCK = 1024;  // pairs per block
@@ -55,6 +138,34 @@ inline int64_t dispatch_blocks(int64_t P) { return P > 0 ? (P + DISPATCH_BLOCK -
 // an upper bound on the tiles of P pairs over E experts with BM rows per tile
 inline int64_t tile_bound(int64_t P, int E, int BM) { return (P + BM - 1) / BM + (P < E ? P : E); }
 
+// exclusive prefix of one value per thread of a DISPATCH_BLOCK block; *total the sum (all threads)
+__device__ __forceinline__ int block_scan(int v, int* total) {
+  __shared__ int wsum[DISPATCH_BLOCK / WAVE];
+  const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < WAVE; o <<= 1) {
+    const int y = __shfl_up(x, o, WAVE);
+    if (lane >= o) x += y;
+  }
+  if (lane == WAVE - 1) wsum[wv] = x;
+  __syncthreads();
+  if (wv == 0) {
+    int s = lane < DISPATCH_BLOCK / WAVE ? wsum[lane] : 0;
+#pragma unroll
+    for (int o = 1; o < DISPATCH_BLOCK / WAVE; o <<= 1) {
+      const int y = __shfl_up(s, o, WAVE);
+      if (lane >= o) s += y;
+    }
+    if (lane < DISPATCH_BLOCK / WAVE) wsum[lane] = s;  // (inclusive over waves)
+  }
+  __syncthreads();
+  const int before = (wv ? wsum[wv - 1] : 0) + x - v;
+  *total = wsum[DISPATCH_BLOCK / WAVE - 1];
+  __syncthreads();
+  return before;
+}
+
 int launch_dispatch(const DispatchBufs& d, hipStream_t s);
 int launch_dispatch_count(const DispatchBufs& d, int64_t nb, hipStream_t s);
 int launch_dispatch_scatter(const DispatchBufs& d, int64_t nb, hipStream_t s);
@@ -68,5 +179,11 @@ struct PlanBufs {
   int64_t* pos;      // P
 };
 int launch_plan(const DispatchBufs& d, const PlanBufs& p, hipStream_t s);
+
+// Small batches (n k <= DISPATCH_BLOCK pairs, E <= MAX_EXPERTS): the top k of n tokens' plain (n, E) logits and the
+// dispatch of their pairs (d.ids receives the ids; counts, offsets, order, slot, tiles, ctrl[CTRL_TILES]) in one
+// workgroup: the results of launch_topk followed by launch_dispatch.
+int launch_route_small(const float* logits, int64_t n, int E, int k, int sigmoid, int32_t* ids, float* w32,
+                       const DispatchBufs& d, hipStream_t s);
 
 }  // namespace artlite

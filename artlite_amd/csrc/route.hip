@@ -6,39 +6,15 @@
 // The weights follow moe_host.cpp:62-72: e^(l - l_max) (or sigmoid(l)) in double, their sum in numpy's pairwise
 // order (moe_host.cpp:25-39), e / sum rounded to fp32.
 #include "route.h"
+#include "xq.h"
 
 #include <algorithm>
 
 namespace artlite {
 
-__device__ __forceinline__ uint64_t logit_key(float l, int e) {
-  uint32_t u = __float_as_uint(l);
-  if (u == 0x80000000u) u = 0;  // (-0 ranks as +0)
-  const uint32_t ord = (u >> 31) ? ~u : (u | 0x80000000u);
-  return (uint64_t(ord) << 32) | uint32_t(~uint32_t(e));
-}
-
-// numpy's pairwise sum of n <= 128 doubles (moe_host.cpp:25-39)
-__device__ double row_sum(const double* a, int n) {
-  if (n < 8) {
-    double s = 0;
-    for (int i = 0; i < n; i++) s += a[i];
-    return s;
-  }
-  double r[8];
-  for (int j = 0; j < 8; j++) r[j] = a[j];
-  int i = 8;
-  for (; i + 8 <= n; i += 8)
-    for (int j = 0; j < 8; j++) r[j] += a[i + j];
-  double s = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
-  for (; i < n; i++) s += a[i];
-  return s;
-}
-
 constexpr int TOPK_WAVES = 4;
 
-// One wave per token: R keys per lane (expert e = lane + 64 r), k rounds of a wave maximum (the winner's key
-// cleared), lane j keeping the j-th; then the weights.
+// one wave per token (topk_wave, route.h)
 template <int R>
 __global__ __launch_bounds__(TOPK_WAVES * WAVE) void k_topk(const float* __restrict__ logits, int64_t n, int64_t row,
                                                             int per_col, int64_t pitch, int E, int k, int sigmoid,
@@ -49,47 +25,9 @@ __global__ __launch_bounds__(TOPK_WAVES * WAVE) void k_topk(const float* __restr
   const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE;
   const int64_t t = int64_t(blockIdx.x) * TOPK_WAVES + wv;
   if (t >= n) return;  // (uniform per wave)
-  const float* p = logits + t * row;
-  uint64_t key[R];
-#pragma unroll
-  for (int r = 0; r < R; r++) {
-    const int e = lane + WAVE * r;
-    key[r] = e < E ? logit_key(p[int64_t(e / per_col) * pitch + e % per_col], e) : 0;
-  }
-  uint64_t mine = 0;
-  for (int j = 0; j < k; j++) {
-    uint64_t m = 0;
-#pragma unroll
-    for (int r = 0; r < R; r++) m = key[r] > m ? key[r] : m;
-    m = wave_max_u64(m);
-#pragma unroll
-    for (int r = 0; r < R; r++)
-      if (key[r] == m) key[r] = 0;
-    if (lane == j) mine = m;
-  }
-  const int id = int(~uint32_t(mine));
-  const bool on = lane < k;
-  const float l = on ? p[int64_t(id / per_col) * pitch + id % per_col] : 0.0f;
-  const double l0 = __shfl(double(l), 0, WAVE);
-  double e = 0;
-  if (on) e = sigmoid ? 1.0 / (1.0 + exp(-double(l))) : exp(double(l) - l0);
-  ev[wv][lane] = e;
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  if (lane == 0) {
-    double s = row_sum(ev[wv], k);
-    if (sigmoid) s = s < 6.103515625e-5 ? 6.103515625e-5 : s;  // (std::max(s, 2^-14): a NaN sum stays NaN)
-    sum[wv] = s;
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  const double s = sum[wv];
-  if (on) {
-    ids[t * k + lane] = id;
-    const double w = e / s;
-    if (w32) w32[t * k + lane] = float(w);
-    if (w64) w64[t * k + lane] = w;
-  }
+  const int id = topk_wave<R>(logits + t * row, per_col, pitch, E, k, sigmoid, ev[wv], &sum[wv], lane, ids + t * k,
+                              w32 ? w32 + t * k : nullptr, w64 ? w64 + t * k : nullptr);
+  (void)id;
 }
 
 int launch_topk(const float* logits, int64_t n, int64_t row, int per_col, int64_t pitch, int E, int k, int sigmoid,
@@ -112,49 +50,75 @@ int launch_topk(const float* logits, int64_t n, int64_t row, int per_col, int64_
   return ARTLITE_OK;
 }
 
-// Router logits: a block of ROUTER_EW waves (one expert each) over a tile of up to ROUTER_TG tokens whose rows are
-// staged in LDS; each lane accumulates float64 partial dot products (exact products of fp32 / bf16 values) over
-// h = 4 lane + 256 j, then a fixed shuffle tree; the sum is rounded once to fp32.
-template <int XT>
-__global__ __launch_bounds__(ROUTER_EW * WAVE) void k_router(const void* __restrict__ xv, const float* __restrict__ W,
-                                                            int H, int E, int64_t T, int tt, float* __restrict__ out,
-                                                            int64_t out_row) {
+// Router logits: a block of EW waves (one expert each) over a tile of up to ROUTER_TG tokens whose rows are staged
+// in LDS; each lane accumulates float64 partial dot products (exact products of fp32 / bf16 values) over
+// h = 4 lane + 256 j, its weights for 8 j at a time loaded up front, then a fixed shuffle tree; the sum is rounded
+// once to fp32. With xq, workgroups past the router's (blockIdx.x >= nbx, first token tile) quantise x into XQ,
+// one wave per (row, unit).
+template <int XT, int EW>
+__global__ __launch_bounds__(EW * WAVE) void k_router(const void* __restrict__ xv, const float* __restrict__ W, int H,
+                                                     int E, int64_t T, int tt, float* __restrict__ out,
+                                                     int64_t out_row, uint32_t* __restrict__ xq, int nbx) {
   extern __shared__ __attribute__((aligned(16))) uint8_t xs[];  // tt rows of H values (x's own dtype)
   constexpr int XB = XT == ARTLITE_X_F32 ? 4 : 2;
   const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE;
+  if (int(blockIdx.x) >= nbx) {  // XQ of x
+    if (blockIdx.y) return;
+    const int64_t w = int64_t(blockIdx.x - nbx) * EW + wv;
+    if (w < T * (H / 256)) xq_quant_unit<XT>(xv, w, H, xq, lane);
+    return;
+  }
   const int64_t t0 = int64_t(blockIdx.y) * tt;
   const int nt = int(min(int64_t(tt), T - t0));
   {  // stage the tile's rows (16-byte pieces)
     const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(xv) + t0 * H * XB);
     uint4* dst = reinterpret_cast<uint4*>(xs);
     const int n16 = nt * H * XB / 16;
-    for (int i = threadIdx.x; i < n16; i += blockDim.x) dst[i] = src[i];
+    int i = threadIdx.x;
+    for (; i + 7 * EW * WAVE < n16; i += 8 * EW * WAVE) {  // (eight loads in flight per lane)
+      uint4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = src[i + j * EW * WAVE];
+#pragma unroll
+      for (int j = 0; j < 8; j++) dst[i + j * EW * WAVE] = v[j];
+    }
+    for (; i < n16; i += EW * WAVE) dst[i] = src[i];
   }
   __syncthreads();
-  const int e = blockIdx.x * ROUTER_EW + wv;
+  const int e = blockIdx.x * EW + wv;
   if (e >= E) return;
   const float* w = W + int64_t(e) * H;
   double acc[ROUTER_TG];
 #pragma unroll
   for (int t = 0; t < ROUTER_TG; t++) acc[t] = 0.0;
-  for (int h = 4 * lane; h < H; h += 4 * WAVE) {
-    const float4 wq = *reinterpret_cast<const float4*>(w + h);
+  for (int h0 = 0; h0 < H; h0 += 8 * 4 * WAVE) {
+    float4 wq[8];
 #pragma unroll
-    for (int t = 0; t < ROUTER_TG; t++) {
-      if (t < nt) {
-        float x0, x1, x2, x3;
-        if (XT == ARTLITE_X_F32) {
-          const float4 v = *reinterpret_cast<const float4*>(xs + (int64_t(t) * H + h) * 4);
-          x0 = v.x, x1 = v.y, x2 = v.z, x3 = v.w;
-        } else {
-          const uint2 v = *reinterpret_cast<const uint2*>(xs + (int64_t(t) * H + h) * 2);
-          x0 = bf16_to_f32(v.x & 0xFFFFu), x1 = bf16_to_f32(v.x >> 16);
-          x2 = bf16_to_f32(v.y & 0xFFFFu), x3 = bf16_to_f32(v.y >> 16);
+    for (int j = 0; j < 8; j++) {
+      const int h = h0 + 4 * lane + 4 * WAVE * j;
+      wq[j] = h < H ? *reinterpret_cast<const float4*>(w + h) : make_float4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int h = h0 + 4 * lane + 4 * WAVE * j;
+      if (h >= H) break;
+#pragma unroll
+      for (int t = 0; t < ROUTER_TG; t++) {
+        if (t < nt) {
+          float x0, x1, x2, x3;
+          if (XT == ARTLITE_X_F32) {
+            const float4 v = *reinterpret_cast<const float4*>(xs + (int64_t(t) * H + h) * 4);
+            x0 = v.x, x1 = v.y, x2 = v.z, x3 = v.w;
+          } else {
+            const uint2 v = *reinterpret_cast<const uint2*>(xs + (int64_t(t) * H + h) * 2);
+            x0 = bf16_to_f32(v.x & 0xFFFFu), x1 = bf16_to_f32(v.x >> 16);
+            x2 = bf16_to_f32(v.y & 0xFFFFu), x3 = bf16_to_f32(v.y >> 16);
+          }
+          acc[t] += double(x0) * double(wq[j].x);
+          acc[t] += double(x1) * double(wq[j].y);
+          acc[t] += double(x2) * double(wq[j].z);
+          acc[t] += double(x3) * double(wq[j].w);
         }
-        acc[t] += double(x0) * double(wq.x);
-        acc[t] += double(x1) * double(wq.y);
-        acc[t] += double(x2) * double(wq.z);
-        acc[t] += double(x3) * double(wq.w);
       }
     }
   }
@@ -167,19 +131,201 @@ __global__ __launch_bounds__(ROUTER_EW * WAVE) void k_router(const void* __restr
   }
 }
 
+// Router logits for small batches (T <= ROUTER_TG tokens per tile, H a multiple of 1024): a workgroup per expert,
+// its 4 waves each a quarter of H (lane: h = quarter + 4 lane + 256 j), x read straight from memory (L2), float64
+// products and per-wave shuffle trees, then the quarters summed in order; rounded once to fp32. With xq, workgroups
+// past the experts' quantise x into XQ as k_router's do.
+template <int XT>
+__global__ __launch_bounds__(4 * WAVE) void k_router_small(const void* __restrict__ xv, const float* __restrict__ W,
+                                                          int H, int E, int64_t T, float* __restrict__ out,
+                                                          int64_t out_row, uint32_t* __restrict__ xq) {
+  __shared__ double part[4][ROUTER_TG];
+  const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE;
+  if (int(blockIdx.x) >= E) {  // XQ of x
+    if (blockIdx.y) return;
+    const int64_t w = int64_t(blockIdx.x - E) * 4 + wv;
+    if (w < T * (H / 256)) xq_quant_unit<XT>(xv, w, H, xq, lane);
+    return;
+  }
+  const int e = blockIdx.x;
+  const int64_t t0 = int64_t(blockIdx.y) * ROUTER_TG;
+  const int nt = int(min(int64_t(ROUTER_TG), T - t0));
+  const int q = H / 4, nj = q / (4 * WAVE);
+  const float* w = W + int64_t(e) * H + wv * q;
+  double acc[ROUTER_TG];
+#pragma unroll
+  for (int t = 0; t < ROUTER_TG; t++) acc[t] = 0.0;
+  for (int j0 = 0; j0 < nj; j0 += 2) {
+    float4 wq[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+      wq[j] = j0 + j < nj ? *reinterpret_cast<const float4*>(w + 4 * lane + 4 * WAVE * (j0 + j)) : make_float4(0, 0, 0, 0);
+    float xf[ROUTER_TG][2][4];
+#pragma unroll
+    for (int t = 0; t < ROUTER_TG; t++)
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const int64_t i = (t0 + min(t, nt - 1)) * H + wv * q + 4 * lane + 4 * WAVE * (j0 + j);
+        if (XT == ARTLITE_X_F32) {
+          const float4 v = *reinterpret_cast<const float4*>(static_cast<const float*>(xv) + i);
+          xf[t][j][0] = v.x, xf[t][j][1] = v.y, xf[t][j][2] = v.z, xf[t][j][3] = v.w;
+        } else {
+          const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(xv) + i);
+          xf[t][j][0] = bf16_to_f32(v.x & 0xFFFFu), xf[t][j][1] = bf16_to_f32(v.x >> 16);
+          xf[t][j][2] = bf16_to_f32(v.y & 0xFFFFu), xf[t][j][3] = bf16_to_f32(v.y >> 16);
+        }
+      }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      if (j0 + j >= nj) break;
+      const double w0 = wq[j].x, w1 = wq[j].y, w2 = wq[j].z, w3 = wq[j].w;
+#pragma unroll
+      for (int t = 0; t < ROUTER_TG; t++) {
+        acc[t] += double(xf[t][j][0]) * w0;
+        acc[t] += double(xf[t][j][1]) * w1;
+        acc[t] += double(xf[t][j][2]) * w2;
+        acc[t] += double(xf[t][j][3]) * w3;
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < ROUTER_TG; t++) {
+    double v = acc[t];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    if (lane == 0) part[wv][t] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < nt) {
+    const int t = threadIdx.x;
+    out[(t0 + t) * out_row + e] = float(((part[0][t] + part[1][t]) + part[2][t]) + part[3][t]);
+  }
+}
+
 int launch_router(const void* x, int x_dtype, const float* W, int H, int E, int64_t T, float* out, int64_t out_row,
-                  hipStream_t s) {
+                  uint32_t* xq, hipStream_t s) {
   if (T <= 0) return ARTLITE_OK;
   if (H % 8) return fail(ARTLITE_EINVAL, "router: H %d not a multiple of 8", H);
+  if (xq && H % 256) return fail(ARTLITE_EINVAL, "router: XQ of H %d (not a multiple of 256)", H);
   const int xb = x_dtype == ARTLITE_X_F32 ? 4 : 2;
   const int tt = int(std::min<int64_t>(ROUTER_TG, std::max<int64_t>(1, ROUTER_LDS / (int64_t(H) * xb))));
   if (int64_t(H) * xb > ROUTER_LDS) return fail(ARTLITE_EINVAL, "router: H %d too wide", H);
-  const dim3 grid(unsigned((E + ROUTER_EW - 1) / ROUTER_EW), unsigned((T + tt - 1) / tt)), block(ROUTER_EW * WAVE);
   const size_t lds = size_t(tt) * H * xb;
-  if (x_dtype == ARTLITE_X_F32)
-    k_router<ARTLITE_X_F32><<<grid, block, lds, s>>>(x, W, H, E, T, tt, out, out_row);
+  if (T <= ROUTER_TG && H % 1024 == 0) {  // (a workgroup per expert)
+    const int nq = xq ? int((T * (H / 256) + 3) / 4) : 0;
+    const dim3 g(unsigned(E + nq), 1), b(4 * WAVE);
+    if (x_dtype == ARTLITE_X_F32)
+      k_router_small<ARTLITE_X_F32><<<g, b, 0, s>>>(x, W, H, E, T, out, out_row, xq);
+    else
+      k_router_small<ARTLITE_X_BF16><<<g, b, 0, s>>>(x, W, H, E, T, out, out_row, xq);
+    ART_HIP(hipGetLastError());
+    return ARTLITE_OK;
+  }
+  // (small batches: 4 experts per workgroup, for more workgroups)
+  const bool small = T <= 4 * ROUTER_TG;
+  const int ew = small ? 4 : ROUTER_EW;
+  const int nbx = (E + ew - 1) / ew;
+  const int nq = xq ? int((T * (H / 256) + ew - 1) / ew) : 0;
+  const dim3 grid(unsigned(nbx + nq), unsigned((T + tt - 1) / tt)), block(ew * WAVE);
+#define ART_ROUTER(XT, EWN) k_router<XT, EWN><<<grid, block, lds, s>>>(x, W, H, E, T, tt, out, out_row, xq, nbx)
+  if (x_dtype == ARTLITE_X_F32) {
+    if (small)
+      ART_ROUTER(ARTLITE_X_F32, 4);
+    else
+      ART_ROUTER(ARTLITE_X_F32, ROUTER_EW);
+  } else {
+    if (small)
+      ART_ROUTER(ARTLITE_X_BF16, 4);
+    else
+      ART_ROUTER(ARTLITE_X_BF16, ROUTER_EW);
+  }
+#undef ART_ROUTER
+  ART_HIP(hipGetLastError());
+  return ARTLITE_OK;
+}
+
+// ---- small batches: the top k of every token, then the stable counting sort of the pairs, in one workgroup
+// (the results of k_topk, k_count and k_scatter for a single block of pairs)
+template <int R>
+__global__ __launch_bounds__(DISPATCH_BLOCK) void k_route_small(const float* __restrict__ logits, int64_t n, int E,
+                                                                int k, int sigmoid, int32_t* __restrict__ ids,
+                                                                float* __restrict__ w32, DispatchBufs d) {
+  constexpr int NW = DISPATCH_BLOCK / WAVE;
+  __shared__ double ev[NW][WAVE];
+  __shared__ double sum[NW];
+  __shared__ int sid[DISPATCH_BLOCK];
+  __shared__ int base[MAX_EXPERTS];
+  __shared__ uint16_t wcnt[NW][MAX_EXPERTS];
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), wv = tid / WAVE;
+  for (int64_t t = wv; t < n; t += NW) {  // (one wave per token)
+    const int id = topk_wave<R>(logits + t * E, E, 0, E, k, sigmoid, ev[wv], &sum[wv], lane, ids + t * k,
+                                w32 + t * k, nullptr);
+    if (lane < k) sid[t * k + lane] = id;
+  }
+  for (int e = tid; e < E; e += DISPATCH_BLOCK) base[e] = 0;
+  for (int i = tid; i < NW * E; i += DISPATCH_BLOCK) wcnt[i / E][i % E] = 0;
+  __syncthreads();
+  const int P = int(n) * k, p = tid;
+  const bool valid = p < P;
+  const int id = valid ? sid[p] : -1;
+  if (valid) atomicAdd(&base[id], 1);  // (counts: order-free)
+  __syncthreads();
+  const int e = tid;
+  const int c = e < E ? base[e] : 0;
+  int total;
+  const int start = block_scan(c, &total);
+  if (e < E) {
+    d.counts[e] = c;
+    d.offsets[e] = start;
+    base[e] = start;
+  }
+  if (e == 0) d.offsets[E] = total;
+  if (d.BM > 0) {  // the expert GEMMs' tiles: experts ascending, BM sorted rows each
+    const int nt = e < E ? (c + d.BM - 1) / d.BM : 0;
+    int nt_total;
+    const int t0 = block_scan(nt, &nt_total);
+    for (int m = 0; m < nt; m++) {
+      d.tiles[2 * (t0 + m)] = e;
+      d.tiles[2 * (t0 + m) + 1] = start + m * d.BM;
+    }
+    if (e == 0) d.ctrl[CTRL_TILES] = nt_total;
+  }
+  // each pair's rank among the earlier pairs of its expert: the lanes of its wave with the same expert (ballots over
+  // the id bits), then the earlier waves' counts
+  uint64_t peers = __ballot(valid);
+  for (int bit = 0; (1 << bit) < E; bit++) {
+    const bool set = (id >> bit) & 1;
+    const uint64_t b = __ballot(set);
+    peers &= set ? b : ~b;
+  }
+  const uint64_t below = (uint64_t(1) << lane) - 1;
+  int rank = __popcll(peers & below);
+  if (valid && !(peers & below)) wcnt[wv][id] = uint16_t(__popcll(peers));
+  __syncthreads();
+  if (!valid) return;
+  for (int w = 0; w < wv; w++) rank += wcnt[w][id];
+  const int dest = base[id] + rank;
+  d.order[dest] = p;
+  d.slot[p] = dest;
+}
+
+int launch_route_small(const float* logits, int64_t n, int E, int k, int sigmoid, int32_t* ids, float* w32,
+                       const DispatchBufs& d, hipStream_t s) {
+  if (n <= 0) return ARTLITE_OK;
+  if (n * k > DISPATCH_BLOCK || E > MAX_EXPERTS)
+    return fail(ARTLITE_EINVAL, "route_small: %lld pairs of %d experts", (long long)(n * k), E);
+#define ART_RS(RR) k_route_small<RR><<<1, DISPATCH_BLOCK, 0, s>>>(logits, n, E, k, sigmoid, ids, w32, d)
+  if (E <= 64)
+    ART_RS(1);
+  else if (E <= 128)
+    ART_RS(2);
+  else if (E <= 256)
+    ART_RS(4);
+  else if (E <= 512)
+    ART_RS(8);
   else
-    k_router<ARTLITE_X_BF16><<<grid, block, lds, s>>>(x, W, H, E, T, tt, out, out_row);
+    ART_RS(16);
+#undef ART_RS
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
 }

@@ -35,7 +35,7 @@ def check_layer(name: str, T: int, seed: int = 0) -> None:
     x = layers.make_x(spec, T, seed)
     with gpu_layer(layer, max_tokens=T) as g:
         y = g(gpu_input(spec, x))
-        gemv = "quant" in g.kernel_names()
+        gemv = "router_quant" in g.kernel_names()
         assert gemv == ((name, T) in GEMV_CASES), (name, T, g.kernel_names())
         lg = g.tap("logits")
         ids, w = g.tap("ids"), g.tap("weights")
