@@ -38,6 +38,7 @@ struct GemvArgs {
   int64_t max_tiles;       // grid bound
   uint32_t* hq;            // SwiGLU: h = silu(gate) up as XQ rows (by sorted row)
   float* y;                // plain: fp32 rows (by sorted row), stride N
+  int rpw;                 // plain: blocks of 64 output rows per workgroup (>= 1), streamed one after the other
 };
 
 // whether the GEMV takes weights of this type with rows of K values

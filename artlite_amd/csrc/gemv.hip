@@ -17,6 +17,7 @@
 #include "gemv.h"
 #include "xq.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <utility>
@@ -293,15 +294,20 @@ __device__ __forceinline__ void gemv_tile(const GemvArgs& a, int e, int s0) {
   u32x4* my = slab + wv * D * WCH;
   u32x4* xslot = slab + 4 * D * WCH;  // 2 x GEMV_BM x 64 chunks
   float* hbuf = reinterpret_cast<float*>(xslot + 2 * GEMV_BM * 64);
-  const int n0 = blockIdx.y * 64, nw = n0 + 16 * wv;
-  const int U = a.K / 256, NV = U * NM;
+  // plain products: a.rpw blocks of 64 rows, one after the other (SwiGLU: one)
+  const int rpw = SWIGLU ? 1 : a.rpw;
+  const int n0 = blockIdx.y * 64 * rpw, nw = n0 + 16 * wv;
+  const int U = a.K / 256, NV = U * NM;                      // units per block of rows
+  const int NVt = min(rpw, (a.N - n0 + 63) / 64) * NV, KKt = NVt / NM;  // units, K-units in all
 
-  // the lane's chunk of each load instruction of a unit (chunk 64 i + lane of the wave's 16 x CH)
-  int32_t off[NI];
+  // the lane's chunk of each load instruction of a unit (chunk 64 i + lane of the wave's 16 x CH): its row and
+  // column offset
+  int rw[NI], cw[NI];
 #pragma unroll
   for (int i = 0; i < NI; i++) {
     const int q = min(64 * i + lane, WCH - 1), row = q / CH;
-    off[i] = min(nw + row, a.N - 1) * a.row_bytes + 16 * (q - row * CH);
+    rw[i] = row;
+    cw[i] = 16 * (q - row * CH);
   }
   const uint8_t* wb[NM];
 #pragma unroll
@@ -314,9 +320,10 @@ __device__ __forceinline__ void gemv_tile(const GemvArgs& a, int e, int s0) {
       const int64_t ar = a.a_gather ? a.order[s0 + t] / a.topk : s0 + t;
       xr[t] = reinterpret_cast<const uint8_t*>(a.xq + ar * xq_row_dwords(a.K)) + 16 * lane;
     }
-  auto issue_x = [&](int ku) {  // (wave 0; ku past the last: the last again, into the idle slot)
-    u32x4* dst = xslot + (ku & 1) * GEMV_BM * 64;
-    ku = min(ku, U - 1);
+  auto issue_x = [&](int kk) {  // (wave 0; K-unit kk of the sequence (past the last: the last again, into the idle
+                                //  slot), K-range kk % U)
+    u32x4* dst = xslot + (kk & 1) * GEMV_BM * 64;
+    const int ku = min(kk, KKt - 1) % U;
 #pragma unroll
     for (int t = 0; t < M; t++)
       __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(xr[t] + ku * (XQ_UNIT * 4)),
@@ -325,12 +332,14 @@ __device__ __forceinline__ void gemv_tile(const GemvArgs& a, int e, int s0) {
   // the weights of unit v (K-range v / NM of matrix v % NM) into this wave's slot v % D
   auto issue_w = [&](int v, auto mtx_c) {
     constexpr int MX = decltype(mtx_c)::value;
-    const uint8_t* src = wb[MX] + int64_t(v / NM) * BY;
+    const int rb = v / NV;
+    const uint8_t* src = wb[MX] + int64_t((v - rb * NV) / NM) * BY;
     u32x4* dst = my + (v % D) * WCH;
 #pragma unroll
     for (int i = 0; i < NI; i++)
       if (i < NI - 1 || lane < LAST)
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src + off[i]),
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(
+                                             src + min(nw + 64 * rb + rw[i], a.N - 1) * a.row_bytes + cw[i]),
                                          (__attribute__((address_space(3))) void*)(dst + 64 * i), 16, 0, 0);
   };
 
@@ -350,38 +359,38 @@ __device__ __forceinline__ void gemv_tile(const GemvArgs& a, int e, int s0) {
   // then past K-unit ku - 1, whose record slot it takes, and sees K-unit ku's records, which wave 0 waited for just
   // before. The loop is unrolled by NM, which fixes each step's matrix.
   if (wv == 0) issue_x(0);
-  for (int v = 0; v < D - 1 && v < NV; v++) {
+  for (int v = 0; v < D - 1 && v < NVt; v++) {
     if (NM == 1 || v % NM == 0)
       issue_w(v, std::integral_constant<int, 0>{});
     else
       issue_w(v, std::integral_constant<int, NM - 1>{});
   }
-  for (int v0 = 0; v0 < NV; v0 += NM) {
+  for (int v0 = 0; v0 < NVt; v0 += NM) {
     static_for<NM>([&](auto jc) {
       constexpr int MX = decltype(jc)::value;
-      const int v = v0 + MX, ku = v0 / NM;
-      if (v >= NV) return;
+      const int v = v0 + MX, kk = v0 / NM;
+      if (v >= NVt) return;
       if (MX == 0) {
-        // wave 0: K-unit ku's records (issued before the weights of the units since its issue that were issued)
+        // wave 0: K-unit kk's records (issued before the weights of the units since its issue that were issued)
         if (wv == 0) {
-          if (ku == 0)
-            wait_vm_c<0, NI, 3>(min(D - 1, NV));
+          if (kk == 0)
+            wait_vm_c<0, NI, 3>(min(D - 1, NVt));
           else
-            wait_vm_c<0, NI, NM>(min(NM, max(0, NV - D + 1 - (ku - 1) * NM)));
+            wait_vm_c<0, NI, NM>(min(NM, max(0, NVt - D + 1 - (kk - 1) * NM)));
         }
         __builtin_amdgcn_s_barrier();
-        if (wv == 0) issue_x(ku + 1);
+        if (wv == 0) issue_x(kk + 1);
       }
-      if (v + D - 1 < NV) issue_w(v + D - 1, std::integral_constant<int, (MX + D - 1) % NM>{});
+      if (v + D - 1 < NVt) issue_w(v + D - 1, std::integral_constant<int, (MX + D - 1) % NM>{});
       // unit v's weights have landed once only the loads issued after them are outstanding: the weights of the
       // `ahead` units after it, and (wave 0) the records issued at the K-unit starts among steps v - D + 2 .. v
-      const int ahead = min(D - 1, NV - 1 - v);
+      const int ahead = min(D - 1, NVt - 1 - v);
       int nx = 0;
       if (wv == 0)
         for (int j = max(0, v - D + 2); j <= v; j++) nx += j % NM == 0;
       uint32_t w[LW];
       u32x4 x[M];
-      const uint32_t sw = wbase + (v % D) * WCH * 16, px = xbase + (ku & 1) * GEMV_BM * 1024;
+      const uint32_t sw = wbase + (v % D) * WCH * 16, px = xbase + (kk & 1) * GEMV_BM * 1024;
       // (the count in one immediate: nx rows of M records plus ahead x NI)
       const int n = ahead * NI + nx * M;
       static_for<(D - 1) * NI + D * M + 1>([&](auto nc) {
@@ -396,18 +405,31 @@ __device__ __forceinline__ void gemv_tile(const GemvArgs& a, int e, int s0) {
 #pragma unroll
         for (int t = 0; t < M; t++) acc[MX][t] = group_term<QT, H>(acc[MX][t], x[t][H], x[t][2], x[t][3], q, d, mn);
       });
+      if constexpr (!SWIGLU) {
+        if (v % NV == NV - 1) {  // a block of rows done: the four lanes of a row summed, then y
+          const int rb = v / NV, n = nw + 64 * rb + r;
+#pragma unroll
+          for (int t = 0; t < M; t++) {
+            float y = acc[0][t];
+            y += __shfl_xor(y, 16);
+            y += __shfl_xor(y, 32);
+            if (p == 0 && n < a.N) a.y[int64_t(s0 + t) * a.N + n] = y;
+            acc[0][t] = 0.0f;
+          }
+        }
+      }
     });
   }
 
-  // the four lanes of a row: their groups' sums
-#pragma unroll
-  for (int mx = 0; mx < NM; mx++)
-#pragma unroll
-    for (int t = 0; t < M; t++) {
-      acc[mx][t] += __shfl_xor(acc[mx][t], 16);
-      acc[mx][t] += __shfl_xor(acc[mx][t], 32);
-    }
   if constexpr (SWIGLU) {
+    // the four lanes of a row: their groups' sums
+#pragma unroll
+    for (int mx = 0; mx < NM; mx++)
+#pragma unroll
+      for (int t = 0; t < M; t++) {
+        acc[mx][t] += __shfl_xor(acc[mx][t], 16);
+        acc[mx][t] += __shfl_xor(acc[mx][t], 32);
+      }
     // h = silu(gate) up of the 64 rows, then quantised by wave 0 into XQ rows of N values (lanes 0..31: one group,
     // 32..63: the next)
     if (p == 0)
@@ -439,11 +461,6 @@ __device__ __forceinline__ void gemv_tile(const GemvArgs& a, int e, int s0) {
       }
       if (v < 16) xq_put_word(ub, g, v, s256, sum, xsum);
     }
-  } else {
-    const int n = nw + r;
-    if (p == 0 && n < a.N)
-#pragma unroll
-      for (int t = 0; t < M; t++) a.y[int64_t(s0 + t) * a.N + n] = acc[0][t];
   }
 }
 
@@ -481,7 +498,8 @@ int launch_t(const GemvArgs& a, hipStream_t s) {
   constexpr int D = 2;
   const int64_t tiles = a.tiles ? a.max_tiles : (a.dense_rows + GEMV_BM - 1) / GEMV_BM;
   if (tiles <= 0) return ARTLITE_OK;
-  const dim3 grid(unsigned(tiles), unsigned((a.N + 63) / 64)), block(256);
+  const int rpw = SWIGLU ? 1 : a.rpw;
+  const dim3 grid(unsigned(tiles), unsigned((a.N + 64 * rpw - 1) / (64 * rpw))), block(256);
   k_gemv<QT, SWIGLU, D><<<grid, block, gemv_lds<QT, D>(), s>>>(a);
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
@@ -503,7 +521,9 @@ int launch_gemv(const GemvArgs& a, hipStream_t s) {
   if (swiglu && (a.N % 256 || !a.hq))
     return fail(ARTLITE_EINVAL, "expert GEMV: SwiGLU width %d is not a multiple of 256", a.N);
   if (!swiglu && !a.y) return fail(ARTLITE_EINVAL, "expert GEMV: no output");
-#define ART_DISPATCH(QT) return swiglu ? launch_t<QT, true>(a, s) : launch_t<QT, false>(a, s)
+  GemvArgs b = a;
+  b.rpw = std::max(1, a.rpw);
+#define ART_DISPATCH(QT) return swiglu ? launch_t<QT, true>(b, s) : launch_t<QT, false>(b, s)
   switch (a.qtype) {
     case ARTLITE_Q4_0: ART_DISPATCH(ARTLITE_Q4_0);
     case ARTLITE_Q8_0: ART_DISPATCH(ARTLITE_Q8_0);
