@@ -31,6 +31,7 @@ struct GemvArgs {
   int a_gather;            // 1: A row of sorted row s = order[s] / topk (tokens); 0: A row = s
   const int32_t* order;
   int topk;
+  int rows_total;          // a_gather: the entries of order
   const int32_t* tiles;    // (expert, first sorted row) per tile of GEMV_BM rows; null: dense rows of expert 0
   const int32_t* n_tiles;  // the tile count (device)
   const int32_t* offsets;  // E + 1 expert offsets in the sorted order
@@ -38,11 +39,10 @@ struct GemvArgs {
   int64_t max_tiles;       // grid bound
   uint32_t* hq;            // SwiGLU: h = silu(gate) up as XQ rows (by sorted row)
   float* y;                // plain: fp32 rows (by sorted row), stride N
-  int rpw;                 // plain: blocks of 64 output rows per workgroup (>= 1), streamed one after the other
 };
 
-// whether the GEMV takes weights of this type with rows of K values
-bool gemv_supported(int qtype, int K);
+// whether the GEMV takes N rows of K values of weights of this type
+bool gemv_supported(int qtype, int K, int N);
 
 int launch_gemv(const GemvArgs& a, hipStream_t s);
 

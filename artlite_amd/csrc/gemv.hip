@@ -62,10 +62,42 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
 }
 
-// After vmcnt(N), the lane's dwords of a unit (at pw; Q4_K: header at pw, its run at pr) and its XQ chunk of each
-// of the M rows of A (at px, 1024 bytes apart), and their completion, in one asm block: the compiler would otherwise
-// wait for every load in flight before reading LDS (it takes the slots' global_load_lds writes for possible
-// producers), and it must not touch the outputs before the final wait.
+// LDS reads by asm, completed before they return: reads the compiler sees in a kernel with LDS DMA in flight make
+// it wait for every load in flight first
+__device__ __forceinline__ int lds_read_i32(const void* p) {
+  int v;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)));
+  return v;
+}
+__device__ __forceinline__ int4 lds_read_i4(const void* p) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)));
+  return make_int4(int(v[0]), int(v[1]), int(v[2]), int(v[3]));
+}
+// *p += 1 after every earlier LDS access of the wave has completed; returns the old value (one lane's call)
+__device__ __forceinline__ int lds_inc(int* p) {
+  int old;
+  asm volatile("s_waitcnt lgkmcnt(0)\n\tds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
+               : "=v"(old)
+               : "v"(lds_addr(p)), "v"(1)
+               : "memory");
+  return old;
+}
+// *p = v after every earlier LDS access of the wave has completed
+__device__ __forceinline__ void lds_store(int* p, int v) {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\tds_write_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : : "v"(lds_addr(p)), "v"(v)
+               : "memory");
+}
+__device__ __forceinline__ float4 lds_read_f4(const void* p) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)));
+  return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+}
+
+// After vmcnt(N), the lane's dwords of a unit (at pw; Q4_K: header at pw, its run at pr) and (MX > 0) its record
+// chunk of each of MX rows of A (at px, 1024 bytes apart), and their completion, in one asm block: the compiler
+// would otherwise wait for every load in flight before reading LDS (it takes the slots' global_load_lds writes for
+// possible producers), and it must not touch the outputs before the final wait.
 #define ART_R2(I, J) "ds_read2_b32 %[w" #I "], %[pw] offset0:" #J " offset1:" #J "+1\n\t"
 #define ART_R1(I, J) "ds_read_b32 %[w" #I "], %[pw] offset:" #J "*4\n\t"
 #define ART_OW2(I) [w##I] "=&v"(w2[I])
@@ -82,25 +114,28 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   "ds_read_b128 %[w2], %[pr] offset:16\n\t"
 #define ART_OW12 [w0] "=&v"(w4[0]), [w1] "=&v"(w4[1]), [w2] "=&v"(w4[2])
 #define ART_RX(T) "ds_read_b128 %[x" #T "], %[px] offset:" #T "*1024\n\t"
+#define ART_X0
 #define ART_X1 ART_RX(0)
 #define ART_X2 ART_X1 ART_RX(1)
 #define ART_X3 ART_X2 ART_RX(2)
 #define ART_X4 ART_X3 ART_RX(3)
-#define ART_OX1 [x0] "=&v"(x[0])
+#define ART_OX0
+#define ART_OX1 , [x0] "=&v"(x[0])
 #define ART_OX2 ART_OX1, [x1] "=&v"(x[1])
 #define ART_OX3 ART_OX2, [x2] "=&v"(x[2])
 #define ART_OX4 ART_OX3, [x3] "=&v"(x[3])
-#define ART_READ(WN, MN)                                                                             \
-  asm volatile("s_waitcnt vmcnt(%[n])\n\t" ART_W##WN ART_X##MN "s_waitcnt lgkmcnt(0)"              \
-               : ART_OW##WN, ART_OX##MN                                                             \
+#define ART_READ(WN, MN)                                                                       \
+  asm volatile("s_waitcnt vmcnt(%[n])\n\t" ART_W##WN ART_X##MN "s_waitcnt lgkmcnt(0)"       \
+               : ART_OW##WN ART_OX##MN                                                          \
                : [pw] "v"(pw), [pr] "v"(pr), [px] "v"(px), [n] "i"(N))
-#define ART_READ_M(WN)         \
-  if constexpr (M == 1) ART_READ(WN, 1); \
-  if constexpr (M == 2) ART_READ(WN, 2); \
-  if constexpr (M == 3) ART_READ(WN, 3); \
-  if constexpr (M == 4) ART_READ(WN, 4);
-template <int N, int QT, int M>
-__device__ __forceinline__ void read_unit(uint32_t (&w)[Unit<QT>::LW], u32x4 (&x)[M], uint32_t pw, uint32_t pr,
+#define ART_READ_M(WN)                   \
+  if constexpr (MX == 0) ART_READ(WN, 0); \
+  if constexpr (MX == 1) ART_READ(WN, 1); \
+  if constexpr (MX == 2) ART_READ(WN, 2); \
+  if constexpr (MX == 3) ART_READ(WN, 3); \
+  if constexpr (MX == 4) ART_READ(WN, 4);
+template <int N, int QT, int MX>
+__device__ __forceinline__ void read_unit(uint32_t (&w)[Unit<QT>::LW], u32x4 (&x)[GEMV_BM], uint32_t pw, uint32_t pr,
                                           uint32_t px) {
   static_assert(N >= 0 && N < 64, "vmcnt");
   constexpr int LW = Unit<QT>::LW;
@@ -128,10 +163,12 @@ __device__ __forceinline__ void read_unit(uint32_t (&w)[Unit<QT>::LW], u32x4 (&x
 #undef ART_OX3
 #undef ART_OX2
 #undef ART_OX1
+#undef ART_OX0
 #undef ART_X4
 #undef ART_X3
 #undef ART_X2
 #undef ART_X1
+#undef ART_X0
 #undef ART_RX
 #undef ART_OW12
 #undef ART_W12
@@ -143,12 +180,6 @@ __device__ __forceinline__ void read_unit(uint32_t (&w)[Unit<QT>::LW], u32x4 (&x
 #undef ART_OW2
 #undef ART_R1
 #undef ART_R2
-
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N));
-}
 
 // Codes of the lane's group H (0, 1) as 8 dwords of int8 (q[j]: values 4 j .. 4 j + 3 of the group), its scale d
 // (Q4_K: d sc) and Q4_K's dmin mn. g: the group's index in the unit (Q4_K's scales).
@@ -260,229 +291,357 @@ __device__ __forceinline__ float group_term(float acc, uint32_t x, uint32_t l, u
 #undef ART_DOTS
 #undef ART_QIN
 
-// LDS of a workgroup: each wave's D slots of 16 rows x BYTES, two record slots (GEMV_BM x 1 KB), then h of the
-// tile (GEMV_BM x 64 fp32)
-template <int QT, int D>
+template <bool SWIGLU>
+struct Shape {
+  static constexpr int RB = SWIGLU ? 2 : 4, S = SWIGLU ? 4 : 1, WAVES = RB * S, THREADS = 64 * WAVES;
+};
+
+// LDS of a workgroup: each wave's D slots of 16 rows x BYTES and its XS record slots (GEMV_BM chunk rows of 1 KB;
+// SwiGLU one, plain products two), then (S > 1) RED_BUFS buffers of the K-ranges' partial sums and their counters
+// (then the item table, sized at launch)
+constexpr int RED_BUFS = 2;
+template <int QT, bool SWIGLU, int D>
 constexpr size_t gemv_lds() {
-  return size_t(4) * D * 16 * Unit<QT>::BYTES + 2 * GEMV_BM * 1024 + GEMV_BM * 64 * 4;
+  using W = Shape<SWIGLU>;
+  return size_t(W::WAVES) * (D * 16 * Unit<QT>::BYTES + (SWIGLU ? 1 : 2) * GEMV_BM * 1024) +
+         (W::S > 1 ? size_t(RED_BUFS) * W::WAVES * (SWIGLU ? 2 : 1) * GEMV_BM * 16 * 4 + 32 : 0);
 }
 
-// choose among waits vmcnt(N0), (N0 + NI), ... by a small runtime count c (< 4)
-template <int N0, int NI, int CMAX>
-__device__ __forceinline__ void wait_vm_c(int c) {
-  if (c <= 0)
-    wait_vm<N0>();
-  else if (c == 1 || CMAX < 2)
-    wait_vm<(CMAX >= 1 ? N0 + NI : N0)>();
-  else if (c == 2 || CMAX < 3)
-    wait_vm<(CMAX >= 2 ? N0 + 2 * NI : N0)>();
-  else
-    wait_vm<(CMAX >= 3 ? N0 + 3 * NI : N0)>();
-}
 
-template <int QT, bool SWIGLU, int D, int M>
-__device__ __forceinline__ void gemv_tile(const GemvArgs& a, int e, int s0) {
-  constexpr int BY = Unit<QT>::BYTES, CH = BY / 16, LW = Unit<QT>::LW, NM = SWIGLU ? 2 : 1;
-  constexpr int WCH = 16 * CH;               // chunks of a wave's unit
-  constexpr int NI = (WCH + 63) / 64;         // its load instructions (the last for LAST lanes)
-  constexpr int LAST = WCH - 64 * (NI - 1);
-  static_assert((D - 1) * NI + D * M < 64, "loads in flight beyond vmcnt");
-  static_assert(D % NM == 0, "slots per matrix");
-  extern __shared__ u32x4 slab[];
-  // (wv through readfirstlane: wave-uniform to the compiler, so the branches on it are scalar)
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, p = lane >> 4, r = lane & 15;
-  u32x4* my = slab + wv * D * WCH;
-  u32x4* xslot = slab + 4 * D * WCH;  // 2 x GEMV_BM x 64 chunks
-  float* hbuf = reinterpret_cast<float*>(xslot + 2 * GEMV_BM * 64);
-  // plain products: a.rpw blocks of 64 rows, one after the other (SwiGLU: one)
-  const int rpw = SWIGLU ? 1 : a.rpw;
-  const int n0 = blockIdx.y * 64 * rpw, nw = n0 + 16 * wv;
-  const int U = a.K / 256, NV = U * NM;                      // units per block of rows
-  const int NVt = min(rpw, (a.N - n0 + 63) / 64) * NV, KKt = NVt / NM;  // units, K-units in all
+// A work item: one tile of rows of A times one block of 16 RB weight rows. A workgroup's items are looked up once,
+// at its start, into a table in LDS (8 ints each: e, s0, m, n0 and the A rows), so that no global or scalar load
+// is in flight in the stream of steps: a scalar load would hold up every LDS wait of a step.
+struct Item {
+  int e, s0, m, n0;
+  int ar[GEMV_BM];  // the A rows (XQ rows) of the tile's rows of A
+};
 
-  // the lane's chunk of each load instruction of a unit (chunk 64 i + lane of the wave's 16 x CH): its row and
-  // column offset
-  int rw[NI], cw[NI];
+// wave 0: items it0, it0 + G, ... (n of them) into tab, 64 at a time, lane j one item
+__device__ __forceinline__ void fill_items(const GemvArgs& a, int it0, int G, int n, int NB, int rows, int4* tab,
+                                           int lane) {
+  for (int j0 = 0; j0 < n; j0 += 64) {
+    const int j = j0 + lane;
+    if (j < n) {
+      const int it = it0 + j * G, tile = it / NB;
+      int e = 0, s0 = tile * GEMV_BM, end = a.dense_rows;
+      if (a.tiles) {
+        e = a.tiles[2 * tile];
+        s0 = a.tiles[2 * tile + 1];
+        end = a.offsets[e + 1];
+      }
+      const int m = min(GEMV_BM, end - s0);
+      int ar[GEMV_BM];
 #pragma unroll
-  for (int i = 0; i < NI; i++) {
-    const int q = min(64 * i + lane, WCH - 1), row = q / CH;
-    rw[i] = row;
-    cw[i] = 16 * (q - row * CH);
-  }
-  const uint8_t* wb[NM];
-#pragma unroll
-  for (int mx = 0; mx < NM; mx++) wb[mx] = a.w[mx] + int64_t(e) * a.expert_bytes;
-  // wave 0 loads the tile's record chunks of each K-unit (row t: one instruction, lane i -> chunk i)
-  const uint8_t* xr[M];
-  if (wv == 0)
-#pragma unroll
-    for (int t = 0; t < M; t++) {
-      const int64_t ar = a.a_gather ? a.order[s0 + t] / a.topk : s0 + t;
-      xr[t] = reinterpret_cast<const uint8_t*>(a.xq + ar * xq_row_dwords(a.K)) + 16 * lane;
+      for (int t = 0; t < GEMV_BM; t++)
+        ar[t] = a.a_gather ? a.order[min(s0 + min(t, m - 1), a.rows_total - 1)] / a.topk : s0 + min(t, m - 1);
+      tab[2 * j] = make_int4(e, s0, m, (it - tile * NB) * rows);
+      tab[2 * j + 1] = make_int4(ar[0], ar[1], ar[2], ar[3]);
     }
-  auto issue_x = [&](int kk) {  // (wave 0; K-unit kk of the sequence (past the last: the last again, into the idle
-                                //  slot), K-range kk % U)
-    u32x4* dst = xslot + (kk & 1) * GEMV_BM * 64;
-    const int ku = min(kk, KKt - 1) % U;
-#pragma unroll
-    for (int t = 0; t < M; t++)
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(xr[t] + ku * (XQ_UNIT * 4)),
-                                       (__attribute__((address_space(3))) void*)(dst + 64 * t), 16, 0, 0);
-  };
-  // the weights of unit v (K-range v / NM of matrix v % NM) into this wave's slot v % D
-  auto issue_w = [&](int v, auto mtx_c) {
-    constexpr int MX = decltype(mtx_c)::value;
-    const int rb = v / NV;
-    const uint8_t* src = wb[MX] + int64_t((v - rb * NV) / NM) * BY;
-    u32x4* dst = my + (v % D) * WCH;
-#pragma unroll
-    for (int i = 0; i < NI; i++)
-      if (i < NI - 1 || lane < LAST)
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(
-                                             src + min(nw + 64 * rb + rw[i], a.N - 1) * a.row_bytes + cw[i]),
-                                         (__attribute__((address_space(3))) void*)(dst + 64 * i), 16, 0, 0);
-  };
+  }
+}
 
-  // the lane's read addresses
-  const uint32_t wbase = lds_addr(my), xbase = lds_addr(xslot) + 16 * lane;
-  const uint32_t o_w = r * BY + (QT == ARTLITE_Q4_K ? 0 : (QT == ARTLITE_Q4_0 ? 36 : 68) * p);
-  const uint32_t o_r = r * BY + 16 + 32 * p;  // (Q4_K)
+__device__ __forceinline__ Item get_item(const int4* tab, int j) {
+  const int4 u = lds_read_i4(tab + 2 * j), v = lds_read_i4(tab + 2 * j + 1);
+  Item I;
+  I.e = __builtin_amdgcn_readfirstlane(u.x);
+  I.s0 = __builtin_amdgcn_readfirstlane(u.y);
+  I.m = __builtin_amdgcn_readfirstlane(u.z);
+  I.n0 = __builtin_amdgcn_readfirstlane(u.w);
+  I.ar[0] = __builtin_amdgcn_readfirstlane(v.x);
+  I.ar[1] = __builtin_amdgcn_readfirstlane(v.y);
+  I.ar[2] = __builtin_amdgcn_readfirstlane(v.z);
+  I.ar[3] = __builtin_amdgcn_readfirstlane(v.w);
+  return I;
+}
 
+// the sum over the four 16-lane rows of lane (p, r), in every lane of column r (rows 0 + 1 and 2 + 3 first)
+__device__ __forceinline__ float row4_sum(float s) {
+  const auto x = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+  s = __uint_as_float(x[0]) + __uint_as_float(x[1]);
+  const auto y = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+  return __uint_as_float(y[0]) + __uint_as_float(y[1]);
+}
+
+// The state of a wave's stream of steps over its items (one step: 16 rows x one K-unit of one matrix). Every load
+// of the stream is a DMA into LDS (the weights into D slots, the records of a K-unit into one slot), counted as it
+// is issued (nl), so that each wait names the exact number of loads issued after the ones it needs: loads of one kind
+// return in order. (Records loaded into registers instead would make the compiler wait for all loads in flight
+// before each use: it cannot order them against the DMAs.)
+template <int QT, bool SWIGLU, int D>
+struct Stream {
+  using W = Shape<SWIGLU>;
+  static constexpr int RB = W::RB, S = W::S, BY = Unit<QT>::BYTES, CH = BY / 16, LW = Unit<QT>::LW;
+  static constexpr int NM = SWIGLU ? 2 : 1, WCH = 16 * CH, NI = (WCH + 63) / 64, LAST = WCH - 64 * (NI - 1);
+  static constexpr int LA = D - 1;                          // steps in flight ahead of the one being read
+  static constexpr int XS = SWIGLU ? 1 : 2, XCH = GEMV_BM * 64;  // record slots, their chunks
+  static constexpr int NMAX = LA * NI + (LA + 1) * GEMV_BM;  // loads issued after a step's, at most
+  static_assert(NMAX < 64, "loads in flight beyond vmcnt");
+  const GemvArgs& a;
+  int wv, lane, p, r, rb, ks, u0, u1, NVw;
+  u32x4* my;  // the wave's weight slots, then its record slot
+  uint32_t wbase, xbase, o_w, o_r;
+  uint32_t lo[NI];   // the lane's byte offset in the 16 rows of each load instruction
+  int nl = 0;        // loads issued so far
+  int xend0 = 0, xend1 = 0;  // nl after each record slot's loads (two scalars: an indexed array would live in memory)
+  int kg = 0;         // K-units of the stream started
+  int wend[D] = {};  // nl after the weights of the last D steps issued (wend[0]: the latest)
+
+  __device__ __forceinline__ explicit Stream(const GemvArgs& args) : a(args) {
+    extern __shared__ u32x4 slab[];
+    wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    lane = threadIdx.x & 63, p = lane >> 4, r = lane & 15;
+    rb = wv / S, ks = wv % S;
+    my = slab + wv * (D * WCH + XS * XCH);
+    const int U = a.K / 256;
+    u0 = ks * U / S, u1 = (ks + 1) * U / S;
+    NVw = (u1 - u0) * NM;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      const int q = min(64 * i + lane, WCH - 1), row = q / CH;
+      lo[i] = uint32_t((16 * rb + row) * a.row_bytes + 16 * (q - row * CH));
+    }
+    wbase = lds_addr(my);
+    xbase = lds_addr(my + D * WCH) + 16 * lane;
+    o_w = r * BY + (QT == ARTLITE_Q4_K ? 0 : (QT == ARTLITE_Q4_0 ? 36 : 68) * p);
+    o_r = r * BY + 16 + 32 * p;  // (Q4_K)
+  }
+  // the weights of local step v of item (e, n0) into slot `slot`; !on: none (the end of the stream), counted alike
+  template <int MX>
+  __device__ __forceinline__ void issue_w(bool on, int e, int n0, int v, int slot) {
+    if (on) {
+      // (rows past N cannot occur: N is a multiple of the item's rows)
+      const uint8_t* src = a.w[MX] + int64_t(e) * a.expert_bytes + int64_t(n0) * a.row_bytes +
+                           int64_t(u0 + v / NM) * BY;
+      u32x4* dst = my + slot * WCH;
+#pragma unroll
+      for (int i = 0; i < NI; i++)
+        if (i < NI - 1 || lane < LAST)
+          __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src + lo[i]),
+                                           (__attribute__((address_space(3))) void*)(dst + 64 * i), 16, 0, 0);
+      nl += NI;
+    }
+#pragma unroll
+    for (int i = D - 1; i > 0; i--) wend[i] = wend[i - 1];
+    wend[0] = nl;
+  }
+  // the records of K-unit ku of item I's rows of A into record slot b (lane l: chunk l of each row)
+  __device__ __forceinline__ void load_x(const Item& I, int ku, int b) {
+    u32x4* dst = my + D * WCH + b * XCH;
+#pragma unroll
+    for (int t = 0; t < GEMV_BM; t++)
+      if (t < I.m)
+        __builtin_amdgcn_global_load_lds(
+            reinterpret_cast<const void*>(a.xq + int64_t(I.ar[t]) * xq_row_dwords(a.K) + ku * XQ_UNIT + 4 * lane),
+            (__attribute__((address_space(3))) void*)(dst + 64 * t), 16, 0, 0);
+    nl += I.m;
+    if (b)
+      xend1 = nl;
+    else
+      xend0 = nl;
+  }
+};
+
+// the wait and read of a step: vmcnt(n) (n at most NMAX), then the weights and (MX) the record chunks
+template <int QT, bool SWIGLU, int D, int MX>
+__device__ __forceinline__ void wait_read(const Stream<QT, SWIGLU, D>& st, int n, uint32_t sw, uint32_t sx,
+                                          uint32_t (&w)[Unit<QT>::LW], u32x4 (&x)[GEMV_BM]) {
+  using SS = Stream<QT, SWIGLU, D>;
+  static_for<SS::NMAX + 1>([&](auto nc) {
+    constexpr int N = decltype(nc)::value;
+    if (n == N) read_unit<N, QT, MX>(w, x, sw + st.o_w, sw + st.o_r, sx);
+  });
+}
+
+// The dot products of one step: the lane's two groups of the unit w against the M rows of A's records x.
+template <int QT, int M>
+__device__ __forceinline__ void step_terms(const uint32_t (&w)[Unit<QT>::LW], const u32x4 (&x)[GEMV_BM], int p,
+                                           float (&acc)[M]) {
+  static_for<2>([&](auto hc) {
+    constexpr int H = decltype(hc)::value;
+    uint32_t q[8];
+    float d, mn;
+    codes<QT, H>(w, 2 * p + H, q, d, mn);
+#pragma unroll
+    for (int t = 0; t < M; t++) acc[t] = group_term<QT, H>(acc[t], x[t][H], x[t][2], x[t][3], q, d, mn);
+  });
+}
+
+// Item `cur` of the stream, whose first step is global step gs; `nxt` is the next item if has_next. Steps run LA
+// ahead in the wave's own slots (a slot refilled right after the step that read it), across items. Each step issues
+// the weights LA steps ahead, then waits for its own; at the start of each K-unit that wait also covers the
+// records, which are read into registers with the weights, and the next K-unit's are loaded into the freed slot.
+// Returns with the sums of the four lanes of a row in every lane.
+template <int QT, bool SWIGLU, int D, int M>
+__device__ __forceinline__ void run_item(Stream<QT, SWIGLU, D>& st, const Item& cur, const Item& nxt, bool has_next,
+                                         int gs, float (&out)[SWIGLU ? 2 : 1][GEMV_BM]) {
+  using SS = Stream<QT, SWIGLU, D>;
+  constexpr int NM = SS::NM, LW = SS::LW, LA = SS::LA;
   float acc[NM][M];
 #pragma unroll
   for (int mx = 0; mx < NM; mx++)
 #pragma unroll
     for (int t = 0; t < M; t++) acc[mx][t] = 0.0f;
-
-  // Weights D - 1 units ahead in each wave's own slots (a slot refilled right after the step that read it); the
-  // records of K-unit ku + 1 issued by wave 0 at ku's first step, right after the barrier that opens it: every wave is
-  // then past K-unit ku - 1, whose record slot it takes, and sees K-unit ku's records, which wave 0 waited for just
-  // before. The loop is unrolled by NM, which fixes each step's matrix.
-  if (wv == 0) issue_x(0);
-  for (int v = 0; v < D - 1 && v < NVt; v++) {
-    if (NM == 1 || v % NM == 0)
-      issue_w(v, std::integral_constant<int, 0>{});
-    else
-      issue_w(v, std::integral_constant<int, NM - 1>{});
-  }
-  for (int v0 = 0; v0 < NVt; v0 += NM) {
+  u32x4 xc[GEMV_BM];
+  for (int v0 = 0; v0 < st.NVw; v0 += NM) {
     static_for<NM>([&](auto jc) {
       constexpr int MX = decltype(jc)::value;
-      const int v = v0 + MX, kk = v0 / NM;
-      if (v >= NVt) return;
-      if (MX == 0) {
-        // wave 0: K-unit kk's records (issued before the weights of the units since its issue that were issued)
-        if (wv == 0) {
-          if (kk == 0)
-            wait_vm_c<0, NI, 3>(min(D - 1, NVt));
-          else
-            wait_vm_c<0, NI, NM>(min(NM, max(0, NVt - D + 1 - (kk - 1) * NM)));
-        }
-        __builtin_amdgcn_s_barrier();
-        if (wv == 0) issue_x(kk + 1);
-      }
-      if (v + D - 1 < NVt) issue_w(v + D - 1, std::integral_constant<int, (MX + D - 1) % NM>{});
-      // unit v's weights have landed once only the loads issued after them are outstanding: the weights of the
-      // `ahead` units after it, and (wave 0) the records issued at the K-unit starts among steps v - D + 2 .. v
-      const int ahead = min(D - 1, NVt - 1 - v);
-      int nx = 0;
-      if (wv == 0)
-        for (int j = max(0, v - D + 2); j <= v; j++) nx += j % NM == 0;
+      const int v = v0 + MX;
+      // the step LA ahead: in this item, or the next item's, or none (counted alike)
+      auto issue = [&] {
+        const int vi = v + LA;
+        const bool here = vi < st.NVw;
+        st.template issue_w<(MX + LA) % NM>(here || has_next, here ? cur.e : nxt.e, here ? cur.n0 : nxt.n0,
+                                            here ? vi : vi - st.NVw, (gs + v + LA) % D);
+      };
+      if constexpr (SWIGLU) issue();
       uint32_t w[LW];
-      u32x4 x[M];
-      const uint32_t sw = wbase + (v % D) * WCH * 16, px = xbase + (kk & 1) * GEMV_BM * 1024;
-      // (the count in one immediate: nx rows of M records plus ahead x NI)
-      const int n = ahead * NI + nx * M;
-      static_for<(D - 1) * NI + D * M + 1>([&](auto nc) {
-        constexpr int NN = decltype(nc)::value;
-        if (n == NN) read_unit<NN, QT, M>(w, x, sw + o_w, sw + o_r, px);
-      });
-      static_for<2>([&](auto hc) {
-        constexpr int H = decltype(hc)::value;
-        uint32_t q[8];
-        float d, mn;
-        codes<QT, H>(w, 2 * p + H, q, d, mn);
-#pragma unroll
-        for (int t = 0; t < M; t++) acc[MX][t] = group_term<QT, H>(acc[MX][t], x[t][H], x[t][2], x[t][3], q, d, mn);
-      });
-      if constexpr (!SWIGLU) {
-        if (v % NV == NV - 1) {  // a block of rows done: the four lanes of a row summed, then y
-          const int rb = v / NV, n = nw + 64 * rb + r;
-#pragma unroll
-          for (int t = 0; t < M; t++) {
-            float y = acc[0][t];
-            y += __shfl_xor(y, 16);
-            y += __shfl_xor(y, 32);
-            if (p == 0 && n < a.N) a.y[int64_t(s0 + t) * a.N + n] = y;
-            acc[0][t] = 0.0f;
-          }
+      const uint32_t sw = st.wbase + ((gs + v) % D) * SS::WCH * 16;
+      if constexpr (MX == 0) {
+        // the next K-unit's records: SwiGLU into the one slot once this K-unit's are read, plain products into
+        // the other slot before the wait
+        const int b = SS::XS == 1 ? 0 : st.kg & 1;
+        auto next_x = [&](int bn) {
+          if (v0 + NM < st.NVw)
+            st.load_x(cur, st.u0 + v0 / NM + 1, bn);
+          else if (has_next)
+            st.load_x(nxt, st.u0, bn);
+        };
+        if constexpr (SS::XS == 2) {
+          next_x(b ^ 1);
+          issue();
         }
+        // (wend[D - 1]: this step's weights)
+        const int nw = st.nl - st.wend[D - 1];
+        wait_read<QT, SWIGLU, D, M>(st, min(nw, st.nl - (b ? st.xend1 : st.xend0)), sw, st.xbase + b * SS::XCH * 16,
+                                    w, xc);
+        if constexpr (SS::XS == 1) next_x(0);
+        st.kg++;
+      } else {
+        wait_read<QT, SWIGLU, D, 0>(st, st.nl - st.wend[D - 1], sw, st.xbase, w, xc);
       }
+      step_terms<QT, M>(w, xc, st.p, acc[MX]);
     });
   }
-
-  if constexpr (SWIGLU) {
-    // the four lanes of a row: their groups' sums
 #pragma unroll
-    for (int mx = 0; mx < NM; mx++)
+  for (int mx = 0; mx < NM; mx++)
 #pragma unroll
-      for (int t = 0; t < M; t++) {
-        acc[mx][t] += __shfl_xor(acc[mx][t], 16);
-        acc[mx][t] += __shfl_xor(acc[mx][t], 32);
+    for (int t = 0; t < GEMV_BM; t++) {
+      if (t < M) {
+        out[mx][t] = row4_sum(acc[mx][t < M ? t : 0]);
+      } else {
+        out[mx][t] = 0.0f;
       }
-    // h = silu(gate) up of the 64 rows, then quantised by wave 0 into XQ rows of N values (lanes 0..31: one group,
-    // 32..63: the next)
-    if (p == 0)
-#pragma unroll
-      for (int t = 0; t < M; t++) {
-        const float gv = acc[0][t];
-        hbuf[t * 64 + 16 * wv + r] = gv / (1.0f + expf(-gv)) * acc[1][t];
-      }
-    __syncthreads();
-    if (wv) return;
-    const int UH = a.N / 256;
-    const int g = ((n0 & 255) >> 5) + (lane >> 5), v = lane & 31;
-#pragma unroll
-    for (int t = 0; t < M; t++) {
-      const float hv[1] = {hbuf[t * 64 + lane]};
-      int qa[1], qb[1], sum;
-      float s256, xsum;
-      quant_group<1>(hv, qa, qb, s256, sum, xsum);
-      uint32_t pa = uint32_t(qa[0] & 0xFF) << (8 * (lane & 3));
-      uint32_t pb = uint32_t(qb[0] & 0xFF) << (8 * (lane & 3));
-      pa |= __shfl_xor(pa, 1);
-      pb |= __shfl_xor(pb, 1);
-      pa |= __shfl_xor(pa, 2);
-      pb |= __shfl_xor(pb, 2);
-      uint32_t* ub = a.hq + int64_t(s0 + t) * UH * XQ_UNIT + (n0 >> 8) * XQ_UNIT;
-      if ((v & 3) == 0) {
-        ub[xq_block(g, v >> 2)] = pa;
-        ub[xq_block(g, 8 + (v >> 2))] = pb;
-      }
-      if (v < 16) xq_put_word(ub, g, v, s256, sum, xsum);
     }
-  }
 }
 
+// A persistent workgroup: items blockIdx.x, blockIdx.x + gridDim.x, ... of (tile, block of 16 RB rows), tile-major.
 template <int QT, bool SWIGLU, int D>
-__global__ __launch_bounds__(256) void k_gemv(const GemvArgs a) {
-  int e = 0, s0, m;
-  if (a.tiles) {
-    if (int64_t(blockIdx.x) >= *a.n_tiles) return;
-    e = a.tiles[2 * blockIdx.x];
-    s0 = a.tiles[2 * blockIdx.x + 1];
-    m = min(GEMV_BM, a.offsets[e + 1] - s0);
-  } else {
-    s0 = blockIdx.x * GEMV_BM;
-    m = min(GEMV_BM, a.dense_rows - s0);
+__global__ __launch_bounds__(Shape<SWIGLU>::THREADS) __attribute__((amdgpu_waves_per_eu(QT == ARTLITE_Q4_0 ? 4 : 2))) void k_gemv(
+    const GemvArgs a) {
+  using W = Shape<SWIGLU>;
+  using SS = Stream<QT, SWIGLU, D>;
+  constexpr int RB = W::RB, S = W::S, NM = SS::NM;
+  const int rows = 16 * RB, NB = (a.N + rows - 1) / rows;
+  const int n_tiles = a.tiles ? *a.n_tiles : (a.dense_rows + GEMV_BM - 1) / GEMV_BM;
+  const int n_items = n_tiles * NB, G = gridDim.x;
+  if (int(blockIdx.x) >= n_items) return;
+  SS st(a);
+  extern __shared__ u32x4 slab[];
+  // [buffer][wave][matrix][row of A][row], after every wave's slots
+  float* red = reinterpret_cast<float*>(slab + W::WAVES * (D * SS::WCH + SS::XS * SS::XCH));
+
+  const int it0 = blockIdx.x, n_my = (n_items - 1 - it0) / G + 1;
+  constexpr int RED = W::WAVES * NM * GEMV_BM * 16;  // floats of one partial-sum buffer
+  int* ctr = reinterpret_cast<int*>(red + (S > 1 ? RED_BUFS * RED : 0));  // [b]: arrivals, [4 + b]: epilogues done
+  int4* tab = reinterpret_cast<int4*>(ctr + (S > 1 ? 8 : 0));
+  // the first item's first LA steps, its expert from a scalar load, ahead of the table
+  if (st.NVw > 0) {
+    const int e0 = a.tiles ? a.tiles[2 * (it0 / NB)] : 0, n00 = (it0 % NB) * rows;
+    for (int v = 0; v < SS::LA; v++) {
+      if (NM == 1 || v % NM == 0)
+        st.template issue_w<0>(true, e0, n00, v, v);
+      else
+        st.template issue_w<NM - 1>(true, e0, n00, v, v);
+    }
   }
-  static_assert(GEMV_BM == 4, "tile rows");
-  switch (m) {
-    case 1: gemv_tile<QT, SWIGLU, D, 1>(a, e, s0); break;
-    case 2: gemv_tile<QT, SWIGLU, D, 2>(a, e, s0); break;
-    case 3: gemv_tile<QT, SWIGLU, D, 3>(a, e, s0); break;
-    case 4: gemv_tile<QT, SWIGLU, D, 4>(a, e, s0); break;
-    default: break;
+  if (st.wv == 0) fill_items(a, it0, G, n_my, NB, rows, tab, st.lane);
+  if (S > 1 && threadIdx.x < 8) ctr[threadIdx.x] = 0;
+  __syncthreads();
+  Item cur = get_item(tab, 0), nxt = cur;
+  if (st.NVw > 0) st.load_x(cur, st.u0, 0);
+  int gs = 0;
+  for (int j = 0; j < n_my; j++) {
+    const bool has_next = j + 1 < n_my;
+    if (has_next) nxt = get_item(tab, j + 1);
+    float out[NM][GEMV_BM];
+    switch (cur.m) {
+      case 1: run_item<QT, SWIGLU, D, 1>(st, cur, nxt, has_next, gs, out); break;
+      case 2: run_item<QT, SWIGLU, D, 2>(st, cur, nxt, has_next, gs, out); break;
+      case 3: run_item<QT, SWIGLU, D, 3>(st, cur, nxt, has_next, gs, out); break;
+      default: run_item<QT, SWIGLU, D, 4>(st, cur, nxt, has_next, gs, out); break;
+    }
+    gs += st.NVw;
+    if constexpr (!SWIGLU) {
+      static_assert(S == 1, "plain products: one wave per row block");
+      const int n = cur.n0 + 16 * st.rb + st.r;
+#pragma unroll
+      for (int t = 0; t < GEMV_BM; t++)
+        if (t < cur.m && st.p == 0) a.y[int64_t(cur.s0 + t) * a.N + n] = out[0][t];
+    } else {
+      // The K-ranges' partial sums through LDS, summed in a fixed order by the last wave to deliver its own (a
+      // counter per buffer, no barrier: the other waves go on with their next items); RED_BUFS buffers, a wave
+      // waiting before it reuses one until the epilogue RED_BUFS items back is done. Then h = silu(gate) up of
+      // the 32 rows, quantised into one group of an XQ row of N values per row of A: lanes 8 t .. 8 t + 7 take row
+      // of A t, 4 rows each. (The lane is recomputed here rather than kept from the start: the registers are
+      // needed by the steps.)
+      const int ln = __lane_id(), b = j % RED_BUFS;
+      float* rd = red + b * RED;
+      if (j >= RED_BUFS) {
+        while (lds_read_i32(ctr + 4 + b) < j / RED_BUFS) __builtin_amdgcn_s_sleep(1);
+      }
+      if (ln < 16)
+#pragma unroll
+        for (int mx = 0; mx < NM; mx++)
+#pragma unroll
+          for (int t = 0; t < GEMV_BM; t++) rd[((st.wv * NM + mx) * GEMV_BM + t) * 16 + ln] = out[mx][t];
+      int arrived = 0;
+      if (ln == 0) arrived = lds_inc(ctr + b);
+      if (__builtin_amdgcn_readfirstlane(arrived) == W::WAVES - 1) {
+        if (ln < 8 * cur.m) {
+          const int t = ln >> 3, l8 = ln & 7, rbb = l8 >> 2, r0 = 4 * (l8 & 3);
+          const int UH = a.N / 256, blk = cur.n0 / 32, g = blk & 7;
+          float4 gsum = {0.0f, 0.0f, 0.0f, 0.0f}, usum = gsum;
+#pragma unroll
+          for (int k = 0; k < S; k++) {
+            gsum += lds_read_f4(rd + (((rbb * S + k) * NM + 0) * GEMV_BM + t) * 16 + r0);
+            usum += lds_read_f4(rd + (((rbb * S + k) * NM + 1) * GEMV_BM + t) * 16 + r0);
+          }
+          const float gv[4] = {gsum.x, gsum.y, gsum.z, gsum.w}, uv[4] = {usum.x, usum.y, usum.z, usum.w};
+          float hv[4];
+#pragma unroll
+          for (int i = 0; i < 4; i++) hv[i] = gv[i] * __builtin_amdgcn_rcpf(1.0f + __expf(-gv[i])) * uv[i];
+          int qa[4], qb[4], sum;
+          float s256, xsum;
+          quant_group(hv, qa, qb, s256, sum, xsum);
+          uint32_t pa = 0, pb = 0;
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            pa |= uint32_t(qa[i] & 0xFF) << (8 * i);
+            pb |= uint32_t(qb[i] & 0xFF) << (8 * i);
+          }
+          uint32_t* ub = a.hq + int64_t(cur.s0 + t) * UH * XQ_UNIT + (blk >> 3) * XQ_UNIT;
+          ub[xq_block(g, l8)] = pa;
+          ub[xq_block(g, 8 + l8)] = pb;
+          xq_put_word(ub, g, l8, s256, sum, xsum);
+          xq_put_word(ub, g, 8 + l8, s256, sum, xsum);
+        }
+        if (ln == 0) {
+          lds_store(ctr + b, 0);
+          lds_inc(ctr + 4 + b);
+        }
+      }
+    }
+    cur = nxt;
   }
 }
 
@@ -493,37 +652,61 @@ __global__ __launch_bounds__(256) void k_quant(const void* __restrict__ x, int64
   if (w < T * (K / 256)) xq_quant_unit<XT>(x, w, K, xq, threadIdx.x & 63);
 }
 
-template <int QT, bool SWIGLU>
-int launch_t(const GemvArgs& a, hipStream_t s) {
-  constexpr int D = 2;
+template <int QT, bool SWIGLU, int D>
+int launch_d(const GemvArgs& a, hipStream_t s) {
+  using W = Shape<SWIGLU>;
   const int64_t tiles = a.tiles ? a.max_tiles : (a.dense_rows + GEMV_BM - 1) / GEMV_BM;
-  if (tiles <= 0) return ARTLITE_OK;
-  const int rpw = SWIGLU ? 1 : a.rpw;
-  const dim3 grid(unsigned(tiles), unsigned((a.N + 64 * rpw - 1) / (64 * rpw))), block(256);
-  k_gemv<QT, SWIGLU, D><<<grid, block, gemv_lds<QT, D>(), s>>>(a);
+  const int64_t items = tiles * ((a.N + 16 * W::RB - 1) / (16 * W::RB));
+  if (items <= 0) return ARTLITE_OK;
+  if (items >= (int64_t(1) << 31)) return fail(ARTLITE_EINVAL, "expert GEMV: %lld work items", (long long)items);
+  // persistent workgroups: as many as the device holds at once (queried once per kernel, with a table of 64
+  // items), at most one per item; their item tables take 32 bytes an item
+  constexpr size_t lds0 = gemv_lds<QT, SWIGLU, D>(), lds_max = lds0 + 8192;
+  static const int resident = [] {
+    const void* f = reinterpret_cast<const void*>(k_gemv<QT, SWIGLU, D>);
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_max)) != hipSuccess ||
+        hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, W::THREADS, lds0 + 64 * 32) != hipSuccess)
+      return 0;
+    return cus * std::max(1, per_cu);
+  }();
+  if (resident <= 0) return fail(ARTLITE_EHIP, "expert GEMV: kernel set-up failed");
+  const unsigned grid = unsigned(std::min<int64_t>(items, resident));
+  const size_t lds = lds0 + size_t((items + grid - 1) / grid) * 32;
+  if (lds > lds_max) return fail(ARTLITE_EINVAL, "expert GEMV: %lld work items", (long long)items);
+  k_gemv<QT, SWIGLU, D><<<grid, W::THREADS, lds, s>>>(a);
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
 }
 
+// Weight slots per wave: two (a step in flight behind the one being read; with the record loads, deeper queues did
+// not pay for the LDS they take from the workgroups a CU holds).
+template <int QT, bool SWIGLU>
+int launch_t(const GemvArgs& a, hipStream_t s) {
+  return launch_d<QT, SWIGLU, 2>(a, s);
+}
+
 }  // namespace
 
-bool gemv_supported(int qtype, int K) {
-  return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0 || qtype == ARTLITE_Q4_K) && K > 0 && K % 256 == 0;
+bool gemv_supported(int qtype, int K, int N) {
+  return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0 || qtype == ARTLITE_Q4_K) && K > 0 && K % 256 == 0 &&
+         N > 0 && N % 64 == 0;
 }
 
 int launch_gemv(const GemvArgs& a, hipStream_t s) {
-  if (!gemv_supported(a.qtype, a.K))
-    return fail(ARTLITE_EINVAL, "expert GEMV: weight type %d with K %d (Q4_0 / Q8_0 / Q4_K, K a multiple of 256)",
-                a.qtype, a.K);
+  if (!gemv_supported(a.qtype, a.K, a.N))
+    return fail(ARTLITE_EINVAL,
+                "expert GEMV: weight type %d with K %d, N %d (Q4_0 / Q8_0 / Q4_K, K a multiple of 256, N of 64)",
+                a.qtype, a.K, a.N);
   if (a.N <= 0 || int64_t(a.N) * a.row_bytes >= (int64_t(1) << 31))
     return fail(ARTLITE_EINVAL, "expert GEMV: %d rows of %d bytes", a.N, a.row_bytes);
   const bool swiglu = a.w[1] != nullptr;
   if (swiglu && (a.N % 256 || !a.hq))
     return fail(ARTLITE_EINVAL, "expert GEMV: SwiGLU width %d is not a multiple of 256", a.N);
   if (!swiglu && !a.y) return fail(ARTLITE_EINVAL, "expert GEMV: no output");
-  GemvArgs b = a;
-  b.rpw = std::max(1, a.rpw);
-#define ART_DISPATCH(QT) return swiglu ? launch_t<QT, true>(b, s) : launch_t<QT, false>(b, s)
+#define ART_DISPATCH(QT) return swiglu ? launch_t<QT, true>(a, s) : launch_t<QT, false>(a, s)
   switch (a.qtype) {
     case ARTLITE_Q4_0: ART_DISPATCH(ARTLITE_Q4_0);
     case ARTLITE_Q8_0: ART_DISPATCH(ARTLITE_Q8_0);

@@ -182,6 +182,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     g.a_gather = 1;
     g.order = L->order.as<int32_t>();
     g.topk = k;
+    g.rows_total = int(P);
     g.tiles = L->tiles.as<int32_t>();
     g.n_tiles = L->ctrl.as<int32_t>() + CTRL_TILES;
     g.offsets = L->offsets.as<int32_t>();
@@ -341,8 +342,10 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
     L->sgate_row = size_t(d.hidden) / sq->per * sq->bytes;
     L->sdown_row = size_t(d.shared_ffn) / sq->per * sq->bytes;
   }
-  L->gemv_ok = gemv_supported(d.gate_type, d.hidden) && gemv_supported(d.down_type, d.expert_ffn);
-  L->shared_gemv_ok = sq && gemv_supported(d.shared_type, d.hidden) && gemv_supported(d.shared_type, d.shared_ffn);
+  L->gemv_ok = gemv_supported(d.gate_type, d.hidden, d.expert_ffn) &&
+               gemv_supported(d.down_type, d.expert_ffn, d.hidden);
+  L->shared_gemv_ok = sq && gemv_supported(d.shared_type, d.hidden, d.shared_ffn) &&
+                      gemv_supported(d.shared_type, d.shared_ffn, d.hidden);
   hipError_t e = hipGetDevice(&L->device);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&L->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {

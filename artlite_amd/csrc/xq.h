@@ -6,12 +6,33 @@
 
 namespace artlite {
 
-// Quantise a 32-value group held by 32 / V consecutive lanes, V values each: this lane's int8 plane values, and the
-// group's s / 256, sum of (256 a + b) and dequantised sum (s / 256 times that sum).
-template <int V>
-__device__ __forceinline__ void quant_group(const float (&x)[V], int (&qa)[V], int (&qb)[V], float& s256, int& sum,
+// Reductions over the 8 lanes of each aligned group of 8 (every lane gets the result) by DPP: lanes i ^ 1, i ^ 2
+// (quad_perm), then the mirror lane 7 - i of the other quad (row_half_mirror).
+template <int C>
+__device__ __forceinline__ int dpp8(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, C, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float max8(float v) {
+  v = fmaxf(v, __int_as_float(dpp8<0xB1>(__float_as_int(v))));  // quad_perm [1, 0, 3, 2]
+  v = fmaxf(v, __int_as_float(dpp8<0x4E>(__float_as_int(v))));  // quad_perm [2, 3, 0, 1]
+  return fmaxf(v, __int_as_float(dpp8<0x141>(__float_as_int(v))));  // row_half_mirror
+}
+__device__ __forceinline__ int sum8(int v) {
+  v += dpp8<0xB1>(v);
+  v += dpp8<0x4E>(v);
+  return v + dpp8<0x141>(v);
+}
+__device__ __forceinline__ int or8(int v) {
+  v |= dpp8<0xB1>(v);
+  v |= dpp8<0x4E>(v);
+  return v | dpp8<0x141>(v);
+}
+
+// Quantise a 32-value group held by 8 consecutive lanes (aligned), 4 values each: this lane's int8 plane values, and
+// the group's s / 256, sum of (256 a + b) and dequantised sum (s / 256 times that sum).
+__device__ __forceinline__ void quant_group(const float (&x)[4], int (&qa)[4], int (&qb)[4], float& s256, int& sum,
                                             float& xsum) {
-  constexpr int L = 32 / V;
+  constexpr int V = 4;
   float amax = 0.0f;
   int bad = 0;
 #pragma unroll
@@ -19,11 +40,8 @@ __device__ __forceinline__ void quant_group(const float (&x)[V], int (&qa)[V], i
     amax = fmaxf(amax, fabsf(x[i]));
     bad |= !__builtin_isfinite(x[i]);
   }
-#pragma unroll
-  for (int o = 1; o < L; o <<= 1) {
-    amax = fmaxf(amax, __shfl_xor(amax, o));
-    bad |= __shfl_xor(bad, o);
-  }
+  amax = max8(amax);
+  bad = or8(bad);
   const float inv = 127.0f / amax;
   const bool skip = bad || !(amax > 0.0f) || !__builtin_isfinite(inv);  // (zero or sub-1e-36 groups: 0)
   sum = 0;
@@ -36,8 +54,7 @@ __device__ __forceinline__ void quant_group(const float (&x)[V], int (&qa)[V], i
     qb[i] = skip ? 0 : int(rb);
     sum += 256 * qa[i] + qb[i];
   }
-#pragma unroll
-  for (int o = 1; o < L; o <<= 1) sum += __shfl_xor(sum, o);
+  sum = sum8(sum);
   s256 = bad ? __builtin_nanf("") : skip ? 0.0f : amax / 32512.0f;  // (127 x 256)
   xsum = s256 * float(sum);
 }
@@ -77,7 +94,7 @@ __device__ __forceinline__ void xq_quant_unit(const void* __restrict__ x, int64_
   }
   int qa[4], qb[4], sum;
   float s256, xsum;
-  quant_group<4>(v, qa, qb, s256, sum, xsum);
+  quant_group(v, qa, qb, s256, sum, xsum);
   uint32_t pa = 0, pb = 0;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
