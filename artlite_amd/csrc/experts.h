@@ -24,13 +24,18 @@ struct GemmArgs {
   const int32_t* offsets;  // E + 1 expert offsets in the sorted order
   int dense_rows;
   int64_t max_tiles;       // grid bound
+  int bm;                  // rows of A per tile of the tile list: DECODE_BM or PREFILL_BM
   uint16_t* h_hi;          // SwiGLU output planes (row stride N)
   uint16_t* h_lo;
   float* y;                // plain output (row stride N)
 };
 
-// rows of A (tokens / pairs) per tile of the decode (GEMV-like) kernel
+// rows of A (tokens / pairs) per tile of the decode (GEMV-like) kernel, and of the prefill tiling
 constexpr int DECODE_BM = 8;
+constexpr int PREFILL_BM = 128;
+
+// whether the prefill tiling takes N rows of K values of weights of this type
+bool prefill_supported(int qtype, int K, int N);
 // the most 32-value groups of a row (K <= 32 MAX_GROUPS)
 constexpr int MAX_GROUPS = 128;
 

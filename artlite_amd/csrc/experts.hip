@@ -329,13 +329,228 @@ int launch_decode(const GemmArgs& a, hipStream_t s) {
   return ARTLITE_OK;
 }
 
+// ---- Prefill tiling (k_gemm_prefill): a workgroup is one tile of PREFILL_BM sorted rows of one expert times 64
+// weight rows (of each matrix), as 2 x 2 waves: wave (wm, wn) takes rows of A 64 wm .. + 64 (4 MFMA row blocks)
+// and weight rows 32 wn .. + 32 (2 column blocks per matrix; SwiGLU: those rows of gate and of up, so h is formed
+// in the wave). K streams in stages of two 32-value groups through two LDS buffers: each thread loads its share of
+// the next stage's A rows and weight blocks into registers while the current stage computes, then stores it. Per
+// group and row block: cin = -OFF sum x from an MFMA against a constant -OFF operand, then one MFMA per column block
+// (per A plane) and the group's scale applied in fp32, as in the decode kernel.
+template <int QT>
+struct PStage {
+  static constexpr int GB = Fmt<QT>::GROUP_BYTES;
+  static constexpr int ROW = 2 * GB;                     // weight bytes of a row per stage
+  static constexpr int DW = ROW / 4;                      // its dwords (9 / 17)
+};
+static_assert(PStage<ARTLITE_Q4_0>::ROW % 4 == 0 && PStage<ARTLITE_Q8_0>::ROW % 4 == 0, "stage rows in dwords");
+
+template <int QT, bool SWIGLU, int AP>
+struct PLayout {
+  static constexpr int NM = SWIGLU ? 2 : 1;
+  static constexpr int WROWS = 64 * NM;                              // weight rows of a workgroup
+  static constexpr int AROW = 128 * AP + 16;                         // bytes of a staged A row (padded)
+  static constexpr int ABUF = PREFILL_BM * AROW;                     // one stage of A
+  static constexpr int BBUF = WROWS * PStage<QT>::ROW;               // one stage of weights
+  static constexpr int BYTES = 2 * (ABUF + BBUF);
+  static constexpr int AL = PREFILL_BM * 8 * AP / 256;               // 16-byte A loads per thread per stage
+  static constexpr int BL = (WROWS * PStage<QT>::DW + 255) / 256;    // dword weight loads per thread per stage
+};
+
+template <int QT, bool SWIGLU, int AP>
+__global__ __launch_bounds__(256, 2) void k_gemm_prefill(const GemmArgs a) {
+  using F = Fmt<QT>;
+  using L = PLayout<QT, SWIGLU, AP>;
+  constexpr int NM = L::NM, NB = 2 * NM;  // column blocks per wave (matrix-major)
+  constexpr int MB = 4;                   // row blocks per wave
+  static_assert(L::AL * 256 == PREFILL_BM * 8 * AP, "A loads");
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE, lg = lane >> 4, lr = lane & 15;
+  const int wm = wv & 1, wn = wv >> 1;
+  int e = 0, s0, m_valid;
+  if (a.tiles) {
+    if (int64_t(blockIdx.x) >= *a.n_tiles) return;
+    e = a.tiles[2 * blockIdx.x];
+    s0 = a.tiles[2 * blockIdx.x + 1];
+    m_valid = min(PREFILL_BM, a.offsets[e + 1] - s0);
+  } else {
+    s0 = blockIdx.x * PREFILL_BM;
+    m_valid = min(PREFILL_BM, a.dense_rows - s0);
+  }
+  const int n0 = blockIdx.y * 64;
+  const int ng = a.K / 32, stages = ng / 2;
+
+  // this thread's loads of a stage: A row pieces (row q / (8 AP), plane, 16-byte piece) and weight dwords, as 32-bit
+  // offsets from per-workgroup bases
+  uint32_t aof[L::AL], aoff[L::AL];
+#pragma unroll
+  for (int i = 0; i < L::AL; i++) {
+    const int q = threadIdx.x + 256 * i, row = q / (8 * AP), rest = q % (8 * AP), pl = rest / 8, c = rest % 8;
+    const int rr = min(row, m_valid - 1);  // (rows past the tile repeat its last: their outputs are not stored)
+    const int ar = a.a_gather ? a.order[s0 + rr] / a.topk : s0 + rr;
+    aof[i] = uint32_t(ar * a.K + 8 * c) | (uint32_t(pl) << 31);  // (elements; the plane in the top bit)
+    aoff[i] = row * L::AROW + pl * 128 + 16 * c;
+  }
+  const uint8_t* wb0 = a.w[0] + int64_t(e) * a.expert_bytes;
+  const uint8_t* wb1 = NM == 2 ? a.w[1] + int64_t(e) * a.expert_bytes : wb0;
+  uint32_t wof[L::BL], woff[L::BL];
+#pragma unroll
+  for (int i = 0; i < L::BL; i++) {
+    const int q = min(threadIdx.x + 256 * i, L::WROWS * PStage<QT>::DW - 1), row = q / PStage<QT>::DW,
+              dw = q % PStage<QT>::DW;
+    const int mtx = NM == 2 ? row / 64 : 0, n = min(n0 + row % 64, a.N - 1);
+    wof[i] = uint32_t(n * a.row_bytes + 4 * dw) | (uint32_t(mtx) << 31);
+    woff[i] = row * PStage<QT>::ROW + 4 * dw;
+  }
+  u32x4 ra[L::AL];
+  uint32_t rw[L::BL];
+  auto load = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < L::AL; i++) {
+      const uint16_t* base = (AP == 2 && (aof[i] >> 31)) ? a.a_lo : a.a_hi;
+      ra[i] = *reinterpret_cast<const u32x4*>(base + (aof[i] & 0x7FFFFFFFu) + 64 * st);
+    }
+#pragma unroll
+    for (int i = 0; i < L::BL; i++) {
+      const uint8_t* base = (NM == 2 && (wof[i] >> 31)) ? wb1 : wb0;
+      rw[i] = *reinterpret_cast<const uint32_t*>(base + (wof[i] & 0x7FFFFFFFu) + st * PStage<QT>::ROW);
+    }
+  };
+  auto store = [&](int buf) {
+    uint8_t* ab = lds + buf * L::ABUF;
+    uint8_t* bb = lds + 2 * L::ABUF + buf * L::BBUF;
+#pragma unroll
+    for (int i = 0; i < L::AL; i++) *reinterpret_cast<u32x4*>(ab + aoff[i]) = ra[i];
+#pragma unroll
+    for (int i = 0; i < L::BL; i++) *reinterpret_cast<uint32_t*>(bb + woff[i]) = rw[i];
+  };
+
+  // the -OFF operand of the group sums (bf16, exact)
+  const uint32_t noff = f32_to_bf16(-F::OFF) * 0x10001u;
+  const u32x4 bneg = {noff, noff, noff, noff};
+  f32x4 acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) acc[mb][nb] = f32x4{0, 0, 0, 0};
+  // row blocks of this wave holding any row of the tile
+  const int mbn = min(MB, max(0, (m_valid - 64 * wm + 15) / 16));
+
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int st = 0; st < stages; st++) {
+    if (st + 1 < stages) load(st + 1);
+    const uint8_t* ab = lds + (st & 1) * L::ABUF + (64 * wm + lr) * L::AROW + 16 * lg;
+    const uint8_t* bb = lds + 2 * L::ABUF + (st & 1) * L::BBUF;
+#pragma unroll 1
+    for (int gl = 0; gl < 2; gl++) {
+      u32x4 av[MB][AP];
+      f32x4 cin[MB];
+#pragma unroll
+      for (int mb = 0; mb < MB; mb++) {
+        if (mb < mbn) {
+#pragma unroll
+          for (int pl = 0; pl < AP; pl++)
+            av[mb][pl] = *reinterpret_cast<const u32x4*>(ab + mb * 16 * L::AROW + pl * 128 + 64 * gl);
+          cin[mb] = mfma(av[mb][0], bneg, f32x4{0, 0, 0, 0});
+          if (AP == 2) cin[mb] = mfma(av[mb][1], bneg, cin[mb]);
+        }
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; nb++) {
+        // column block nb: matrix nb / 2, weight rows 32 wn + 16 (nb % 2) .. + 16 of it; this lane's row lr
+        const int wrow = (nb / 2) * 64 + 32 * wn + 16 * (nb % 2) + lr;
+        float sc, mn = 0.0f;
+        const u32x4 b = b_operand<QT>(bb + wrow * PStage<QT>::ROW, gl, lg, sc, mn);
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++) {
+          if (mb < mbn) {
+            f32x4 p = mfma(av[mb][0], b, cin[mb]);
+            if (AP == 2) p = mfma(av[mb][1], b, p);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[mb][nb][i] = __builtin_fmaf(sc, p[i], acc[mb][nb][i]);
+          }
+        }
+      }
+    }
+    if (st + 1 < stages) {
+      // (the other buffer was last read in stage st - 1, before the barrier that ended it)
+      store((st + 1) & 1);
+      __syncthreads();
+    }
+  }
+
+  // epilogue: lane output i of block (mb, nb): row of A 64 wm + 16 mb + 4 lg + i, weight row n0 + 32 wn + 16 (nb % 2)
+  // + lr of matrix nb / 2
+#pragma unroll
+  for (int mb = 0; mb < MB; mb++) {
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int n = n0 + 32 * wn + 16 * j + lr;
+      if (n >= a.N) continue;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int m = 64 * wm + 16 * mb + 4 * lg + i;
+        if (m >= m_valid) continue;
+        const int64_t o = int64_t(s0 + m) * a.N + n;
+        if constexpr (SWIGLU) {
+          const float g = acc[mb][j][i], u = acc[mb][2 + j][i];
+          const float h = g / (1.0f + expf(-g)) * u;
+          const uint32_t hi = f32_to_bf16(h);
+          a.h_hi[o] = uint16_t(hi);
+          a.h_lo[o] = uint16_t(f32_to_bf16(h - bf16_to_f32(hi)));
+        } else {
+          a.y[o] = acc[mb][j][i];
+        }
+      }
+    }
+  }
+}
+
+template <int QT, bool SWIGLU>
+int launch_prefill(const GemmArgs& a, hipStream_t s) {
+  const int64_t tiles = a.tiles ? a.max_tiles : (a.dense_rows + PREFILL_BM - 1) / PREFILL_BM;
+  const dim3 grid(unsigned(tiles), unsigned((a.N + 63) / 64)), block(256);
+  if (a.a_lo) {
+    constexpr size_t lds = PLayout<QT, SWIGLU, 2>::BYTES;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_prefill<QT, SWIGLU, 2>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    ART_HIP(attr);
+    k_gemm_prefill<QT, SWIGLU, 2><<<grid, block, lds, s>>>(a);
+  } else {
+    constexpr size_t lds = PLayout<QT, SWIGLU, 1>::BYTES;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_prefill<QT, SWIGLU, 1>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    ART_HIP(attr);
+    k_gemm_prefill<QT, SWIGLU, 1><<<grid, block, lds, s>>>(a);
+  }
+  ART_HIP(hipGetLastError());
+  return ARTLITE_OK;
+}
+
+bool prefill_supported(int qtype, int K, int N) {
+  return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0) && K > 0 && K % 64 == 0 && N > 0 && N % 64 == 0;
+}
+
 int launch_expert_gemm(const GemmArgs& a, hipStream_t s) {
   if (a.K % 32 || (a.qtype == ARTLITE_Q4_K && a.K % 256))
     return fail(ARTLITE_EINVAL, "expert GEMM: K %d is not a multiple of the format's block", a.K);
   if (a.K / 32 > MAX_GROUPS) return fail(ARTLITE_EINVAL, "expert GEMM: K %d beyond %d", a.K, 32 * MAX_GROUPS);
+  const bool swiglu = a.w[1] != nullptr;
+  // tiles of PREFILL_BM rows (a tile list made for them, or dense rows enough to fill them): the prefill tiling
+  const bool pre = a.tiles ? a.bm == PREFILL_BM
+                            : a.dense_rows >= PREFILL_BM / 2 && prefill_supported(a.qtype, a.K, a.N);
+  if (pre) {
+    if (!prefill_supported(a.qtype, a.K, a.N))
+      return fail(ARTLITE_EINVAL, "expert GEMM: prefill tiles of weight type %d, K %d, N %d", a.qtype, a.K, a.N);
+    const int64_t tiles = a.tiles ? a.max_tiles : (a.dense_rows + PREFILL_BM - 1) / PREFILL_BM;
+    if (tiles <= 0) return ARTLITE_OK;
+    if (a.qtype == ARTLITE_Q4_0) return swiglu ? launch_prefill<ARTLITE_Q4_0, true>(a, s) : launch_prefill<ARTLITE_Q4_0, false>(a, s);
+    return swiglu ? launch_prefill<ARTLITE_Q8_0, true>(a, s) : launch_prefill<ARTLITE_Q8_0, false>(a, s);
+  }
+  if (a.tiles && a.bm != DECODE_BM) return fail(ARTLITE_EINVAL, "expert GEMM: tiles of %d rows", a.bm);
   const int64_t tiles = a.tiles ? a.max_tiles : (a.dense_rows + DECODE_BM - 1) / DECODE_BM;
   if (tiles <= 0) return ARTLITE_OK;
-  const bool swiglu = a.w[1] != nullptr;
 #define ART_DISPATCH(QT) return swiglu ? launch_decode<QT, true, 2>(a, s) : launch_decode<QT, false, 2>(a, s)
   switch (a.qtype) {
     case ARTLITE_Q4_0: ART_DISPATCH(ARTLITE_Q4_0);

@@ -27,7 +27,7 @@ struct artlite_moe_layer {
   DevBuf table, ctrl, counts, offsets, order, slot, tiles;
   DevBuf hhi, hlo, ypairs, shhi, shlo, ys, y;
   DevBuf xq, hq, shq;  // the decode path's XQ activations
-  bool gemv_ok = false, shared_gemv_ok = false;
+  bool gemv_ok = false, shared_gemv_ok = false, prefill_ok = false;
   int64_t last_T = -1;
   bool last_gemv = false;
 };
@@ -87,6 +87,7 @@ struct Path {
   bool split;        // bf16 hi / lo planes of fp32 x needed
   bool quant;        // XQ of x needed (made by the router's launch)
   bool small;        // top k and dispatch in one workgroup
+  bool prefill;      // routed experts on the MFMA prefill tiling (else the MFMA decode tiling, or the GEMV)
 };
 
 Path path_of(const artlite_moe_layer* L, int64_t T) {
@@ -97,6 +98,8 @@ Path path_of(const artlite_moe_layer* L, int64_t T) {
   p.split = mfma_x && L->x_dtype == ARTLITE_X_F32;
   p.quant = p.gemv;
   p.small = p.gemv && T * L->d.top_k <= DISPATCH_BLOCK && L->d.n_experts <= MAX_EXPERTS;
+  // (16 rows per expert on average fill enough of a PREFILL_BM tile)
+  p.prefill = !p.gemv && L->prefill_ok && T * L->d.top_k >= int64_t(16) * L->d.n_experts;
   return p;
 }
 
@@ -151,7 +154,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     ART_TRY(mark());
     ART_TRY(launch_router(L->x.p, L->x_dtype, L->sinp.as<float>(), H, 1, T, L->sg.as<float>(), 1, nullptr, s));
   }
-  const int BM = path.gemv ? GEMV_BM : DECODE_BM;
+  const int BM = path.gemv ? GEMV_BM : path.prefill ? PREFILL_BM : DECODE_BM;
   DispatchBufs db{L->ids.as<int32_t>(), P, E, k, L->table.as<int32_t>(), L->ctrl.as<int32_t>(),
                   L->counts.as<int32_t>(), L->offsets.as<int32_t>(), L->order.as<int32_t>(), L->slot.as<int32_t>(),
                   L->tiles.as<int32_t>(), BM, nullptr, 0};
@@ -222,6 +225,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     g.n_tiles = L->ctrl.as<int32_t>() + CTRL_TILES;
     g.offsets = L->offsets.as<int32_t>();
     g.max_tiles = tile_bound(P, E, BM);
+    g.bm = BM;
     g.h_hi = L->hhi.as<uint16_t>();
     g.h_lo = L->hlo.as<uint16_t>();
     ART_TRY(mark());
@@ -344,6 +348,8 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
   }
   L->gemv_ok = gemv_supported(d.gate_type, d.hidden, d.expert_ffn) &&
                gemv_supported(d.down_type, d.expert_ffn, d.hidden);
+  L->prefill_ok = prefill_supported(d.gate_type, d.hidden, d.expert_ffn) &&
+                  prefill_supported(d.down_type, d.expert_ffn, d.hidden);
   L->shared_gemv_ok = sq && gemv_supported(d.shared_type, d.hidden, d.shared_ffn) &&
                       gemv_supported(d.shared_type, d.shared_ffn, d.hidden);
   hipError_t e = hipGetDevice(&L->device);
