@@ -329,43 +329,89 @@ int launch_decode(const GemmArgs& a, hipStream_t s) {
   return ARTLITE_OK;
 }
 
-// ---- Prefill tiling (k_gemm_prefill): a workgroup is one tile of PREFILL_BM sorted rows of one expert times 64
-// weight rows (of each matrix), as 2 x 2 waves: wave (wm, wn) takes rows of A 64 wm .. + 64 (4 MFMA row blocks)
-// and weight rows 32 wn .. + 32 (2 column blocks per matrix; SwiGLU: those rows of gate and of up, so h is formed
-// in the wave). K streams in stages of two 32-value groups through two LDS buffers: each thread loads its share of
-// the next stage's A rows and weight blocks into registers while the current stage computes, then stores it. Per
-// group and row block: cin = -OFF sum x from an MFMA against a constant -OFF operand, then one MFMA per column block
-// (per A plane) and the group's scale applied in fp32, as in the decode kernel.
+// ---- Prefill tiling (k_gemm_prefill): a workgroup is one tile of PREFILL_BM sorted rows of one expert times 128
+// weight rows (of each matrix), as 2 x 4 waves: wave (wm, wn) takes rows of A 64 wm .. + 64 (4 MFMA row blocks) and
+// weight rows 32 wn .. + 32 (2 column blocks per matrix; SwiGLU: those rows of gate and of up, so h is formed in
+// the wave). K streams in stages of two 32-value groups through a ring of R LDS stages filled by DMA
+// (global_load_lds, issued by asm so that the compiler, which would wait for every DMA in flight before any LDS read
+// it sees, does not know of them): every wave issues the same number of loads per stage (past the last stage, loads
+// of stage 0 again), so each wait is a fixed count of this wave's loads, and R - 1 stages are in flight while one
+// computes. The operands of the next group are read from LDS while the current group computes; stage st + 1's wait
+// and barrier sit between stage st's two groups, after which the slot of stage st (both groups in registers by
+// then) takes stage st + R.
+// A rows sit in LDS as 16-byte chunks of 8 values, XOR-swizzled by row, so the 16 rows of an operand read fall in
+// different banks; a weight row's stage bytes (two blocks) sit packed, read as aligned dwords (a block's codes start
+// 2 bytes into it: the first block's are shifted into place with alignbit).
 template <int QT>
 struct PStage {
   static constexpr int GB = Fmt<QT>::GROUP_BYTES;
-  static constexpr int ROW = 2 * GB;                     // weight bytes of a row per stage
-  static constexpr int DW = ROW / 4;                      // its dwords (9 / 17)
+  static constexpr int ROW = 2 * GB;  // weight bytes of a row per stage
+  static constexpr int DW = ROW / 4;  // its dwords (9 / 17)
 };
 static_assert(PStage<ARTLITE_Q4_0>::ROW % 4 == 0 && PStage<ARTLITE_Q8_0>::ROW % 4 == 0, "stage rows in dwords");
 
 template <int QT, bool SWIGLU, int AP>
 struct PLayout {
   static constexpr int NM = SWIGLU ? 2 : 1;
-  static constexpr int WROWS = 64 * NM;                              // weight rows of a workgroup
-  static constexpr int AROW = 128 * AP + 16;                         // bytes of a staged A row (padded)
-  static constexpr int ABUF = PREFILL_BM * AROW;                     // one stage of A
-  static constexpr int BBUF = WROWS * PStage<QT>::ROW;               // one stage of weights
-  static constexpr int BYTES = 2 * (ABUF + BBUF);
-  static constexpr int AL = PREFILL_BM * 8 * AP / 256;               // 16-byte A loads per thread per stage
-  static constexpr int BL = (WROWS * PStage<QT>::DW + 255) / 256;    // dword weight loads per thread per stage
+  static constexpr int WAVES = 8, THREADS = 64 * WAVES;
+  static constexpr int WROWS = 128 * NM;                        // weight rows of a workgroup
+  static constexpr int ACH = 8 * AP;                            // 16-byte chunks of an A row per stage
+  static constexpr int ABYTES = PREFILL_BM * ACH * 16;          // one stage of A
+  static constexpr int AI = PREFILL_BM * ACH / 64 / WAVES;      // A DMA instructions per wave per stage
+  static constexpr int BI = (WROWS * PStage<QT>::DW + 64 * WAVES - 1) / (64 * WAVES);  // weight dword DMAs per wave
+  static constexpr int BBYTES = WAVES * BI * 256;               // one stage of weights (padded)
+  static constexpr int SBYTES = ABYTES + BBYTES;
+  static constexpr int R = (150 * 1024 / SBYTES) < 5 ? (150 * 1024 / SBYTES) : 5;  // stages in the ring
+  static constexpr int LOADS = AI + BI;                         // DMA instructions per wave per stage
+  static_assert(R >= 3, "ring");
+  static_assert((R - 1) * LOADS < 64, "vmcnt");
+  static_assert(AI * 64 * WAVES == PREFILL_BM * ACH, "A stage in whole instructions");
+};
+
+template <int N>
+__device__ __forceinline__ void pf_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory");
+}
+
+// every wave's LDS reads done, then the workgroup barrier
+__device__ __forceinline__ void pf_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+__device__ __forceinline__ uint32_t pf_lds_addr(const void* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
+
+// one DMA of SIZE bytes per lane from g into LDS at lds (wave-uniform) + SIZE lane. M0 carries the LDS address; no
+// compiler-generated code in these kernels uses M0 (the asm sets it before each load, with the one wait state a
+// load after an M0 write needs).
+template <int SIZE>
+__device__ __forceinline__ void pf_dma(const void* g, uint32_t lds) {
+  if constexpr (SIZE == 16)
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+
+// the operands of one 32-value group: per row block and A plane, the lane's 8 bf16 of A; per column block, the
+// weight row's fp16 scale and 8 of its code bytes (Q4_0: 16 nibbles, 8 of them the lane's)
+template <int QT, int NB, int AP>
+struct POps {
+  u32x4 a[4][AP];
+  uint32_t sc[NB];
+  uint32_t cw[NB][2];
 };
 
 template <int QT, bool SWIGLU, int AP>
-__global__ __launch_bounds__(256, 2) void k_gemm_prefill(const GemmArgs a) {
+__global__ __launch_bounds__(512) void k_gemm_prefill(const GemmArgs a) {
   using F = Fmt<QT>;
   using L = PLayout<QT, SWIGLU, AP>;
   constexpr int NM = L::NM, NB = 2 * NM;  // column blocks per wave (matrix-major)
   constexpr int MB = 4;                   // row blocks per wave
-  static_assert(L::AL * 256 == PREFILL_BM * 8 * AP, "A loads");
+  constexpr int R = L::R;
+  constexpr int ROW = PStage<QT>::ROW, GB = F::GROUP_BYTES;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE, lg = lane >> 4, lr = lane & 15;
-  const int wm = wv & 1, wn = wv >> 1;
+  const int lane = threadIdx.x & (WAVE - 1), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int lg = lane >> 4, lr = lane & 15, wm = wv & 1, wn = wv >> 1;
   int e = 0, s0, m_valid;
   if (a.tiles) {
     if (int64_t(blockIdx.x) >= *a.n_tiles) return;
@@ -376,52 +422,84 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(const GemmArgs a) {
     s0 = blockIdx.x * PREFILL_BM;
     m_valid = min(PREFILL_BM, a.dense_rows - s0);
   }
-  const int n0 = blockIdx.y * 64;
-  const int ng = a.K / 32, stages = ng / 2;
+  const int n0 = blockIdx.y * 128;
+  const int stages = a.K / 64;
 
-  // this thread's loads of a stage: A row pieces (row q / (8 AP), plane, 16-byte piece) and weight dwords, as 32-bit
-  // offsets from per-workgroup bases
-  uint32_t aof[L::AL], aoff[L::AL];
+  // chunk swizzle of row r: the 16 rows an operand read touches hit 16 different 16-byte bank slots
+  auto swz = [](int r) { return AP == 2 ? (r & 15) : ((r >> 1) & 7); };
+  // The lane's DMA sources. A: instruction i writes chunks (wv AI + i) 64 + lane of the stage's A region; chunk p
+  // holds row r = p / ACH, physical chunk c = p % ACH, which is logical chunk c ^ swz(r) (logical: plane c / 8, K
+  // values 8 (c % 8) .. + 8 of the stage).
+  const uint16_t* asrc[L::AI];
 #pragma unroll
-  for (int i = 0; i < L::AL; i++) {
-    const int q = threadIdx.x + 256 * i, row = q / (8 * AP), rest = q % (8 * AP), pl = rest / 8, c = rest % 8;
-    const int rr = min(row, m_valid - 1);  // (rows past the tile repeat its last: their outputs are not stored)
+  for (int i = 0; i < L::AI; i++) {
+    const int p = (wv * L::AI + i) * 64 + lane, r = p / L::ACH, c = (p % L::ACH) ^ swz(r);
+    const int rr = min(r, m_valid - 1);  // (rows past the tile repeat its last: their outputs are not stored)
     const int ar = a.a_gather ? a.order[s0 + rr] / a.topk : s0 + rr;
-    aof[i] = uint32_t(ar * a.K + 8 * c) | (uint32_t(pl) << 31);  // (elements; the plane in the top bit)
-    aoff[i] = row * L::AROW + pl * 128 + 16 * c;
+    asrc[i] = (AP == 2 && c >= 8 ? a.a_lo : a.a_hi) + int64_t(ar) * a.K + 8 * (c % 8);
   }
-  const uint8_t* wb0 = a.w[0] + int64_t(e) * a.expert_bytes;
-  const uint8_t* wb1 = NM == 2 ? a.w[1] + int64_t(e) * a.expert_bytes : wb0;
-  uint32_t wof[L::BL], woff[L::BL];
+  // weights: instruction j writes dwords (wv BI + j) 64 + lane of the stage's weight region, row q / DW (matrix-major,
+  // 128 rows each), dword q % DW of the row's stage bytes; dwords past the rows load the last one again (padding)
+  const uint8_t* wsrc[L::BI];
 #pragma unroll
-  for (int i = 0; i < L::BL; i++) {
-    const int q = min(threadIdx.x + 256 * i, L::WROWS * PStage<QT>::DW - 1), row = q / PStage<QT>::DW,
-              dw = q % PStage<QT>::DW;
-    const int mtx = NM == 2 ? row / 64 : 0, n = min(n0 + row % 64, a.N - 1);
-    wof[i] = uint32_t(n * a.row_bytes + 4 * dw) | (uint32_t(mtx) << 31);
-    woff[i] = row * PStage<QT>::ROW + 4 * dw;
+  for (int j = 0; j < L::BI; j++) {
+    const int q = min((wv * L::BI + j) * 64 + lane, L::WROWS * PStage<QT>::DW - 1);
+    const int row = q / PStage<QT>::DW, dw = q % PStage<QT>::DW;
+    const int mtx = NM == 2 ? row / 128 : 0, n = min(n0 + row % 128, a.N - 1);
+    wsrc[j] = a.w[mtx] + int64_t(e) * a.expert_bytes + int64_t(n) * a.row_bytes + 4 * dw;
   }
-  u32x4 ra[L::AL];
-  uint32_t rw[L::BL];
-  auto load = [&](int st) {
+  const uint32_t lbase = pf_lds_addr(lds);
+  const uint32_t adst = lbase + wv * L::AI * 1024, bdst = lbase + L::ABYTES + wv * L::BI * 256;
+  // the loads of stage j (past the last stage: stage 0 again) into ring slot j % R
+  auto issue = [&](int j) {
+    const int st = j < stages ? j : 0;
+    const uint32_t so = (j % R) * L::SBYTES;
 #pragma unroll
-    for (int i = 0; i < L::AL; i++) {
-      const uint16_t* base = (AP == 2 && (aof[i] >> 31)) ? a.a_lo : a.a_hi;
-      ra[i] = *reinterpret_cast<const u32x4*>(base + (aof[i] & 0x7FFFFFFFu) + 64 * st);
-    }
+    for (int i = 0; i < L::AI; i++) pf_dma<16>(asrc[i] + 64 * st, adst + so + i * 1024);
 #pragma unroll
-    for (int i = 0; i < L::BL; i++) {
-      const uint8_t* base = (NM == 2 && (wof[i] >> 31)) ? wb1 : wb0;
-      rw[i] = *reinterpret_cast<const uint32_t*>(base + (wof[i] & 0x7FFFFFFFu) + st * PStage<QT>::ROW);
-    }
+    for (int i = 0; i < L::BI; i++) pf_dma<4>(wsrc[i] + st * ROW, bdst + so + i * 256);
   };
-  auto store = [&](int buf) {
-    uint8_t* ab = lds + buf * L::ABUF;
-    uint8_t* bb = lds + 2 * L::ABUF + buf * L::BBUF;
+
+  // the lane's LDS read offsets in ring slot 0. A, row 64 wm + lr (row block mb at + 16 mb rows), group gl, plane pl:
+  // the chunk of K 8 lg .. + 8. B, row 32 wn + lr (+ the column block's rows): its block gl.
+  constexpr int AMB = 16 * L::ACH * 16;
+  uint32_t aof[2][AP];
+  {
+    const int r = 64 * wm + lr, s = swz(r);
 #pragma unroll
-    for (int i = 0; i < L::AL; i++) *reinterpret_cast<u32x4*>(ab + aoff[i]) = ra[i];
+    for (int gl = 0; gl < 2; gl++)
 #pragma unroll
-    for (int i = 0; i < L::BL; i++) *reinterpret_cast<uint32_t*>(bb + woff[i]) = rw[i];
+      for (int pl = 0; pl < AP; pl++) aof[gl][pl] = r * L::ACH * 16 + ((8 * pl + 4 * gl + lg) ^ s) * 16;
+  }
+  const uint32_t bof = L::ABYTES + (32 * wn + lr) * ROW;
+  const int sh = 4 * (lg >> 1);  // (Q4_0: the nibble half of lane group lg)
+  auto brow = [](int nb) { return (nb / 2) * 128 + 16 * (nb % 2); };
+
+  auto read = [&](POps<QT, NB, AP>& o, uint32_t so, int gl) {
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+      for (int pl = 0; pl < AP; pl++) {
+        o.a[mb][pl] = *reinterpret_cast<const u32x4*>(lds + so + aof[gl][pl] + mb * AMB);
+      }
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+      const uint8_t* b = lds + so + bof + brow(nb) * ROW + gl * GB;  // (4-byte aligned: gl GB is 0 or 2 mod 4)
+      o.sc[nb] = *reinterpret_cast<const uint16_t*>(b);
+      // the 8 code bytes at b + 2 + CB: Q4_0 bytes 8 (lg & 1) .. + 8 (of which lane group lg takes the low nibbles
+      // for lg < 2, else the high ones), Q8_0 bytes 8 lg .. + 8
+      const int cb = QT == ARTLITE_Q4_0 ? 8 * (lg & 1) : 8 * lg;
+      if (gl == 0) {
+        const uint32_t* d = reinterpret_cast<const uint32_t*>(b + cb);
+        const uint32_t d0 = d[0], d1 = d[1], d2 = d[2];
+        o.cw[nb][0] = __builtin_amdgcn_alignbit(d1, d0, 16);
+        o.cw[nb][1] = __builtin_amdgcn_alignbit(d2, d1, 16);
+      } else {
+        const uint32_t* d = reinterpret_cast<const uint32_t*>(b + 2 + cb);
+        o.cw[nb][0] = d[0];
+        o.cw[nb][1] = d[1];
+      }
+    }
   };
 
   // the -OFF operand of the group sums (bf16, exact)
@@ -432,53 +510,77 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(const GemmArgs a) {
   for (int mb = 0; mb < MB; mb++)
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) acc[mb][nb] = f32x4{0, 0, 0, 0};
-  // row blocks of this wave holding any row of the tile
-  const int mbn = min(MB, max(0, (m_valid - 64 * wm + 15) / 16));
-
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int st = 0; st < stages; st++) {
-    if (st + 1 < stages) load(st + 1);
-    const uint8_t* ab = lds + (st & 1) * L::ABUF + (64 * wm + lr) * L::AROW + 16 * lg;
-    const uint8_t* bb = lds + 2 * L::ABUF + (st & 1) * L::BBUF;
-#pragma unroll 1
-    for (int gl = 0; gl < 2; gl++) {
-      u32x4 av[MB][AP];
-      f32x4 cin[MB];
+  // One group's products: the -OFF group sums (MFMAs against bneg) with the B operands decoded between them, then
+  // the MB x NB products, each followed by the scale FMAs of the product two before it (the MFMA result's latency),
+  // as sched_group_barrier orders them.
+  auto compute = [&](const POps<QT, NB, AP>& o) {
+    f32x4 cin[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+      cin[mb] = mfma(o.a[mb][0], bneg, f32x4{0, 0, 0, 0});
+      if (AP == 2) cin[mb] = mfma(o.a[mb][AP - 1], bneg, cin[mb]);
+    }
+    u32x4 b[NB];
+    float d[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+      if constexpr (QT == ARTLITE_Q4_0)
+        b[nb] = nib8((o.cw[nb][0] >> sh) & 0x0F0F0F0Fu, (o.cw[nb][1] >> sh) & 0x0F0F0F0Fu);
+      else
+        b[nb] = byte8(o.cw[nb][0] ^ 0x80808080u, o.cw[nb][1] ^ 0x80808080u);
+      d[nb] = h2f(o.sc[nb]);
+    }
+    f32x4 p[NB][MB];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++)
 #pragma unroll
       for (int mb = 0; mb < MB; mb++) {
-        if (mb < mbn) {
-#pragma unroll
-          for (int pl = 0; pl < AP; pl++)
-            av[mb][pl] = *reinterpret_cast<const u32x4*>(ab + mb * 16 * L::AROW + pl * 128 + 64 * gl);
-          cin[mb] = mfma(av[mb][0], bneg, f32x4{0, 0, 0, 0});
-          if (AP == 2) cin[mb] = mfma(av[mb][1], bneg, cin[mb]);
-        }
+        p[nb][mb] = mfma(o.a[mb][0], b[nb], cin[mb]);
+        if (AP == 2) p[nb][mb] = mfma(o.a[mb][AP - 1], b[nb], p[nb][mb]);
       }
 #pragma unroll
-      for (int nb = 0; nb < NB; nb++) {
-        // column block nb: matrix nb / 2, weight rows 32 wn + 16 (nb % 2) .. + 16 of it; this lane's row lr
-        const int wrow = (nb / 2) * 64 + 32 * wn + 16 * (nb % 2) + lr;
-        float sc, mn = 0.0f;
-        const u32x4 b = b_operand<QT>(bb + wrow * PStage<QT>::ROW, gl, lg, sc, mn);
+    for (int nb = 0; nb < NB; nb++)
 #pragma unroll
-        for (int mb = 0; mb < MB; mb++) {
-          if (mb < mbn) {
-            f32x4 p = mfma(av[mb][0], b, cin[mb]);
-            if (AP == 2) p = mfma(av[mb][1], b, p);
+      for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[mb][nb][i] = __builtin_fmaf(sc, p[i], acc[mb][nb][i]);
-          }
-        }
-      }
+        for (int i = 0; i < 4; i++) acc[mb][nb][i] = __builtin_fmaf(d[nb], p[nb][mb][i], acc[mb][nb][i]);
+    constexpr int DEC = QT == ARTLITE_Q4_0 ? 7 : 18;  // decode VALU per column block (about)
+#pragma unroll
+    for (int mb = 0; mb < MB * AP; mb++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, (DEC * NB + MB * AP - 1) / (MB * AP), 0);
+    }
+#pragma unroll
+    for (int t = 0; t < MB * NB; t++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, AP, 0);
+      if (t >= 2) __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+  };
+  // waves whose 64 rows of A are all past the tile skip the products (rows past it otherwise repeat its last row)
+  const bool active = 64 * wm < m_valid;
+
+  POps<QT, NB, AP> cur, nxt;
+#pragma unroll
+  for (int j = 0; j < R; j++) issue(j);
+  pf_wait<(R - 1) * L::LOADS>();  // (stage 0: R - 1 stages issued after it)
+  pf_barrier();
+  if (active) read(cur, 0, 0);
+  for (int st = 0; st < stages; st++) {
+    const uint32_t so = (st % R) * L::SBYTES;
+    if (active) {
+      read(nxt, so, 1);
+      compute(cur);
     }
     if (st + 1 < stages) {
-      // (the other buffer was last read in stage st - 1, before the barrier that ended it)
-      store((st + 1) & 1);
-      __syncthreads();
+      pf_wait<(R - 2) * L::LOADS>();  // (stage st + 1: stages up to st + R - 1 issued)
+      pf_barrier();
+      issue(st + R);  // (into the slot of stage st, whose operands every wave holds in registers)
+      if (active) read(cur, ((st + 1) % R) * L::SBYTES, 0);
     }
+    if (active) compute(nxt);
   }
+  pf_wait<0>();  // (the loads past the last stage land before the workgroup's LDS is released)
 
   // epilogue: lane output i of block (mb, nb): row of A 64 wm + 16 mb + 4 lg + i, weight row n0 + 32 wn + 16 (nb % 2)
   // + lr of matrix nb / 2
@@ -507,29 +609,27 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(const GemmArgs a) {
   }
 }
 
-template <int QT, bool SWIGLU>
-int launch_prefill(const GemmArgs& a, hipStream_t s) {
+template <int QT, bool SWIGLU, int AP>
+int launch_prefill_ap(const GemmArgs& a, hipStream_t s) {
+  using L = PLayout<QT, SWIGLU, AP>;
   const int64_t tiles = a.tiles ? a.max_tiles : (a.dense_rows + PREFILL_BM - 1) / PREFILL_BM;
-  const dim3 grid(unsigned(tiles), unsigned((a.N + 63) / 64)), block(256);
-  if (a.a_lo) {
-    constexpr size_t lds = PLayout<QT, SWIGLU, 2>::BYTES;
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_prefill<QT, SWIGLU, 2>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
-    ART_HIP(attr);
-    k_gemm_prefill<QT, SWIGLU, 2><<<grid, block, lds, s>>>(a);
-  } else {
-    constexpr size_t lds = PLayout<QT, SWIGLU, 1>::BYTES;
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_prefill<QT, SWIGLU, 1>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
-    ART_HIP(attr);
-    k_gemm_prefill<QT, SWIGLU, 1><<<grid, block, lds, s>>>(a);
-  }
+  const dim3 grid(unsigned(tiles), unsigned((a.N + 127) / 128)), block(L::THREADS);
+  constexpr size_t lds = size_t(L::R) * L::SBYTES;
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_prefill<QT, SWIGLU, AP>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+  ART_HIP(attr);
+  k_gemm_prefill<QT, SWIGLU, AP><<<grid, block, lds, s>>>(a);
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
 }
 
+template <int QT, bool SWIGLU>
+int launch_prefill(const GemmArgs& a, hipStream_t s) {
+  return a.a_lo ? launch_prefill_ap<QT, SWIGLU, 2>(a, s) : launch_prefill_ap<QT, SWIGLU, 1>(a, s);
+}
+
 bool prefill_supported(int qtype, int K, int N) {
-  return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0) && K > 0 && K % 64 == 0 && N > 0 && N % 64 == 0;
+  return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0) && K > 0 && K % 64 == 0 && N > 0 && N % 128 == 0;
 }
 
 int launch_expert_gemm(const GemmArgs& a, hipStream_t s) {
