@@ -329,19 +329,27 @@ int launch_decode(const GemmArgs& a, hipStream_t s) {
   return ARTLITE_OK;
 }
 
-// ---- Prefill tiling (k_gemm_prefill): a workgroup is one tile of PREFILL_BM sorted rows of one expert times 128
-// weight rows (of each matrix), as 2 x 4 waves: wave (wm, wn) takes rows of A 64 wm .. + 64 (4 MFMA row blocks) and
-// weight rows 32 wn .. + 32 (2 column blocks per matrix; SwiGLU: those rows of gate and of up, so h is formed in
-// the wave). K streams in stages of two 32-value groups through a ring of R LDS stages filled by DMA
-// (global_load_lds, issued by asm so that the compiler, which would wait for every DMA in flight before any LDS read
-// it sees, does not know of them): every wave issues the same number of loads per stage (past the last stage, loads
-// of stage 0 again), so each wait is a fixed count of this wave's loads, and R - 1 stages are in flight while one
-// computes. The operands of the next group are read from LDS while the current group computes; stage st + 1's wait
-// and barrier sit between stage st's two groups, after which the slot of stage st (both groups in registers by
-// then) takes stage st + R.
+// ---- Prefill tiling (k_prefill): fp16 products on v_mfma_f32_16x16x32_f16. A is fp16 rows, each token's row
+// scaled by a power of two (2^-in_exp[token]) into [2^14, 2^15) at its largest, so bf16 activations convert
+// exactly and fp32 ones round once (2^-11). The weights' blocks are decoded in registers to fp16 d (q - 8) (Q4_0)
+// or d q (Q8_0): the code exactly, the product with the fp16 scale rounded once (2^-11 relative), so the MFMA's
+// fp32 sums need no per-group scale FMA. The SwiGLU launch writes h in fp16 scaled by 2^-out_exp[token], where
+// out_exp bounds |h| <= (sum |x|)^2 max|w_gate| max|w_up| below 2^15; the plain launch scales its fp32 outputs back
+// by 2^in_exp[token].
+// A workgroup is one tile of PREFILL_BM sorted rows of one expert times 256 staged weight rows (SwiGLU: 128 of gate
+// and the same 128 of up; plain: 256), as 8 waves: wave w takes all 128 rows (MB = 8 MFMA row blocks) and two
+// 16-row column blocks (SwiGLU: gate and up rows 16 w .. + 16, so h forms in the wave; plain: rows 32 w .. + 32), so
+// each lane's decode of a block's codes feeds 8 MFMAs. K streams in stages of two 32-value groups through a ring of
+// R LDS stages filled by DMA (global_load_lds, issued by asm so that the compiler, which would wait for every DMA
+// in flight before any LDS read it sees, does not know of them): every wave issues the same number of loads per
+// stage (past the last stage, loads of stage 0 again), so each wait is a fixed count of this wave's loads, and
+// R - 1 stages are in flight while one computes. The operands of the next group are read from LDS while the
+// current group computes; stage st + 1's wait and barrier sit between stage st's two groups, after which the slot
+// of stage st (both groups in registers by then) takes stage st + R.
 // A rows sit in LDS as 16-byte chunks of 8 values, XOR-swizzled by row, so the 16 rows of an operand read fall in
 // different banks; a weight row's stage bytes (two blocks) sit packed, read as aligned dwords (a block's codes start
-// 2 bytes into it: the first block's are shifted into place with alignbit).
+// 2 bytes into it: the first block's are shifted into place with alignbit). MFMA layout (16x16x32): lane l holds A
+// row l % 16 and B column l % 16, both with K values 8 (l / 16) .. + 8; C column l % 16, rows 4 (l / 16) .. + 4.
 template <int QT>
 struct PStage {
   static constexpr int GB = Fmt<QT>::GROUP_BYTES;
@@ -350,12 +358,11 @@ struct PStage {
 };
 static_assert(PStage<ARTLITE_Q4_0>::ROW % 4 == 0 && PStage<ARTLITE_Q8_0>::ROW % 4 == 0, "stage rows in dwords");
 
-template <int QT, bool SWIGLU, int AP>
+template <int QT>
 struct PLayout {
-  static constexpr int NM = SWIGLU ? 2 : 1;
   static constexpr int WAVES = 8, THREADS = 64 * WAVES;
-  static constexpr int WROWS = 128 * NM;                        // weight rows of a workgroup
-  static constexpr int ACH = 8 * AP;                            // 16-byte chunks of an A row per stage
+  static constexpr int WROWS = 256;                             // staged weight rows of a workgroup
+  static constexpr int ACH = 8;                                 // 16-byte chunks of an A row per stage
   static constexpr int ABYTES = PREFILL_BM * ACH * 16;          // one stage of A
   static constexpr int AI = PREFILL_BM * ACH / 64 / WAVES;      // A DMA instructions per wave per stage
   static constexpr int BI = (WROWS * PStage<QT>::DW + 64 * WAVES - 1) / (64 * WAVES);  // weight dword DMAs per wave
@@ -392,103 +399,168 @@ __device__ __forceinline__ void pf_dma(const void* g, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
 }
 
-// the operands of one 32-value group: per row block and A plane, the lane's 8 bf16 of A; per column block, the
-// weight row's fp16 scale and 8 of its code bytes (Q4_0: 16 nibbles, 8 of them the lane's)
-template <int QT, int NB, int AP>
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// the operands of one 32-value group: per row block, the lane's 8 fp16 of A; per column block, the weight row's
+// fp16 scale and 8 of its code bytes (Q4_0: 16 nibbles, 8 of them the lane's)
+template <int MB>
 struct POps {
-  u32x4 a[4][AP];
-  uint32_t sc[NB];
-  uint32_t cw[NB][2];
+  u32x4 a[MB];
+  uint32_t sc[2];
+  uint32_t cw[2][2];
 };
 
-template <int QT, bool SWIGLU, int AP>
-__global__ __launch_bounds__(512) void k_gemm_prefill(const GemmArgs a) {
-  using F = Fmt<QT>;
-  using L = PLayout<QT, SWIGLU, AP>;
-  constexpr int NM = L::NM, NB = 2 * NM;  // column blocks per wave (matrix-major)
-  constexpr int MB = 4;                   // row blocks per wave
-  constexpr int R = L::R;
-  constexpr int ROW = PStage<QT>::ROW, GB = F::GROUP_BYTES;
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const int lane = threadIdx.x & (WAVE - 1), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
-  const int lg = lane >> 4, lr = lane & 15, wm = wv & 1, wn = wv >> 1;
-  int e = 0, s0, m_valid;
-  if (a.tiles) {
-    if (int64_t(blockIdx.x) >= *a.n_tiles) return;
-    e = a.tiles[2 * blockIdx.x];
-    s0 = a.tiles[2 * blockIdx.x + 1];
-    m_valid = min(PREFILL_BM, a.offsets[e + 1] - s0);
-  } else {
-    s0 = blockIdx.x * PREFILL_BM;
-    m_valid = min(PREFILL_BM, a.dense_rows - s0);
+// Decode of a lane's 8 weights to fp16: the code bytes spread into fp16 1024 + c (c < 256 exact, one perm per two),
+// the offset taken off exactly by one packed FMA (Q4_0's high nibbles, kept in place as 16 q, are scaled by 1/16 in
+// it), then the product with the block's scale, rounded once.
+template <int QT>
+struct PDecode {
+  uint32_t msk;
+  f16x2 mul, add;
+  __device__ __forceinline__ explicit PDecode(int lg) {
+    if constexpr (QT == ARTLITE_Q4_0) {
+      const bool hi = lg >= 2;  // (lane groups 2, 3 hold K values 16 .. 31: the high nibbles)
+      msk = hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+      mul = hi ? f16x2{_Float16(0.0625f), _Float16(0.0625f)} : f16x2{_Float16(1.0f), _Float16(1.0f)};
+      add = hi ? f16x2{_Float16(-72.0f), _Float16(-72.0f)} : f16x2{_Float16(-1032.0f), _Float16(-1032.0f)};
+    } else {
+      msk = 0x80808080u;  // (Q8_0: the sign bits flipped, c = q + 128)
+      mul = f16x2{_Float16(1.0f), _Float16(1.0f)};
+      add = f16x2{_Float16(-1152.0f), _Float16(-1152.0f)};
+    }
   }
-  const int n0 = blockIdx.y * 128;
-  const int stages = a.K / 64;
+  __device__ __forceinline__ u32x4 operator()(const uint32_t (&cw)[2], uint32_t sc) const {
+    const uint32_t v0 = QT == ARTLITE_Q4_0 ? cw[0] & msk : cw[0] ^ msk;
+    const uint32_t v1 = QT == ARTLITE_Q4_0 ? cw[1] & msk : cw[1] ^ msk;
+    const uint32_t w[4] = {__builtin_amdgcn_perm(0x64646464u, v0, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, v0, 0x04030402u),
+                           __builtin_amdgcn_perm(0x64646464u, v1, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, v1, 0x04030402u)};
+    const f16x2 d = __builtin_bit_cast(f16x2, sc | (sc << 16));
+    u32x4 b;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const f16x2 c = __builtin_bit_cast(f16x2, w[j]) * mul + add;  // (exact: the code less its offset)
+      b[j] = __builtin_bit_cast(uint32_t, c * d);
+    }
+    return b;
+  }
+};
 
-  // chunk swizzle of row r: the 16 rows an operand read touches hit 16 different 16-byte bank slots
-  auto swz = [](int r) { return AP == 2 ? (r & 15) : ((r >> 1) & 7); };
-  // The lane's DMA sources. A: instruction i writes chunks (wv AI + i) 64 + lane of the stage's A region; chunk p
-  // holds row r = p / ACH, physical chunk c = p % ACH, which is logical chunk c ^ swz(r) (logical: plane c / 8, K
-  // values 8 (c % 8) .. + 8 of the stage).
-  const uint16_t* asrc[L::AI];
-#pragma unroll
-  for (int i = 0; i < L::AI; i++) {
-    const int p = (wv * L::AI + i) * 64 + lane, r = p / L::ACH, c = (p % L::ACH) ^ swz(r);
-    const int rr = min(r, m_valid - 1);  // (rows past the tile repeat its last: their outputs are not stored)
-    const int ar = a.a_gather ? a.order[s0 + rr] / a.topk : s0 + rr;
-    asrc[i] = (AP == 2 && c >= 8 ? a.a_lo : a.a_hi) + int64_t(ar) * a.K + 8 * (c % 8);
+__device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                 0);
+}
+
+// The items (tile, column block) of a launch, in tile-major order, dealt to the 8 XCDs in contiguous runs: workgroup
+// b runs on XCD b % 8 (the dispatcher's round robin), and the G = grid / 8 workgroups of an XCD take its run's items
+// in turn, so the column blocks of a tile, and the tiles of an expert, run close in time on one XCD and share its L2
+// (the tile's A rows, the expert's weights).
+struct PItem {
+  int e, s0, m_valid, n0;
+};
+
+template <bool SWIGLU>
+__device__ __forceinline__ PItem prefill_item(const PrefillArgs& a, int64_t w, int nbk) {
+  constexpr int WN = SWIGLU ? 128 : 256;
+  const int tl = int(w / nbk);
+  PItem I;
+  I.n0 = int(w % nbk) * WN;
+  if (a.tiles) {
+    I.e = a.tiles[2 * tl];
+    I.s0 = a.tiles[2 * tl + 1];
+    I.m_valid = min(PREFILL_BM, a.offsets[I.e + 1] - I.s0);
+  } else {
+    I.e = 0;
+    I.s0 = tl * PREFILL_BM;
+    I.m_valid = min(PREFILL_BM, a.dense_rows - I.s0);
   }
-  // weights: instruction j writes dwords (wv BI + j) 64 + lane of the stage's weight region, row q / DW (matrix-major,
-  // 128 rows each), dword q % DW of the row's stage bytes; dwords past the rows load the last one again (padding)
-  const uint8_t* wsrc[L::BI];
-#pragma unroll
-  for (int j = 0; j < L::BI; j++) {
-    const int q = min((wv * L::BI + j) * 64 + lane, L::WROWS * PStage<QT>::DW - 1);
-    const int row = q / PStage<QT>::DW, dw = q % PStage<QT>::DW;
-    const int mtx = NM == 2 ? row / 128 : 0, n = min(n0 + row % 128, a.N - 1);
-    wsrc[j] = a.w[mtx] + int64_t(e) * a.expert_bytes + int64_t(n) * a.row_bytes + 4 * dw;
+  return I;
+}
+
+// The lane's DMA sources of an item. A: instruction i writes chunks (wv AI + i) 64 + lane of a stage's A region;
+// chunk p holds row r = p / ACH, physical chunk c = p % ACH, which is logical chunk c ^ swz(r) (K values 8 c .. + 8
+// of the stage); rows past the tile repeat its last (their outputs are not stored). Weights: instruction j writes
+// dwords (wv BI + j) 64 + lane of the stage's weight region, staged row q / DW (SwiGLU: gate rows n0 .. + 128, then
+// up's; plain: rows n0 .. + 256), dword q % DW of the row's stage bytes; dwords past the rows load the last one
+// again (padding), rows past N the last row. Held as 32-bit offsets (A: elements from a.a; weights: bytes from the
+// instruction's matrix, which is uniform: 128 rows of gate are a whole number of instructions).
+template <int QT, bool SWIGLU>
+struct PSrc {
+  using L = PLayout<QT>;
+  static constexpr int GATE_INSTS = 128 * PStage<QT>::DW / 64;  // (SwiGLU: instructions of the gate rows)
+  static_assert(128 * PStage<QT>::DW % 64 == 0, "matrix-uniform weight instructions");
+  uint32_t a[L::AI];
+  uint32_t w[L::BI];
+  __device__ __forceinline__ static int swz(int r) { return (r >> 1) & 7; }
+  __device__ __forceinline__ static const uint8_t* wbase(const PrefillArgs& g, int wv, int j) {
+    return SWIGLU && wv * L::BI + j >= GATE_INSTS ? g.w[1] : g.w[0];
   }
+  __device__ __forceinline__ void set(const PrefillArgs& g, const PItem& I, int wv, int lane) {
+#pragma unroll
+    for (int i = 0; i < L::AI; i++) {
+      const int p = (wv * L::AI + i) * 64 + lane, r = p / L::ACH, c = (p % L::ACH) ^ swz(r);
+      const int s = I.s0 + min(r, I.m_valid - 1);
+      const int ar = g.a_gather ? (g.order ? g.order[s] / g.topk : s) : s;
+      a[i] = uint32_t(ar) * uint32_t(g.K) + 8 * c;
+    }
+#pragma unroll
+    for (int j = 0; j < L::BI; j++) {
+      const int q = min((wv * L::BI + j) * 64 + lane, L::WROWS * PStage<QT>::DW - 1);
+      const int row = q / PStage<QT>::DW, dw = q % PStage<QT>::DW;
+      const int n = min(I.n0 + (SWIGLU ? row % 128 : row), g.N - 1);
+      w[j] = uint32_t(I.e) * uint32_t(g.expert_bytes) + uint32_t(n) * uint32_t(g.row_bytes) + 4 * dw;
+    }
+  }
+};
+
+// The K loop of one item over MBN row blocks of A (the tile's rows, rounded up to 16-row blocks that hold any), in
+// the workgroup's continuous stream of stages: the item's stage st is global step g0 + st in ring slot
+// (g0 + st) % R; the R steps issued ahead reach into the next item's first stages (or, after the last item, load
+// stage 0 again). On entry cur holds group 0 of stage 0 (read from LDS); on exit, group 0 of the next item's stage 0.
+template <int QT, bool SWIGLU, int MBN>
+__device__ __forceinline__ void prefill_loop(const PrefillArgs& a, uint8_t* lds, int64_t g0, const PSrc<QT, SWIGLU>& src,
+                                             const PSrc<QT, SWIGLU>& nsrc, bool has_next, POps<8>& cur,
+                                             POps<8>& nxt, f32x4 (&acc)[8][2]) {
+  using F = Fmt<QT>;
+  using L = PLayout<QT>;
+  constexpr int R = L::R, ROW = PStage<QT>::ROW, GB = F::GROUP_BYTES;
+  const int lane = threadIdx.x & (WAVE - 1), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int lg = lane >> 4, lr = lane & 15;
+  const int stages = a.K / 64;
   const uint32_t lbase = pf_lds_addr(lds);
   const uint32_t adst = lbase + wv * L::AI * 1024, bdst = lbase + L::ABYTES + wv * L::BI * 256;
-  // the loads of stage j (past the last stage: stage 0 again) into ring slot j % R
+  auto slot = [&](int64_t g) { return uint32_t(g % R) * L::SBYTES; };
+  // the loads of the item's step j (j >= stages: the next item's stage j - stages, or stage 0 again)
   auto issue = [&](int j) {
-    const int st = j < stages ? j : 0;
-    const uint32_t so = (j % R) * L::SBYTES;
+    const uint32_t so = slot(g0 + j);
+    const bool nx = j >= stages && has_next;
+    const int st = j < stages ? j : nx ? j - stages : 0;
 #pragma unroll
-    for (int i = 0; i < L::AI; i++) pf_dma<16>(asrc[i] + 64 * st, adst + so + i * 1024);
+    for (int i = 0; i < L::AI; i++) pf_dma<16>(a.a + (nx ? nsrc.a[i] : src.a[i]) + 64 * st, adst + so + i * 1024);
 #pragma unroll
-    for (int i = 0; i < L::BI; i++) pf_dma<4>(wsrc[i] + st * ROW, bdst + so + i * 256);
+    for (int i = 0; i < L::BI; i++)
+      pf_dma<4>(PSrc<QT, SWIGLU>::wbase(a, wv, i) + (nx ? nsrc.w[i] : src.w[i]) + st * ROW, bdst + so + i * 256);
   };
-
-  // the lane's LDS read offsets in ring slot 0. A, row 64 wm + lr (row block mb at + 16 mb rows), group gl, plane pl:
-  // the chunk of K 8 lg .. + 8. B, row 32 wn + lr (+ the column block's rows): its block gl.
+  // the lane's LDS read offsets in a slot: A row lr (row block mb at + 16 mb rows), group gl: the chunk of K
+  // 8 lg .. + 8; B: the staged row of column block nb, its block gl
   constexpr int AMB = 16 * L::ACH * 16;
-  uint32_t aof[2][AP];
-  {
-    const int r = 64 * wm + lr, s = swz(r);
+  const uint32_t aof[2] = {uint32_t(lr * L::ACH * 16 + ((0 + lg) ^ PSrc<QT, SWIGLU>::swz(lr)) * 16),
+                           uint32_t(lr * L::ACH * 16 + ((4 + lg) ^ PSrc<QT, SWIGLU>::swz(lr)) * 16)};
+  const uint32_t bof[2] = {uint32_t(L::ABYTES + (SWIGLU ? 16 * wv + lr : 32 * wv + lr) * ROW),
+                           uint32_t(L::ABYTES + (SWIGLU ? 128 + 16 * wv + lr : 32 * wv + 16 + lr) * ROW)};
+  // the code bytes of lane group lg at the block + 2 + cb: Q4_0 bytes 8 (lg & 1) .. + 8 (lane groups 0, 1 take the
+  // low nibbles, 2, 3 the high ones), Q8_0 bytes 8 lg .. + 8
+  const int cb = QT == ARTLITE_Q4_0 ? 8 * (lg & 1) : 8 * lg;
+  auto read = [&](POps<8>& o, uint32_t so, int gl, auto nr) {
 #pragma unroll
-    for (int gl = 0; gl < 2; gl++)
+    for (int mb = 0; mb < decltype(nr)::value; mb++)
+      o.a[mb] = *reinterpret_cast<const u32x4*>(lds + so + aof[gl] + mb * AMB);
 #pragma unroll
-      for (int pl = 0; pl < AP; pl++) aof[gl][pl] = r * L::ACH * 16 + ((8 * pl + 4 * gl + lg) ^ s) * 16;
-  }
-  const uint32_t bof = L::ABYTES + (32 * wn + lr) * ROW;
-  const int sh = 4 * (lg >> 1);  // (Q4_0: the nibble half of lane group lg)
-  auto brow = [](int nb) { return (nb / 2) * 128 + 16 * (nb % 2); };
-
-  auto read = [&](POps<QT, NB, AP>& o, uint32_t so, int gl) {
-#pragma unroll
-    for (int mb = 0; mb < MB; mb++)
-#pragma unroll
-      for (int pl = 0; pl < AP; pl++) {
-        o.a[mb][pl] = *reinterpret_cast<const u32x4*>(lds + so + aof[gl][pl] + mb * AMB);
-      }
-#pragma unroll
-    for (int nb = 0; nb < NB; nb++) {
-      const uint8_t* b = lds + so + bof + brow(nb) * ROW + gl * GB;  // (4-byte aligned: gl GB is 0 or 2 mod 4)
+    for (int nb = 0; nb < 2; nb++) {
+      const uint8_t* b = lds + so + bof[nb] + gl * GB;  // (4-byte aligned: gl GB is 0 or 2 mod 4)
       o.sc[nb] = *reinterpret_cast<const uint16_t*>(b);
-      // the 8 code bytes at b + 2 + CB: Q4_0 bytes 8 (lg & 1) .. + 8 (of which lane group lg takes the low nibbles
-      // for lg < 2, else the high ones), Q8_0 bytes 8 lg .. + 8
-      const int cb = QT == ARTLITE_Q4_0 ? 8 * (lg & 1) : 8 * lg;
       if (gl == 0) {
         const uint32_t* d = reinterpret_cast<const uint32_t*>(b + cb);
         const uint32_t d0 = d[0], d1 = d[1], d2 = d[2];
@@ -501,135 +573,273 @@ __global__ __launch_bounds__(512) void k_gemm_prefill(const GemmArgs a) {
       }
     }
   };
-
-  // the -OFF operand of the group sums (bf16, exact)
-  const uint32_t noff = f32_to_bf16(-F::OFF) * 0x10001u;
-  const u32x4 bneg = {noff, noff, noff, noff};
-  f32x4 acc[MB][NB];
+  const PDecode<QT> dec(lg);
+  auto compute = [&](const POps<8>& o) {
 #pragma unroll
-  for (int mb = 0; mb < MB; mb++)
+    for (int nb = 0; nb < 2; nb++) {
+      const u32x4 b = dec(o.cw[nb], o.sc[nb]);
 #pragma unroll
-    for (int nb = 0; nb < NB; nb++) acc[mb][nb] = f32x4{0, 0, 0, 0};
-  // One group's products: the -OFF group sums (MFMAs against bneg) with the B operands decoded between them, then
-  // the MB x NB products, each followed by the scale FMAs of the product two before it (the MFMA result's latency),
-  // as sched_group_barrier orders them.
-  auto compute = [&](const POps<QT, NB, AP>& o) {
-    f32x4 cin[MB];
-#pragma unroll
-    for (int mb = 0; mb < MB; mb++) {
-      cin[mb] = mfma(o.a[mb][0], bneg, f32x4{0, 0, 0, 0});
-      if (AP == 2) cin[mb] = mfma(o.a[mb][AP - 1], bneg, cin[mb]);
+      for (int mb = 0; mb < MBN; mb++) acc[mb][nb] = mfma16(o.a[mb], b, acc[mb][nb]);
     }
-    u32x4 b[NB];
-    float d[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; nb++) {
-      if constexpr (QT == ARTLITE_Q4_0)
-        b[nb] = nib8((o.cw[nb][0] >> sh) & 0x0F0F0F0Fu, (o.cw[nb][1] >> sh) & 0x0F0F0F0Fu);
-      else
-        b[nb] = byte8(o.cw[nb][0] ^ 0x80808080u, o.cw[nb][1] ^ 0x80808080u);
-      d[nb] = h2f(o.sc[nb]);
-    }
-    f32x4 p[NB][MB];
-#pragma unroll
-    for (int nb = 0; nb < NB; nb++)
-#pragma unroll
-      for (int mb = 0; mb < MB; mb++) {
-        p[nb][mb] = mfma(o.a[mb][0], b[nb], cin[mb]);
-        if (AP == 2) p[nb][mb] = mfma(o.a[mb][AP - 1], b[nb], p[nb][mb]);
-      }
-#pragma unroll
-    for (int nb = 0; nb < NB; nb++)
-#pragma unroll
-      for (int mb = 0; mb < MB; mb++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) acc[mb][nb][i] = __builtin_fmaf(d[nb], p[nb][mb][i], acc[mb][nb][i]);
-    constexpr int DEC = QT == ARTLITE_Q4_0 ? 7 : 18;  // decode VALU per column block (about)
-#pragma unroll
-    for (int mb = 0; mb < MB * AP; mb++) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, (DEC * NB + MB * AP - 1) / (MB * AP), 0);
-    }
-#pragma unroll
-    for (int t = 0; t < MB * NB; t++) {
-      __builtin_amdgcn_sched_group_barrier(0x008, AP, 0);
-      if (t >= 2) __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
   };
-  // waves whose 64 rows of A are all past the tile skip the products (rows past it otherwise repeat its last row)
-  const bool active = 64 * wm < m_valid;
-
-  POps<QT, NB, AP> cur, nxt;
-#pragma unroll
-  for (int j = 0; j < R; j++) issue(j);
-  pf_wait<(R - 1) * L::LOADS>();  // (stage 0: R - 1 stages issued after it)
-  pf_barrier();
-  if (active) read(cur, 0, 0);
-  for (int st = 0; st < stages; st++) {
-    const uint32_t so = (st % R) * L::SBYTES;
-    if (active) {
-      read(nxt, so, 1);
-      compute(cur);
-    }
-    if (st + 1 < stages) {
-      pf_wait<(R - 2) * L::LOADS>();  // (stage st + 1: stages up to st + R - 1 issued)
-      pf_barrier();
-      issue(st + R);  // (into the slot of stage st, whose operands every wave holds in registers)
-      if (active) read(cur, ((st + 1) % R) * L::SBYTES, 0);
-    }
-    if (active) compute(nxt);
+  using NR = std::integral_constant<int, MBN>;
+  using N8 = std::integral_constant<int, 8>;
+  for (int st = 0; st + 1 < stages; st++) {
+    read(nxt, slot(g0 + st), 1, NR{});
+    compute(cur);
+    pf_wait<(R - 2) * L::LOADS>();  // (step g0 + st + 1: steps up to g0 + st + R - 1 issued)
+    pf_barrier();
+    issue(st + R);  // (into the slot of step g0 + st, whose operands every wave holds in registers)
+    read(cur, slot(g0 + st + 1), 0, NR{});
+    compute(nxt);
   }
-  pf_wait<0>();  // (the loads past the last stage land before the workgroup's LDS is released)
+  read(nxt, slot(g0 + stages - 1), 1, NR{});
+  compute(cur);
+  pf_wait<(R - 2) * L::LOADS>();
+  pf_barrier();
+  issue(stages - 1 + R);
+  // (the next item's first group: all 8 row blocks, whatever its rows; after the last item, data not used)
+  read(cur, slot(g0 + stages), 0, N8{});
+  compute(nxt);
+}
 
-  // epilogue: lane output i of block (mb, nb): row of A 64 wm + 16 mb + 4 lg + i, weight row n0 + 32 wn + 16 (nb % 2)
-  // + lr of matrix nb / 2
+template <int QT, bool SWIGLU>
+__global__ __launch_bounds__(512) void k_prefill(const PrefillArgs a) {
+  using L = PLayout<QT>;
+  constexpr int R = L::R;
+  constexpr int WN = SWIGLU ? 128 : 256;  // output columns per item
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  float2* rowf = reinterpret_cast<float2*>(lds + R * L::SBYTES);  // per row of an item: (2^in_exp, 2^-out_exp), x 2
+  const int lane = threadIdx.x & (WAVE - 1), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int lg = lane >> 4, lr = lane & 15;
+  const int nbk = (a.N + WN - 1) / WN, stages = a.K / 64;
+  const int64_t ntl = a.tiles ? int64_t(*a.n_tiles) : (a.dense_rows + PREFILL_BM - 1) / PREFILL_BM;
+  const int64_t items = ntl * nbk, per = (items + 7) / 8;
+  const int G = gridDim.x / 8, x = blockIdx.x % 8, j0 = blockIdx.x / 8;
+  const int64_t first = x * per + j0, end = min(items, (x + 1) * per);
+  if (first >= end) return;
+  const int nq = int((end - first + G - 1) / G);  // this workgroup's items: first + q G
+  // the row scales of item I into buffer b
+  auto row_info = [&](const PItem& I, int b) {
+    if (threadIdx.x < PREFILL_BM) {
+      const int m = threadIdx.x;
+      float2 f = {1.0f, 1.0f};
+      if (m < I.m_valid) {
+        const int s = I.s0 + m, t = a.order ? a.order[s] / a.topk : s;
+        f.x = __builtin_ldexpf(1.0f, a.in_exp[t]);
+        if (SWIGLU) f.y = __builtin_ldexpf(1.0f, -a.out_exp[t]);
+      }
+      rowf[b * PREFILL_BM + m] = f;
+    }
+  };
+
+  PItem I = prefill_item<SWIGLU>(a, first, nbk);
+  PSrc<QT, SWIGLU> src, nsrc;
+  src.set(a, I, wv, lane);
+  row_info(I, 0);
+  // the first item's first R stages, then its stage 0 read
+  {
+    const uint32_t lbase = pf_lds_addr(lds);
+    const uint32_t adst = lbase + wv * L::AI * 1024, bdst = lbase + L::ABYTES + wv * L::BI * 256;
 #pragma unroll
-  for (int mb = 0; mb < MB; mb++) {
+    for (int j = 0; j < R; j++) {
+      const int st = j < stages ? j : 0;
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int n = n0 + 32 * wn + 16 * j + lr;
-      if (n >= a.N) continue;
+      for (int i = 0; i < L::AI; i++) pf_dma<16>(a.a + src.a[i] + 64 * st, adst + j * L::SBYTES + i * 1024);
+#pragma unroll
+      for (int i = 0; i < L::BI; i++)
+        pf_dma<4>(PSrc<QT, SWIGLU>::wbase(a, wv, i) + src.w[i] + st * PStage<QT>::ROW, bdst + j * L::SBYTES + i * 256);
+    }
+  }
+  pf_wait<(R - 1) * L::LOADS>();  // (stage 0: R - 1 stages issued after it)
+  __syncthreads();                // (and the row scales)
+  POps<8> cur, nxt;
+  {
+    using F = Fmt<QT>;
+    constexpr int AMB = 16 * L::ACH * 16, ROW = PStage<QT>::ROW;
+    const uint32_t aof0 = uint32_t(lr * L::ACH * 16 + (lg ^ PSrc<QT, SWIGLU>::swz(lr)) * 16);
+#pragma unroll
+    for (int mb = 0; mb < 8; mb++) cur.a[mb] = *reinterpret_cast<const u32x4*>(lds + aof0 + mb * AMB);
+    const int cb = QT == ARTLITE_Q4_0 ? 8 * (lg & 1) : 8 * lg;
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) {
+      const uint8_t* b = lds + L::ABYTES + (SWIGLU ? 128 * nb + 16 * wv + lr : 32 * wv + 16 * nb + lr) * ROW;
+      cur.sc[nb] = *reinterpret_cast<const uint16_t*>(b);
+      const uint32_t* d = reinterpret_cast<const uint32_t*>(b + cb);
+      cur.cw[nb][0] = __builtin_amdgcn_alignbit(d[1], d[0], 16);
+      cur.cw[nb][1] = __builtin_amdgcn_alignbit(d[2], d[1], 16);
+      (void)F::OFF;
+    }
+  }
+
+  for (int q = 0; q < nq; q++) {
+    const bool has_next = q + 1 < nq;
+    PItem J{};
+    if (has_next) {
+      J = prefill_item<SWIGLU>(a, first + int64_t(q + 1) * G, nbk);
+      nsrc.set(a, J, wv, lane);
+      row_info(J, (q + 1) & 1);  // (read after this item's barriers)
+    }
+    f32x4 acc[8][2];
+#pragma unroll
+    for (int mb = 0; mb < 8; mb++) acc[mb][0] = acc[mb][1] = f32x4{0, 0, 0, 0};
+    const int64_t g0 = int64_t(q) * stages;
+    const int mbn = (I.m_valid + 15) / 16;
+    if (mbn <= 2)
+      prefill_loop<QT, SWIGLU, 2>(a, lds, g0, src, nsrc, has_next, cur, nxt, acc);
+    else if (mbn <= 4)
+      prefill_loop<QT, SWIGLU, 4>(a, lds, g0, src, nsrc, has_next, cur, nxt, acc);
+    else
+      prefill_loop<QT, SWIGLU, 8>(a, lds, g0, src, nsrc, has_next, cur, nxt, acc);
+
+    // epilogue: lane output i of block (mb, nb): row 16 mb + 4 lg + i of the tile; column (SwiGLU) n0 + 16 wv + lr
+    // of gate (nb 0) and up (nb 1), (plain) n0 + 32 wv + 16 nb + lr
+    const float2* rf = rowf + (q & 1) * PREFILL_BM;
+#pragma unroll
+    for (int mb = 0; mb < 8; mb++) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const int m = 64 * wm + 16 * mb + 4 * lg + i;
-        if (m >= m_valid) continue;
-        const int64_t o = int64_t(s0 + m) * a.N + n;
+        const int m = 16 * mb + 4 * lg + i;
+        if (m >= I.m_valid) continue;
+        const int64_t o = int64_t(I.s0 + m) * a.N;
+        const float2 f = rf[m];
         if constexpr (SWIGLU) {
-          const float g = acc[mb][j][i], u = acc[mb][2 + j][i];
+          const int n = I.n0 + 16 * wv + lr;
+          if (n >= a.N) continue;
+          const float g = acc[mb][0][i] * f.x, u = acc[mb][1][i] * f.x;
           const float h = g / (1.0f + expf(-g)) * u;
-          const uint32_t hi = f32_to_bf16(h);
-          a.h_hi[o] = uint16_t(hi);
-          a.h_lo[o] = uint16_t(f32_to_bf16(h - bf16_to_f32(hi)));
+          a.h[o + n] = __builtin_bit_cast(uint16_t, _Float16(h * f.y));
         } else {
-          a.y[o] = acc[mb][j][i];
+#pragma unroll
+          for (int nb = 0; nb < 2; nb++) {
+            const int n = I.n0 + 32 * wv + 16 * nb + lr;
+            if (n < a.N) a.y[o + n] = acc[mb][nb][i] * f.x;
+          }
         }
       }
     }
+    I = J;
+    src = nsrc;
   }
+  pf_wait<0>();  // (the loads past the last stage land before the workgroup's LDS is released)
 }
 
-template <int QT, bool SWIGLU, int AP>
-int launch_prefill_ap(const GemmArgs& a, hipStream_t s) {
-  using L = PLayout<QT, SWIGLU, AP>;
+template <int QT, bool SWIGLU>
+int launch_prefill_t(const PrefillArgs& a, hipStream_t s) {
+  using L = PLayout<QT>;
   const int64_t tiles = a.tiles ? a.max_tiles : (a.dense_rows + PREFILL_BM - 1) / PREFILL_BM;
-  const dim3 grid(unsigned(tiles), unsigned((a.N + 127) / 128)), block(L::THREADS);
-  constexpr size_t lds = size_t(L::R) * L::SBYTES;
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_prefill<QT, SWIGLU, AP>),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
-  ART_HIP(attr);
-  k_gemm_prefill<QT, SWIGLU, AP><<<grid, block, lds, s>>>(a);
+  const int64_t items = tiles * ((a.N + (SWIGLU ? 127 : 255)) / (SWIGLU ? 128 : 256));
+  if (items <= 0) return ARTLITE_OK;
+  if (items >= (int64_t(1) << 31)) return fail(ARTLITE_EINVAL, "prefill GEMM: %lld work items", (long long)items);
+  if (a.K / 64 < L::R) return fail(ARTLITE_EINVAL, "prefill GEMM: K %d below %d", a.K, 64 * L::R);
+  constexpr size_t lds = size_t(L::R) * L::SBYTES + 2 * PREFILL_BM * 8;
+  // persistent workgroups: as many as the device holds at once (a multiple of 8, the XCDs), at most the items
+  static const int resident = [] {
+    const void* f = reinterpret_cast<const void*>(k_prefill<QT, SWIGLU>);
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess ||
+        hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, L::THREADS, lds) != hipSuccess)
+      return 0;
+    return cus * std::max(1, per_cu);
+  }();
+  if (resident < 8) return fail(ARTLITE_EHIP, "prefill GEMM: kernel set-up failed");
+  const unsigned grid = unsigned(std::min<int64_t>((items + 7) / 8 * 8, resident / 8 * 8));
+  k_prefill<QT, SWIGLU><<<grid, L::THREADS, lds, s>>>(a);
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
 }
 
-template <int QT, bool SWIGLU>
-int launch_prefill(const GemmArgs& a, hipStream_t s) {
-  return a.a_lo ? launch_prefill_ap<QT, SWIGLU, 2>(a, s) : launch_prefill_ap<QT, SWIGLU, 1>(a, s);
+bool prefill_supported(int qtype, int K, int N) {
+  const int r = qtype == ARTLITE_Q4_0 ? PLayout<ARTLITE_Q4_0>::R : PLayout<ARTLITE_Q8_0>::R;
+  return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0) && K >= 64 * r && K % 64 == 0 && N > 0 && N % 16 == 0;
 }
 
-bool prefill_supported(int qtype, int K, int N) {
-  return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0) && K > 0 && K % 64 == 0 && N > 0 && N % 128 == 0;
+int launch_prefill(const PrefillArgs& a, hipStream_t s) {
+  if (!prefill_supported(a.qtype, a.K, a.N))
+    return fail(ARTLITE_EINVAL, "prefill GEMM: weight type %d, K %d, N %d", a.qtype, a.K, a.N);
+  if (!a.a || !a.in_exp || (a.w[1] ? !a.h || !a.out_exp : !a.y) || (a.tiles && (!a.n_tiles || !a.offsets)))
+    return fail(ARTLITE_EINVAL, "prefill GEMM: null argument");
+  const bool swiglu = a.w[1] != nullptr;
+  if (a.qtype == ARTLITE_Q4_0) return swiglu ? launch_prefill_t<ARTLITE_Q4_0, true>(a, s) : launch_prefill_t<ARTLITE_Q4_0, false>(a, s);
+  return swiglu ? launch_prefill_t<ARTLITE_Q8_0, true>(a, s) : launch_prefill_t<ARTLITE_Q8_0, false>(a, s);
+}
+
+// ---- the prefill's activations: per token t, x's row in fp16 scaled by 2^-x_exp[t] (its largest |x| into
+// [2^14, 2^15); exact for bf16 x unless below 2^-14 of that), and the exponents h_exp[t] of h's scale: the bound
+// B = 2 (sum |x|)^2 (max |w_gate|) (max |w_up|) >= |silu(g) u| >= |h| (|g| <= sum |x| max |w_gate|, |silu(g)| <=
+// |g|), h_exp = ilogb(B) - 14, so |h| 2^-h_exp < 2^15 (fp16 holds it). wmax[j]: max |w| of the bound's two matrices
+// (pair j: wmax[2 j], wmax[2 j + 1]). One workgroup per token.
+__global__ __launch_bounds__(256) void k_prefill_x(const void* __restrict__ x, int x_dtype, int H,
+                                                   const float* __restrict__ wmax, int pairs,
+                                                   uint16_t* __restrict__ x16, int32_t* __restrict__ x_exp,
+                                                   int32_t* __restrict__ h_exp, int32_t* __restrict__ h_exp2) {
+  __shared__ float red[2][8];
+  const int64_t t = blockIdx.x;
+  auto at = [&](int i) -> float {
+    return x_dtype == ARTLITE_X_F32 ? static_cast<const float*>(x)[t * H + i]
+                                    : bf16_to_f32(static_cast<const uint16_t*>(x)[t * H + i]);
+  };
+  float mx = 0.0f, l1 = 0.0f;
+  for (int i = threadIdx.x; i < H; i += 256) {
+    const float v = fabsf(at(i));
+    mx = fmaxf(mx, v);
+    l1 += v;
+  }
+  for (int o = 32; o; o >>= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, o));
+    l1 += __shfl_xor(l1, o);
+  }
+  if ((threadIdx.x & 63) == 0) red[0][threadIdx.x / 64] = mx, red[1][threadIdx.x / 64] = l1;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+  l1 = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+  const int xe = (mx > 0.0f && mx <= 3.4e38f) ? ilogbf(mx) - 14 : 0;
+  for (int i = threadIdx.x; i < H; i += 256)
+    x16[t * H + i] = __builtin_bit_cast(uint16_t, _Float16(__builtin_ldexpf(at(i), -xe)));
+  if (threadIdx.x < pairs) {
+    // (in double: the square of a large sum stays finite)
+    const double b = 2.0 * double(l1) * double(l1) * double(wmax[2 * threadIdx.x]) * double(wmax[2 * threadIdx.x + 1]);
+    const int he = (b > 0.0 && b < 1e300) ? ilogb(b) - 14 : 0;
+    (threadIdx.x ? h_exp2 : h_exp)[t] = max(-126, min(126, he));
+  }
+  if (threadIdx.x == 0) x_exp[t] = xe;
+}
+
+int launch_prefill_x(const void* x, int x_dtype, int64_t T, int H, const float* wmax, int pairs, uint16_t* x16,
+                     int32_t* x_exp, int32_t* h_exp, int32_t* h_exp2, hipStream_t s) {
+  if (T <= 0) return ARTLITE_OK;
+  if (pairs < 1 || pairs > 2 || (pairs == 2 && !h_exp2)) return fail(ARTLITE_EINVAL, "prefill x: %d bounds", pairs);
+  k_prefill_x<<<unsigned(T), 256, 0, s>>>(x, x_dtype, H, wmax, pairs, x16, x_exp, h_exp, h_exp2);
+  ART_HIP(hipGetLastError());
+  return ARTLITE_OK;
+}
+
+// ---- max |w| of a weight tensor's blocks: the fp16 scale's magnitude times the format's largest code (Q4_0: 8,
+// Q8_0: 128), by an atomic max on the float's bits (non-negative floats order as their bits)
+__global__ void k_weight_max(const uint8_t* __restrict__ w, int block_bytes, float code_max, int64_t nblocks,
+                             uint32_t* __restrict__ out) {
+  float mx = 0.0f;
+  for (int64_t b = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; b < nblocks; b += int64_t(gridDim.x) * blockDim.x) {
+    uint16_t d;
+    __builtin_memcpy(&d, w + b * block_bytes, 2);
+    mx = fmaxf(mx, fabsf(f16_to_f32(d)));
+  }
+  for (int o = 32; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((threadIdx.x & 63) == 0) atomicMax(out, __float_as_uint(mx * code_max));
+}
+
+int launch_weight_max(const uint8_t* w, int qtype, int64_t nblocks, float* out, hipStream_t s) {
+  if (qtype != ARTLITE_Q4_0 && qtype != ARTLITE_Q8_0) return fail(ARTLITE_EINVAL, "weight max: type %d", qtype);
+  ART_HIP(hipMemsetAsync(out, 0, 4, s));
+  if (nblocks <= 0) return ARTLITE_OK;
+  const int bb = qtype == ARTLITE_Q4_0 ? 18 : 34;
+  const unsigned grid = unsigned(std::min<int64_t>((nblocks + 255) / 256, 1024));
+  k_weight_max<<<grid, 256, 0, s>>>(w, bb, qtype == ARTLITE_Q4_0 ? 8.0f : 128.0f, nblocks,
+                                    reinterpret_cast<uint32_t*>(out));
+  ART_HIP(hipGetLastError());
+  return ARTLITE_OK;
 }
 
 int launch_expert_gemm(const GemmArgs& a, hipStream_t s) {
@@ -637,17 +847,6 @@ int launch_expert_gemm(const GemmArgs& a, hipStream_t s) {
     return fail(ARTLITE_EINVAL, "expert GEMM: K %d is not a multiple of the format's block", a.K);
   if (a.K / 32 > MAX_GROUPS) return fail(ARTLITE_EINVAL, "expert GEMM: K %d beyond %d", a.K, 32 * MAX_GROUPS);
   const bool swiglu = a.w[1] != nullptr;
-  // tiles of PREFILL_BM rows (a tile list made for them, or dense rows enough to fill them): the prefill tiling
-  const bool pre = a.tiles ? a.bm == PREFILL_BM
-                            : a.dense_rows >= PREFILL_BM / 2 && prefill_supported(a.qtype, a.K, a.N);
-  if (pre) {
-    if (!prefill_supported(a.qtype, a.K, a.N))
-      return fail(ARTLITE_EINVAL, "expert GEMM: prefill tiles of weight type %d, K %d, N %d", a.qtype, a.K, a.N);
-    const int64_t tiles = a.tiles ? a.max_tiles : (a.dense_rows + PREFILL_BM - 1) / PREFILL_BM;
-    if (tiles <= 0) return ARTLITE_OK;
-    if (a.qtype == ARTLITE_Q4_0) return swiglu ? launch_prefill<ARTLITE_Q4_0, true>(a, s) : launch_prefill<ARTLITE_Q4_0, false>(a, s);
-    return swiglu ? launch_prefill<ARTLITE_Q8_0, true>(a, s) : launch_prefill<ARTLITE_Q8_0, false>(a, s);
-  }
   if (a.tiles && a.bm != DECODE_BM) return fail(ARTLITE_EINVAL, "expert GEMM: tiles of %d rows", a.bm);
   const int64_t tiles = a.tiles ? a.max_tiles : (a.dense_rows + DECODE_BM - 1) / DECODE_BM;
   if (tiles <= 0) return ARTLITE_OK;

@@ -2,6 +2,7 @@
 // forward pass on one HIP stream: router -> top k -> dispatch -> gate / up (SwiGLU) -> down -> combine, plus the
 // shared expert. The semantics are the reference's oracle (tests/moe/ref.py:43-60) with its routing
 // (csrc/artlite/moe_host.cpp:45-73) and combine (src/artlite/moe/gather.py:12-18).
+#include <cmath>
 #include <string>
 #include <vector>
 
@@ -23,13 +24,16 @@ struct artlite_moe_layer {
   int x_dtype = ARTLITE_X_BF16;
   int64_t staged = -1;  // tokens staged, -1: none
   DevBuf x, xhi, xlo;
+  DevBuf x16, xexp, hexp, shexp;  // the prefill's fp16 activations and their per-token scale exponents
+  DevBuf wmax;                    // max |w| of gate, up, shared gate, shared up (the bound on |h|)
   DevBuf logits, ids, w, sg;
   DevBuf table, ctrl, counts, offsets, order, slot, tiles;
   DevBuf hhi, hlo, ypairs, shhi, shlo, ys, y;
+  DevBuf h16, sh16;  // the prefill's h (fp16, scaled per token)
   DevBuf xq, hq, shq;  // the decode path's XQ activations
-  bool gemv_ok = false, shared_gemv_ok = false, prefill_ok = false;
+  bool gemv_ok = false, shared_gemv_ok = false, prefill_ok = false, shared_prefill_ok = false;
   int64_t last_T = -1;
-  bool last_gemv = false;
+  bool last_gemv = false, last_prefill = false;
 };
 
 namespace {
@@ -80,26 +84,29 @@ int check_ready(const artlite_moe_layer* L) {
 }
 
 // The kernels a forward pass of T tokens takes. Decode-sized passes (at most GEMV_BM pairs per expert on
-// average) run the experts on the VALU GEMV over XQ activations; larger ones on the MFMA tiles over bf16 planes.
+// average) run the experts on the VALU GEMV over XQ activations; prefill-sized ones (16 pairs per expert on
+// average, enough to fill PREFILL_BM tiles) on the fp16 MFMA prefill tiles; those between on the MFMA decode tiles
+// over bf16 planes.
 struct Path {
-  bool gemv;         // routed experts on the GEMV
-  bool shared_gemv;  // the shared expert on the GEMV
-  bool split;        // bf16 hi / lo planes of fp32 x needed
-  bool quant;        // XQ of x needed (made by the router's launch)
-  bool small;        // top k and dispatch in one workgroup
-  bool prefill;      // routed experts on the MFMA prefill tiling (else the MFMA decode tiling, or the GEMV)
+  bool gemv;            // routed experts on the GEMV
+  bool shared_gemv;     // the shared expert on the GEMV
+  bool prefill;         // routed experts on the prefill tiles
+  bool shared_prefill;  // the shared expert on the prefill tiles
+  bool split;           // bf16 hi / lo planes of fp32 x needed (the MFMA decode tiles)
+  bool quant;           // XQ of x needed (made by the router's launch)
+  bool small;           // top k and dispatch in one workgroup
 };
 
 Path path_of(const artlite_moe_layer* L, int64_t T) {
   Path p{};
   p.gemv = L->gemv_ok && T * L->d.top_k <= int64_t(GEMV_BM) * L->d.n_experts;
   p.shared_gemv = L->d.shared_ffn && p.gemv && L->shared_gemv_ok;
-  const bool mfma_x = !p.gemv || (L->d.shared_ffn && !p.shared_gemv);
-  p.split = mfma_x && L->x_dtype == ARTLITE_X_F32;
+  p.prefill = !p.gemv && L->prefill_ok && T * L->d.top_k >= int64_t(16) * L->d.n_experts;
+  p.shared_prefill = L->d.shared_ffn && p.prefill && L->shared_prefill_ok && T >= PREFILL_BM / 2;
+  const bool planes = (!p.gemv && !p.prefill) || (L->d.shared_ffn && !p.shared_gemv && !p.shared_prefill);
+  p.split = planes && L->x_dtype == ARTLITE_X_F32;
   p.quant = p.gemv;
   p.small = p.gemv && T * L->d.top_k <= DISPATCH_BLOCK && L->d.n_experts <= MAX_EXPERTS;
-  // (16 rows per expert on average fill enough of a PREFILL_BM tile)
-  p.prefill = !p.gemv && L->prefill_ok && T * L->d.top_k >= int64_t(16) * L->d.n_experts;
   return p;
 }
 
@@ -107,6 +114,7 @@ Path path_of(const artlite_moe_layer* L, int64_t T) {
 std::vector<std::string> kernel_list(const artlite_moe_layer* L, int64_t T) {
   const Path p = path_of(L, T);
   std::vector<std::string> k;
+  if (p.prefill) k.push_back("prefill_x");
   if (p.split) k.push_back("split");
   k.push_back(p.quant ? "router_quant" : "router");
   if (L->d.shared_ffn && L->d.shared_gated) k.push_back("shared_gate");
@@ -141,6 +149,12 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
   };
   const Path path = path_of(L, T);
   const uint16_t *ahi = L->x.as<uint16_t>(), *alo = nullptr;
+  if (path.prefill) {
+    ART_TRY(mark());
+    ART_TRY(launch_prefill_x(L->x.p, L->x_dtype, T, H, L->wmax.as<float>(), path.shared_prefill ? 2 : 1,
+                             L->x16.as<uint16_t>(), L->xexp.as<int32_t>(), L->hexp.as<int32_t>(),
+                             L->shexp.as<int32_t>(), s));
+  }
   if (path.split) {
     ART_TRY(mark());
     ART_TRY(launch_split(L->x.as<float>(), T * H, L->xhi.as<uint16_t>(), L->xlo.as<uint16_t>(), s));
@@ -207,6 +221,44 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     dn.y = L->ypairs.as<float>();
     ART_TRY(mark());
     ART_TRY(launch_gemv(dn, s));
+  } else if (path.prefill) {
+    PrefillArgs g{};
+    g.w[0] = L->gate.as<uint8_t>();
+    g.w[1] = L->up.as<uint8_t>();
+    g.expert_bytes = int64_t(F) * L->gate_row;
+    g.row_bytes = int(L->gate_row);
+    g.N = F;
+    g.K = H;
+    g.qtype = d.gate_type;
+    g.a = L->x16.as<uint16_t>();
+    g.a_gather = 1;
+    g.order = L->order.as<int32_t>();
+    g.topk = k;
+    g.tiles = L->tiles.as<int32_t>();
+    g.n_tiles = L->ctrl.as<int32_t>() + CTRL_TILES;
+    g.offsets = L->offsets.as<int32_t>();
+    g.max_tiles = tile_bound(P, E, BM);
+    g.in_exp = L->xexp.as<int32_t>();
+    g.out_exp = L->hexp.as<int32_t>();
+    g.h = L->h16.as<uint16_t>();
+    ART_TRY(mark());
+    ART_TRY(launch_prefill(g, s));
+    PrefillArgs dn = g;
+    dn.w[0] = L->down.as<uint8_t>();
+    dn.w[1] = nullptr;
+    dn.expert_bytes = int64_t(H) * L->down_row;
+    dn.row_bytes = int(L->down_row);
+    dn.N = H;
+    dn.K = F;
+    dn.qtype = d.down_type;
+    dn.a = L->h16.as<uint16_t>();
+    dn.a_gather = 0;
+    dn.in_exp = L->hexp.as<int32_t>();
+    dn.out_exp = nullptr;
+    dn.h = nullptr;
+    dn.y = L->ypairs.as<float>();
+    ART_TRY(mark());
+    ART_TRY(launch_prefill(dn, s));
   } else {
     GemmArgs g{};
     g.w[0] = L->gate.as<uint8_t>();
@@ -271,6 +323,36 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     ART_TRY(mark());
     ART_TRY(launch_gemv(sd, s));
     ys = L->ys.as<float>();
+  } else if (d.shared_ffn && path.shared_prefill) {
+    PrefillArgs sg{};
+    sg.w[0] = L->sgate.as<uint8_t>();
+    sg.w[1] = L->sup.as<uint8_t>();
+    sg.row_bytes = int(L->sgate_row);
+    sg.N = d.shared_ffn;
+    sg.K = H;
+    sg.qtype = d.shared_type;
+    sg.a = L->x16.as<uint16_t>();
+    sg.dense_rows = int(T);
+    sg.in_exp = L->xexp.as<int32_t>();
+    sg.out_exp = L->shexp.as<int32_t>();
+    sg.h = L->sh16.as<uint16_t>();
+    ART_TRY(mark());
+    ART_TRY(launch_prefill(sg, s));
+    PrefillArgs sd = sg;
+    sd.w[0] = L->sdown.as<uint8_t>();
+    sd.w[1] = nullptr;
+    sd.row_bytes = int(L->sdown_row);
+    sd.N = H;
+    sd.K = d.shared_ffn;
+    sd.qtype = d.shared_type;
+    sd.a = L->sh16.as<uint16_t>();
+    sd.in_exp = L->shexp.as<int32_t>();
+    sd.out_exp = nullptr;
+    sd.h = nullptr;
+    sd.y = L->ys.as<float>();
+    ART_TRY(mark());
+    ART_TRY(launch_prefill(sd, s));
+    ys = L->ys.as<float>();
   } else if (d.shared_ffn) {
     GemmArgs sg{};
     sg.w[0] = L->sgate.as<uint8_t>();
@@ -306,6 +388,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
   ART_TRY(mark());
   L->last_T = T;
   L->last_gemv = path.gemv;
+  L->last_prefill = path.prefill;
   return ARTLITE_OK;
 }
 
@@ -352,6 +435,8 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
                   prefill_supported(d.down_type, d.expert_ffn, d.hidden);
   L->shared_gemv_ok = sq && gemv_supported(d.shared_type, d.hidden, d.shared_ffn) &&
                       gemv_supported(d.shared_type, d.shared_ffn, d.hidden);
+  L->shared_prefill_ok = sq && prefill_supported(d.shared_type, d.hidden, d.shared_ffn) &&
+                         prefill_supported(d.shared_type, d.shared_ffn, d.hidden);
   hipError_t e = hipGetDevice(&L->device);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&L->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
@@ -382,6 +467,17 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
   res(L->hlo, size_t(P * F) * 2);
   res(L->ypairs, size_t(P * H) * 4);
   res(L->y, size_t(T * H) * 4);
+  res(L->wmax, 4 * 4);
+  if (L->prefill_ok) {
+    res(L->x16, size_t(T * H) * 2);
+    res(L->xexp, size_t(T) * 4);
+    res(L->hexp, size_t(T) * 4);
+    res(L->h16, size_t(P * F) * 2);
+    if (L->shared_prefill_ok) {
+      res(L->shexp, size_t(T) * 4);
+      res(L->sh16, size_t(T) * d.shared_ffn * 2);
+    }
+  }
   if (L->gemv_ok) {
     res(L->xq, size_t(T * xq_row_dwords(d.hidden)) * 4);
     res(L->hq, size_t(P * xq_row_dwords(d.expert_ffn)) * 4);
@@ -421,6 +517,15 @@ extern "C" int artlite_moe_layer_upload(artlite_moe_layer* L, int t, const void*
   ART_TRY(b->reserve(want));
   ART_HIP(hipMemcpyAsync(b->p, data, want, hipMemcpyHostToDevice, L->stream));
   ART_HIP(hipMemsetAsync(static_cast<uint8_t*>(b->p) + want, 0, 256, L->stream));  // (the tail the loaders touch)
+  // the prefill's bound on |h| takes max |w| of the gate and up matrices
+  const int wm = t == ARTLITE_GATE_EXPS ? 0 : t == ARTLITE_UP_EXPS ? 1 : t == ARTLITE_GATE_SHEXP ? 2
+               : t == ARTLITE_UP_SHEXP ? 3 : -1;
+  const bool pre = wm < 2 ? L->prefill_ok : L->shared_prefill_ok;
+  if (wm >= 0 && pre) {
+    const QType* q = wm < 2 ? L->gq : L->sq;
+    ART_TRY(launch_weight_max(static_cast<const uint8_t*>(b->p), q->id, int64_t(want / q->bytes),
+                              L->wmax.as<float>() + wm, L->stream));
+  }
   ART_HIP(hipStreamSynchronize(L->stream));
   L->have[t] = true;
   return ARTLITE_OK;
@@ -503,6 +608,19 @@ extern "C" int artlite_moe_layer_tap(artlite_moe_layer* L, int tap, void* out, s
         std::vector<uint32_t> q(size_t(P * rw));
         if (P) ART_HIP(hipMemcpy(q.data(), L->hq.p, q.size() * 4, hipMemcpyDeviceToHost));
         for (int64_t r = 0; r < P; r++) xq_dequant_row(q.data() + r * rw, L->d.expert_ffn, o + r * L->d.expert_ffn);
+        return ARTLITE_OK;
+      }
+      if (L->last_prefill) {
+        // fp16 h, scaled by 2^-hexp[token]: token(s) = order[s] / k
+        const int F = L->d.expert_ffn;
+        std::vector<uint16_t> h(n);
+        std::vector<int32_t> order(static_cast<size_t>(P)), he(static_cast<size_t>(T));
+        ART_HIP(hipMemcpy(h.data(), L->h16.p, n * 2, hipMemcpyDeviceToHost));
+        ART_HIP(hipMemcpy(order.data(), L->order.p, size_t(P) * 4, hipMemcpyDeviceToHost));
+        ART_HIP(hipMemcpy(he.data(), L->hexp.p, size_t(T) * 4, hipMemcpyDeviceToHost));
+        for (int64_t r = 0; r < P; r++)
+          for (int c = 0; c < F; c++)
+            o[r * F + c] = std::ldexp(float(__builtin_bit_cast(_Float16, h[size_t(r) * F + c])), he[order[r] / L->d.top_k]);
         return ARTLITE_OK;
       }
       std::vector<uint16_t> hi(n), lo(n);

@@ -54,6 +54,10 @@ CONFIGS = {
                     tokens=(16,)),
     "mix_k8": Spec("mix_k8", H=1536, E=16, k=2, F=768, gate_type="Q4_K", down_type="Q8_0", scale=2e-4,
                    dmin_scale=1.5e-3, shared_F=256, shared_type="Q8_0", tokens=(24,)),
+    # test-only prefill-sized mix: fp32 x, Q8_0 gate / up, Q4_0 down, a gated Q8_0 shared expert (every product on
+    # the prefill tiles)
+    "mix_pf": Spec("mix_pf", H=1024, E=16, k=2, F=512, gate_type="Q8_0", down_type="Q4_0", scale=0.01,
+                   x_dtype="f32", shared_F=512, shared_type="Q8_0", shared_gated=True, tokens=(256,)),
 }
 
 ZIPF_S, ZIPF_ACTIVE, ZIPF_BETA = 1.2, 26, 0.7
