@@ -399,6 +399,17 @@ __device__ __forceinline__ void pf_dma(const void* g, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
 }
 
+// the same from a uniform base (SGPRs) plus the lane's 32-bit byte offset (no 64-bit address arithmetic per load)
+template <int SIZE>
+__device__ __forceinline__ void pf_dma_s(const void* base, uint32_t off, uint32_t lds) {
+  if constexpr (SIZE == 16)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
+
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
@@ -484,7 +495,7 @@ __device__ __forceinline__ PItem prefill_item(const PrefillArgs& a, int64_t w, i
 // of the stage); rows past the tile repeat its last (their outputs are not stored). Weights: instruction j writes
 // dwords (wv BI + j) 64 + lane of the stage's weight region, staged row q / DW (SwiGLU: gate rows n0 .. + 128, then
 // up's; plain: rows n0 .. + 256), dword q % DW of the row's stage bytes; dwords past the rows load the last one
-// again (padding), rows past N the last row. Held as 32-bit offsets (A: elements from a.a; weights: bytes from the
+// again (padding), rows past N the last row. Held as 32-bit byte offsets (A: from a.a; weights: from the
 // instruction's matrix, which is uniform: 128 rows of gate are a whole number of instructions).
 template <int QT, bool SWIGLU>
 struct PSrc {
@@ -503,7 +514,7 @@ struct PSrc {
       const int p = (wv * L::AI + i) * 64 + lane, r = p / L::ACH, c = (p % L::ACH) ^ swz(r);
       const int s = I.s0 + min(r, I.m_valid - 1);
       const int ar = g.a_gather ? (g.order ? g.order[s] / g.topk : s) : s;
-      a[i] = uint32_t(ar) * uint32_t(g.K) + 8 * c;
+      a[i] = (uint32_t(ar) * uint32_t(g.K) + 8 * c) * 2;  // (bytes)
     }
 #pragma unroll
     for (int j = 0; j < L::BI; j++) {
@@ -519,10 +530,31 @@ struct PSrc {
 // the workgroup's continuous stream of stages: the item's stage st is global step g0 + st in ring slot
 // (g0 + st) % R; the R steps issued ahead reach into the next item's first stages (or, after the last item, load
 // stage 0 again). On entry cur holds group 0 of stage 0 (read from LDS); on exit, group 0 of the next item's stage 0.
+// The loads of stage st of an item (sources src) into the ring slot at byte offset so: A from a.a + 128 st, the
+// weights from their matrix + ROW st (uniform bases), each lane at its own offset.
+template <int QT, bool SWIGLU>
+__device__ __forceinline__ void prefill_issue(const PrefillArgs& a, uint32_t lds_base, int wv,
+                                              const PSrc<QT, SWIGLU>& src, int st, uint32_t so) {
+  using L = PLayout<QT>;
+  const uint32_t adst = lds_base + so + wv * L::AI * 1024, bdst = lds_base + so + L::ABYTES + wv * L::BI * 256;
+  const uint8_t* ab = reinterpret_cast<const uint8_t*>(a.a) + 128 * st;
+#pragma unroll
+  for (int i = 0; i < L::AI; i++) pf_dma_s<16>(ab, src.a[i], adst + i * 1024);
+#pragma unroll
+  for (int i = 0; i < L::BI; i++)
+    pf_dma_s<4>(PSrc<QT, SWIGLU>::wbase(a, wv, i) + st * PStage<QT>::ROW, src.w[i], bdst + i * 256);
+}
+
+// The K loop of one item over MBN row blocks of A (the tile's rows, rounded up to 16-row blocks that hold any), in
+// the workgroup's continuous stream of stages through the ring: the item's stage st sits in slot (so0 + st SBYTES)
+// mod R SBYTES; the step issued as stage st completes (into stage st's slot) is stage st + R, which past the item's
+// last stage is the next item's stage st + R - stages (or, after the last item, stage 0 again). On entry cur holds
+// group 0 of stage 0; on exit, group 0 of the next item's stage 0 (all 8 row blocks), and the slot it came from is
+// returned.
 template <int QT, bool SWIGLU, int MBN>
-__device__ __forceinline__ void prefill_loop(const PrefillArgs& a, uint8_t* lds, int64_t g0, const PSrc<QT, SWIGLU>& src,
-                                             const PSrc<QT, SWIGLU>& nsrc, bool has_next, POps<8>& cur,
-                                             POps<8>& nxt, f32x4 (&acc)[8][2]) {
+__device__ __forceinline__ uint32_t prefill_loop(const PrefillArgs& a, uint8_t* lds, uint32_t so,
+                                                 const PSrc<QT, SWIGLU>& src, const PSrc<QT, SWIGLU>& nsrc,
+                                                 bool has_next, POps<8>& cur, POps<8>& nxt, f32x4 (&acc)[8][2]) {
   using F = Fmt<QT>;
   using L = PLayout<QT>;
   constexpr int R = L::R, ROW = PStage<QT>::ROW, GB = F::GROUP_BYTES;
@@ -530,19 +562,6 @@ __device__ __forceinline__ void prefill_loop(const PrefillArgs& a, uint8_t* lds,
   const int lg = lane >> 4, lr = lane & 15;
   const int stages = a.K / 64;
   const uint32_t lbase = pf_lds_addr(lds);
-  const uint32_t adst = lbase + wv * L::AI * 1024, bdst = lbase + L::ABYTES + wv * L::BI * 256;
-  auto slot = [&](int64_t g) { return uint32_t(g % R) * L::SBYTES; };
-  // the loads of the item's step j (j >= stages: the next item's stage j - stages, or stage 0 again)
-  auto issue = [&](int j) {
-    const uint32_t so = slot(g0 + j);
-    const bool nx = j >= stages && has_next;
-    const int st = j < stages ? j : nx ? j - stages : 0;
-#pragma unroll
-    for (int i = 0; i < L::AI; i++) pf_dma<16>(a.a + (nx ? nsrc.a[i] : src.a[i]) + 64 * st, adst + so + i * 1024);
-#pragma unroll
-    for (int i = 0; i < L::BI; i++)
-      pf_dma<4>(PSrc<QT, SWIGLU>::wbase(a, wv, i) + (nx ? nsrc.w[i] : src.w[i]) + st * ROW, bdst + so + i * 256);
-  };
   // the lane's LDS read offsets in a slot: A row lr (row block mb at + 16 mb rows), group gl: the chunk of K
   // 8 lg .. + 8; B: the staged row of column block nb, its block gl
   constexpr int AMB = 16 * L::ACH * 16;
@@ -553,13 +572,13 @@ __device__ __forceinline__ void prefill_loop(const PrefillArgs& a, uint8_t* lds,
   // the code bytes of lane group lg at the block + 2 + cb: Q4_0 bytes 8 (lg & 1) .. + 8 (lane groups 0, 1 take the
   // low nibbles, 2, 3 the high ones), Q8_0 bytes 8 lg .. + 8
   const int cb = QT == ARTLITE_Q4_0 ? 8 * (lg & 1) : 8 * lg;
-  auto read = [&](POps<8>& o, uint32_t so, int gl, auto nr) {
+  auto read = [&](POps<8>& o, uint32_t sl, int gl, auto nr) {
+    const uint8_t* ap = lds + sl + aof[gl];
 #pragma unroll
-    for (int mb = 0; mb < decltype(nr)::value; mb++)
-      o.a[mb] = *reinterpret_cast<const u32x4*>(lds + so + aof[gl] + mb * AMB);
+    for (int mb = 0; mb < decltype(nr)::value; mb++) o.a[mb] = *reinterpret_cast<const u32x4*>(ap + mb * AMB);
 #pragma unroll
     for (int nb = 0; nb < 2; nb++) {
-      const uint8_t* b = lds + so + bof[nb] + gl * GB;  // (4-byte aligned: gl GB is 0 or 2 mod 4)
+      const uint8_t* b = lds + sl + bof[nb] + gl * GB;  // (4-byte aligned: gl GB is 0 or 2 mod 4)
       o.sc[nb] = *reinterpret_cast<const uint16_t*>(b);
       if (gl == 0) {
         const uint32_t* d = reinterpret_cast<const uint32_t*>(b + cb);
@@ -584,23 +603,24 @@ __device__ __forceinline__ void prefill_loop(const PrefillArgs& a, uint8_t* lds,
   };
   using NR = std::integral_constant<int, MBN>;
   using N8 = std::integral_constant<int, 8>;
-  for (int st = 0; st + 1 < stages; st++) {
-    read(nxt, slot(g0 + st), 1, NR{});
+  auto next_slot = [](uint32_t x) { return x + L::SBYTES == R * L::SBYTES ? 0u : x + L::SBYTES; };
+  // one stage: group 1 read while group 0 computes; the wait for the next stage, the barrier, the step into this
+  // stage's slot; the next stage's group 0 read while group 1 computes
+  auto step = [&](const PSrc<QT, SWIGLU>& isrc, int ist, auto nr) {
+    read(nxt, so, 1, NR{});
     compute(cur);
-    pf_wait<(R - 2) * L::LOADS>();  // (step g0 + st + 1: steps up to g0 + st + R - 1 issued)
+    pf_wait<(R - 2) * L::LOADS>();  // (the next stage: the R - 2 steps after it issued)
     pf_barrier();
-    issue(st + R);  // (into the slot of step g0 + st, whose operands every wave holds in registers)
-    read(cur, slot(g0 + st + 1), 0, NR{});
+    prefill_issue<QT, SWIGLU>(a, lbase, wv, isrc, ist, so);  // (into the slot every wave is past)
+    so = next_slot(so);
+    read(cur, so, 0, nr);
     compute(nxt);
-  }
-  read(nxt, slot(g0 + stages - 1), 1, NR{});
-  compute(cur);
-  pf_wait<(R - 2) * L::LOADS>();
-  pf_barrier();
-  issue(stages - 1 + R);
-  // (the next item's first group: all 8 row blocks, whatever its rows; after the last item, data not used)
-  read(cur, slot(g0 + stages), 0, N8{});
-  compute(nxt);
+  };
+  int st = 0;
+  for (; st < stages - R; st++) step(src, st + R, NR{});
+  for (; st + 1 < stages; st++) step(has_next ? nsrc : src, has_next ? st + R - stages : 0, NR{});
+  step(has_next ? nsrc : src, has_next ? st + R - stages : 0, N8{});
+  return so;
 }
 
 template <int QT, bool SWIGLU>
@@ -637,20 +657,9 @@ __global__ __launch_bounds__(512) void k_prefill(const PrefillArgs a) {
   PSrc<QT, SWIGLU> src, nsrc;
   src.set(a, I, wv, lane);
   row_info(I, 0);
-  // the first item's first R stages, then its stage 0 read
-  {
-    const uint32_t lbase = pf_lds_addr(lds);
-    const uint32_t adst = lbase + wv * L::AI * 1024, bdst = lbase + L::ABYTES + wv * L::BI * 256;
+  // the first item's first R stages (stages >= R: the launch checks), then its stage 0 read
 #pragma unroll
-    for (int j = 0; j < R; j++) {
-      const int st = j < stages ? j : 0;
-#pragma unroll
-      for (int i = 0; i < L::AI; i++) pf_dma<16>(a.a + src.a[i] + 64 * st, adst + j * L::SBYTES + i * 1024);
-#pragma unroll
-      for (int i = 0; i < L::BI; i++)
-        pf_dma<4>(PSrc<QT, SWIGLU>::wbase(a, wv, i) + src.w[i] + st * PStage<QT>::ROW, bdst + j * L::SBYTES + i * 256);
-    }
-  }
+  for (int j = 0; j < R; j++) prefill_issue<QT, SWIGLU>(a, pf_lds_addr(lds), wv, src, j, j * L::SBYTES);
   pf_wait<(R - 1) * L::LOADS>();  // (stage 0: R - 1 stages issued after it)
   __syncthreads();                // (and the row scales)
   POps<8> cur, nxt;
@@ -672,6 +681,7 @@ __global__ __launch_bounds__(512) void k_prefill(const PrefillArgs a) {
     }
   }
 
+  uint32_t so = 0;  // the ring slot (byte offset) of the current item's stage 0
   for (int q = 0; q < nq; q++) {
     const bool has_next = q + 1 < nq;
     PItem J{};
@@ -683,14 +693,13 @@ __global__ __launch_bounds__(512) void k_prefill(const PrefillArgs a) {
     f32x4 acc[8][2];
 #pragma unroll
     for (int mb = 0; mb < 8; mb++) acc[mb][0] = acc[mb][1] = f32x4{0, 0, 0, 0};
-    const int64_t g0 = int64_t(q) * stages;
     const int mbn = (I.m_valid + 15) / 16;
     if (mbn <= 2)
-      prefill_loop<QT, SWIGLU, 2>(a, lds, g0, src, nsrc, has_next, cur, nxt, acc);
+      so = prefill_loop<QT, SWIGLU, 2>(a, lds, so, src, nsrc, has_next, cur, nxt, acc);
     else if (mbn <= 4)
-      prefill_loop<QT, SWIGLU, 4>(a, lds, g0, src, nsrc, has_next, cur, nxt, acc);
+      so = prefill_loop<QT, SWIGLU, 4>(a, lds, so, src, nsrc, has_next, cur, nxt, acc);
     else
-      prefill_loop<QT, SWIGLU, 8>(a, lds, g0, src, nsrc, has_next, cur, nxt, acc);
+      so = prefill_loop<QT, SWIGLU, 8>(a, lds, so, src, nsrc, has_next, cur, nxt, acc);
 
     // epilogue: lane output i of block (mb, nb): row 16 mb + 4 lg + i of the tile; column (SwiGLU) n0 + 16 wv + lr
     // of gate (nb 0) and up (nb 1), (plain) n0 + 32 wv + 16 nb + lr
