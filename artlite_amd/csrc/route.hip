@@ -202,6 +202,60 @@ __global__ __launch_bounds__(4 * WAVE) void k_router_small(const void* __restric
   }
 }
 
+// Router logits for prefill-sized batches on the fp64 MFMA (v_mfma_f64_16x16x4_f64; fp32 x fp32 products are exact
+// in fp64, the sums in fp64, rounded once to fp32 like the other router kernels): a workgroup is 16 tokens times all
+// experts, a wave per 16 experts. Layout: lane l holds A row l % 16 (token) and B column l % 16 (expert), both at K
+// position l / 16 of the step; result element i of lane l is row 4 i + l / 16, column l % 16. The K values of a
+// 16-value block are dealt as step s, lane group g -> k0 + 4 g + s, so each lane's four steps are one 16-byte load of
+// its W row and one 8 / 16-byte load of its x row.
+template <int XT>
+__global__ __launch_bounds__(1024) void k_router_mfma(const void* __restrict__ xv, const float* __restrict__ W, int H,
+                                                      int E, int64_t T, float* __restrict__ out, int64_t out_row) {
+  typedef double d4 __attribute__((ext_vector_type(4)));
+  const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE;
+  const int g = lane >> 4, r = lane & 15;
+  const int64_t t0 = int64_t(blockIdx.x) * 16;
+  const int e0 = 16 * wv;
+  const int64_t t = min(t0 + r, T - 1);  // (rows past T and experts past E load the last one; not stored)
+  const float* wr = W + int64_t(min(e0 + r, E - 1)) * H + 4 * g;
+  d4 c = {0, 0, 0, 0};
+  auto x4 = [&](int k0) -> float4 {
+    if (XT == ARTLITE_X_F32) return *reinterpret_cast<const float4*>(static_cast<const float*>(xv) + t * H + k0 + 4 * g);
+    const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(xv) + t * H + k0 + 4 * g);
+    return make_float4(bf16_to_f32(v.x & 0xFFFFu), bf16_to_f32(v.x >> 16), bf16_to_f32(v.y & 0xFFFFu),
+                       bf16_to_f32(v.y >> 16));
+  };
+  int k0 = 0;
+  for (; k0 + 64 <= H; k0 += 64) {  // (four blocks' loads in flight)
+    float4 xa[4], wa[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      xa[j] = x4(k0 + 16 * j);
+      wa[j] = *reinterpret_cast<const float4*>(wr + k0 + 16 * j);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      c = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xa[j].x), double(wa[j].x), c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xa[j].y), double(wa[j].y), c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xa[j].z), double(wa[j].z), c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xa[j].w), double(wa[j].w), c, 0, 0, 0);
+    }
+  }
+  for (; k0 < H; k0 += 16) {
+    const float4 xv4 = x4(k0), wv4 = *reinterpret_cast<const float4*>(wr + k0);
+    c = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xv4.x), double(wv4.x), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xv4.y), double(wv4.y), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xv4.z), double(wv4.z), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xv4.w), double(wv4.w), c, 0, 0, 0);
+  }
+  const int e = e0 + r;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int64_t tt = t0 + 4 * i + g;
+    if (tt < T && e < E) out[tt * out_row + e] = float(c[i]);
+  }
+}
+
 int launch_router(const void* x, int x_dtype, const float* W, int H, int E, int64_t T, float* out, int64_t out_row,
                   uint32_t* xq, hipStream_t s) {
   if (T <= 0) return ARTLITE_OK;
@@ -211,6 +265,15 @@ int launch_router(const void* x, int x_dtype, const float* W, int H, int E, int6
   const int tt = int(std::min<int64_t>(ROUTER_TG, std::max<int64_t>(1, ROUTER_LDS / (int64_t(H) * xb))));
   if (int64_t(H) * xb > ROUTER_LDS) return fail(ARTLITE_EINVAL, "router: H %d too wide", H);
   const size_t lds = size_t(tt) * H * xb;
+  if (!xq && T >= 64 && E >= 16 && E <= 16 * 16 && H % 16 == 0) {  // (prefill-sized: the fp64 MFMA)
+    const dim3 g(unsigned((T + 15) / 16)), b(unsigned((E + 15) / 16) * WAVE);
+    if (x_dtype == ARTLITE_X_F32)
+      k_router_mfma<ARTLITE_X_F32><<<g, b, 0, s>>>(x, W, H, E, T, out, out_row);
+    else
+      k_router_mfma<ARTLITE_X_BF16><<<g, b, 0, s>>>(x, W, H, E, T, out, out_row);
+    ART_HIP(hipGetLastError());
+    return ARTLITE_OK;
+  }
   if (T <= ROUTER_TG && H % 1024 == 0) {  // (a workgroup per expert)
     const int nq = xq ? int((T * (H / 256) + 3) / 4) : 0;
     const dim3 g(unsigned(E + nq), 1), b(4 * WAVE);
