@@ -20,7 +20,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
-MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 / fp16 MFMA, TFLOP/s
 METRIC = "MoE-layer tok/s at decode B=16 and prefill 4096; % of HBM / MFMA roofline"
 
 
@@ -169,7 +169,7 @@ def main() -> None:
     out = {
         "metric": METRIC, "value": T / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16", "data": "synthetic",
+        "dtype": "i8", "data": "synthetic",
         "config": {"workload": "qwen3-30b-a3b-shaped MoE layer, Q4_0 experts, decode", "tokens": T, "hidden": H,
                    "experts": E, "top_k": k, "expert_ffn": F, "weights": shape["qtype"], "activations": "bf16",
                    "weight_sets": args.weight_sets, "experts_touched": U},
@@ -189,6 +189,7 @@ def main() -> None:
         gu_flops = 2 * Tp * k * 2 * H * F
         pgu = pre["kernels"].get("gate_up", float("nan"))
         out["prefill"] = {"tokens": Tp, "value": Tp / (pre["ms"] * 1e-3), "unit": "tokens/s", "ms_per_step": pre["ms"],
+                          "dtype": "f16",
                           "steps": args.prefill_steps, "kernel_ms": pre["kernels"],
                           "roofline": {"bound": "mfma", "kernel": "gate_up", "achieved": gu_flops / (pgu * 1e-3) / 1e12,
                                        "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
