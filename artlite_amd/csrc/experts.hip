@@ -1,6 +1,7 @@
-// The experts' products over raw GGUF blocks on gfx950's bf16 MFMA (v_mfma_f32_16x16x32_bf16), and the combine.
+// The experts' products over raw GGUF blocks on gfx950's MFMA, and the combine: the MFMA decode tiles (bf16, for
+// batches between the GEMV's and the prefill's; every Q4_K product), the prefill tiles (fp16, below), the combine.
 //
-// Exactness of the operands: a block's integer codes are exact in bf16 -- Q4_0 as 128 + q and Q4_K as 128 + q
+// MFMA decode tiles. Exactness of the operands: a block's integer codes are exact in bf16 -- Q4_0 as 128 + q and Q4_K as 128 + q
 // (a byte 0x43 above the nibble: bf16 128 + q), Q8_0 as 128 + q through an unsigned byte conversion -- and bf16
 // activations are exact; fp32 activations and the SwiGLU intermediate are split into bf16 hi + lo planes. One MFMA
 // per 32-value group gives S = sum (128 + q) x exactly rounded once into fp32, its C input pre-loaded with

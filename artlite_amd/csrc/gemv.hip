@@ -1,14 +1,19 @@
 // Decode expert products on the VALU, and the XQ activations they read.
 //
-// A workgroup is one tile of at most GEMV_BM sorted rows of A (tokens for gate / up, pairs for down) of one expert,
-// times 64 weight rows (SwiGLU: those rows of gate and of up), as 4 independent waves of 16 rows. A wave streams its
-// rows in units of 8 groups of 32 values (Q4_0 / Q4_K: 144 bytes of a row, Q8_0: 272) with global_load_lds_dwordx4
-// into one of D LDS slots of its own (consecutive lanes load consecutive 16-byte chunks), D - 1 units ahead. Lane
-// (p, r) -- 16-lane row p, lane r in it -- takes row r and groups 2 p, 2 p + 1 of each unit, so four lanes share a
-// row and a unit's products of 64 rows are spread over four waves (one wave per SIMD issues VALU at well under half
-// rate). The activations come straight into registers, one 16-byte XQ chunk per lane per row of A: DPP
-// row_newbcast:j hands every lane of 16-lane row p dword j of its groups' blocks as the broadcast operand of
-// v_dot4c_i32_i8, and the per-group words the same way. The four lanes of a row are summed at the end.
+// Persistent workgroups (as many as the device holds) take work items in turn: an item is one tile of at most
+// GEMV_BM sorted rows of A (tokens for gate / up, pairs for down) of one expert times a block of 16 RB weight rows
+// (SwiGLU: those rows of gate and of up). Plain products: 4 waves, one per 16-row block (RB 4, 64 rows). SwiGLU:
+// 8 waves, 2 row blocks (32 rows) x 4 waves that split K four ways, whose partial sums meet in LDS. Each wave
+// streams its own steps (16 rows x one K-unit of 8 groups of 32 values: Q4_0 / Q4_K 144 bytes a row, Q8_0 272)
+// with global_load_lds_dwordx4 into D LDS slots of its own, one step ahead, across item boundaries; the XQ records
+// of A's rows for a K-unit come the same way. Every load is a DMA counted as it is issued, so each wait names the
+// exact count (the compiler, which cannot order DMAs against register loads, would otherwise wait for all of them).
+// Lane (p, r) -- 16-lane row p, lane r in it -- takes row r and groups 2 p, 2 p + 1 of each unit, so four lanes
+// share a row. The activations are read once per K-unit into registers, one 16-byte XQ chunk per lane per row of A:
+// DPP row_newbcast:j hands every lane of 16-lane row p dword j of its groups' blocks as the broadcast operand of
+// v_dot4c_i32_i8, and the per-group words the same way. The four lanes of a row are summed at the end. The SwiGLU
+// epilogue has no barrier: the last of the four K-split waves to deliver its partial sums (an LDS counter per
+// buffer) adds them in a fixed order, forms h = silu(gate) up and writes it as XQ for the down product.
 //
 // Arithmetic of one (row of A, group): A = sum_j dot4(a_j, q_j) and B = C + sum_j dot4(b_j, q_j), exactly in int32,
 // with q_j the group's codes as int8 (Q4_0 / Q4_K: nibbles 0..15, Q8_0: the signed bytes) and C the code offset's
