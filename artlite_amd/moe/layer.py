@@ -11,7 +11,7 @@ import ctypes
 import numpy as np
 
 from .. import _hip
-from ..gguf_model import TYPE_ID
+from ..gguf_model import TYPE_ID, GGUFFile
 
 TENSORS = {"ffn_gate_inp": 0, "ffn_gate_exps": 1, "ffn_up_exps": 2, "ffn_down_exps": 3, "ffn_gate_shexp": 4,
            "ffn_up_shexp": 5, "ffn_down_shexp": 6, "ffn_gate_inp_shexp": 7}
@@ -56,6 +56,50 @@ class MoELayer:
 
     def __exit__(self, *exc: object) -> None:
         self.close()
+
+    @classmethod
+    def from_gguf(cls, gguf: "GGUFFile", block: int, *, max_tokens: int) -> "MoELayer":
+        """Block ``block``'s MoE FFN of a GGUF file (``gguf_model.GGUFFile``): its shape from the architecture's
+        metadata (``embedding_length``, ``expert_count``, ``expert_used_count``, ``expert_feed_forward_length``,
+        ``expert_shared_feed_forward_length``, ``expert_gating_func``: 2 sigmoid, else softmax; the reference's
+        ``model_config.py:735-766``), its tensors ``blk.{block}.ffn_*`` uploaded as the file holds them (the router
+        and a shared gate converted to fp32 exactly when stored as F16 / BF16)."""
+        b = f"blk.{block}."
+        m = gguf.arch_meta
+        need = [b + n + ".weight" for n in ("ffn_gate_inp", "ffn_gate_exps", "ffn_up_exps", "ffn_down_exps")]
+        missing = [n for n in need if n not in gguf]
+        if missing:
+            raise ValueError(f"{gguf.path}: block {block} has no MoE FFN ({', '.join(missing)} missing)")
+        H, E, k, F = (int(m(key)) for key in ("embedding_length", "expert_count", "expert_used_count",
+                                              "expert_feed_forward_length"))
+        dims, gtype, _, _ = gguf.tensor_info[b + "ffn_gate_exps.weight"]
+        _, utype, _, _ = gguf.tensor_info[b + "ffn_up_exps.weight"]
+        ddims, dtype, _, _ = gguf.tensor_info[b + "ffn_down_exps.weight"]
+        if tuple(dims) != (H, F, E) or tuple(ddims) != (F, H, E) or utype != gtype:
+            raise ValueError(f"{gguf.path}: block {block} expert tensors {dims} / {ddims} ({gtype}, {utype}), "
+                             f"expected ({H}, {F}, {E}) / ({F}, {H}, {E})")
+        shared = b + "ffn_gate_shexp.weight" in gguf
+        sF, stype = 0, ""
+        if shared:
+            sdims, stype, _, _ = gguf.tensor_info[b + "ffn_gate_shexp.weight"]
+            sF = int(m("expert_shared_feed_forward_length", sdims[1]))
+        gated = b + "ffn_gate_inp_shexp.weight" in gguf
+        gating = "sigmoid" if int(m("expert_gating_func", 1)) == 2 else "softmax"
+        layer = cls(hidden=H, n_experts=E, top_k=k, expert_ffn=F, gate_type=gtype, down_type=dtype,
+                    max_tokens=max_tokens, shared_ffn=sF, shared_type=stype, shared_gated=gated, gating=gating)
+        try:
+            for name in ("ffn_gate_inp", "ffn_gate_inp_shexp"):
+                if b + name + ".weight" in gguf:
+                    t = gguf.tensor(b + name + ".weight")
+                    raw = t.raw if t.qtype != "BF16" else (t.raw.astype(np.uint32) << 16).view(np.float32)
+                    layer.upload(name, np.ascontiguousarray(raw, np.float32))
+            for name in ("ffn_gate_exps", "ffn_up_exps", "ffn_down_exps") + (
+                    ("ffn_gate_shexp", "ffn_up_shexp", "ffn_down_shexp") if shared else ()):
+                layer.upload(name, gguf.tensor(b + name + ".weight").raw)
+        except BaseException:
+            layer.close()
+            raise
+        return layer
 
     def upload(self, name: str, data: np.ndarray) -> None:
         """A tensor's bytes (its GGUF layout, exactly its size)."""
