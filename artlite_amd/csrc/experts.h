@@ -78,8 +78,9 @@ constexpr int MAX_GROUPS = 128;
 int launch_expert_gemm(const GemmArgs& a, hipStream_t s);
 
 // y[t] = ws[t] ys[t] + sum_i w[t, i] Y[slot[t k + i]] in fp32 (ys / ws optional)
+// res (optional; x_dtype res_dtype): added last, y[t] += res[t] (the block's residual)
 int launch_combine(const float* Y, const int32_t* slot, const float* w, int k, const float* ys, const float* ws_logit,
-                   int ws_sigmoid, int64_t T, int H, float* y, hipStream_t s);
+                   int ws_sigmoid, int64_t T, int H, const void* res, int res_dtype, float* y, hipStream_t s);
 
 // fp32 activations -> bf16 hi + lo planes (x = hi + lo to 2^-16 relative)
 int launch_split(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, hipStream_t s);

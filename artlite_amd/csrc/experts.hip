@@ -874,7 +874,7 @@ int launch_expert_gemm(const GemmArgs& a, hipStream_t s) {
 // src/artlite/moe/gather.py:12-18: the shared term first, then the slots in order, fp32)
 __global__ void k_combine(const float* __restrict__ Y, const int32_t* __restrict__ slot, const float* __restrict__ w,
                           int k, const float* __restrict__ ys, const float* __restrict__ ws_logit, int ws_sigmoid,
-                          int64_t T, int H, float* __restrict__ y) {
+                          int64_t T, int H, const void* __restrict__ res, int res_dtype, float* __restrict__ y) {
   const int64_t t = blockIdx.y;
   const int h4 = blockIdx.x * blockDim.x + threadIdx.x;
   if (h4 * 4 >= H) return;
@@ -893,15 +893,26 @@ __global__ void k_combine(const float* __restrict__ Y, const int32_t* __restrict
     acc.z = __builtin_fmaf(wi, v.z, acc.z);
     acc.w = __builtin_fmaf(wi, v.w, acc.w);
   }
+  if (res) {  // (the residual add after the block: y = moe + x)
+    float4 r;
+    if (res_dtype == ARTLITE_X_F32) {
+      r = reinterpret_cast<const float4*>(static_cast<const float*>(res) + t * H)[h4];
+    } else {
+      const uint2 v = reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(res) + t * H)[h4];
+      r = make_float4(bf16_to_f32(v.x & 0xFFFFu), bf16_to_f32(v.x >> 16), bf16_to_f32(v.y & 0xFFFFu),
+                      bf16_to_f32(v.y >> 16));
+    }
+    acc.x = acc.x + r.x, acc.y = acc.y + r.y, acc.z = acc.z + r.z, acc.w = acc.w + r.w;
+  }
   reinterpret_cast<float4*>(y + t * H)[h4] = acc;
 }
 
 int launch_combine(const float* Y, const int32_t* slot, const float* w, int k, const float* ys, const float* ws_logit,
-                   int ws_sigmoid, int64_t T, int H, float* y, hipStream_t s) {
+                   int ws_sigmoid, int64_t T, int H, const void* res, int res_dtype, float* y, hipStream_t s) {
   if (T <= 0) return ARTLITE_OK;
   if (H % 4) return fail(ARTLITE_EINVAL, "combine: H %d not a multiple of 4", H);
   const dim3 grid(unsigned((H / 4 + 255) / 256), unsigned(T)), block(256);
-  k_combine<<<grid, block, 0, s>>>(Y, slot, w, k, ys, ws_logit, ws_sigmoid, T, H, y);
+  k_combine<<<grid, block, 0, s>>>(Y, slot, w, k, ys, ws_logit, ws_sigmoid, T, H, res, res_dtype, y);
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
 }

@@ -18,12 +18,13 @@ struct artlite_moe_layer {
   hipStream_t stream = nullptr;
   const QType *gq = nullptr, *dq = nullptr, *sq = nullptr;
   size_t gate_row = 0, down_row = 0, sgate_row = 0, sdown_row = 0;  // row bytes
-  DevBuf router, gate, up, down, sgate, sup, sdown, sinp;
-  bool have[8] = {};
+  DevBuf router, gate, up, down, sgate, sup, sdown, sinp, norm;
+  bool have[9] = {};
   // activations of the staged input
   int x_dtype = ARTLITE_X_BF16;
   int64_t staged = -1;  // tokens staged, -1: none
   DevBuf x, xhi, xlo;
+  DevBuf xn;  // the RMS-normalised x (norm_eps > 0)
   DevBuf x16, xexp, hexp, shexp;  // the prefill's fp16 activations and their per-token scale exponents
   DevBuf wmax;                    // max |w| of gate, up, shared gate, shared up (the bound on |h|)
   DevBuf logits, ids, w, sg;
@@ -49,6 +50,7 @@ size_t tensor_bytes(const artlite_moe_layer* L, int t) {
     case ARTLITE_UP_SHEXP: return size_t(d.shared_ffn) * L->sgate_row;
     case ARTLITE_DOWN_SHEXP: return size_t(d.hidden) * L->sdown_row;
     case ARTLITE_GATE_INP_SHEXP: return size_t(d.hidden) * 4;
+    case ARTLITE_FFN_NORM: return d.norm_eps > 0 ? size_t(d.hidden) * 4 : 0;
     default: return 0;
   }
 }
@@ -63,6 +65,7 @@ DevBuf* tensor_buf(artlite_moe_layer* L, int t) {
     case ARTLITE_UP_SHEXP: return &L->sup;
     case ARTLITE_DOWN_SHEXP: return &L->sdown;
     case ARTLITE_GATE_INP_SHEXP: return &L->sinp;
+    case ARTLITE_FFN_NORM: return &L->norm;
     default: return nullptr;
   }
 }
@@ -80,6 +83,7 @@ int check_ready(const artlite_moe_layer* L) {
     if (L->d.shared_gated && !L->have[ARTLITE_GATE_INP_SHEXP])
       return fail(ARTLITE_EINVAL, "moe layer: shared gate not uploaded");
   }
+  if (L->d.norm_eps > 0 && !L->have[ARTLITE_FFN_NORM]) return fail(ARTLITE_EINVAL, "moe layer: ffn_norm not uploaded");
   return ARTLITE_OK;
 }
 
@@ -104,7 +108,7 @@ Path path_of(const artlite_moe_layer* L, int64_t T) {
   p.prefill = !p.gemv && L->prefill_ok && T * L->d.top_k >= int64_t(16) * L->d.n_experts;
   p.shared_prefill = L->d.shared_ffn && p.prefill && L->shared_prefill_ok && T >= PREFILL_BM / 2;
   const bool planes = (!p.gemv && !p.prefill) || (L->d.shared_ffn && !p.shared_gemv && !p.shared_prefill);
-  p.split = planes && L->x_dtype == ARTLITE_X_F32;
+  p.split = planes && (L->x_dtype == ARTLITE_X_F32 || L->d.norm_eps > 0);  // (the normalised x is fp32)
   p.quant = p.gemv;
   p.small = p.gemv && T * L->d.top_k <= DISPATCH_BLOCK && L->d.n_experts <= MAX_EXPERTS;
   return p;
@@ -114,6 +118,7 @@ Path path_of(const artlite_moe_layer* L, int64_t T) {
 std::vector<std::string> kernel_list(const artlite_moe_layer* L, int64_t T) {
   const Path p = path_of(L, T);
   std::vector<std::string> k;
+  if (L->d.norm_eps > 0) k.push_back("rmsnorm");
   if (p.prefill) k.push_back("prefill_x");
   if (p.split) k.push_back("split");
   k.push_back(p.quant ? "router_quant" : "router");
@@ -148,25 +153,34 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     return ARTLITE_OK;
   };
   const Path path = path_of(L, T);
-  const uint16_t *ahi = L->x.as<uint16_t>(), *alo = nullptr;
+  // the block's input: x as staged, or (norm_eps > 0) its RMS normalisation in fp32
+  const void* xin = L->x.p;
+  int xdt = L->x_dtype;
+  if (d.norm_eps > 0) {
+    ART_TRY(mark());
+    ART_TRY(launch_rmsnorm(L->x.p, L->x_dtype, L->norm.as<float>(), d.norm_eps, T, H, L->xn.as<float>(), s));
+    xin = L->xn.p;
+    xdt = ARTLITE_X_F32;
+  }
+  const uint16_t *ahi = static_cast<const uint16_t*>(xin), *alo = nullptr;
   if (path.prefill) {
     ART_TRY(mark());
-    ART_TRY(launch_prefill_x(L->x.p, L->x_dtype, T, H, L->wmax.as<float>(), path.shared_prefill ? 2 : 1,
+    ART_TRY(launch_prefill_x(xin, xdt, T, H, L->wmax.as<float>(), path.shared_prefill ? 2 : 1,
                              L->x16.as<uint16_t>(), L->xexp.as<int32_t>(), L->hexp.as<int32_t>(),
                              L->shexp.as<int32_t>(), s));
   }
   if (path.split) {
     ART_TRY(mark());
-    ART_TRY(launch_split(L->x.as<float>(), T * H, L->xhi.as<uint16_t>(), L->xlo.as<uint16_t>(), s));
+    ART_TRY(launch_split(static_cast<const float*>(xin), T * H, L->xhi.as<uint16_t>(), L->xlo.as<uint16_t>(), s));
     ahi = L->xhi.as<uint16_t>();
     alo = L->xlo.as<uint16_t>();
   }
   ART_TRY(mark());
-  ART_TRY(launch_router(L->x.p, L->x_dtype, L->router.as<float>(), H, E, T, L->logits.as<float>(), E,
+  ART_TRY(launch_router(xin, xdt, L->router.as<float>(), H, E, T, L->logits.as<float>(), E,
                         path.quant ? L->xq.as<uint32_t>() : nullptr, s));
   if (d.shared_ffn && d.shared_gated) {
     ART_TRY(mark());
-    ART_TRY(launch_router(L->x.p, L->x_dtype, L->sinp.as<float>(), H, 1, T, L->sg.as<float>(), 1, nullptr, s));
+    ART_TRY(launch_router(xin, xdt, L->sinp.as<float>(), H, 1, T, L->sg.as<float>(), 1, nullptr, s));
   }
   const int BM = path.gemv ? GEMV_BM : path.prefill ? PREFILL_BM : DECODE_BM;
   DispatchBufs db{L->ids.as<int32_t>(), P, E, k, L->table.as<int32_t>(), L->ctrl.as<int32_t>(),
@@ -384,7 +398,8 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
   }
   ART_TRY(mark());
   ART_TRY(launch_combine(L->ypairs.as<float>(), L->slot.as<int32_t>(), L->w.as<float>(), k, ys,
-                         d.shared_gated ? L->sg.as<float>() : nullptr, 1, T, H, L->y.as<float>(), s));
+                         d.shared_gated ? L->sg.as<float>() : nullptr, 1, T, H, d.residual ? L->x.p : nullptr,
+                         L->x_dtype, L->y.as<float>(), s));
   ART_TRY(mark());
   L->last_T = T;
   L->last_gemv = path.gemv;
@@ -416,6 +431,8 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
       return fail(ARTLITE_EINVAL, "moe layer: shared expert type %d / width %d", d.shared_type, d.shared_ffn);
   }
   if (d.gating != 0 && d.gating != 1) return fail(ARTLITE_EINVAL, "moe layer: gating %d", d.gating);
+  if (!(d.norm_eps >= 0.0f && d.norm_eps < 1.0f) || (d.residual != 0 && d.residual != 1))
+    return fail(ARTLITE_EINVAL, "moe layer: norm eps %g, residual %d", double(d.norm_eps), d.residual);
   int n = 0;
   if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(ARTLITE_EHIP, "moe layer: no HIP device");
   auto* L = new artlite_moe_layer();
@@ -450,6 +467,7 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
     if (rc == ARTLITE_OK) rc = b.reserve(bytes);
   };
   res(L->x, size_t(T * H) * 4);
+  if (d.norm_eps > 0) res(L->xn, size_t(T * H) * 4);
   res(L->xhi, size_t(T * H) * 2);
   res(L->xlo, size_t(T * H) * 2);
   res(L->logits, size_t(T * E) * 4);
@@ -598,6 +616,10 @@ extern "C" int artlite_moe_layer_tap(artlite_moe_layer* L, int tap, void* out, s
     case ARTLITE_TAP_ORDER: src = L->order.p, bytes = size_t(P) * 4; break;
     case ARTLITE_TAP_SLOT: src = L->slot.p, bytes = size_t(P) * 4; break;
     case ARTLITE_TAP_Y: src = L->ypairs.p, bytes = size_t(P) * L->d.hidden * 4; break;
+    case ARTLITE_TAP_XN:
+      if (!(L->d.norm_eps > 0)) return fail(ARTLITE_EINVAL, "moe layer tap: no norm in this layer");
+      src = L->xn.p, bytes = size_t(T) * L->d.hidden * 4;
+      break;
     case ARTLITE_TAP_H: {
       const size_t n = size_t(P) * L->d.expert_ffn;
       if (nbytes < n * 4) return fail(ARTLITE_EINVAL, "moe layer tap: %zu bytes, need %zu", nbytes, n * 4);

@@ -102,6 +102,10 @@ int launch_topk(const float* logits, int64_t n, int64_t row, int per_col, int64_
 int launch_router(const void* x, int x_dtype, const float* W, int H, int E, int64_t T, float* out, int64_t out_row,
                   uint32_t* xq, hipStream_t s);
 
+// out (T x H fp32) = x / sqrt(mean(x^2) + eps) * w per row (float64 mean and quotient, rounded once, then fp32 w)
+int launch_rmsnorm(const void* x, int x_dtype, const float* w, float eps, int64_t T, int H, float* out,
+                   hipStream_t s);
+
 // ---- dispatch: the stable counting sort of the (token, slot) pairs by expert
 constexpr int DISPATCH_BLOCK = 1024;  // pairs per block
 

@@ -256,6 +256,41 @@ __global__ __launch_bounds__(1024) void k_router_mfma(const void* __restrict__ x
   }
 }
 
+// ---- RMSNorm of the block's input (the reference's rms_norm, tests/np_ops.py:27-32): the mean of x^2 in float64
+// (the squares of fp32 values exact), x / sqrt(mean + eps) in float64 rounded once to fp32, then times w in fp32
+// (this file is built without FMA contraction, so the product rounds on its own). One workgroup per token.
+template <int XT>
+__global__ __launch_bounds__(256) void k_rmsnorm(const void* __restrict__ xv, const float* __restrict__ w, float eps,
+                                                 int H, float* __restrict__ out) {
+  __shared__ double part[4];
+  const int64_t t = blockIdx.x;
+  auto at = [&](int i) -> float {
+    return XT == ARTLITE_X_F32 ? static_cast<const float*>(xv)[t * H + i]
+                               : bf16_to_f32(static_cast<const uint16_t*>(xv)[t * H + i]);
+  };
+  double ss = 0.0;
+  for (int i = threadIdx.x; i < H; i += 256) {
+    const double v = at(i);
+    ss += v * v;
+  }
+  for (int o = 32; o; o >>= 1) ss += __shfl_xor(ss, o);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x / 64] = ss;
+  __syncthreads();
+  const double d = sqrt((((part[0] + part[1]) + part[2]) + part[3]) / double(H) + double(eps));
+  for (int i = threadIdx.x; i < H; i += 256) out[t * H + i] = float(double(at(i)) / d) * w[i];
+}
+
+int launch_rmsnorm(const void* x, int x_dtype, const float* w, float eps, int64_t T, int H, float* out,
+                   hipStream_t s) {
+  if (T <= 0) return ARTLITE_OK;
+  if (x_dtype == ARTLITE_X_F32)
+    k_rmsnorm<ARTLITE_X_F32><<<unsigned(T), 256, 0, s>>>(x, w, eps, H, out);
+  else
+    k_rmsnorm<ARTLITE_X_BF16><<<unsigned(T), 256, 0, s>>>(x, w, eps, H, out);
+  ART_HIP(hipGetLastError());
+  return ARTLITE_OK;
+}
+
 int launch_router(const void* x, int x_dtype, const float* W, int H, int E, int64_t T, float* out, int64_t out_row,
                   uint32_t* xq, hipStream_t s) {
   if (T <= 0) return ARTLITE_OK;

@@ -14,8 +14,9 @@ from .. import _hip
 from ..gguf_model import TYPE_ID, GGUFFile
 
 TENSORS = {"ffn_gate_inp": 0, "ffn_gate_exps": 1, "ffn_up_exps": 2, "ffn_down_exps": 3, "ffn_gate_shexp": 4,
-           "ffn_up_shexp": 5, "ffn_down_shexp": 6, "ffn_gate_inp_shexp": 7}
-TAPS = {"logits": 0, "ids": 1, "weights": 2, "counts": 3, "offsets": 4, "order": 5, "slot": 6, "h": 7, "y_pairs": 8}
+           "ffn_up_shexp": 5, "ffn_down_shexp": 6, "ffn_gate_inp_shexp": 7, "ffn_norm": 8}
+TAPS = {"logits": 0, "ids": 1, "weights": 2, "counts": 3, "offsets": 4, "order": 5, "slot": 6, "h": 7, "y_pairs": 8,
+        "x_norm": 9}
 X_F32, X_BF16 = 0, 1
 
 
@@ -24,14 +25,17 @@ class MoELayer:
 
     def __init__(self, *, hidden: int, n_experts: int, top_k: int, expert_ffn: int, gate_type: str, down_type: str,
                  max_tokens: int, shared_ffn: int = 0, shared_type: str = "", shared_gated: bool = False,
-                 gating: str = "softmax"):
+                 gating: str = "softmax", norm_eps: float = 0.0, residual: bool = False):
+        """norm_eps > 0: x is first RMS-normalised by the uploaded ``ffn_norm`` (the steps before the block's router);
+        residual: y += x (the block's residual add after the combine)."""
         assert gating in ("softmax", "sigmoid"), gating
         self.H, self.E, self.k, self.F = hidden, n_experts, top_k, expert_ffn
         self.max_tokens = max_tokens
         d = _hip.Desc(hidden=hidden, n_experts=n_experts, top_k=top_k, expert_ffn=expert_ffn,
                       gate_type=TYPE_ID[gate_type], down_type=TYPE_ID[down_type], shared_ffn=shared_ffn,
                       shared_type=TYPE_ID[shared_type] if shared_ffn else 0, shared_gated=int(shared_gated),
-                      gating=int(gating == "sigmoid"), max_tokens=max_tokens)
+                      gating=int(gating == "sigmoid"), max_tokens=max_tokens, norm_eps=norm_eps,
+                      residual=int(residual))
         h = ctypes.c_void_p()
         _hip.check(_hip.lib().artlite_moe_layer_create(ctypes.byref(d), ctypes.byref(h)))
         self._h = h
@@ -58,12 +62,13 @@ class MoELayer:
         self.close()
 
     @classmethod
-    def from_gguf(cls, gguf: "GGUFFile", block: int, *, max_tokens: int) -> "MoELayer":
+    def from_gguf(cls, gguf: "GGUFFile", block: int, *, max_tokens: int, norm: bool = False) -> "MoELayer":
         """Block ``block``'s MoE FFN of a GGUF file (``gguf_model.GGUFFile``): its shape from the architecture's
         metadata (``embedding_length``, ``expert_count``, ``expert_used_count``, ``expert_feed_forward_length``,
         ``expert_shared_feed_forward_length``, ``expert_gating_func``: 2 sigmoid, else softmax; the reference's
         ``model_config.py:735-766``), its tensors ``blk.{block}.ffn_*`` uploaded as the file holds them (the router
-        and a shared gate converted to fp32 exactly when stored as F16 / BF16)."""
+        and a shared gate converted to fp32 exactly when stored as F16 / BF16). norm: with the steps either side,
+        the block's ``ffn_norm`` (RMS, eps ``attention.layer_norm_rms_epsilon``) before and the residual add after."""
         b = f"blk.{block}."
         m = gguf.arch_meta
         need = [b + n + ".weight" for n in ("ffn_gate_inp", "ffn_gate_exps", "ffn_up_exps", "ffn_down_exps")]
@@ -85,10 +90,14 @@ class MoELayer:
             sF = int(m("expert_shared_feed_forward_length", sdims[1]))
         gated = b + "ffn_gate_inp_shexp.weight" in gguf
         gating = "sigmoid" if int(m("expert_gating_func", 1)) == 2 else "softmax"
+        eps = float(m("attention.layer_norm_rms_epsilon", 1e-6)) if norm else 0.0
+        if norm and b + "ffn_norm.weight" not in gguf:
+            raise ValueError(f"{gguf.path}: block {block} has no ffn_norm")
         layer = cls(hidden=H, n_experts=E, top_k=k, expert_ffn=F, gate_type=gtype, down_type=dtype,
-                    max_tokens=max_tokens, shared_ffn=sF, shared_type=stype, shared_gated=gated, gating=gating)
+                    max_tokens=max_tokens, shared_ffn=sF, shared_type=stype, shared_gated=gated, gating=gating,
+                    norm_eps=eps, residual=norm)
         try:
-            for name in ("ffn_gate_inp", "ffn_gate_inp_shexp"):
+            for name in ("ffn_gate_inp", "ffn_gate_inp_shexp") + (("ffn_norm",) if norm else ()):
                 if b + name + ".weight" in gguf:
                     t = gguf.tensor(b + name + ".weight")
                     raw = t.raw if t.qtype != "BF16" else (t.raw.astype(np.uint32) << 16).view(np.float32)
@@ -144,12 +153,12 @@ class MoELayer:
 
     def tap(self, name: str) -> np.ndarray:
         """An intermediate result of the last run: logits (T, E), ids / weights (T, k), counts (E,), offsets (E + 1,),
-        order / slot (T k,), h (T k, F) (sorted pairs), y_pairs (T k, H) (sorted pairs)."""
+        order / slot (T k,), h (T k, F) (sorted pairs), y_pairs (T k, H) (sorted pairs), x_norm (T, H)."""
         T, k, E = self.T, self.k, self.E
         shape, dtype = {"logits": ((T, E), np.float32), "ids": ((T, k), np.int32), "weights": ((T, k), np.float32),
                         "counts": ((E,), np.int32), "offsets": ((E + 1,), np.int32), "order": ((T * k,), np.int32),
                         "slot": ((T * k,), np.int32), "h": ((T * k, self.F), np.float32),
-                        "y_pairs": ((T * k, self.H), np.float32)}[name]
+                        "y_pairs": ((T * k, self.H), np.float32), "x_norm": ((T, self.H), np.float32)}[name]
         out = np.empty(shape, dtype)
         _hip.check(_hip.lib().artlite_moe_layer_tap(self.handle, TAPS[name], out.ctypes.data, out.nbytes))
         return out

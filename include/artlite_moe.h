@@ -82,6 +82,10 @@ typedef struct artlite_moe_desc {
   int32_t shared_gated; /* 1: the shared expert times sigmoid(x . ffn_gate_inp_shexp) */
   int32_t gating;       /* 0: softmax, 1: sigmoid */
   int32_t max_tokens;   /* the most tokens of one call */
+  float norm_eps;       /* > 0: x is first RMS-normalised by ffn_norm, x / sqrt(mean(x^2) + eps) * w (the steps
+                           before the block's router: llama.cpp's ffn_norm, the reference's tests/np_ops.py:27-32);
+                           0: none */
+  int32_t residual;     /* 1: y += x (the block's residual add after the combine, x as given, before any norm) */
 } artlite_moe_desc;
 
 /* Tensors of artlite_moe_layer_upload, as laid out in a GGUF file. */
@@ -94,6 +98,7 @@ enum artlite_tensor {
   ARTLITE_UP_SHEXP = 5,
   ARTLITE_DOWN_SHEXP = 6,  /* H rows of Fs */
   ARTLITE_GATE_INP_SHEXP = 7, /* H fp32 */
+  ARTLITE_FFN_NORM = 8,    /* ffn_norm: H fp32 (with norm_eps > 0) */
 };
 
 /* Activation dtypes. */
@@ -122,8 +127,9 @@ enum artlite_tap {
   ARTLITE_TAP_OFFSETS = 4, /* E + 1 int32: exclusive prefix of counts */
   ARTLITE_TAP_ORDER = 5,   /* T k int32: pair indices t k + i sorted by expert, pair order within an expert */
   ARTLITE_TAP_SLOT = 6,    /* T k int32: each pair's position in that order */
-  ARTLITE_TAP_H = 7,       /* T k x F fp32: silu(gate) up of each sorted pair (bf16 hi + lo) */
+  ARTLITE_TAP_H = 7,       /* T k x F fp32: silu(gate) up of each sorted pair (as the run's path holds it) */
   ARTLITE_TAP_Y = 8,       /* T k x H fp32: each sorted pair's expert output (before the weights) */
+  ARTLITE_TAP_XN = 9,      /* T x H fp32: the RMS-normalised x (norm_eps > 0) */
 };
 int artlite_moe_layer_tap(artlite_moe_layer* layer, int tap, void* out, size_t nbytes);
 

@@ -251,3 +251,27 @@ def test_zipf_config_routing() -> None:
     ids, _ = moe_ref.moe_route(layers.logits(layer, x), spec.k)
     c = np.bincount(ids.ravel(), minlength=spec.E)
     assert (c == 0).sum() == 6 and 0.4 < np.sort(c)[::-1][:4].sum() / c.sum() < 0.6
+
+
+def test_rms_norm_pins() -> None:
+    """rms_norm (tests/np_ops.py:27-32 restated): closed forms and a per-element float64 loop."""
+    # a constant row c: c / sqrt(c^2 + eps), then times w
+    for c in (3.0, -0.5, 1e-3):
+        x = np.full((1, 64), c, np.float32)
+        w = np.linspace(0.5, 1.5, 64).astype(np.float32)
+        want = np.float32(np.float64(np.float32(c)) / np.sqrt(np.float64(np.float32(c)) ** 2 + 1e-6)) * w
+        assert np.array_equal(np_ops.rms_norm(x, w, 1e-6), want[None])
+    # zeros stay zeros; eps = 0 makes the row's RMS exactly 1 (up to one rounding)
+    assert not np_ops.rms_norm(np.zeros((2, 8), np.float32), None, 1e-5).any()
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((5, 96)).astype(np.float32) * 7
+    y = np_ops.rms_norm(x, None, 0.0).astype(np.float64)
+    assert np.allclose(np.sqrt((y ** 2).mean(1)), 1.0, rtol=1e-6)
+    # per element: the float64 mean of squares, the quotient in float64 rounded once, then the fp32 product
+    w = rng.uniform(0.5, 1.5, 96).astype(np.float32)
+    got = np_ops.rms_norm(x, w, 1e-6)
+    for t in range(5):
+        ms = sum(float(v) * float(v) for v in x[t].astype(np.float64)) / 96
+        d = np.sqrt(ms + 1e-6)
+        for i in range(96):
+            assert got[t, i] == np.float32(np.float32(np.float64(x[t, i]) / d) * w[i])
