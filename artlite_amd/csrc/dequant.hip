@@ -1,92 +1,132 @@
 // GGUF rows dequantized on the GPU to the reference's fp32 values bit for bit (reference
-// csrc/artlite/dequant.cpp:21-82, gguf_model.QTensor.dequantize): one thread per block, the reference's fp32
-// operations in its order, no fused multiply-add (this file is compiled with -ffp-contract=off, and the Q4_K
-// products and difference are explicit round-to-nearest operations as well); the C entry points
+// csrc/artlite/dequant.cpp:21-160, gguf_model.QTensor.dequantize): the reference's native types (F32, F16, BF16,
+// Q4_0, Q4_1, Q8_0, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS). One thread per output value: the value's fields are
+// read from its block (the neighbouring threads read the same block, so the reads stay in L1 / L2) and combined by
+// the reference's fp32 operations in its order, each rounded on its own (explicit round-to-nearest operations, and
+// this file is compiled with -ffp-contract=off); the writes are coalesced rows of fp32. The C entry points
 // artlite_dequant_supported / artlite_dequant_rows.
 #include "common.h"
 
 namespace artlite {
 
+namespace {
+
 __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) { return uint32_t(p[0]) | (uint32_t(p[1]) << 8); }
 
-// Q4_0 (18 B per 32): w = (q - 8) d, values 0..15 the low nibbles of bytes 2.., 16..31 the high nibbles
-__device__ __forceinline__ void block_q4_0(const uint8_t* b, float* o) {
-  const float d = f16_to_f32(ld_u16(b));
-#pragma unroll
-  for (int j = 0; j < 16; j++) {
-    const uint32_t c = b[2 + j];
-    o[j] = __fmul_rn(float(c & 15u) - 8.0f, d);
-    o[j + 16] = __fmul_rn(float(c >> 4) - 8.0f, d);
+// a 32-value group's code j in Q4_0's order: the low nibbles of its 16 bytes are values 0..15, the high nibbles 16..31
+__device__ __forceinline__ uint32_t nibble32(const uint8_t* q, int j) {
+  return j < 16 ? q[j] & 15u : uint32_t(q[j - 16]) >> 4;
+}
+
+// IQ4_NL / IQ4_XS's 16 values (ggml's kvalues_iq4nl; reference dequant.cpp:121)
+__constant__ int8_t IQ4_VALUES[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+// Q4_K / Q5_K's 6-bit scale and min of group g (of 8) from the 12 bytes at s: groups 0..3 in the low 6 bits of
+// bytes 0..3 (scales) and 4..7 (mins); groups 4..7 a nibble of bytes 8..11 plus the top two bits of bytes 0..7
+__device__ __forceinline__ void k_scale_min(const uint8_t* s, int g, int& sc, int& mn) {
+  if (g < 4) {
+    sc = s[g] & 63;
+    mn = s[4 + g] & 63;
+  } else {
+    sc = (s[8 + g - 4] & 15) | ((s[g - 4] >> 6) << 4);
+    mn = (s[8 + g - 4] >> 4) | ((s[4 + g - 4] >> 6) << 4);
   }
 }
 
-// Q8_0 (34 B per 32): w = d q, q int8
-__device__ __forceinline__ void block_q8_0(const uint8_t* b, float* o) {
-  const float d = f16_to_f32(ld_u16(b));
-#pragma unroll
-  for (int j = 0; j < 32; j++) o[j] = __fmul_rn(d, float(int8_t(b[2 + j])));
-}
-
-// Q4_K (144 B per 256): w = q (d sc_g) - dmin mn_g, 8 groups of 32 (6-bit sc / mn in the 12 bytes at 4; group g's
-// value l at byte 16 + 32 (g / 2) + l, the low nibble for even g)
-__device__ __forceinline__ void block_q4_k(const uint8_t* b, float* o) {
-  const float d = f16_to_f32(ld_u16(b)), dmin = f16_to_f32(ld_u16(b + 2));
-  const uint8_t *lo = b + 4, *hi = b + 8, *top = b + 12, *qs = b + 16;
-  for (int g = 0; g < 8; g++) {
-    const int sc = g < 4 ? lo[g] & 63 : (top[g - 4] & 15) | ((lo[g - 4] >> 6) << 4);
-    const int mn = g < 4 ? hi[g] & 63 : (top[g - 4] >> 4) | ((hi[g - 4] >> 6) << 4);
-    const float dsc = __fmul_rn(d, float(sc)), dmn = __fmul_rn(dmin, float(mn));
-    for (int l = 0; l < 32; l++) {
-      const uint32_t c = qs[32 * (g >> 1) + l];
-      const float t = __fmul_rn(float((g & 1) ? c >> 4 : c & 15u), dsc);
-      o[32 * g + l] = __fsub_rn(t, dmn);
-    }
-  }
-}
-
+// value j of the block at b, as the reference computes it (dequant.cpp line ranges per format)
 template <int QT>
-__global__ void k_dequant(const uint8_t* __restrict__ raw, size_t n, size_t row_bytes, size_t blocks_per_row,
-                          float* __restrict__ out, size_t cols) {
-  const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= n * blocks_per_row) return;
-  const size_t r = i / blocks_per_row, k = i % blocks_per_row;
-  const uint8_t* row = raw + r * row_bytes;
-  float* o = out + r * cols;
-  if (QT == ARTLITE_Q4_0) {
-    float v[32];
-    block_q4_0(row + k * 18, v);
-    for (int j = 0; j < 32; j++) o[k * 32 + j] = v[j];
-  } else if (QT == ARTLITE_Q8_0) {
-    float v[32];
-    block_q8_0(row + k * 34, v);
-    for (int j = 0; j < 32; j++) o[k * 32 + j] = v[j];
-  } else if (QT == ARTLITE_Q4_K) {
-    block_q4_k(row + k * 144, o + k * 256);
-  } else if (QT == ARTLITE_F32) {
-    const uint8_t* p = row + 4 * k;
-    o[k] = __uint_as_float(uint32_t(p[0]) | uint32_t(p[1]) << 8 | uint32_t(p[2]) << 16 | uint32_t(p[3]) << 24);
-  } else if (QT == ARTLITE_F16) {
-    o[k] = f16_to_f32(ld_u16(row + 2 * k));
+__device__ __forceinline__ float value(const uint8_t* b, int j) {
+  if constexpr (QT == ARTLITE_Q4_0) {  // (q - 8) d (:41-48)
+    return __fmul_rn(float(nibble32(b + 2, j)) - 8.0f, f16_to_f32(ld_u16(b)));
+  } else if constexpr (QT == ARTLITE_Q4_1) {  // d q + m (:50-57)
+    return __fadd_rn(__fmul_rn(f16_to_f32(ld_u16(b)), float(nibble32(b + 4, j))), f16_to_f32(ld_u16(b + 2)));
+  } else if constexpr (QT == ARTLITE_Q8_0) {  // d q, q int8 (:59-63)
+    return __fmul_rn(f16_to_f32(ld_u16(b)), float(int8_t(b[2 + j])));
+  } else if constexpr (QT == ARTLITE_Q4_K || QT == ARTLITE_Q5_K) {  // q (d sc_g) - dmin mn_g (:65-84)
+    const int g = j >> 5, l = j & 31;
+    int sc, mn;
+    k_scale_min(b + 4, g, sc, mn);
+    const float dsc = __fmul_rn(f16_to_f32(ld_u16(b)), float(sc));
+    const float dmn = __fmul_rn(f16_to_f32(ld_u16(b + 2)), float(mn));
+    const uint8_t* qs = b + (QT == ARTLITE_Q5_K ? 48 : 16);
+    const uint32_t c = qs[32 * (g >> 1) + l];
+    uint32_t q = (g & 1) ? c >> 4 : c & 15u;
+    if constexpr (QT == ARTLITE_Q5_K) q |= ((uint32_t(b[16 + l]) >> g) & 1u) << 4;  // (qh at 16)
+    return __fsub_rn(__fmul_rn(float(q), dsc), dmn);
+  } else if constexpr (QT == ARTLITE_Q6_K) {  // (q - 32) (sc_j d), value 128 h + 32 jj + l (:86-106)
+    const int h = j >> 7, jj = (j >> 5) & 3, l = j & 31;
+    const uint32_t c = b[64 * h + 32 * (jj & 1) + l], e = b[128 + 32 * h + l];
+    const int q = int(((c >> (jj < 2 ? 0 : 4)) & 15u) | (((e >> (2 * jj)) & 3u) << 4)) - 32;
+    const float s = __fmul_rn(float(int8_t(b[192 + (j >> 4)])), f16_to_f32(ld_u16(b + 208)));
+    return __fmul_rn(float(q), s);
+  } else if constexpr (QT == ARTLITE_Q3_K) {  // (d sc_j) (q - 4), value 128 n + 32 jj + 16 h + l (:108-123)
+    const int n = j >> 7, jj = (j >> 5) & 3, hl = j & 31, sb = j >> 4;
+    const uint8_t* s = b + 96;
+    const int lo = sb < 8 ? s[sb] & 15 : s[sb - 8] >> 4, hi = (s[8 + (sb & 3)] >> (2 * (sb >> 2))) & 3;
+    const int q = ((b[32 + 32 * n + hl] >> (2 * jj)) & 3) | (((b[hl] >> (4 * n + jj)) & 1) << 2);
+    const float a = __fmul_rn(f16_to_f32(ld_u16(b + 108)), float((lo | (hi << 4)) - 32));
+    return __fmul_rn(a, float(q) - 4.0f);
+  } else if constexpr (QT == ARTLITE_IQ4_NL) {  // d IQ4[q] (:126-130)
+    return __fmul_rn(f16_to_f32(ld_u16(b)), float(IQ4_VALUES[nibble32(b + 2, j)]));
+  } else if constexpr (QT == ARTLITE_IQ4_XS) {  // (d (ls_g - 32)) IQ4[q] (:132-143)
+    const int g = j >> 5;
+    const int ls = ((b[4 + g / 2] >> (4 * (g & 1))) & 15) | (((int(ld_u16(b + 2)) >> (2 * g)) & 3) << 4);
+    const float dl = __fmul_rn(f16_to_f32(ld_u16(b)), float(ls - 32));
+    return __fmul_rn(dl, float(IQ4_VALUES[nibble32(b + 8 + 16 * g, j & 31)]));
+  } else if constexpr (QT == ARTLITE_F32) {
+    return __uint_as_float(uint32_t(b[0]) | uint32_t(b[1]) << 8 | uint32_t(b[2]) << 16 | uint32_t(b[3]) << 24);
+  } else if constexpr (QT == ARTLITE_F16) {
+    return f16_to_f32(ld_u16(b));
   } else {  // BF16: the high half of the fp32 value
-    o[k] = bf16_to_f32(ld_u16(row + 2 * k));
+    return bf16_to_f32(ld_u16(b));
   }
 }
+
+constexpr int CHUNK = 1024;  // values of a row per workgroup pass
+
+// workgroup pass i takes values [c0, c0 + CHUNK) of row r (i = r chunks_per_row + c0 / CHUNK), a value per thread
+template <int QT, int PER, int BYTES>
+__global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ raw, size_t n, size_t row_bytes,
+                                                 size_t cols, float* __restrict__ out) {
+  const size_t cpr = (cols + CHUNK - 1) / CHUNK;
+  for (size_t i = blockIdx.x; i < n * cpr; i += gridDim.x) {
+    const size_t r = i / cpr, c0 = (i % cpr) * CHUNK;
+    const uint8_t* row = raw + r * row_bytes;
+    float* o = out + r * cols;
+    for (size_t c = c0 + threadIdx.x; c < c0 + CHUNK && c < cols; c += 256)
+      o[c] = value<QT>(row + (c / PER) * BYTES, int(c % PER));
+  }
+}
+
+template <int QT, int PER, int BYTES>
+int launch_t(const uint8_t* raw, size_t n, size_t row_bytes, size_t cols, float* out, hipStream_t s) {
+  const size_t passes = n * ((cols + CHUNK - 1) / CHUNK);
+  const unsigned grid = unsigned(passes < 65536 ? passes : 65536);
+  k_dequant<QT, PER, BYTES><<<grid, 256, 0, s>>>(raw, n, row_bytes, cols, out);
+  ART_HIP(hipGetLastError());
+  return ARTLITE_OK;
+}
+
+}  // namespace
 
 int launch_dequant(const QType* t, const uint8_t* raw, size_t n, size_t row_bytes, size_t cols, float* out,
                    hipStream_t s) {
-  const size_t bpr = cols / t->per, total = n * bpr;
-  if (!total) return ARTLITE_OK;
-  const dim3 grid(unsigned((total + 255) / 256)), block(256);
+  if (!n || !cols) return ARTLITE_OK;
   switch (t->id) {
-    case ARTLITE_Q4_0: k_dequant<ARTLITE_Q4_0><<<grid, block, 0, s>>>(raw, n, row_bytes, bpr, out, cols); break;
-    case ARTLITE_Q8_0: k_dequant<ARTLITE_Q8_0><<<grid, block, 0, s>>>(raw, n, row_bytes, bpr, out, cols); break;
-    case ARTLITE_Q4_K: k_dequant<ARTLITE_Q4_K><<<grid, block, 0, s>>>(raw, n, row_bytes, bpr, out, cols); break;
-    case ARTLITE_F32: k_dequant<ARTLITE_F32><<<grid, block, 0, s>>>(raw, n, row_bytes, bpr, out, cols); break;
-    case ARTLITE_F16: k_dequant<ARTLITE_F16><<<grid, block, 0, s>>>(raw, n, row_bytes, bpr, out, cols); break;
-    default: k_dequant<ARTLITE_BF16><<<grid, block, 0, s>>>(raw, n, row_bytes, bpr, out, cols); break;
+    case ARTLITE_F32: return launch_t<ARTLITE_F32, 1, 4>(raw, n, row_bytes, cols, out, s);
+    case ARTLITE_F16: return launch_t<ARTLITE_F16, 1, 2>(raw, n, row_bytes, cols, out, s);
+    case ARTLITE_BF16: return launch_t<ARTLITE_BF16, 1, 2>(raw, n, row_bytes, cols, out, s);
+    case ARTLITE_Q4_0: return launch_t<ARTLITE_Q4_0, 32, 18>(raw, n, row_bytes, cols, out, s);
+    case ARTLITE_Q4_1: return launch_t<ARTLITE_Q4_1, 32, 20>(raw, n, row_bytes, cols, out, s);
+    case ARTLITE_Q8_0: return launch_t<ARTLITE_Q8_0, 32, 34>(raw, n, row_bytes, cols, out, s);
+    case ARTLITE_Q3_K: return launch_t<ARTLITE_Q3_K, 256, 110>(raw, n, row_bytes, cols, out, s);
+    case ARTLITE_Q4_K: return launch_t<ARTLITE_Q4_K, 256, 144>(raw, n, row_bytes, cols, out, s);
+    case ARTLITE_Q5_K: return launch_t<ARTLITE_Q5_K, 256, 176>(raw, n, row_bytes, cols, out, s);
+    case ARTLITE_Q6_K: return launch_t<ARTLITE_Q6_K, 256, 210>(raw, n, row_bytes, cols, out, s);
+    case ARTLITE_IQ4_NL: return launch_t<ARTLITE_IQ4_NL, 32, 18>(raw, n, row_bytes, cols, out, s);
+    case ARTLITE_IQ4_XS: return launch_t<ARTLITE_IQ4_XS, 256, 136>(raw, n, row_bytes, cols, out, s);
+    default: return fail(ARTLITE_EINVAL, "dequant: type %d", t->id);
   }
-  ART_HIP(hipGetLastError());
-  return ARTLITE_OK;
 }
 
 }  // namespace artlite

@@ -3,8 +3,9 @@ the ggml block table, ``QTensor`` (raw blocks, ``dequantize`` on the GPU), ``deq
 (the reference's ``_native`` entry points), and ``GGUFFile``, a reader of the file's memory map (metadata, tensor
 infos, ``tensor``, ``rows``) that feeds ``moe.layer.MoELayer.upload``.
 
-Dequantization runs in ``libartlite_moe`` (Q4_0, Q8_0, Q4_K, F32, F16, BF16), bit for bit the reference's fp32
-values; other ggml types are listed but not read (``NotImplementedError``, as the reference does for unknown types)."""
+Dequantization runs in ``libartlite_moe`` for the types the reference's native dequantizer takes (F32, F16, BF16,
+Q4_0, Q4_1, Q8_0, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS), bit for bit the reference's fp32 values; other ggml types
+are listed but not read (``NotImplementedError``, as the reference does for unknown types)."""
 
 import math
 import struct

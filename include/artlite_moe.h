@@ -24,8 +24,9 @@ enum artlite_status {
 };
 
 /* ggml tensor type ids of the supported weight formats (src/artlite/gguf_model.py:385-390 of the reference) */
-enum artlite_qtype { ARTLITE_F32 = 0, ARTLITE_F16 = 1, ARTLITE_Q4_0 = 2, ARTLITE_Q8_0 = 8, ARTLITE_Q4_K = 12,
-                     ARTLITE_BF16 = 30 };
+enum artlite_qtype { ARTLITE_F32 = 0, ARTLITE_F16 = 1, ARTLITE_Q4_0 = 2, ARTLITE_Q4_1 = 3, ARTLITE_Q8_0 = 8,
+                     ARTLITE_Q3_K = 11, ARTLITE_Q4_K = 12, ARTLITE_Q5_K = 13, ARTLITE_Q6_K = 14, ARTLITE_IQ4_NL = 20,
+                     ARTLITE_IQ4_XS = 23, ARTLITE_BF16 = 30 };
 
 /* The calling thread's last error message into buf (NUL-terminated, truncated to cap); returns its full length. */
 size_t artlite_last_error(char* buf, size_t cap);
@@ -59,8 +60,9 @@ int artlite_moe_plan(const int32_t* ids, int64_t n, int k, int E, int cols, int 
                      int32_t* counts, int32_t* sizes, int32_t* rows, int64_t* pos);
 
 /* ---- dequantization: replaces _native.dequant_supported / dequant_rows (reference csrc/bindings/gguf.cpp:62-76 ->
- * artlite::dequant_rows, csrc/artlite/dequant.h:12-17). n rows of qtype ("Q4_0", "Q8_0", "Q4_K", "F32", "F16",
- * "BF16"), row_bytes apart in raw, into out (n x cols fp32): the reference's fp32 values bit for bit. */
+ * artlite::dequant_rows, csrc/artlite/dequant.h:12-17). n rows of qtype (the reference's native types: "F32", "F16",
+ * "BF16", "Q4_0", "Q4_1", "Q8_0", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "IQ4_NL", "IQ4_XS"), row_bytes apart in raw, into
+ * out (n x cols fp32): the reference's fp32 values bit for bit. */
 int artlite_dequant_supported(const char* qtype);
 int artlite_dequant_rows(const char* qtype, const uint8_t* raw, size_t n, size_t row_bytes, size_t cols, float* out);
 

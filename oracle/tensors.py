@@ -10,7 +10,9 @@ import numpy as np
 
 from .gguf_ref import BLOCKS
 
-F16_OFFSETS = {"Q4_0": (0,), "Q8_0": (0,), "Q4_K": (0, 2)}  # (``tests/tensors.py:9-12``)
+# the offsets of each block type's fp16 fields (``tests/tensors.py:9-12``)
+F16_OFFSETS = {"Q4_0": (0,), "Q4_1": (0, 2), "Q8_0": (0,), "Q3_K": (108,), "Q4_K": (0, 2), "Q5_K": (0, 2),
+               "Q6_K": (208,), "IQ4_NL": (0,), "IQ4_XS": (0,)}
 
 
 def random_blocks(qtype: str, rows: int, cols: int, seed: int | np.random.Generator, *, scale: float = 0.01,

@@ -19,7 +19,10 @@ def _same_bits(a: np.ndarray, b: np.ndarray) -> bool:
     return bool(np.array_equal(na, nb) and np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32)))
 
 
-@pytest.mark.parametrize("qtype", ["Q4_0", "Q8_0", "Q4_K"])
+QTYPES = ("Q4_0", "Q4_1", "Q8_0", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "IQ4_NL", "IQ4_XS")
+
+
+@pytest.mark.parametrize("qtype", QTYPES)
 def test_dequant_golden(qtype: str) -> None:
     z = np.load(GOLDEN)
     cols = int(z["cols"])
@@ -29,7 +32,7 @@ def test_dequant_golden(qtype: str) -> None:
     assert _same_bits(out, z[f"out_{qtype}"].view(np.float32))
 
 
-@pytest.mark.parametrize("qtype", ["Q4_0", "Q8_0", "Q4_K"])
+@pytest.mark.parametrize("qtype", QTYPES)
 def test_dequant_rows(qtype: str) -> None:
     """The reference's test: 33 x 1024 random blocks (seed 1), bit-identical; and a row subset of fewer columns."""
     raw = tensors.random_blocks(qtype, 33, 1024, 1)
@@ -51,8 +54,9 @@ def test_dequant_plain_types() -> None:
 
 
 def test_dequant_errors() -> None:
-    assert gguf_model.dequant_supported("Q4_0") and not gguf_model.dequant_supported("IQ2_XS")
-    with pytest.raises(Error, match="no native Q5_K"):
-        gguf_model.dequant_rows("Q5_K", np.zeros((1, 176), np.uint8), np.empty((1, 256), np.float32))
+    assert all(gguf_model.dequant_supported(q) for q in QTYPES + ("F32", "F16", "BF16"))
+    assert not gguf_model.dequant_supported("IQ2_XS") and not gguf_model.dequant_supported("Q2_K")
+    with pytest.raises(Error, match="no native Q2_K"):
+        gguf_model.dequant_rows("Q2_K", np.zeros((1, 84), np.uint8), np.empty((1, 256), np.float32))
     with pytest.raises(Error, match="64 columns of rows of 18 B"):
         gguf_model.dequant_rows("Q4_0", np.zeros((1, 18), np.uint8), np.empty((1, 64), np.float32))

@@ -12,7 +12,7 @@ import pytest
 from oracle import gguf_ref, host_ref, layers, moe_ref, np_ops, ref_lib, tensors
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "dequant_golden.npz"
-QTYPES = ("Q4_0", "Q8_0", "Q4_K")
+QTYPES = ("Q4_0", "Q4_1", "Q8_0", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "IQ4_NL", "IQ4_XS")
 
 
 def _same_bits(a: np.ndarray, b: np.ndarray) -> bool:
@@ -66,6 +66,56 @@ def test_dequant_closed_forms() -> None:
     w = gguf_ref.dequantize("Q4_K", b, 256)[0].reshape(8, 32)
     want = [(1 if g % 2 == 0 else 2) * sc[g] - 0.5 * mn[g] for g in range(8)]
     assert np.array_equal(w, np.repeat(np.array(want, np.float32)[:, None], 32, 1))
+
+
+def _f16_bytes(*v: float) -> np.ndarray:
+    return np.array(v, np.float16).view(np.uint8)
+
+
+def test_dequant_closed_forms_more_types() -> None:
+    """Q4_1's added min, Q5_K's fifth bit (bit g of qh[l]), Q6_K's crumb order, offset 32 and int8 sub-block scales,
+    Q3_K's offset 4, high bit (hmask bit 4 n + j) and scales - 32, IQ4's table and IQ4_XS's 6-bit group scales, each on
+    a hand-built block whose values the formats' layout fixes."""
+    b = np.zeros((1, 20), np.uint8)
+    b[0, :4] = _f16_bytes(2.0, -1.0)
+    b[0, 4:] = np.arange(16, dtype=np.uint8) | (15 << 4)
+    assert gguf_ref.dequantize("Q4_1", b, 32)[0].tolist() == [2.0 * q - 1 for q in range(16)] + [29.0] * 16
+    b = np.zeros((1, 176), np.uint8)
+    b[0, :4] = _f16_bytes(1.0, 0.0)
+    b[0, 4:8] = 1  # groups 0..3: scale 1 (groups 4..7: 0)
+    b[0, 16:48] = 0b00000010  # the fifth bit for group 1 only
+    b[0, 48:] = 0x53  # group 0 (low nibble) 3, group 1 (high) 5 | 16
+    w = gguf_ref.dequantize("Q5_K", b, 256)[0].reshape(8, 32)
+    assert w[0].tolist() == [3.0] * 32 and w[1].tolist() == [21.0] * 32 and w[2:4].tolist() == [[3.0] * 32, [5.0] * 32]
+    assert not w[4:].any()
+    b = np.zeros((1, 210), np.uint8)
+    b[0, 208:] = _f16_bytes(0.5)
+    b[0, 192:208] = np.arange(-8, 8, dtype=np.int8).view(np.uint8)  # sub-block j: scale j - 8
+    b[0, 0:128] = 0x21  # low nibble 1 (jj 0, 1), high nibble 2 (jj 2, 3)
+    b[0, 128:192] = 0b11100100  # crumb jj = jj
+    w = gguf_ref.dequantize("Q6_K", b, 256)[0].reshape(16, 16)
+    want = [((1 if (j % 8) // 2 < 2 else 2) + 16 * ((j % 8) // 2) - 32) * 0.5 * (j - 8) for j in range(16)]
+    assert np.array_equal(w, np.repeat(np.array(want, np.float32)[:, None], 16, 1))
+    b = np.zeros((1, 110), np.uint8)
+    b[0, 108:] = _f16_bytes(1.0)
+    b[0, 96:104] = 0x21  # sub-blocks 0..7: low nibble 1, 8..15: 2 (no high crumbs): scales - 32
+    b[0, 32:96] = 0b11100100  # crumb j = j
+    b[0, 0:32] = 0x0F  # the high bit for n = 0 (bits 0..3), not for n = 1
+    w = gguf_ref.dequantize("Q3_K", b, 256)[0].reshape(16, 16)  # sub-block 2 (4 n + j) + h
+    want = [((j // 2) % 4 + (4 if j < 8 else 0) - 4) * ((1 if j < 8 else 2) - 32) for j in range(16)]
+    assert np.array_equal(w, np.repeat(np.array(want, np.float32)[:, None], 16, 1))
+    b = np.zeros((1, 18), np.uint8)
+    b[0, :2] = _f16_bytes(1.0)
+    b[0, 2:] = np.arange(16, dtype=np.uint8) | (np.arange(16, dtype=np.uint8)[::-1] << 4)
+    iq4 = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
+    assert gguf_ref.dequantize("IQ4_NL", b, 32)[0].tolist() == iq4 + iq4[::-1]
+    b = np.zeros((1, 136), np.uint8)
+    b[0, :2] = _f16_bytes(0.25)
+    b[0, 2:4] = np.array([0b1110010011100100], np.uint16).view(np.uint8)  # crumb g = g % 4
+    b[0, 4:8] = [0x10, 0x32, 0x54, 0x76]  # nibble g = g
+    b[0, 8:] = 0x88  # code 8: IQ4 value 1
+    w = gguf_ref.dequantize("IQ4_XS", b, 256)[0].reshape(8, 32)
+    assert w.tolist() == [[0.25 * (g + 16 * (g % 4) - 32)] * 32 for g in range(8)]
 
 
 def test_dequant_subnormal_scales() -> None:
