@@ -31,7 +31,8 @@ class Desc(ctypes.Structure):
 
     _fields_ = [(name, ctypes.c_int32) for name in (
         "hidden", "n_experts", "top_k", "expert_ffn", "gate_type", "down_type", "shared_ffn", "shared_type",
-        "shared_gated", "gating", "max_tokens")] + [("norm_eps", ctypes.c_float), ("residual", ctypes.c_int32)]
+        "shared_gated", "gating", "max_tokens")] + [("norm_eps", ctypes.c_float), ("residual", ctypes.c_int32),
+                                                    ("shared_down_type", ctypes.c_int32)]
 
 
 # every exported function: (restype, argtypes)

@@ -106,5 +106,10 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 }
 
 constexpr int WAVE = 64;
+constexpr int LDS_BYTES = 160 * 1024;  // a gfx950 workgroup's LDS
+
+// bytes past the end of an uploaded weight tensor that the expert kernels' loads may touch (zeros): a K-range's
+// 16-byte-aligned cover of a row's last partial run
+constexpr int WEIGHT_TAIL = 1024;
 
 }  // namespace artlite

@@ -60,90 +60,179 @@ __device__ __forceinline__ u32x4 byte8(uint32_t v0, uint32_t v1) {
   return u32x4{byte2(v0, 0), byte2(v0, 1), byte2(v1, 0), byte2(v1, 1)};
 }
 
-// Per format: bytes per 32-value group (in a run of whole blocks), the 32-value groups of one K-range (a stage:
-// ~560 bytes of each row, so a 16-row stage is 16 long runs; a straddled cache line is read again by the next range
-// of the same wave, from L2), the offset of the codes' bf16 encoding.
+// Per format: a block's bytes and 32-value groups; the groups of one K-range (a stage: ~300..600 bytes of each row,
+// so a 16-row stage is 16 long runs; a straddled cache line is read again by the next range of the same wave, from
+// L2) and its bytes; the offset of the codes' bf16 encoding (the B operand holds 128 + c for a code byte c, or
+// 128 + IQ4[c], so OFF = 128 + the format's zero point); whether the format has a min term (w = s q - m: Q4_1,
+// Q4_K, Q5_K); whether its scales cover 16 values (Q3_K, Q6_K: one MFMA per half of a group, each with the other
+// half's B lanes zero).
+template <int BB, int GPB_, int KR_, int OFF_, bool MIN_ = false, bool SUB16_ = false>
+struct FmtT {
+  static constexpr int BLOCK_BYTES = BB;
+  static constexpr int GPB = GPB_;  // 32-value groups per block (1 or 8)
+  static constexpr int GROUP_BYTES = GPB_ == 1 ? BB : 0;  // (32-value blocks only)
+  static constexpr int KR = KR_;
+  static constexpr int RUN = KR_ / GPB_ * BB;  // bytes of a row's K-range
+  static constexpr float OFF = float(OFF_);
+  static constexpr bool MIN = MIN_;
+  static constexpr bool SUB16 = SUB16_;
+  static_assert(KR_ % GPB_ == 0, "K-ranges of whole blocks");
+};
 template <int QT>
 struct Fmt;
 template <>
-struct Fmt<ARTLITE_Q4_0> {
-  static constexpr int GROUP_BYTES = 18;
-  static constexpr int KR = 32;
-  static constexpr float OFF = 136.0f;  // (128 + q) - (q - 8)
-};
+struct Fmt<ARTLITE_Q4_0> : FmtT<18, 1, 32, 136> {};  // (128 + q) - (q - 8)
 template <>
-struct Fmt<ARTLITE_Q8_0> {
-  static constexpr int GROUP_BYTES = 34;
-  static constexpr int KR = 16;
-  static constexpr float OFF = 128.0f;
-};
+struct Fmt<ARTLITE_Q4_1> : FmtT<20, 1, 24, 128, true> {};
 template <>
-struct Fmt<ARTLITE_Q4_K> {
-  static constexpr int GROUP_BYTES = 18;  // (144 bytes per super-block of 8 groups)
-  static constexpr int KR = 32;
-  static constexpr float OFF = 128.0f;
-};
+struct Fmt<ARTLITE_Q8_0> : FmtT<34, 1, 16, 128> {};  // (q + 128 through an unsigned byte)
+template <>
+struct Fmt<ARTLITE_Q3_K> : FmtT<110, 8, 32, 132, false, true> {};  // (128 + q) - (q - 4)
+template <>
+struct Fmt<ARTLITE_Q4_K> : FmtT<144, 8, 32, 128, true> {};
+template <>
+struct Fmt<ARTLITE_Q5_K> : FmtT<176, 8, 24, 128, true> {};
+template <>
+struct Fmt<ARTLITE_Q6_K> : FmtT<210, 8, 16, 160, false, true> {};  // (128 + q) - (q - 32)
+template <>
+struct Fmt<ARTLITE_IQ4_NL> : FmtT<18, 1, 32, 128> {};
+template <>
+struct Fmt<ARTLITE_IQ4_XS> : FmtT<136, 8, 32, 128> {};
 
 // the 16-byte chunks of a 16-row stage: the aligned cover of each row's run; a row's LDS slot is an odd number of
 // 16-byte units, so the 16 rows' same-offset dwords fall in 16 different banks
 template <int QT>
 struct Stage {
-  static constexpr int BYTES = Fmt<QT>::KR * Fmt<QT>::GROUP_BYTES;
+  static constexpr int BYTES = Fmt<QT>::RUN;
   static constexpr int CPR = (BYTES + 15 + 15) / 16;
   static constexpr int SLOT = 16 * (CPR | 1);
   static constexpr int LOADS = (16 * CPR + WAVE - 1) / WAVE;  // per lane
+  static_assert(16 * CPR <= WEIGHT_TAIL, "a K-range's cover stays within a weight tensor's tail");
 };
 
-// B operand of group gl of a row's run (row: its first byte in LDS) for lane group lg: 8 codes as 4 dwords of bf16,
-// and the scale (Q4_K: d sc, with dmin mn in mn)
+// four codes (bytes < 16) -> the bytes 128 + IQ4[code] (IQ4_NL / IQ4_XS's values, ggml's kvalues_iq4nl): two byte
+// permutes over the 16-byte table, one per half, the code's bit 3 choosing between them
+__device__ __forceinline__ uint32_t iq4_bytes(uint32_t c) {
+  constexpr int V[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+  constexpr auto pack = [](const int* v) {
+    return uint32_t(128 + v[0]) | uint32_t(128 + v[1]) << 8 | uint32_t(128 + v[2]) << 16 | uint32_t(128 + v[3]) << 24;
+  };
+  constexpr uint32_t T0 = pack(V), T1 = pack(V + 4), T2 = pack(V + 8), T3 = pack(V + 12);
+  const uint32_t s = c & 0x07070707u, hi = ((c >> 3) & 0x01010101u) * 0xFFu;
+  return (__builtin_amdgcn_perm(T3, T2, s) & hi) | (__builtin_amdgcn_perm(T1, T0, s) & ~hi);
+}
+
+// Q4_K / Q5_K's 6-bit scale and min of group g from the 12 bytes at s6
+__device__ __forceinline__ void k_scale_min(const uint8_t* s6, int g, int& q6, int& m6) {
+  q6 = g < 4 ? s6[g] & 63 : (s6[8 + g - 4] & 15) | ((s6[g - 4] >> 6) << 4);
+  m6 = g < 4 ? s6[4 + g] & 63 : (s6[8 + g - 4] >> 4) | ((s6[4 + g - 4] >> 6) << 4);
+}
+
+// Q3_K's scale of sub-block sb (of 16), minus 32, from the 12 bytes at s
+__device__ __forceinline__ int q3k_scale(const uint8_t* s, int sb) {
+  const int lo = sb < 8 ? s[sb] & 15 : s[sb - 8] >> 4, hi = (s[8 + (sb & 3)] >> (2 * (sb >> 2))) & 3;
+  return (lo | (hi << 4)) - 32;
+}
+
+// B operand of group gl of a row's run (row: its first byte in LDS) for lane group lg (values 8 lg .. + 8 of the
+// group): 8 codes as 4 dwords of bf16, and the scales: sc (the whole group's, or SUB16: its first half's, with sc2
+// the second half's) and, for the formats with a min, mn with w = sc q - mn (Q4_1's w = d q + m: mn = -m)
 template <int QT>
-__device__ __forceinline__ u32x4 b_operand(const uint8_t* row, int gl, int lg, float& sc, float& mn) {
-  if (QT == ARTLITE_Q4_0) {
-    const uint8_t* blk = row + 18 * gl;
+__device__ __forceinline__ u32x4 b_operand(const uint8_t* row, int gl, int lg, float& sc, float& mn, float& sc2) {
+  using F = Fmt<QT>;
+  const uint8_t* blk = row + F::BLOCK_BYTES * (gl / F::GPB);
+  const int g = gl % F::GPB;
+  if constexpr (QT == ARTLITE_Q4_0 || QT == ARTLITE_Q4_1 || QT == ARTLITE_IQ4_NL) {
+    constexpr int QS = QT == ARTLITE_Q4_1 ? 4 : 2;
     sc = h2f(lds_u16(blk));
+    if constexpr (QT == ARTLITE_Q4_1) mn = -h2f(lds_u16(blk + 2));
     const int sh = 4 * (lg >> 1);
-    const uint32_t u0 = (lds_u32(blk + 2 + 8 * (lg & 1)) >> sh) & 0x0F0F0F0Fu;
-    const uint32_t u1 = (lds_u32(blk + 6 + 8 * (lg & 1)) >> sh) & 0x0F0F0F0Fu;
+    const uint32_t u0 = (lds_u32(blk + QS + 8 * (lg & 1)) >> sh) & 0x0F0F0F0Fu;
+    const uint32_t u1 = (lds_u32(blk + QS + 4 + 8 * (lg & 1)) >> sh) & 0x0F0F0F0Fu;
+    if constexpr (QT == ARTLITE_IQ4_NL) return byte8(iq4_bytes(u0), iq4_bytes(u1));
     return nib8(u0, u1);
-  } else if (QT == ARTLITE_Q8_0) {
-    const uint8_t* blk = row + 34 * gl;
+  } else if constexpr (QT == ARTLITE_Q8_0) {
     sc = h2f(lds_u16(blk));
     return byte8(lds_u32(blk + 2 + 8 * lg) ^ 0x80808080u, lds_u32(blk + 6 + 8 * lg) ^ 0x80808080u);
-  } else {  // Q4_K: group gl % 8 of the super-block at gl / 8
-    const uint8_t* sb = row + 144 * (gl >> 3);
-    const int g = gl & 7;
-    const float d = h2f(lds_u16(sb)), dmin = h2f(lds_u16(sb + 2));
-    const uint8_t* s6 = sb + 4;
-    const int q6 = g < 4 ? s6[g] & 63 : (s6[8 + g - 4] & 15) | ((s6[g - 4] >> 6) << 4);
-    const int m6 = g < 4 ? s6[4 + g] & 63 : (s6[8 + g - 4] >> 4) | ((s6[4 + g - 4] >> 6) << 4);
-    sc = __fmul_rn(d, float(q6));
-    mn = __fmul_rn(dmin, float(m6));
-    const uint8_t* qs = sb + 16 + 32 * (g >> 1) + 8 * lg;
+  } else if constexpr (QT == ARTLITE_Q4_K || QT == ARTLITE_Q5_K) {  // group g of the super-block
+    int q6, m6;
+    k_scale_min(blk + 4, g, q6, m6);
+    sc = __fmul_rn(h2f(lds_u16(blk)), float(q6));
+    mn = __fmul_rn(h2f(lds_u16(blk + 2)), float(m6));
+    const uint8_t* qs = blk + (QT == ARTLITE_Q5_K ? 48 : 16) + 32 * (g >> 1) + 8 * lg;
     const int sh = 4 * (g & 1);
-    return nib8((lds_u32(qs) >> sh) & 0x0F0F0F0Fu, (lds_u32(qs + 4) >> sh) & 0x0F0F0F0Fu);
+    uint32_t u0 = (lds_u32(qs) >> sh) & 0x0F0F0F0Fu, u1 = (lds_u32(qs + 4) >> sh) & 0x0F0F0F0Fu;
+    if constexpr (QT == ARTLITE_Q5_K) {  // bit g of qh[l] (at 16) is the code's bit 4
+      u0 |= ((lds_u32(blk + 16 + 8 * lg) >> g) & 0x01010101u) << 4;
+      u1 |= ((lds_u32(blk + 20 + 8 * lg) >> g) & 0x01010101u) << 4;
+    }
+    return nib8(u0, u1);
+  } else if constexpr (QT == ARTLITE_Q6_K) {  // group g = 4 h + jj: value l at ql[64 h + 32 (jj % 2) + l], qh[32 h + l]
+    const int h = g >> 2, jj = g & 3;
+    const float d = h2f(lds_u16(blk + 208));
+    sc = __fmul_rn(float(int8_t(blk[192 + 2 * g])), d);
+    sc2 = __fmul_rn(float(int8_t(blk[193 + 2 * g])), d);
+    const uint8_t *ql = blk + 64 * h + 32 * (jj & 1) + 8 * lg, *qh = blk + 128 + 32 * h + 8 * lg;
+    const int sh = jj < 2 ? 0 : 4;
+    const uint32_t u0 = ((lds_u32(ql) >> sh) & 0x0F0F0F0Fu) | (((lds_u32(qh) >> (2 * jj)) & 0x03030303u) << 4);
+    const uint32_t u1 = ((lds_u32(ql + 4) >> sh) & 0x0F0F0F0Fu) | (((lds_u32(qh + 4) >> (2 * jj)) & 0x03030303u) << 4);
+    return nib8(u0, u1);
+  } else if constexpr (QT == ARTLITE_Q3_K) {  // group g = 4 n + j: value 16 h + l at qs[32 n + 16 h + l], hm[16 h + l]
+    const int n = g >> 2, j = g & 3;
+    const float d = h2f(lds_u16(blk + 108));
+    sc = __fmul_rn(d, float(q3k_scale(blk + 96, 2 * g)));
+    sc2 = __fmul_rn(d, float(q3k_scale(blk + 96, 2 * g + 1)));
+    const uint8_t *qs = blk + 32 + 32 * n + 8 * lg, *hm = blk + 8 * lg;
+    const int hb = 4 * n + j;
+    const uint32_t u0 = ((lds_u32(qs) >> (2 * j)) & 0x03030303u) | (((lds_u32(hm) >> hb) & 0x01010101u) << 2);
+    const uint32_t u1 = ((lds_u32(qs + 4) >> (2 * j)) & 0x03030303u) | (((lds_u32(hm + 4) >> hb) & 0x01010101u) << 2);
+    return nib8(u0, u1);
+  } else {  // IQ4_XS: group g's codes at 8 + 16 g, its scale d (ls - 32)
+    const int ls = ((blk[4 + g / 2] >> (4 * (g & 1))) & 15) | (((int(lds_u16(blk + 2)) >> (2 * g)) & 3) << 4);
+    sc = __fmul_rn(h2f(lds_u16(blk)), float(ls - 32));
+    const uint8_t* qs = blk + 8 + 16 * g + 8 * (lg & 1);
+    const int sh = 4 * (lg >> 1);
+    return byte8(iq4_bytes((lds_u32(qs) >> sh) & 0x0F0F0F0Fu), iq4_bytes((lds_u32(qs + 4) >> sh) & 0x0F0F0F0Fu));
   }
 }
 
 // One 16-row block's products over groups [0, gn) of its K-range (rows at rowp in LDS; this lane's A row at arow
-// in LDS; cin: -OFF group sums), ni scale FMAs per group (the lane's output rows that hold tokens).
+// in LDS; gsum: -OFF times the A sums of each group, or SUB16 of each half group), ni scale FMAs per group (the
+// lane's output rows that hold tokens).
 template <int QT, int AP, int KR, bool FULL>
 __device__ __forceinline__ f32x4 block_products(f32x4 acc, const uint8_t* rowp, const uint8_t* arow, int a_plane,
                                                 const float (*gsum)[16], int g0, int gn, int lg, int ni) {
+  using F = Fmt<QT>;
 #pragma unroll 8
   for (int gl = 0; gl < (FULL ? KR : gn); gl++) {
     const int g = g0 + gl;
     const u32x4 ahi = *reinterpret_cast<const u32x4*>(arow + 64 * g);
-    const f32x4 cin = *reinterpret_cast<const f32x4*>(&gsum[g][4 * lg]);
-    float sc, mn = 0.0f;
-    const u32x4 b = b_operand<QT>(rowp, gl, lg, sc, mn);
-    f32x4 p = mfma(ahi, b, cin);
-    if (AP == 2) p = mfma(*reinterpret_cast<const u32x4*>(arow + a_plane + 64 * g), b, p);
+    float sc, mn = 0.0f, sc2 = 0.0f;
+    const u32x4 b = b_operand<QT>(rowp, gl, lg, sc, mn, sc2);
+    if constexpr (!F::SUB16) {
+      const f32x4 cin = *reinterpret_cast<const f32x4*>(&gsum[g][4 * lg]);
+      f32x4 p = mfma(ahi, b, cin);
+      if (AP == 2) p = mfma(*reinterpret_cast<const u32x4*>(arow + a_plane + 64 * g), b, p);
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-      if (i < ni) {
-        acc[i] = __builtin_fmaf(sc, p[i], acc[i]);
-        if (QT == ARTLITE_Q4_K) acc[i] = __builtin_fmaf(mn, cin[i] * (1.0f / Fmt<QT>::OFF), acc[i]);
+      for (int i = 0; i < 4; i++)
+        if (i < ni) {
+          acc[i] = __builtin_fmaf(sc, p[i], acc[i]);
+          if (F::MIN) acc[i] = __builtin_fmaf(mn, cin[i] * (1.0f / F::OFF), acc[i]);
+        }
+    } else {  // lane groups 0, 1 hold the group's first 16 values, 2, 3 its second 16
+      const u32x4 zero{0, 0, 0, 0};
+      const u32x4 b0 = lg < 2 ? b : zero, b1 = lg < 2 ? zero : b;
+      f32x4 p0 = mfma(ahi, b0, *reinterpret_cast<const f32x4*>(&gsum[2 * g][4 * lg]));
+      f32x4 p1 = mfma(ahi, b1, *reinterpret_cast<const f32x4*>(&gsum[2 * g + 1][4 * lg]));
+      if (AP == 2) {
+        const u32x4 alo = *reinterpret_cast<const u32x4*>(arow + a_plane + 64 * g);
+        p0 = mfma(alo, b0, p0);
+        p1 = mfma(alo, b1, p1);
       }
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        if (i < ni) acc[i] = __builtin_fmaf(sc2, p1[i], __builtin_fmaf(sc, p0[i], acc[i]));
+    }
   }
   return acc;
 }
@@ -169,11 +258,12 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs a) {
   const int ng = a.K / 32;
   const int a_plane = a.K * 2;               // bytes of one plane of a staged A row
   const int arow_bytes = a_plane * AP + 16;  // (padded: the 16 lanes' rows fall in 16 bank groups)
-  // LDS: the waves' slots (4 x 16 rows) | the tile's A rows | group sums [ng][16] (by MFMA row) | up accumulators
+  constexpr int NSUM = F::SUB16 ? 2 : 1;     // A sums per group (SUB16: per half)
+  // LDS: the waves' slots (4 x 16 rows) | the tile's A rows | A sums [NSUM ng][16] (by MFMA row) | up accumulators
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   uint8_t* as = lds + 4 * 16 * S::SLOT;
   float(*gsum)[16] = reinterpret_cast<float(*)[16]>(as + DECODE_BM * arow_bytes);
-  f32x4* xch = reinterpret_cast<f32x4*>(as + DECODE_BM * arow_bytes + ng * 16 * 4);
+  f32x4* xch = reinterpret_cast<f32x4*>(as + DECODE_BM * arow_bytes + NSUM * ng * 16 * 4);
 
   const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE, lg = lane >> 4, lr = lane & 15;
   int e = 0, s0, m_valid;
@@ -198,7 +288,7 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs a) {
   auto load_unit = [&](int u, u32x4(&w)[S::LOADS]) {
     const int j = u / ns, kr = u % ns;
     const int r0 = n0 + 16 * (sub + WPM * j);
-    const int64_t koff = int64_t(kr) * F::KR * F::GROUP_BYTES;
+    const int64_t koff = int64_t(kr) * F::RUN;
 #pragma unroll
     for (int i = 0; i < S::LOADS; i++) {
       const int q = min(lane + WAVE * i, 16 * S::CPR - 1);
@@ -228,16 +318,17 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs a) {
     }
   }
   __syncthreads();
-  // group sums by MFMA row m: gsum[g][m] = -OFF sum over group g of A[token_of_row(m)] (zero past the tile)
-  for (int i = threadIdx.x; i < ng * 16; i += 256) {
+  // A sums by MFMA row m: gsum[g][m] = -OFF sum over group g (SUB16: half group g) of A[token_of_row(m)] (zero
+  // past the tile)
+  for (int i = threadIdx.x; i < NSUM * ng * 16; i += 256) {
     const int g = i / 16, m = i % 16, t = token_of_row(m);
     float sum = 0.0f;
     if (t < m_valid)
 #pragma unroll
       for (int pl = 0; pl < AP; pl++) {
-        const u32x4* p = reinterpret_cast<const u32x4*>(as + t * arow_bytes + pl * a_plane + 64 * g);
+        const u32x4* p = reinterpret_cast<const u32x4*>(as + t * arow_bytes + pl * a_plane + 64 / NSUM * g);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
+        for (int j = 0; j < 4 / NSUM; j++) {
           const u32x4 v = p[j];
 #pragma unroll
           for (int q = 0; q < 4; q++) sum += bf16_to_f32(v[q] & 0xFFFFu) + bf16_to_f32(v[q] >> 16);
@@ -270,7 +361,7 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs a) {
     __builtin_amdgcn_wave_barrier();
     const int r = min(n0 + 16 * (sub + WPM * j) + lr, a.N - 1);
     const uint8_t* rowp =
-        my + lr * S::SLOT + ((int64_t(r) * a.row_bytes + int64_t(kr) * F::KR * F::GROUP_BYTES) & 15);
+        my + lr * S::SLOT + ((int64_t(r) * a.row_bytes + int64_t(kr) * F::RUN) & 15);
     const int g0 = kr * F::KR, gn = min(F::KR, ng - g0);
     f32x4 accj = (BLK > 1 && j) ? acc[BLK - 1] : acc[0];
     if (gn == F::KR)
@@ -321,7 +412,9 @@ int launch_decode(const GemmArgs& a, hipStream_t s) {
   const int64_t tiles = a.tiles ? a.max_tiles : (a.dense_rows + DECODE_BM - 1) / DECODE_BM;
   const dim3 grid(unsigned(tiles), unsigned((a.N + RB - 1) / RB)), block(256);
   const size_t lds = 4 * 16 * Stage<QT>::SLOT + size_t(DECODE_BM) * (size_t(a.K) * 2 * (a.a_lo ? 2 : 1) + 16) +
-                     size_t(a.K / 32) * 16 * 4 + (SWIGLU ? 2 * BLK * WAVE * 16 : 0);
+                     size_t(a.K / 32) * (Fmt<QT>::SUB16 ? 2 : 1) * 16 * 4 + (SWIGLU ? 2 * BLK * WAVE * 16 : 0);
+  if (lds > LDS_BYTES)
+    return fail(ARTLITE_EINVAL, "expert GEMM: K %d takes %zu B of LDS per workgroup (of %d)", a.K, lds, LDS_BYTES);
   if (a.a_lo)
     k_gemm_decode<QT, SWIGLU, 2, BLK><<<grid, block, lds, s>>>(a);
   else
@@ -853,7 +946,9 @@ int launch_weight_max(const uint8_t* w, int qtype, int64_t nblocks, float* out, 
 }
 
 int launch_expert_gemm(const GemmArgs& a, hipStream_t s) {
-  if (a.K % 32 || (a.qtype == ARTLITE_Q4_K && a.K % 256))
+  const QType* qt = qtype_by_id(a.qtype);
+  if (!qt || qt->per < 32) return fail(ARTLITE_EINVAL, "expert GEMM: unsupported weight type %d", a.qtype);
+  if (a.K <= 0 || a.K % qt->per)
     return fail(ARTLITE_EINVAL, "expert GEMM: K %d is not a multiple of the format's block", a.K);
   if (a.K / 32 > MAX_GROUPS) return fail(ARTLITE_EINVAL, "expert GEMM: K %d beyond %d", a.K, 32 * MAX_GROUPS);
   const bool swiglu = a.w[1] != nullptr;
@@ -863,8 +958,14 @@ int launch_expert_gemm(const GemmArgs& a, hipStream_t s) {
 #define ART_DISPATCH(QT) return swiglu ? launch_decode<QT, true, 2>(a, s) : launch_decode<QT, false, 2>(a, s)
   switch (a.qtype) {
     case ARTLITE_Q4_0: ART_DISPATCH(ARTLITE_Q4_0);
+    case ARTLITE_Q4_1: ART_DISPATCH(ARTLITE_Q4_1);
     case ARTLITE_Q8_0: ART_DISPATCH(ARTLITE_Q8_0);
+    case ARTLITE_Q3_K: ART_DISPATCH(ARTLITE_Q3_K);
     case ARTLITE_Q4_K: ART_DISPATCH(ARTLITE_Q4_K);
+    case ARTLITE_Q5_K: ART_DISPATCH(ARTLITE_Q5_K);
+    case ARTLITE_Q6_K: ART_DISPATCH(ARTLITE_Q6_K);
+    case ARTLITE_IQ4_NL: ART_DISPATCH(ARTLITE_IQ4_NL);
+    case ARTLITE_IQ4_XS: ART_DISPATCH(ARTLITE_IQ4_XS);
     default: return fail(ARTLITE_EINVAL, "expert GEMM: unsupported weight type %d", a.qtype);
   }
 #undef ART_DISPATCH

@@ -16,7 +16,7 @@ struct artlite_moe_layer {
   artlite_moe_desc d{};
   int device = 0;
   hipStream_t stream = nullptr;
-  const QType *gq = nullptr, *dq = nullptr, *sq = nullptr;
+  const QType *gq = nullptr, *dq = nullptr, *sq = nullptr, *sdq = nullptr;  // (sdq: the shared down's)
   size_t gate_row = 0, down_row = 0, sgate_row = 0, sdown_row = 0;  // row bytes
   DevBuf router, gate, up, down, sgate, sup, sdown, sinp, norm;
   bool have[9] = {};
@@ -70,9 +70,8 @@ DevBuf* tensor_buf(artlite_moe_layer* L, int t) {
   }
 }
 
-bool is_expert_type(const QType* q) {
-  return q && (q->id == ARTLITE_Q4_0 || q->id == ARTLITE_Q8_0 || q->id == ARTLITE_Q4_K);
-}
+// the block formats of the experts' kernels (every quantized type the dequantizer reads)
+bool is_expert_type(const QType* q) { return q && q->per >= 32; }
 
 int check_ready(const artlite_moe_layer* L) {
   for (int t = ARTLITE_ROUTER; t <= ARTLITE_DOWN_EXPS; t++)
@@ -331,6 +330,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     sd.row_bytes = int(L->sdown_row);
     sd.N = H;
     sd.K = d.shared_ffn;
+    sd.qtype = L->sdq->id;
     sd.xq = L->shq.as<uint32_t>();
     sd.hq = nullptr;
     sd.y = L->ys.as<float>();
@@ -358,7 +358,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     sd.row_bytes = int(L->sdown_row);
     sd.N = H;
     sd.K = d.shared_ffn;
-    sd.qtype = d.shared_type;
+    sd.qtype = L->sdq->id;
     sd.a = L->sh16.as<uint16_t>();
     sd.in_exp = L->shexp.as<int32_t>();
     sd.out_exp = nullptr;
@@ -389,6 +389,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     sd.row_bytes = int(L->sdown_row);
     sd.N = H;
     sd.K = d.shared_ffn;
+    sd.qtype = L->sdq->id;
     sd.a_hi = L->shhi.as<uint16_t>();
     sd.a_lo = L->shlo.as<uint16_t>();
     sd.y = L->ys.as<float>();
@@ -419,16 +420,18 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
   ART_TRY(check_route_args(1, d.n_experts, d.n_experts, d.top_k));
   const QType *gq = qtype_by_id(d.gate_type), *dq = qtype_by_id(d.down_type);
   if (!is_expert_type(gq) || !is_expert_type(dq))
-    return fail(ARTLITE_EINVAL, "moe layer: expert types %d / %d (Q4_0, Q8_0, Q4_K)", d.gate_type, d.down_type);
+    return fail(ARTLITE_EINVAL, "moe layer: expert types %d / %d (not a block format)", d.gate_type, d.down_type);
   if (d.hidden % gq->per || d.expert_ffn % dq->per)
     return fail(ARTLITE_EINVAL, "moe layer: H %d / F %d not multiples of the blocks (%d / %d)", d.hidden,
                 d.expert_ffn, gq->per, dq->per);
   if (d.hidden % 4) return fail(ARTLITE_EINVAL, "moe layer: H %d not a multiple of 4", d.hidden);
-  const QType* sq = nullptr;
+  const QType *sq = nullptr, *sdq = nullptr;
   if (d.shared_ffn) {
     sq = qtype_by_id(d.shared_type);
-    if (!is_expert_type(sq) || d.hidden % sq->per || d.shared_ffn % sq->per)
-      return fail(ARTLITE_EINVAL, "moe layer: shared expert type %d / width %d", d.shared_type, d.shared_ffn);
+    sdq = d.shared_down_type ? qtype_by_id(d.shared_down_type) : sq;
+    if (!is_expert_type(sq) || !is_expert_type(sdq) || d.hidden % sq->per || d.shared_ffn % sdq->per)
+      return fail(ARTLITE_EINVAL, "moe layer: shared expert types %d / %d, width %d", d.shared_type,
+                  d.shared_down_type, d.shared_ffn);
   }
   if (d.gating != 0 && d.gating != 1) return fail(ARTLITE_EINVAL, "moe layer: gating %d", d.gating);
   if (!(d.norm_eps >= 0.0f && d.norm_eps < 1.0f) || (d.residual != 0 && d.residual != 1))
@@ -440,20 +443,21 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
   L->gq = gq;
   L->dq = dq;
   L->sq = sq;
+  L->sdq = sdq;
   L->gate_row = size_t(d.hidden) / gq->per * gq->bytes;
   L->down_row = size_t(d.expert_ffn) / dq->per * dq->bytes;
   if (sq) {
     L->sgate_row = size_t(d.hidden) / sq->per * sq->bytes;
-    L->sdown_row = size_t(d.shared_ffn) / sq->per * sq->bytes;
+    L->sdown_row = size_t(d.shared_ffn) / sdq->per * sdq->bytes;
   }
   L->gemv_ok = gemv_supported(d.gate_type, d.hidden, d.expert_ffn) &&
                gemv_supported(d.down_type, d.expert_ffn, d.hidden);
   L->prefill_ok = prefill_supported(d.gate_type, d.hidden, d.expert_ffn) &&
                   prefill_supported(d.down_type, d.expert_ffn, d.hidden);
-  L->shared_gemv_ok = sq && gemv_supported(d.shared_type, d.hidden, d.shared_ffn) &&
-                      gemv_supported(d.shared_type, d.shared_ffn, d.hidden);
-  L->shared_prefill_ok = sq && prefill_supported(d.shared_type, d.hidden, d.shared_ffn) &&
-                         prefill_supported(d.shared_type, d.shared_ffn, d.hidden);
+  L->shared_gemv_ok = sq && gemv_supported(sq->id, d.hidden, d.shared_ffn) &&
+                      gemv_supported(sdq->id, d.shared_ffn, d.hidden);
+  L->shared_prefill_ok = sq && prefill_supported(sq->id, d.hidden, d.shared_ffn) &&
+                         prefill_supported(sdq->id, d.shared_ffn, d.hidden);
   hipError_t e = hipGetDevice(&L->device);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&L->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
@@ -532,9 +536,9 @@ extern "C" int artlite_moe_layer_upload(artlite_moe_layer* L, int t, const void*
   const size_t want = tensor_bytes(L, t);
   if (!b || !want) return fail(ARTLITE_EINVAL, "moe layer upload: tensor %d not in this layer", t);
   if (nbytes != want) return fail(ARTLITE_EINVAL, "moe layer upload: tensor %d is %zu bytes, not %zu", t, nbytes, want);
-  ART_TRY(b->reserve(want));
+  ART_TRY(b->reserve(want + WEIGHT_TAIL));
   ART_HIP(hipMemcpyAsync(b->p, data, want, hipMemcpyHostToDevice, L->stream));
-  ART_HIP(hipMemsetAsync(static_cast<uint8_t*>(b->p) + want, 0, 256, L->stream));  // (the tail the loaders touch)
+  ART_HIP(hipMemsetAsync(static_cast<uint8_t*>(b->p) + want, 0, WEIGHT_TAIL, L->stream));  // (the loaders' tail)
   // the prefill's bound on |h| takes max |w| of the gate and up matrices
   const int wm = t == ARTLITE_GATE_EXPS ? 0 : t == ARTLITE_UP_EXPS ? 1 : t == ARTLITE_GATE_SHEXP ? 2
                : t == ARTLITE_UP_SHEXP ? 3 : -1;
@@ -619,6 +623,10 @@ extern "C" int artlite_moe_layer_tap(artlite_moe_layer* L, int tap, void* out, s
     case ARTLITE_TAP_XN:
       if (!(L->d.norm_eps > 0)) return fail(ARTLITE_EINVAL, "moe layer tap: no norm in this layer");
       src = L->xn.p, bytes = size_t(T) * L->d.hidden * 4;
+      break;
+    case ARTLITE_TAP_YS:
+      if (!L->d.shared_ffn) return fail(ARTLITE_EINVAL, "moe layer tap: no shared expert in this layer");
+      src = L->ys.p, bytes = size_t(T) * L->d.hidden * 4;
       break;
     case ARTLITE_TAP_H: {
       const size_t n = size_t(P) * L->d.expert_ffn;

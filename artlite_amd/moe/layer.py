@@ -16,7 +16,7 @@ from ..gguf_model import TYPE_ID, GGUFFile
 TENSORS = {"ffn_gate_inp": 0, "ffn_gate_exps": 1, "ffn_up_exps": 2, "ffn_down_exps": 3, "ffn_gate_shexp": 4,
            "ffn_up_shexp": 5, "ffn_down_shexp": 6, "ffn_gate_inp_shexp": 7, "ffn_norm": 8}
 TAPS = {"logits": 0, "ids": 1, "weights": 2, "counts": 3, "offsets": 4, "order": 5, "slot": 6, "h": 7, "y_pairs": 8,
-        "x_norm": 9}
+        "x_norm": 9, "y_shared": 10}
 X_F32, X_BF16 = 0, 1
 
 
@@ -25,9 +25,10 @@ class MoELayer:
 
     def __init__(self, *, hidden: int, n_experts: int, top_k: int, expert_ffn: int, gate_type: str, down_type: str,
                  max_tokens: int, shared_ffn: int = 0, shared_type: str = "", shared_gated: bool = False,
-                 gating: str = "softmax", norm_eps: float = 0.0, residual: bool = False):
+                 gating: str = "softmax", norm_eps: float = 0.0, residual: bool = False, shared_down_type: str = ""):
         """norm_eps > 0: x is first RMS-normalised by the uploaded ``ffn_norm`` (the steps before the block's router);
-        residual: y += x (the block's residual add after the combine)."""
+        residual: y += x (the block's residual add after the combine); shared_down_type: the format of
+        ``ffn_down_shexp`` when it is not ``shared_type``'s."""
         assert gating in ("softmax", "sigmoid"), gating
         self.H, self.E, self.k, self.F = hidden, n_experts, top_k, expert_ffn
         self.max_tokens = max_tokens
@@ -35,7 +36,8 @@ class MoELayer:
                       gate_type=TYPE_ID[gate_type], down_type=TYPE_ID[down_type], shared_ffn=shared_ffn,
                       shared_type=TYPE_ID[shared_type] if shared_ffn else 0, shared_gated=int(shared_gated),
                       gating=int(gating == "sigmoid"), max_tokens=max_tokens, norm_eps=norm_eps,
-                      residual=int(residual))
+                      residual=int(residual),
+                      shared_down_type=TYPE_ID[shared_down_type] if shared_ffn and shared_down_type else 0)
         h = ctypes.c_void_p()
         _hip.check(_hip.lib().artlite_moe_layer_create(ctypes.byref(d), ctypes.byref(h)))
         self._h = h
@@ -84,9 +86,13 @@ class MoELayer:
             raise ValueError(f"{gguf.path}: block {block} expert tensors {dims} / {ddims} ({gtype}, {utype}), "
                              f"expected ({H}, {F}, {E}) / ({F}, {H}, {E})")
         shared = b + "ffn_gate_shexp.weight" in gguf
-        sF, stype = 0, ""
+        sF, stype, sdtype = 0, "", ""
         if shared:
             sdims, stype, _, _ = gguf.tensor_info[b + "ffn_gate_shexp.weight"]
+            _, sutype, _, _ = gguf.tensor_info[b + "ffn_up_shexp.weight"]
+            _, sdtype, _, _ = gguf.tensor_info[b + "ffn_down_shexp.weight"]
+            if sutype != stype:
+                raise ValueError(f"{gguf.path}: block {block} shared gate / up types {stype} / {sutype} differ")
             sF = int(m("expert_shared_feed_forward_length", sdims[1]))
         gated = b + "ffn_gate_inp_shexp.weight" in gguf
         gating = "sigmoid" if int(m("expert_gating_func", 1)) == 2 else "softmax"
@@ -95,7 +101,7 @@ class MoELayer:
             raise ValueError(f"{gguf.path}: block {block} has no ffn_norm")
         layer = cls(hidden=H, n_experts=E, top_k=k, expert_ffn=F, gate_type=gtype, down_type=dtype,
                     max_tokens=max_tokens, shared_ffn=sF, shared_type=stype, shared_gated=gated, gating=gating,
-                    norm_eps=eps, residual=norm)
+                    norm_eps=eps, residual=norm, shared_down_type=sdtype if sdtype != stype else "")
         try:
             for name in ("ffn_gate_inp", "ffn_gate_inp_shexp") + (("ffn_norm",) if norm else ()):
                 if b + name + ".weight" in gguf:
@@ -153,12 +159,14 @@ class MoELayer:
 
     def tap(self, name: str) -> np.ndarray:
         """An intermediate result of the last run: logits (T, E), ids / weights (T, k), counts (E,), offsets (E + 1,),
-        order / slot (T k,), h (T k, F) (sorted pairs), y_pairs (T k, H) (sorted pairs), x_norm (T, H)."""
+        order / slot (T k,), h (T k, F) (sorted pairs), y_pairs (T k, H) (sorted pairs), x_norm (T, H), y_shared (T, H)
+        (the shared expert's output before its gate)."""
         T, k, E = self.T, self.k, self.E
         shape, dtype = {"logits": ((T, E), np.float32), "ids": ((T, k), np.int32), "weights": ((T, k), np.float32),
                         "counts": ((E,), np.int32), "offsets": ((E + 1,), np.int32), "order": ((T * k,), np.int32),
                         "slot": ((T * k,), np.int32), "h": ((T * k, self.F), np.float32),
-                        "y_pairs": ((T * k, self.H), np.float32), "x_norm": ((T, self.H), np.float32)}[name]
+                        "y_pairs": ((T * k, self.H), np.float32), "x_norm": ((T, self.H), np.float32),
+                        "y_shared": ((T, self.H), np.float32)}[name]
         out = np.empty(shape, dtype)
         _hip.check(_hip.lib().artlite_moe_layer_tap(self.handle, TAPS[name], out.ctypes.data, out.nbytes))
         return out

@@ -77,10 +77,10 @@ typedef struct artlite_moe_desc {
   int32_t n_experts;    /* E */
   int32_t top_k;        /* k */
   int32_t expert_ffn;   /* F */
-  int32_t gate_type;    /* artlite_qtype of ffn_gate_exps / ffn_up_exps (Q4_0, Q8_0, Q4_K) */
+  int32_t gate_type;    /* artlite_qtype of ffn_gate_exps / ffn_up_exps (any quantized type of the enum) */
   int32_t down_type;    /* artlite_qtype of ffn_down_exps */
   int32_t shared_ffn;   /* the shared expert's width, 0: none */
-  int32_t shared_type;  /* artlite_qtype of the shared expert's three matrices */
+  int32_t shared_type;  /* artlite_qtype of the shared expert's gate / up (and down, see shared_down_type) */
   int32_t shared_gated; /* 1: the shared expert times sigmoid(x . ffn_gate_inp_shexp) */
   int32_t gating;       /* 0: softmax, 1: sigmoid */
   int32_t max_tokens;   /* the most tokens of one call */
@@ -88,6 +88,8 @@ typedef struct artlite_moe_desc {
                            before the block's router: llama.cpp's ffn_norm, the reference's tests/np_ops.py:27-32);
                            0: none */
   int32_t residual;     /* 1: y += x (the block's residual add after the combine, x as given, before any norm) */
+  int32_t shared_down_type; /* artlite_qtype of ffn_down_shexp when it differs from shared_type (a GGUF file's
+                               mixed quantisation, e.g. Q4_K gate / up with a Q6_K down); 0: shared_type */
 } artlite_moe_desc;
 
 /* Tensors of artlite_moe_layer_upload, as laid out in a GGUF file. */
@@ -132,6 +134,7 @@ enum artlite_tap {
   ARTLITE_TAP_H = 7,       /* T k x F fp32: silu(gate) up of each sorted pair (as the run's path holds it) */
   ARTLITE_TAP_Y = 8,       /* T k x H fp32: each sorted pair's expert output (before the weights) */
   ARTLITE_TAP_XN = 9,      /* T x H fp32: the RMS-normalised x (norm_eps > 0) */
+  ARTLITE_TAP_YS = 10,     /* T x H fp32: the shared expert's output, before its gate (shared_ffn > 0) */
 };
 int artlite_moe_layer_tap(artlite_moe_layer* layer, int tap, void* out, size_t nbytes);
 

@@ -30,10 +30,16 @@ class Spec:
     router: str = "normal"  # "normal" N(0, 0.02), "uniform" U(-0.035, 0.035), "zipf" (config 5)
     x_dtype: str = "bf16"  # activations: "bf16" (values of bf16) or "f32"
     shared_F: int = 0  # one shared FFN of this width (0: none)
-    shared_type: str = ""
+    shared_type: str = ""  # the shared gate / up format
     shared_gated: bool = False
     tokens: tuple[int, ...] = (16,)
-    dmin_scale: float = 0.0  # Q4_K: the fp16 dmin std
+    dmin_scale: float = 0.0  # Q4_K / Q5_K: the fp16 dmin std
+    shared_down_type: str = ""  # the shared down's format, when not shared_type's
+    shared_scale: float = 0.0  # the shared expert's fp16 scale std (0: scale)
+
+    @property
+    def sdown_type(self) -> str:
+        return self.shared_down_type or self.shared_type
 
 
 CONFIGS = {
@@ -58,6 +64,13 @@ CONFIGS = {
     # the prefill tiles)
     "mix_pf": Spec("mix_pf", H=1024, E=16, k=2, F=512, gate_type="Q8_0", down_type="Q4_0", scale=0.01,
                    x_dtype="f32", shared_F=512, shared_type="Q8_0", shared_gated=True, tokens=(256,)),
+    # test-only: the other block formats of real GGUF files, on the MFMA decode tiles -- K-quants (Q5_K gate / up,
+    # Q6_K down, a Q4_K / Q3_K shared expert: 16-value sub-block scales) with bf16 x, and IQ4_XS / IQ4_NL with a
+    # Q4_1 shared expert and fp32 x
+    "kquants": Spec("kquants", H=1024, E=16, k=2, F=512, gate_type="Q5_K", down_type="Q6_K", scale=1e-4,
+                    dmin_scale=1e-3, shared_F=512, shared_type="Q4_K", shared_down_type="Q3_K", tokens=(32,)),
+    "iq4": Spec("iq4", H=768, E=16, k=4, F=512, gate_type="IQ4_XS", down_type="IQ4_NL", scale=5e-5, x_dtype="f32",
+                shared_F=256, shared_type="Q4_1", shared_scale=4e-3, shared_gated=True, tokens=(24,)),
 }
 
 ZIPF_S, ZIPF_ACTIVE, ZIPF_BETA = 1.2, 26, 0.7
@@ -75,12 +88,12 @@ class Layer:
     meta: dict = field(default_factory=dict)
 
 
-def _blocks(qtype: str, rows: int, cols: int, rng: np.random.Generator, spec: Spec) -> np.ndarray:
-    raw = random_blocks(qtype, rows, cols, rng, scale=spec.scale, abs_scales=True)
-    if qtype == "Q4_K":  # (dmin: its own, larger scale, so the weights are about centred)
-        n = cols // 256
+def _blocks(qtype: str, rows: int, cols: int, rng: np.random.Generator, spec: Spec, scale: float = 0.0) -> np.ndarray:
+    raw = random_blocks(qtype, rows, cols, rng, scale=scale or spec.scale, abs_scales=True)
+    if qtype in ("Q4_K", "Q5_K"):  # (dmin: its own, larger scale, so the weights are about centred)
+        n, nb = cols // 256, gguf_ref.BLOCKS[qtype][1]
         dmin = (np.abs(rng.standard_normal((rows, n))) * spec.dmin_scale).astype(np.float16)
-        raw.reshape(rows, n, 144)[..., 2:4] = dmin.view(np.uint8).reshape(rows, n, 2)
+        raw.reshape(rows, n, nb)[..., 2:4] = dmin.view(np.uint8).reshape(rows, n, 2)
     return raw
 
 
@@ -106,8 +119,9 @@ def make_layer(spec: Spec, seed: int = 0) -> Layer:
     shared = None
     if spec.shared_F:
         Fs = spec.shared_F
-        shared = (_blocks(spec.shared_type, Fs, H, rng, spec), _blocks(spec.shared_type, Fs, H, rng, spec),
-                  _blocks(spec.shared_type, H, Fs, rng, spec))
+        sc = spec.shared_scale
+        shared = (_blocks(spec.shared_type, Fs, H, rng, spec, sc), _blocks(spec.shared_type, Fs, H, rng, spec, sc),
+                  _blocks(spec.sdown_type, H, Fs, rng, spec, sc))
     shared_inp = (rng.standard_normal(H) * 0.02).astype(np.float32) if spec.shared_gated else None
     return Layer(spec, router, gate, up, down, shared, shared_inp, meta)
 
@@ -148,7 +162,7 @@ def shared_out(layer: Layer, x: np.ndarray) -> np.ndarray:
     g, u, d = layer.shared
     return moe_ref.shared_expert(x, gguf_ref.dequantize(s.shared_type, g, s.H),
                                  gguf_ref.dequantize(s.shared_type, u, s.H),
-                                 gguf_ref.dequantize(s.shared_type, d, s.shared_F), layer.shared_inp)
+                                 gguf_ref.dequantize(s.sdown_type, d, s.shared_F), layer.shared_inp)
 
 
 def forward(layer: Layer, x: np.ndarray, ids: np.ndarray | None = None, w: np.ndarray | None = None) -> dict:
@@ -178,7 +192,7 @@ def forward_f64(layer: Layer, x: np.ndarray, ids: np.ndarray, w: np.ndarray) -> 
     if layer.shared is not None:
         g, u, d = layer.shared
         ys = ffn(xv, gguf_ref.dequantize(s.shared_type, g, s.H), gguf_ref.dequantize(s.shared_type, u, s.H),
-                 gguf_ref.dequantize(s.shared_type, d, s.shared_F))
+                 gguf_ref.dequantize(s.sdown_type, d, s.shared_F))
         if layer.shared_inp is not None:
             ys = ys / (1.0 + np.exp(-(xv @ layer.shared_inp.astype(np.float64))))[:, None]
         y += ys

@@ -7,10 +7,15 @@ from oracle import layers
 from oracle.tensors import bf16_bits
 
 
+def layer_args(s: layers.Spec, max_tokens: int) -> dict:
+    """``MoELayer``'s keyword arguments for an oracle configuration."""
+    return dict(hidden=s.H, n_experts=s.E, top_k=s.k, expert_ffn=s.F, gate_type=s.gate_type, down_type=s.down_type,
+                max_tokens=max_tokens, shared_ffn=s.shared_F, shared_type=s.shared_type, shared_gated=s.shared_gated,
+                shared_down_type=s.shared_down_type)
+
+
 def gpu_layer(layer: layers.Layer, max_tokens: int) -> MoELayer:
-    s = layer.spec
-    g = MoELayer(hidden=s.H, n_experts=s.E, top_k=s.k, expert_ffn=s.F, gate_type=s.gate_type, down_type=s.down_type,
-                 max_tokens=max_tokens, shared_ffn=s.shared_F, shared_type=s.shared_type, shared_gated=s.shared_gated)
+    g = MoELayer(**layer_args(layer.spec, max_tokens))
     g.upload("ffn_gate_inp", layer.router)
     g.upload("ffn_gate_exps", layer.gate)
     g.upload("ffn_up_exps", layer.up)

@@ -9,7 +9,7 @@ from artlite_amd.gguf_model import TYPE_ID, GGUFFile
 from oracle import layers
 
 from .gguf_write import write_gguf
-from .helpers import gpu_input, gpu_layer
+from .helpers import gpu_input, gpu_layer, layer_args
 
 
 def block_file(path, spec: layers.Spec, layer: layers.Layer, block: int = 3, gating: int = 1) -> None:
@@ -21,9 +21,9 @@ def block_file(path, spec: layers.Spec, layer: layers.Layer, block: int = 3, gat
          (b + "ffn_down_exps.weight", (F, H, E), TYPE_ID[spec.down_type], layer.down)]
     if layer.shared is not None:
         g, u, d = layer.shared
-        st = TYPE_ID[spec.shared_type]
+        st, sdt = TYPE_ID[spec.shared_type], TYPE_ID[spec.sdown_type]
         t += [(b + "ffn_gate_shexp.weight", (H, spec.shared_F), st, g), (b + "ffn_up_shexp.weight", (H, spec.shared_F), st, u),
-              (b + "ffn_down_shexp.weight", (spec.shared_F, H), st, d)]
+              (b + "ffn_down_shexp.weight", (spec.shared_F, H), sdt, d)]
     if layer.shared_inp is not None:
         t.append((b + "ffn_gate_inp_shexp.weight", (H,), 0, layer.shared_inp))
     meta = {"general.architecture": "qwen3moe", "general.alignment": 64, "qwen3moe.block_count": block + 1,
@@ -56,7 +56,8 @@ def test_gguf_reader(tmp_path) -> None:
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize(("name", "T", "gating"), [("decode", 16, 1), ("mix_q8k", 16, 2), ("prefill", 256, 1)])
+@pytest.mark.parametrize(("name", "T", "gating"), [("decode", 16, 1), ("mix_q8k", 16, 2), ("prefill", 256, 1),
+                                                ("kquants", 32, 1)])
 def test_layer_from_gguf(tmp_path, name: str, T: int, gating: int) -> None:
     from artlite_amd.moe.layer import MoELayer
 
@@ -70,10 +71,7 @@ def test_layer_from_gguf(tmp_path, name: str, T: int, gating: int) -> None:
     if g is None:
         from artlite_amd.moe.layer import MoELayer as L
 
-        s = layer.spec
-        g = L(hidden=s.H, n_experts=s.E, top_k=s.k, expert_ffn=s.F, gate_type=s.gate_type, down_type=s.down_type,
-              max_tokens=T, shared_ffn=s.shared_F, shared_type=s.shared_type, shared_gated=s.shared_gated,
-              gating="sigmoid")
+        g = L(**layer_args(layer.spec, T), gating="sigmoid")
         for n, t in (("ffn_gate_inp", layer.router), ("ffn_gate_exps", layer.gate), ("ffn_up_exps", layer.up),
                      ("ffn_down_exps", layer.down), ("ffn_gate_shexp", layer.shared[0]),
                      ("ffn_up_shexp", layer.shared[1]), ("ffn_down_shexp", layer.shared[2]),

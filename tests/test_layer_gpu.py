@@ -14,14 +14,15 @@ Config sizes are reduced where the oracle would take long; the full sizes follow
 import numpy as np
 import pytest
 
-from oracle import host_ref, layers, moe_ref
+from oracle import gguf_ref, host_ref, layers, moe_ref
 
 from .helpers import gpu_input, gpu_layer, rel_l2, ulp_diff
 
 pytestmark = pytest.mark.gpu
 
 CASES = [("cpu", 16), ("decode", 1), ("decode", 4), ("decode", 16), ("decode", 64), ("prefill", 256),
-         ("deepseek", 64), ("skewed", 192), ("mix_q8k", 16), ("mix_k8", 24), ("mix_pf", 256)]
+         ("deepseek", 64), ("skewed", 192), ("mix_q8k", 16), ("mix_k8", 24), ("mix_pf", 256), ("kquants", 32),
+         ("iq4", 24)]
 
 # Decode-sized passes (at most 4 pairs per expert on average, K a multiple of 256) take the GEMV over XQ activations:
 # int8 hi / lo planes per 32 values, |x - xq| <= max|x| / 65024 per group, so h (itself held in XQ) and the pair
@@ -75,6 +76,14 @@ def check_layer(name: str, T: int, seed: int = 0) -> None:
             h64 = a / (1 + np.exp(-a)) * (xt @ uw.T)
             assert rel_l2(h[s0:s1], h64) < tol, (name, e, rel_l2(h[s0:s1], h64))
             assert rel_l2(yp[s0:s1], h64 @ dw.T) < max(tol, 1e-4), (name, e, rel_l2(yp[s0:s1], h64 @ dw.T))
+        # the shared expert's output (before its gate) against float64 math
+        if layer.shared is not None:
+            sg, su, sd = (gguf_ref.dequantize(q, m, c).astype(np.float64) for q, m, c in
+                          zip((spec.shared_type, spec.shared_type, spec.sdown_type), layer.shared,
+                              (spec.H, spec.H, spec.shared_F)))
+            a = x64 @ sg.T
+            ys64 = (a / (1 + np.exp(-a)) * (x64 @ su.T)) @ sd.T
+            assert rel_l2(g.tap("y_shared"), ys64) < (1e-3 if prefill else max(tol, 1e-4)), name
         # output: the fp32 oracle and float64 math for the GPU's routing
         want = moe_ref.moe_ffn(x, ids, w, get) + layers.shared_out(layer, x)
         assert rel_l2(y, want) < 1e-3, (name, T, rel_l2(y, want))

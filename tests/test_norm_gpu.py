@@ -6,7 +6,7 @@ import pytest
 
 from oracle import layers, moe_ref, np_ops
 
-from .helpers import gpu_input, rel_l2, ulp_diff
+from .helpers import gpu_input, layer_args, rel_l2, ulp_diff
 
 pytestmark = pytest.mark.gpu
 
@@ -21,9 +21,7 @@ def test_norm_and_residual(name: str, T: int) -> None:
     w = np.random.default_rng(7).normal(1.0, 0.1, spec.H).astype(np.float32)
     eps = 1e-6
     s = spec
-    with MoELayer(hidden=s.H, n_experts=s.E, top_k=s.k, expert_ffn=s.F, gate_type=s.gate_type, down_type=s.down_type,
-                  max_tokens=T, shared_ffn=s.shared_F, shared_type=s.shared_type, shared_gated=s.shared_gated,
-                  norm_eps=eps, residual=True) as g:
+    with MoELayer(**layer_args(s, T), norm_eps=eps, residual=True) as g:
         for n, t in (("ffn_gate_inp", layer.router), ("ffn_gate_exps", layer.gate), ("ffn_up_exps", layer.up),
                      ("ffn_down_exps", layer.down), ("ffn_norm", w)):
             g.upload(n, t)
