@@ -79,32 +79,6 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
-// a wave's 64-bit maximum (all 64 lanes hold the result)
-// the largest of the 64 lanes' values, in every lane: within each 16-lane row by DPP (lanes i ^ 1, i ^ 2, the mirror
-// lane of the other 8 and of the other half-row), then across rows by the permlane swaps (rows 0 <-> 1, 2 <-> 3, then
-// lanes 0..31 <-> 32..63)
-template <int C>
-__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
-  const uint32_t lo = uint32_t(__builtin_amdgcn_update_dpp(0, int(uint32_t(v)), C, 0xF, 0xF, false));
-  const uint32_t hi = uint32_t(__builtin_amdgcn_update_dpp(0, int(uint32_t(v >> 32)), C, 0xF, 0xF, false));
-  return (uint64_t(hi) << 32) | lo;
-}
-__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-  v = max_u64(v, dpp_u64<0xB1>(v));   // quad_perm [1, 0, 3, 2]
-  v = max_u64(v, dpp_u64<0x4E>(v));   // quad_perm [2, 3, 0, 1]
-  v = max_u64(v, dpp_u64<0x141>(v));  // row_half_mirror
-  v = max_u64(v, dpp_u64<0x140>(v));  // row_mirror
-  const uint32_t lo = uint32_t(v), hi = uint32_t(v >> 32);
-  const auto l16 = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
-  const auto h16 = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
-  v = max_u64((uint64_t(h16[0]) << 32) | l16[0], (uint64_t(h16[1]) << 32) | l16[1]);
-  const uint32_t lo2 = uint32_t(v), hi2 = uint32_t(v >> 32);
-  const auto l32 = __builtin_amdgcn_permlane32_swap(lo2, lo2, false, false);
-  const auto h32 = __builtin_amdgcn_permlane32_swap(hi2, hi2, false, false);
-  return max_u64((uint64_t(h32[0]) << 32) | l32[0], (uint64_t(h32[1]) << 32) | l32[1]);
-}
-
 constexpr int WAVE = 64;
 constexpr int LDS_BYTES = 160 * 1024;  // a gfx950 workgroup's LDS
 

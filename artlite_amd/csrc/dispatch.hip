@@ -4,8 +4,10 @@
 //
 // Two launches over blocks of DISPATCH_BLOCK consecutive pairs:
 //  1. k_count: per-block histograms (LDS atomics: counts are order-free) into table[b][e]; the last block to finish
-//     (a device-scope ticket) sums them into counts, scans them into offsets and per-(block, expert) bases, and
-//     writes the tile list of the expert GEMMs and the plan's chunk prefix.
+//     (a device-scope ticket) sums them into counts, scans them into offsets and per-(block, expert) bases (the
+//     table staged through LDS in tiles of whole rows), and writes the tile list of the expert GEMMs and the plan's
+//     chunk prefix. When the whole table fits in LDS (e.g. 32 blocks of 128 experts), k_count_one does the same in
+//     one workgroup, without the ticket and its device-scope fences.
 //  2. k_scatter: each pair's rank among the earlier pairs of its block with the same expert (wave ballots over the
 //     id bits give the peers and the in-wave rank; a per-wave count table orders the waves) plus its block's base:
 //     its position in the sorted order. Stable by construction: no atomics decide any position.
@@ -13,48 +15,25 @@
 
 namespace artlite {
 
-__global__ __launch_bounds__(DISPATCH_BLOCK) void k_count(DispatchBufs d) {
-  __shared__ int hist[MAX_EXPERTS];
-  __shared__ int last;
-  const int tid = threadIdx.x;
-  const int64_t nb = gridDim.x;
-  for (int e = tid; e < d.E; e += DISPATCH_BLOCK) hist[e] = 0;
-  __syncthreads();
-  const int64_t p = int64_t(blockIdx.x) * DISPATCH_BLOCK + tid;
-  if (p < d.P) {
-    const int id = d.ids[p];
-    if (id < 0 || id >= d.E) {
-      atomicOr(&d.ctrl[CTRL_BAD], 1);
-      atomicMax(&d.ctrl[CTRL_BAD_FIRST], int(d.P - p));
-    } else {
-      atomicAdd(&hist[id], 1);
-    }
+constexpr int COUNT_TILE = 8192;  // table cells staged in LDS at a time
+
+// one pair's id into a histogram (LDS); a bad id is flagged instead (the first in pair order kept)
+__device__ __forceinline__ void count_pair(const DispatchBufs& d, int64_t p, int id, int* hist) {
+  if (id < 0 || id >= d.E) {
+    atomicOr(&d.ctrl[CTRL_BAD], 1);
+    atomicMax(&d.ctrl[CTRL_BAD_FIRST], int(d.P - p));
+  } else {
+    atomicAdd(&hist[id], 1);
   }
-  __syncthreads();
-  for (int e = tid; e < d.E; e += DISPATCH_BLOCK) d.table[int64_t(blockIdx.x) * d.E + e] = hist[e];
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) last = atomicAdd(&d.ctrl[CTRL_DONE], 1) == int(nb - 1);
-  __syncthreads();
-  if (!last) return;
-  __threadfence();  // (acquire: the other blocks' tables)
-  // counts, offsets, per-block bases (one expert per thread: E <= MAX_EXPERTS == DISPATCH_BLOCK)
-  const int e = tid;
-  int c = 0;
-  if (e < d.E)
-    for (int64_t b = 0; b < nb; b++) c += __builtin_nontemporal_load(&d.table[b * d.E + e]);
-  int total;
-  const int start = block_scan(c, &total);
+}
+
+// The end of a count, in one block of DISPATCH_BLOCK threads, for expert e = thread: c its count, `start` and
+// `total` the scan's; writes counts, offsets, the expert GEMMs' tile list and the plan's chunk prefix.
+__device__ void count_tail(const DispatchBufs& d, int c, int start, int total) {
+  const int e = threadIdx.x;
   if (e < d.E) {
     d.counts[e] = c;
     d.offsets[e] = start;
-    int run = start;
-    for (int64_t b = 0; b < nb; b++) {
-      int* cell = &d.table[b * d.E + e];
-      const int v = __builtin_nontemporal_load(cell);
-      *cell = run;
-      run += v;
-    }
   }
   if (e == 0) d.offsets[d.E] = total;
   if (d.BM > 0) {  // the expert GEMMs' tiles: experts ascending, BM sorted rows each
@@ -77,6 +56,100 @@ __global__ __launch_bounds__(DISPATCH_BLOCK) void k_count(DispatchBufs d) {
       d.ctrl[CTRL_CHUNKS] = nc_total;
     }
   }
+}
+
+// Dispatches whose table (blocks x experts) fits in LDS: one workgroup counts every block's pairs into its row of
+// the table in LDS (no ticket, no device-scope fences), then scans it as k_count's last block does.
+__global__ __launch_bounds__(DISPATCH_BLOCK) void k_count_one(DispatchBufs d, int nb) {
+  __shared__ int hist[COUNT_TILE];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < nb * d.E; i += DISPATCH_BLOCK) hist[i] = 0;
+  __syncthreads();
+  constexpr int U = 8;  // (blocks' ids loaded together)
+  for (int b0 = 0; b0 < nb; b0 += U) {
+    int id[U];
+#pragma unroll
+    for (int j = 0; j < U; j++) {
+      const int64_t p = int64_t(b0 + j) * DISPATCH_BLOCK + tid;
+      id[j] = b0 + j < nb && p < d.P ? d.ids[p] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < U; j++) {
+      const int64_t p = int64_t(b0 + j) * DISPATCH_BLOCK + tid;
+      if (b0 + j < nb && p < d.P) count_pair(d, p, id[j], hist + (b0 + j) * d.E);
+    }
+  }
+  __syncthreads();
+  const int e = tid;
+  int c = 0;
+  if (e < d.E)
+    for (int b = 0; b < nb; b++) c += hist[b * d.E + e];
+  int total;
+  const int start = block_scan(c, &total);
+  if (e < d.E) {
+    int run = start;
+    for (int b = 0; b < nb; b++) {
+      const int v = hist[b * d.E + e];
+      hist[b * d.E + e] = run;
+      run += v;
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < nb * d.E; i += DISPATCH_BLOCK) d.table[i] = hist[i];
+  count_tail(d, c, start, total);
+}
+
+__global__ __launch_bounds__(DISPATCH_BLOCK) void k_count(DispatchBufs d) {
+  __shared__ int hist[MAX_EXPERTS];
+  __shared__ int tile[COUNT_TILE];
+  __shared__ int last;
+  const int tid = threadIdx.x;
+  const int64_t nb = gridDim.x;
+  for (int e = tid; e < d.E; e += DISPATCH_BLOCK) hist[e] = 0;
+  __syncthreads();
+  const int64_t p = int64_t(blockIdx.x) * DISPATCH_BLOCK + tid;
+  if (p < d.P) count_pair(d, p, d.ids[p], hist);
+  __syncthreads();
+  for (int e = tid; e < d.E; e += DISPATCH_BLOCK) d.table[int64_t(blockIdx.x) * d.E + e] = hist[e];
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) last = atomicAdd(&d.ctrl[CTRL_DONE], 1) == int(nb - 1);
+  __syncthreads();
+  if (!last) return;
+  __threadfence();  // (acquire: the other blocks' tables)
+  // counts, offsets, per-block bases (one expert per thread: E <= MAX_EXPERTS == DISPATCH_BLOCK), the table read
+  // (and rewritten) in tiles of whole blocks' rows staged in LDS by all threads, coalesced
+  const int e = tid;
+  const int64_t rows = COUNT_TILE / d.E;
+  auto stage = [&](int64_t b0, int64_t nr) {
+    for (int64_t i = tid; i < nr * d.E; i += DISPATCH_BLOCK) tile[i] = __builtin_nontemporal_load(&d.table[b0 * d.E + i]);
+    __syncthreads();
+  };
+  int c = 0;
+  for (int64_t b0 = 0; b0 < nb; b0 += rows) {
+    const int64_t nr = nb - b0 < rows ? nb - b0 : rows;
+    stage(b0, nr);
+    if (e < d.E)
+      for (int64_t r = 0; r < nr; r++) c += tile[r * d.E + e];
+    __syncthreads();
+  }
+  int total;
+  const int start = block_scan(c, &total);
+  int run = start;
+  for (int64_t b0 = 0; b0 < nb; b0 += rows) {
+    const int64_t nr = nb - b0 < rows ? nb - b0 : rows;
+    stage(b0, nr);
+    if (e < d.E)
+      for (int64_t r = 0; r < nr; r++) {
+        const int v = tile[r * d.E + e];
+        tile[r * d.E + e] = run;
+        run += v;
+      }
+    __syncthreads();
+    for (int64_t i = tid; i < nr * d.E; i += DISPATCH_BLOCK) d.table[b0 * d.E + i] = tile[i];
+    __syncthreads();
+  }
+  count_tail(d, c, start, total);
   if (e == 0) d.ctrl[CTRL_DONE] = 0;  // (ready for the next dispatch)
 }
 
@@ -144,7 +217,10 @@ __global__ void k_plan_fill(DispatchBufs d, PlanBufs pl) {
 
 int launch_dispatch_count(const DispatchBufs& d, int64_t nb, hipStream_t s) {
   if (d.E < 1 || d.E > MAX_EXPERTS) return fail(ARTLITE_EINVAL, "dispatch: E %d outside [1, %d]", d.E, MAX_EXPERTS);
-  k_count<<<unsigned(nb), DISPATCH_BLOCK, 0, s>>>(d);
+  if (nb * d.E <= COUNT_TILE)
+    k_count_one<<<1, DISPATCH_BLOCK, 0, s>>>(d, int(nb));
+  else
+    k_count<<<unsigned(nb), DISPATCH_BLOCK, 0, s>>>(d);
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
 }
@@ -164,8 +240,7 @@ int launch_dispatch(const DispatchBufs& d, hipStream_t s) {
 int launch_plan(const DispatchBufs& d, const PlanBufs& pl, hipStream_t s) {
   if (d.E < 1 || d.E > MAX_EXPERTS) return fail(ARTLITE_EINVAL, "dispatch: E %d outside [1, %d]", d.E, MAX_EXPERTS);
   const int64_t nb = dispatch_blocks(d.P);
-  k_count<<<unsigned(nb), DISPATCH_BLOCK, 0, s>>>(d);
-  ART_HIP(hipGetLastError());
+  ART_TRY(launch_dispatch_count(d, nb, s));
   k_scatter<<<unsigned(nb), DISPATCH_BLOCK, 0, s>>>(d, pl);
   ART_HIP(hipGetLastError());
   const int64_t bound = d.E + (d.P + d.chunk - 1) / d.chunk;

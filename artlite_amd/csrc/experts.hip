@@ -723,7 +723,10 @@ __global__ __launch_bounds__(512) void k_prefill(const PrefillArgs a) {
   constexpr int R = L::R;
   constexpr int WN = SWIGLU ? 128 : 256;  // output columns per item
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  float2* rowf = reinterpret_cast<float2*>(lds + R * L::SBYTES);  // per row of an item: (2^in_exp, 2^-out_exp), x 2
+  // per row of an item: (2^in_exp, 2^-out_exp), in three buffers: item q's in buffer q % 3, filled while item q - 1
+  // computes (waves 0, 1); item q - 2's epilogue, the last reader of that buffer, is behind every wave by then
+  // (item q - 1's barriers), while item q - 1's may still be running in other waves (two buffers would race)
+  float2* rowf = reinterpret_cast<float2*>(lds + R * L::SBYTES);
   const int lane = threadIdx.x & (WAVE - 1), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
   const int lg = lane >> 4, lr = lane & 15;
   const int nbk = (a.N + WN - 1) / WN, stages = a.K / 64;
@@ -782,7 +785,7 @@ __global__ __launch_bounds__(512) void k_prefill(const PrefillArgs a) {
     if (has_next) {
       J = prefill_item<SWIGLU>(a, first + int64_t(q + 1) * G, nbk);
       nsrc.set(a, J, wv, lane);
-      row_info(J, (q + 1) & 1);  // (read after this item's barriers)
+      row_info(J, (q + 1) % 3);  // (read after this item's barriers)
     }
     f32x4 acc[8][2];
 #pragma unroll
@@ -797,7 +800,7 @@ __global__ __launch_bounds__(512) void k_prefill(const PrefillArgs a) {
 
     // epilogue: lane output i of block (mb, nb): row 16 mb + 4 lg + i of the tile; column (SwiGLU) n0 + 16 wv + lr
     // of gate (nb 0) and up (nb 1), (plain) n0 + 32 wv + 16 nb + lr
-    const float2* rf = rowf + (q & 1) * PREFILL_BM;
+    const float2* rf = rowf + (q % 3) * PREFILL_BM;
 #pragma unroll
     for (int mb = 0; mb < 8; mb++) {
 #pragma unroll
@@ -835,7 +838,7 @@ int launch_prefill_t(const PrefillArgs& a, hipStream_t s) {
   if (items <= 0) return ARTLITE_OK;
   if (items >= (int64_t(1) << 31)) return fail(ARTLITE_EINVAL, "prefill GEMM: %lld work items", (long long)items);
   if (a.K / 64 < L::R) return fail(ARTLITE_EINVAL, "prefill GEMM: K %d below %d", a.K, 64 * L::R);
-  constexpr size_t lds = size_t(L::R) * L::SBYTES + 2 * PREFILL_BM * 8;
+  constexpr size_t lds = size_t(L::R) * L::SBYTES + 3 * PREFILL_BM * 8;
   // persistent workgroups: as many as the device holds at once (a multiple of 8, the XCDs), at most the items
   static const int resident = [] {
     const void* f = reinterpret_cast<const void*>(k_prefill<QT, SWIGLU>);
@@ -910,10 +913,87 @@ __global__ __launch_bounds__(256) void k_prefill_x(const void* __restrict__ x, i
   if (threadIdx.x == 0) x_exp[t] = xe;
 }
 
+// The same for H a multiple of 8 up to 2048 NP: the row read once, 8 values per thread per piece (one 16-byte load for
+// bf16, two for fp32), kept in registers for the fp16 pass, written as 16-byte pieces.
+template <int XT, int NP>
+__global__ __launch_bounds__(256) void k_prefill_x_rows(const void* __restrict__ x, int H,
+                                                        const float* __restrict__ wmax, int pairs,
+                                                        uint16_t* __restrict__ x16, int32_t* __restrict__ x_exp,
+                                                        int32_t* __restrict__ h_exp, int32_t* __restrict__ h_exp2) {
+  __shared__ float red[2][4];
+  const int64_t t = blockIdx.x;
+  const int n8 = H / 8;
+  float v[NP][8];
+  float mx = 0.0f, l1 = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NP; j++) {
+    const int i = threadIdx.x + 256 * j;
+    if (i < n8) {
+      if (XT == ARTLITE_X_F32) {
+        const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + t * H) + 2 * i;
+        const float4 a = p[0], b = p[1];
+        v[j][0] = a.x, v[j][1] = a.y, v[j][2] = a.z, v[j][3] = a.w, v[j][4] = b.x, v[j][5] = b.y, v[j][6] = b.z,
+        v[j][7] = b.w;
+      } else {
+        const uint4 q = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + t * H)[i];
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[j][2 * c] = bf16_to_f32(w[c] & 0xFFFFu), v[j][2 * c + 1] = bf16_to_f32(w[c] >> 16);
+      }
+#pragma unroll
+      for (int c = 0; c < 8; c++) {
+        mx = fmaxf(mx, fabsf(v[j][c]));
+        l1 += fabsf(v[j][c]);
+      }
+    }
+  }
+  for (int o = 32; o; o >>= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, o));
+    l1 += __shfl_xor(l1, o);
+  }
+  if ((threadIdx.x & 63) == 0) red[0][threadIdx.x / 64] = mx, red[1][threadIdx.x / 64] = l1;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+  l1 = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+  const int xe = (mx > 0.0f && mx <= 3.4e38f) ? ilogbf(mx) - 14 : 0;
+#pragma unroll
+  for (int j = 0; j < NP; j++) {
+    const int i = threadIdx.x + 256 * j;
+    if (i < n8) {
+      uint32_t w[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++)
+        w[c] = uint32_t(__builtin_bit_cast(uint16_t, _Float16(__builtin_ldexpf(v[j][2 * c], -xe)))) |
+               uint32_t(__builtin_bit_cast(uint16_t, _Float16(__builtin_ldexpf(v[j][2 * c + 1], -xe)))) << 16;
+      reinterpret_cast<uint4*>(x16 + t * H)[i] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+  if (threadIdx.x < pairs) {
+    const double b = 2.0 * double(l1) * double(l1) * double(wmax[2 * threadIdx.x]) * double(wmax[2 * threadIdx.x + 1]);
+    const int he = (b > 0.0 && b < 1e300) ? ilogb(b) - 14 : 0;
+    (threadIdx.x ? h_exp2 : h_exp)[t] = max(-126, min(126, he));
+  }
+  if (threadIdx.x == 0) x_exp[t] = xe;
+}
+
 int launch_prefill_x(const void* x, int x_dtype, int64_t T, int H, const float* wmax, int pairs, uint16_t* x16,
                      int32_t* x_exp, int32_t* h_exp, int32_t* h_exp2, hipStream_t s) {
   if (T <= 0) return ARTLITE_OK;
   if (pairs < 1 || pairs > 2 || (pairs == 2 && !h_exp2)) return fail(ARTLITE_EINVAL, "prefill x: %d bounds", pairs);
+  if (H % 8 == 0 && H <= 4 * 2048) {
+    const bool f32 = x_dtype == ARTLITE_X_F32;
+#define ART_PX(XT, NP) k_prefill_x_rows<XT, NP><<<unsigned(T), 256, 0, s>>>(x, H, wmax, pairs, x16, x_exp, h_exp, h_exp2)
+    if (H <= 2048) {
+      if (f32) ART_PX(ARTLITE_X_F32, 1); else ART_PX(ARTLITE_X_BF16, 1);
+    } else if (H <= 4096) {
+      if (f32) ART_PX(ARTLITE_X_F32, 2); else ART_PX(ARTLITE_X_BF16, 2);
+    } else {
+      if (f32) ART_PX(ARTLITE_X_F32, 4); else ART_PX(ARTLITE_X_BF16, 4);
+    }
+#undef ART_PX
+    ART_HIP(hipGetLastError());
+    return ARTLITE_OK;
+  }
   k_prefill_x<<<unsigned(T), 256, 0, s>>>(x, x_dtype, H, wmax, pairs, x16, x_exp, h_exp, h_exp2);
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;

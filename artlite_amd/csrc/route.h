@@ -41,32 +41,57 @@ __device__ __forceinline__ double row_sum(const double* a, int n) {
   return s;
 }
 
-// One token's top k by one wave: R keys per lane (expert e = lane + 64 r of the logits p, expert e at
-// (e / per_col) pitch + e % per_col), k rounds of a wave maximum (the winner's key cleared), lane j keeping the j-th;
-// then the weights. ev (64 doubles) and sum (1): the wave's LDS scratch. Lane j < k writes ids[j] and the weights
-// (w32 / w64 when given) and returns its id; other lanes return -1.
+// a wave's 32-bit maximum, in every lane: DPP within 16-lane rows, then the permlane swaps across rows
+template <int C>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), C, 0xF, 0xF, false));
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+  v = max(v, dpp_u32<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+  v = max(v, dpp_u32<0x141>(v));  // row_half_mirror
+  v = max(v, dpp_u32<0x140>(v));  // row_mirror
+  const auto s16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max(uint32_t(s16[0]), uint32_t(s16[1]));
+  const auto s32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max(uint32_t(s32[0]), uint32_t(s32[1]));
+}
+
+// One token's top k by one wave: R logits per lane (expert e = lane + 64 r of the logits p, expert e at
+// (e / per_col) pitch + e % per_col) as their ordered bits (the high half of logit_key), k rounds of: the largest
+// ordered bits among the experts not yet taken (a 32-bit wave maximum), then the lowest id holding them (ballots: the
+// low half of logit_key decides ties), lane j keeping the j-th; then the weights. ev (64 doubles) and sum (1): the
+// wave's LDS scratch. Lane j < k writes ids[j] and the weights (w32 / w64 when given) and returns its id; other lanes
+// return -1.
 template <int R>
 __device__ __forceinline__ int topk_wave(const float* __restrict__ p, int per_col, int64_t pitch, int E, int k,
                                          int sigmoid, double* ev, double* sum, int lane, int32_t* __restrict__ ids,
                                          float* __restrict__ w32, double* __restrict__ w64) {
-  uint64_t key[R];
+  static_assert(R <= 32, "keys per lane");
+  uint32_t ord[R], live = 0;
 #pragma unroll
   for (int r = 0; r < R; r++) {
     const int e = lane + WAVE * r;
-    key[r] = e < E ? logit_key(p[int64_t(e / per_col) * pitch + e % per_col], e) : 0;
+    ord[r] = e < E ? uint32_t(logit_key(p[int64_t(e / per_col) * pitch + e % per_col], e) >> 32) : 0;
+    if (e < E) live |= 1u << r;
   }
-  uint64_t mine = 0;
+  int mine = 0;
   for (int j = 0; j < k; j++) {
-    uint64_t m = 0;
+    uint32_t m = 0;
 #pragma unroll
-    for (int r = 0; r < R; r++) m = key[r] > m ? key[r] : m;
-    m = wave_max_u64(m);
+    for (int r = 0; r < R; r++) m = ((live >> r) & 1) && ord[r] > m ? ord[r] : m;
+    m = wave_max_u32(m);
+    // the lowest id among the live keys equal to m: the first r with a hit, its lowest lane
+    int wr = 0, wl = 0;
 #pragma unroll
-    for (int r = 0; r < R; r++)
-      if (key[r] == m) key[r] = 0;
-    if (lane == j) mine = m;
+    for (int r = R - 1; r >= 0; r--) {
+      const uint64_t b = __ballot(((live >> r) & 1) && ord[r] == m);
+      if (b) wr = r, wl = __builtin_ctzll(b);
+    }
+    if (lane == wl) live &= ~(1u << wr);
+    if (lane == j) mine = wl + WAVE * wr;
   }
-  const int id = int(~uint32_t(mine));
+  const int id = mine;
   const bool on = lane < k;
   const float l = on ? p[int64_t(id / per_col) * pitch + id % per_col] : 0.0f;
   const double l0 = __shfl(double(l), 0, WAVE);

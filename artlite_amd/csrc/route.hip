@@ -188,12 +188,27 @@ __global__ __launch_bounds__(4 * WAVE) void k_router_small(const void* __restric
       }
     }
   }
+  // the 16 tokens' sums across the wave by halving exchanges: at lane bit b (32, 16, 8, 4) a lane keeps the half
+  // of its remaining tokens its bit selects and adds the partner's sums of those, then bits 2 and 1 add up the four
+  // lanes left per token; lane 4 t ends with token t's sum
+  static_assert(ROUTER_TG == 16, "halving exchanges of 16 tokens");
+  double v[ROUTER_TG];
 #pragma unroll
-  for (int t = 0; t < ROUTER_TG; t++) {
-    double v = acc[t];
+  for (int t = 0; t < ROUTER_TG; t++) v[t] = acc[t];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-    if (lane == 0) part[wv][t] = v;
+  for (int n = ROUTER_TG / 2, o = 32; n >= 1; n >>= 1, o >>= 1) {
+    const bool hi = lane & o;
+#pragma unroll
+    for (int i = 0; i < n; i++) {
+      const double keep = hi ? v[n + i] : v[i], give = hi ? v[i] : v[n + i];
+      v[i] = keep + __shfl_xor(give, o, WAVE);
+    }
+  }
+  v[0] += __shfl_xor(v[0], 2, WAVE);
+  v[0] += __shfl_xor(v[0], 1, WAVE);
+  if ((lane & 3) == 0) {
+    const int t = ((lane >> 5) & 1) * 8 + ((lane >> 4) & 1) * 4 + ((lane >> 3) & 1) * 2 + ((lane >> 2) & 1);
+    part[wv][t] = v[0];
   }
   __syncthreads();
   if (threadIdx.x < nt) {
@@ -225,22 +240,41 @@ __global__ __launch_bounds__(1024) void k_router_mfma(const void* __restrict__ x
     return make_float4(bf16_to_f32(v.x & 0xFFFFu), bf16_to_f32(v.x >> 16), bf16_to_f32(v.y & 0xFFFFu),
                        bf16_to_f32(v.y >> 16));
   };
+  // 64 values of K per step, the next step's loads issued before this step's products; two accumulators (even and
+  // odd 16-value blocks), summed at the end
+  d4 c1 = {0, 0, 0, 0};
+  float4 xa[4], wa[4], xb[4], wb[4];
+  auto load = [&](int k, float4(&xs)[4], float4(&ws)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      xs[j] = x4(k + 16 * j);
+      ws[j] = *reinterpret_cast<const float4*>(wr + k + 16 * j);
+    }
+  };
+  auto products = [&](const float4(&xs)[4], const float4(&ws)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      d4& acc = (j & 1) ? c1 : c;
+      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xs[j].x), double(ws[j].x), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xs[j].y), double(ws[j].y), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xs[j].z), double(ws[j].z), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xs[j].w), double(ws[j].w), acc, 0, 0, 0);
+    }
+  };
+  const int steps = H / 64;
+  if (steps > 0) load(0, xa, wa);
   int k0 = 0;
-  for (; k0 + 64 <= H; k0 += 64) {  // (four blocks' loads in flight)
-    float4 xa[4], wa[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      xa[j] = x4(k0 + 16 * j);
-      wa[j] = *reinterpret_cast<const float4*>(wr + k0 + 16 * j);
+  for (int st = 0; st < steps; st += 2, k0 += 128) {
+    if (st + 1 < steps) load(k0 + 64, xb, wb);
+    products(xa, wa);
+    if (st + 1 >= steps) {
+      k0 += 64;
+      break;
     }
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      c = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xa[j].x), double(wa[j].x), c, 0, 0, 0);
-      c = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xa[j].y), double(wa[j].y), c, 0, 0, 0);
-      c = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xa[j].z), double(wa[j].z), c, 0, 0, 0);
-      c = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xa[j].w), double(wa[j].w), c, 0, 0, 0);
-    }
+    if (st + 2 < steps) load(k0 + 128, xa, wa);
+    products(xb, wb);
   }
+  c += c1;
   for (; k0 < H; k0 += 16) {
     const float4 xv4 = x4(k0), wv4 = *reinterpret_cast<const float4*>(wr + k0);
     c = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xv4.x), double(wv4.x), c, 0, 0, 0);
@@ -368,10 +402,14 @@ __global__ __launch_bounds__(DISPATCH_BLOCK) void k_route_small(const float* __r
   const int id = valid ? sid[p] : -1;
   if (valid) atomicAdd(&base[id], 1);  // (counts: order-free)
   __syncthreads();
+  // one scan for both prefixes: the expert's count (low 16 bits) and its tiles of the expert GEMMs (high 16 bits;
+  // both sums stay below 2^16: at most DISPATCH_BLOCK pairs)
   const int e = tid;
   const int c = e < E ? base[e] : 0;
-  int total;
-  const int start = block_scan(c, &total);
+  const int nt = e < E && d.BM > 0 ? (c + d.BM - 1) / d.BM : 0;
+  int packed_total;
+  const int packed = block_scan(c | (nt << 16), &packed_total);
+  const int start = packed & 0xFFFF, total = packed_total & 0xFFFF;
   if (e < E) {
     d.counts[e] = c;
     d.offsets[e] = start;
@@ -379,14 +417,12 @@ __global__ __launch_bounds__(DISPATCH_BLOCK) void k_route_small(const float* __r
   }
   if (e == 0) d.offsets[E] = total;
   if (d.BM > 0) {  // the expert GEMMs' tiles: experts ascending, BM sorted rows each
-    const int nt = e < E ? (c + d.BM - 1) / d.BM : 0;
-    int nt_total;
-    const int t0 = block_scan(nt, &nt_total);
+    const int t0 = packed >> 16;
     for (int m = 0; m < nt; m++) {
       d.tiles[2 * (t0 + m)] = e;
       d.tiles[2 * (t0 + m) + 1] = start + m * d.BM;
     }
-    if (e == 0) d.ctrl[CTRL_TILES] = nt_total;
+    if (e == 0) d.ctrl[CTRL_TILES] = packed_total >> 16;
   }
   // each pair's rank among the earlier pairs of its expert: the lanes of its wave with the same expert (ballots over
   // the id bits), then the earlier waves' counts
