@@ -729,7 +729,7 @@ __global__ __launch_bounds__(512) void k_prefill(const PrefillArgs a) {
   float2* rowf = reinterpret_cast<float2*>(lds + R * L::SBYTES);
   const int lane = threadIdx.x & (WAVE - 1), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
   const int lg = lane >> 4, lr = lane & 15;
-  const int nbk = (a.N + WN - 1) / WN, stages = a.K / 64;
+  const int nbk = (a.N + WN - 1) / WN;
   const int64_t ntl = a.tiles ? int64_t(*a.n_tiles) : (a.dense_rows + PREFILL_BM - 1) / PREFILL_BM;
   const int64_t items = ntl * nbk, per = (items + 7) / 8;
   const int G = gridDim.x / 8, x = blockIdx.x % 8, j0 = blockIdx.x / 8;

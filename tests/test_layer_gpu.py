@@ -22,7 +22,7 @@ pytestmark = pytest.mark.gpu
 
 CASES = [("cpu", 16), ("decode", 1), ("decode", 4), ("decode", 16), ("decode", 64), ("prefill", 256),
          ("deepseek", 64), ("skewed", 192), ("mix_q8k", 16), ("mix_k8", 24), ("mix_pf", 256), ("kquants", 32),
-         ("iq4", 24)]
+         ("kquants", 160), ("iq4", 24), ("iq4", 96)]
 
 # Decode-sized passes (at most 4 pairs per expert on average, K a multiple of 256) take the GEMV over XQ activations:
 # int8 hi / lo planes per 32 values, |x - xq| <= max|x| / 65024 per group, so h (itself held in XQ) and the pair
