@@ -24,7 +24,7 @@ struct GemmArgs {
   const int32_t* offsets;  // E + 1 expert offsets in the sorted order
   int dense_rows;
   int64_t max_tiles;       // grid bound
-  int bm;                  // rows of A per tile of the tile list: DECODE_BM
+  int bm;                  // rows of A per tile of the tile list (at most DECODE_BM)
   uint16_t* h_hi;          // SwiGLU output planes (row stride N)
   uint16_t* h_lo;
   float* y;                // plain output (row stride N)

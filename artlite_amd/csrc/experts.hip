@@ -271,7 +271,7 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs a) {
     if (int64_t(blockIdx.x) >= *a.n_tiles) return;
     e = a.tiles[2 * blockIdx.x];
     s0 = a.tiles[2 * blockIdx.x + 1];
-    m_valid = min(DECODE_BM, a.offsets[e + 1] - s0);
+    m_valid = min(a.bm, a.offsets[e + 1] - s0);
   } else {
     s0 = blockIdx.x * DECODE_BM;
     m_valid = min(DECODE_BM, a.dense_rows - s0);
@@ -1032,7 +1032,7 @@ int launch_expert_gemm(const GemmArgs& a, hipStream_t s) {
     return fail(ARTLITE_EINVAL, "expert GEMM: K %d is not a multiple of the format's block", a.K);
   if (a.K / 32 > MAX_GROUPS) return fail(ARTLITE_EINVAL, "expert GEMM: K %d beyond %d", a.K, 32 * MAX_GROUPS);
   const bool swiglu = a.w[1] != nullptr;
-  if (a.tiles && a.bm != DECODE_BM) return fail(ARTLITE_EINVAL, "expert GEMM: tiles of %d rows", a.bm);
+  if (a.tiles && (a.bm < 1 || a.bm > DECODE_BM)) return fail(ARTLITE_EINVAL, "expert GEMM: tiles of %d rows", a.bm);
   const int64_t tiles = a.tiles ? a.max_tiles : (a.dense_rows + DECODE_BM - 1) / DECODE_BM;
   if (tiles <= 0) return ARTLITE_OK;
 #define ART_DISPATCH(QT) return swiglu ? launch_decode<QT, true, 2>(a, s) : launch_decode<QT, false, 2>(a, s)

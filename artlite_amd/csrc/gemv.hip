@@ -733,6 +733,36 @@ int launch_quant(const void* x, int x_dtype, int64_t T, int K, uint32_t* xq, hip
   return ARTLITE_OK;
 }
 
+// a thread per plane dword (4 values) of a group: the value s/256 (256 a + b) rounded once to fp32, then split
+__global__ void k_xq_planes(const uint32_t* __restrict__ xq, int64_t rows, int K, uint16_t* __restrict__ hi,
+                            uint16_t* __restrict__ lo) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x, per_row = K / 4;
+  if (i >= rows * per_row) return;
+  const int64_t r = i / per_row;
+  const int d = int(i - r * per_row), u = d / 64, g = (d % 64) / 8, j = d % 8;
+  const uint32_t* ub = xq + r * xq_row_dwords(K) + int64_t(u) * XQ_UNIT;
+  const uint32_t pa = ub[xq_block(g, j)], pb = ub[xq_block(g, 8 + j)];
+  const float s256 = __uint_as_float(ub[4 * (16 * (g >> 1) + 2 * (g & 1)) + 2]);
+  const int64_t o = r * K + int64_t(u) * 256 + 32 * g + 4 * j;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const int qa = int8_t((pa >> (8 * c)) & 0xFFu), qb = int8_t((pb >> (8 * c)) & 0xFFu);
+    const float v = s256 * float(256 * qa + qb);
+    const uint32_t h = f32_to_bf16(v);
+    hi[o + c] = uint16_t(h);
+    lo[o + c] = uint16_t(f32_to_bf16(v - bf16_to_f32(h)));
+  }
+}
+
+int launch_xq_planes(const uint32_t* xq, int64_t rows, int K, uint16_t* hi, uint16_t* lo, hipStream_t s) {
+  if (K <= 0 || K % 256) return fail(ARTLITE_EINVAL, "XQ planes: K %d", K);
+  const int64_t n = rows * (K / 4);
+  if (n <= 0) return ARTLITE_OK;
+  k_xq_planes<<<unsigned((n + 255) / 256), 256, 0, s>>>(xq, rows, K, hi, lo);
+  ART_HIP(hipGetLastError());
+  return ARTLITE_OK;
+}
+
 void xq_dequant_row(const uint32_t* row, int K, float* out) {
   for (int u = 0; u < K / 256; u++) {
     const uint32_t* ub = row + int64_t(u) * XQ_UNIT;

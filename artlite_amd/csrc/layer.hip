@@ -33,6 +33,7 @@ struct artlite_moe_layer {
   DevBuf h16, sh16;  // the prefill's h (fp16, scaled per token)
   DevBuf xq, hq, shq;  // the decode path's XQ activations
   bool gemv_ok = false, shared_gemv_ok = false, prefill_ok = false, shared_prefill_ok = false;
+  bool gemv_gu_ok = false;  // the routed gate / up on the GEMV (gemv_ok: the down as well)
   int64_t last_T = -1;
   bool last_gemv = false, last_prefill = false;
 };
@@ -89,9 +90,12 @@ int check_ready(const artlite_moe_layer* L) {
 // The kernels a forward pass of T tokens takes. Decode-sized passes (at most GEMV_BM pairs per expert on
 // average) run the experts on the VALU GEMV over XQ activations; prefill-sized ones (16 pairs per expert on
 // average, enough to fill PREFILL_BM tiles) on the fp16 MFMA prefill tiles; those between on the MFMA decode tiles
-// over bf16 planes.
+// over bf16 planes. A decode-sized pass whose down format the GEMV does not take (a Q6_K down after Q4_K gate / up,
+// as mixed GGUF quantisations store them) runs gate / up on the GEMV and the down on the decode tiles, h turned from
+// XQ into bf16 planes between them.
 struct Path {
-  bool gemv;            // routed experts on the GEMV
+  bool gemv_gu;         // routed gate / up on the GEMV (XQ of x; tiles of GEMV_BM rows)
+  bool gemv;            // routed experts (gate / up and down) on the GEMV
   bool shared_gemv;     // the shared expert on the GEMV
   bool prefill;         // routed experts on the prefill tiles
   bool shared_prefill;  // the shared expert on the prefill tiles
@@ -102,14 +106,15 @@ struct Path {
 
 Path path_of(const artlite_moe_layer* L, int64_t T) {
   Path p{};
-  p.gemv = L->gemv_ok && T * L->d.top_k <= int64_t(GEMV_BM) * L->d.n_experts;
-  p.shared_gemv = L->d.shared_ffn && p.gemv && L->shared_gemv_ok;
-  p.prefill = !p.gemv && L->prefill_ok && T * L->d.top_k >= int64_t(16) * L->d.n_experts;
+  p.gemv_gu = L->gemv_gu_ok && T * L->d.top_k <= int64_t(GEMV_BM) * L->d.n_experts;
+  p.gemv = p.gemv_gu && L->gemv_ok;
+  p.shared_gemv = L->d.shared_ffn && p.gemv_gu && L->shared_gemv_ok;
+  p.prefill = !p.gemv_gu && L->prefill_ok && T * L->d.top_k >= int64_t(16) * L->d.n_experts;
   p.shared_prefill = L->d.shared_ffn && p.prefill && L->shared_prefill_ok && T >= PREFILL_BM / 2;
-  const bool planes = (!p.gemv && !p.prefill) || (L->d.shared_ffn && !p.shared_gemv && !p.shared_prefill);
+  const bool planes = (!p.gemv_gu && !p.prefill) || (L->d.shared_ffn && !p.shared_gemv && !p.shared_prefill);
   p.split = planes && (L->x_dtype == ARTLITE_X_F32 || L->d.norm_eps > 0);  // (the normalised x is fp32)
-  p.quant = p.gemv;
-  p.small = p.gemv && T * L->d.top_k <= DISPATCH_BLOCK && L->d.n_experts <= MAX_EXPERTS;
+  p.quant = p.gemv_gu;
+  p.small = p.gemv_gu && T * L->d.top_k <= DISPATCH_BLOCK && L->d.n_experts <= MAX_EXPERTS;
   return p;
 }
 
@@ -130,6 +135,7 @@ std::vector<std::string> kernel_list(const artlite_moe_layer* L, int64_t T) {
     k.push_back("dispatch_scatter");
   }
   k.push_back("gate_up");
+  if (p.gemv_gu && !p.gemv) k.push_back("h_planes");
   k.push_back("down");
   if (L->d.shared_ffn) {
     k.push_back("shared_gate_up");
@@ -181,7 +187,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     ART_TRY(mark());
     ART_TRY(launch_router(xin, xdt, L->sinp.as<float>(), H, 1, T, L->sg.as<float>(), 1, nullptr, s));
   }
-  const int BM = path.gemv ? GEMV_BM : path.prefill ? PREFILL_BM : DECODE_BM;
+  const int BM = path.gemv_gu ? GEMV_BM : path.prefill ? PREFILL_BM : DECODE_BM;
   DispatchBufs db{L->ids.as<int32_t>(), P, E, k, L->table.as<int32_t>(), L->ctrl.as<int32_t>(),
                   L->counts.as<int32_t>(), L->offsets.as<int32_t>(), L->order.as<int32_t>(), L->slot.as<int32_t>(),
                   L->tiles.as<int32_t>(), BM, nullptr, 0};
@@ -199,7 +205,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     ART_TRY(mark());
     ART_TRY(launch_dispatch_scatter(db, nb, s));
   }
-  if (path.gemv) {
+  if (path.gemv_gu) {
     GemvArgs g{};
     g.w[0] = L->gate.as<uint8_t>();
     g.w[1] = L->up.as<uint8_t>();
@@ -220,20 +226,45 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     g.hq = L->hq.as<uint32_t>();
     ART_TRY(mark());
     ART_TRY(launch_gemv(g, s));
-    GemvArgs dn = g;
-    dn.w[0] = L->down.as<uint8_t>();
-    dn.w[1] = nullptr;
-    dn.expert_bytes = int64_t(H) * L->down_row;
-    dn.row_bytes = int(L->down_row);
-    dn.N = H;
-    dn.K = F;
-    dn.qtype = d.down_type;
-    dn.xq = L->hq.as<uint32_t>();
-    dn.a_gather = 0;
-    dn.hq = nullptr;
-    dn.y = L->ypairs.as<float>();
-    ART_TRY(mark());
-    ART_TRY(launch_gemv(dn, s));
+    if (path.gemv) {
+      GemvArgs dn = g;
+      dn.w[0] = L->down.as<uint8_t>();
+      dn.w[1] = nullptr;
+      dn.expert_bytes = int64_t(H) * L->down_row;
+      dn.row_bytes = int(L->down_row);
+      dn.N = H;
+      dn.K = F;
+      dn.qtype = d.down_type;
+      dn.xq = L->hq.as<uint32_t>();
+      dn.a_gather = 0;
+      dn.hq = nullptr;
+      dn.y = L->ypairs.as<float>();
+      ART_TRY(mark());
+      ART_TRY(launch_gemv(dn, s));
+    } else {  // (the down on the MFMA decode tiles, over the GEMV's tiles of GEMV_BM rows)
+      ART_TRY(mark());
+      ART_TRY(launch_xq_planes(L->hq.as<uint32_t>(), P, F, L->hhi.as<uint16_t>(), L->hlo.as<uint16_t>(), s));
+      GemmArgs dn{};
+      dn.w[0] = L->down.as<uint8_t>();
+      dn.expert_bytes = int64_t(H) * L->down_row;
+      dn.row_bytes = int(L->down_row);
+      dn.N = H;
+      dn.K = F;
+      dn.qtype = d.down_type;
+      dn.a_hi = L->hhi.as<uint16_t>();
+      dn.a_lo = L->hlo.as<uint16_t>();
+      dn.a_gather = 0;
+      dn.order = L->order.as<int32_t>();
+      dn.topk = k;
+      dn.tiles = L->tiles.as<int32_t>();
+      dn.n_tiles = L->ctrl.as<int32_t>() + CTRL_TILES;
+      dn.offsets = L->offsets.as<int32_t>();
+      dn.max_tiles = tile_bound(P, E, BM);
+      dn.bm = BM;
+      dn.y = L->ypairs.as<float>();
+      ART_TRY(mark());
+      ART_TRY(launch_expert_gemm(dn, s));
+    }
   } else if (path.prefill) {
     PrefillArgs g{};
     g.w[0] = L->gate.as<uint8_t>();
@@ -403,7 +434,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
                          L->x_dtype, L->y.as<float>(), s));
   ART_TRY(mark());
   L->last_T = T;
-  L->last_gemv = path.gemv;
+  L->last_gemv = path.gemv_gu;
   L->last_prefill = path.prefill;
   return ARTLITE_OK;
 }
@@ -450,8 +481,8 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
     L->sgate_row = size_t(d.hidden) / sq->per * sq->bytes;
     L->sdown_row = size_t(d.shared_ffn) / sdq->per * sdq->bytes;
   }
-  L->gemv_ok = gemv_supported(d.gate_type, d.hidden, d.expert_ffn) &&
-               gemv_supported(d.down_type, d.expert_ffn, d.hidden);
+  L->gemv_gu_ok = gemv_supported(d.gate_type, d.hidden, d.expert_ffn) && d.expert_ffn % 256 == 0;
+  L->gemv_ok = L->gemv_gu_ok && gemv_supported(d.down_type, d.expert_ffn, d.hidden);
   L->prefill_ok = prefill_supported(d.gate_type, d.hidden, d.expert_ffn) &&
                   prefill_supported(d.down_type, d.expert_ffn, d.hidden);
   L->shared_gemv_ok = sq && gemv_supported(sq->id, d.hidden, d.shared_ffn) &&
@@ -500,7 +531,7 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
       res(L->sh16, size_t(T) * d.shared_ffn * 2);
     }
   }
-  if (L->gemv_ok) {
+  if (L->gemv_gu_ok) {
     res(L->xq, size_t(T * xq_row_dwords(d.hidden)) * 4);
     res(L->hq, size_t(P * xq_row_dwords(d.expert_ffn)) * 4);
     if (L->shared_gemv_ok) res(L->shq, size_t(T * xq_row_dwords(d.shared_ffn)) * 4);

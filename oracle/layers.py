@@ -69,6 +69,10 @@ CONFIGS = {
     # Q4_1 shared expert and fp32 x
     "kquants": Spec("kquants", H=1024, E=16, k=2, F=512, gate_type="Q5_K", down_type="Q6_K", scale=1e-4,
                     dmin_scale=1e-3, shared_F=512, shared_type="Q4_K", shared_down_type="Q3_K", tokens=(32,)),
+    # test-only: a mixed quantisation as GGUF files store it (Q4_K gate / up, Q6_K down; the shared expert likewise) at
+    # decode size: gate / up on the GEMV, the downs on the MFMA decode tiles
+    "kmix": Spec("kmix", H=1024, E=32, k=4, F=512, gate_type="Q4_K", down_type="Q6_K", scale=2e-4, dmin_scale=1.5e-3,
+                 shared_F=512, shared_type="Q4_K", shared_down_type="Q6_K", shared_gated=True, tokens=(16,)),
     "iq4": Spec("iq4", H=768, E=16, k=4, F=512, gate_type="IQ4_XS", down_type="IQ4_NL", scale=5e-5, x_dtype="f32",
                 shared_F=256, shared_type="Q4_1", shared_scale=4e-3, shared_gated=True, tokens=(24,)),
 }
