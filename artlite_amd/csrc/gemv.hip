@@ -4,7 +4,7 @@
 // GEMV_BM sorted rows of A (tokens for gate / up, pairs for down) of one expert times a block of 16 RB weight rows
 // (SwiGLU: those rows of gate and of up). Plain products: 4 waves, one per 16-row block (RB 4, 64 rows). SwiGLU:
 // 8 waves, 2 row blocks (32 rows) x 4 waves that split K four ways, whose partial sums meet in LDS. Each wave
-// streams its own steps (16 rows x one K-unit of 8 groups of 32 values: Q4_0 / Q4_K 144 bytes a row, Q8_0 272)
+// streams its own steps (16 rows x one K-unit of 8 groups of 32 values: Q4_0 / Q4_K 144 bytes a row, Q5_K 176, Q8_0 272)
 // with global_load_lds_dwordx4 into D LDS slots of its own, one step ahead, across item boundaries; the XQ records
 // of A's rows for a K-unit come the same way. Every load is a DMA counted as it is issued, so each wait names the
 // exact count (the compiler, which cannot order DMAs against register loads, would otherwise wait for all of them).
@@ -16,9 +16,9 @@
 // buffer) adds them in a fixed order, forms h = silu(gate) up and writes it as XQ for the down product.
 //
 // Arithmetic of one (row of A, group): A = sum_j dot4(a_j, q_j) and B = C + sum_j dot4(b_j, q_j), exactly in int32,
-// with q_j the group's codes as int8 (Q4_0 / Q4_K: nibbles 0..15, Q8_0: the signed bytes) and C the code offset's
+// with q_j the group's codes as int8 (Q4_0 / Q4_K: nibbles 0..15, Q5_K: 0..31, Q8_0: the signed bytes) and C the code offset's
 // correction (Q4_0: -8 sum(256 a + b), else 0); then acc += (d s / 256) float(256 A + B), which is
-// d s sum (q - 8)(a + b / 256) for Q4_0. Q4_K adds -(dmin mn) times the group's dequantised activation sum.
+// d s sum (q - 8)(a + b / 256) for Q4_0. Q4_K and Q5_K add -(dmin mn) times the group's dequantised activation sum.
 #include "gemv.h"
 #include "xq.h"
 
@@ -36,8 +36,8 @@ namespace {
 
 __device__ __forceinline__ float h2f(uint32_t h) { return float(__builtin_bit_cast(_Float16, uint16_t(h))); }
 
-// per format: bytes of a row's unit, dwords a lane reads of it (Q4_0 / Q8_0: its two groups; Q4_K: the super-block
-// header and the 32-byte run holding its two groups)
+// per format: bytes of a row's unit, dwords a lane reads of it (Q4_0 / Q8_0: its two groups; Q4_K / Q5_K: the
+// super-block header, Q5_K's 32 high-bit bytes, and the 32-byte run holding its two groups)
 template <int QT>
 struct Unit;
 template <>
@@ -51,6 +51,10 @@ struct Unit<ARTLITE_Q8_0> {
 template <>
 struct Unit<ARTLITE_Q4_K> {
   static constexpr int BYTES = 144, LW = 12;
+};
+template <>
+struct Unit<ARTLITE_Q5_K> {  // (the header, the 32 high-bit bytes, the lane's 32-byte run)
+  static constexpr int BYTES = 176, LW = 20;
 };
 
 template <typename F, int... I>
@@ -99,7 +103,7 @@ __device__ __forceinline__ float4 lds_read_f4(const void* p) {
   return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
 }
 
-// After vmcnt(N), the lane's dwords of a unit (at pw; Q4_K: header at pw, its run at pr) and (MX > 0) its record
+// After vmcnt(N), the lane's dwords of a unit (at pw; Q4_K / Q5_K: header, Q5_K high bits, at pw, its run at pr) and (MX > 0) its record
 // chunk of each of MX rows of A (at px, 1024 bytes apart), and their completion, in one asm block: the compiler
 // would otherwise wait for every load in flight before reading LDS (it takes the slots' global_load_lds writes for
 // possible producers), and it must not touch the outputs before the final wait.
@@ -118,6 +122,13 @@ __device__ __forceinline__ float4 lds_read_f4(const void* p) {
   "ds_read_b128 %[w1], %[pr]\n\t"  \
   "ds_read_b128 %[w2], %[pr] offset:16\n\t"
 #define ART_OW12 [w0] "=&v"(w4[0]), [w1] "=&v"(w4[1]), [w2] "=&v"(w4[2])
+#define ART_W20                                \
+  "ds_read_b128 %[w0], %[pw]\n\t"             \
+  "ds_read_b128 %[w1], %[pw] offset:16\n\t"   \
+  "ds_read_b128 %[w2], %[pw] offset:32\n\t"   \
+  "ds_read_b128 %[w3], %[pr]\n\t"             \
+  "ds_read_b128 %[w4], %[pr] offset:16\n\t"
+#define ART_OW20 [w0] "=&v"(w4[0]), [w1] "=&v"(w4[1]), [w2] "=&v"(w4[2]), [w3] "=&v"(w4[3]), [w4] "=&v"(w4[4])
 #define ART_RX(T) "ds_read_b128 %[x" #T "], %[px] offset:" #T "*1024\n\t"
 #define ART_X0
 #define ART_X1 ART_RX(0)
@@ -149,6 +160,11 @@ __device__ __forceinline__ void read_unit(uint32_t (&w)[Unit<QT>::LW], u32x4 (&x
     ART_READ_M(12)
 #pragma unroll
     for (int i = 0; i < 12; i++) w[i] = w4[i >> 2][i & 3];
+  } else if constexpr (LW == 20) {
+    u32x4 w4[5];
+    ART_READ_M(20)
+#pragma unroll
+    for (int i = 0; i < 20; i++) w[i] = w4[i >> 2][i & 3];
   } else {
     u32x2 w2[LW / 2];
     uint32_t w1;
@@ -177,6 +193,8 @@ __device__ __forceinline__ void read_unit(uint32_t (&w)[Unit<QT>::LW], u32x4 (&x
 #undef ART_RX
 #undef ART_OW12
 #undef ART_W12
+#undef ART_OW20
+#undef ART_W20
 #undef ART_OW17
 #undef ART_W17
 #undef ART_OW9
@@ -187,7 +205,7 @@ __device__ __forceinline__ void read_unit(uint32_t (&w)[Unit<QT>::LW], u32x4 (&x
 #undef ART_R2
 
 // Codes of the lane's group H (0, 1) as 8 dwords of int8 (q[j]: values 4 j .. 4 j + 3 of the group), its scale d
-// (Q4_K: d sc) and Q4_K's dmin mn. g: the group's index in the unit (Q4_K's scales).
+// (Q4_K / Q5_K: d sc) and their dmin mn. g: the group's index in the unit (their scales, Q5_K's high bits).
 template <int QT, int H>
 __device__ __forceinline__ void codes(const uint32_t (&w)[Unit<QT>::LW], int g, uint32_t (&q)[8], float& d,
                                       float& mn) {
@@ -224,8 +242,14 @@ __device__ __forceinline__ void codes(const uint32_t (&w)[Unit<QT>::LW], int g, 
     const uint32_t m = g < 4 ? b4 & 63u : (b4 >> 4) | ((b0 >> 6) << 4);
     d = h2f(w[0] & 0xFFFFu) * float(sc);  // (exact: 11 x 6 significant bits)
     mn = h2f(w[0] >> 16) * float(m);
+    if constexpr (QT == ARTLITE_Q4_K) {
 #pragma unroll
-    for (int j = 0; j < 8; j++) q[j] = H ? (w[4 + j] >> 4) & 0x0F0F0F0Fu : w[4 + j] & 0x0F0F0F0Fu;
+      for (int j = 0; j < 8; j++) q[j] = H ? (w[4 + j] >> 4) & 0x0F0F0F0Fu : w[4 + j] & 0x0F0F0F0Fu;
+    } else {  // Q5_K: the run at w[12..19]; bit g of high-bit byte l (w[4..11]) is bit 4 of value l's code
+#pragma unroll
+      for (int j = 0; j < 8; j++)
+        q[j] = (H ? (w[12 + j] >> 4) & 0x0F0F0F0Fu : w[12 + j] & 0x0F0F0F0Fu) | (((w[4 + j] >> g) & 0x01010101u) << 4);
+    }
   }
 }
 
@@ -407,8 +431,8 @@ struct Stream {
     }
     wbase = lds_addr(my);
     xbase = lds_addr(my + D * WCH) + 16 * lane;
-    o_w = r * BY + (QT == ARTLITE_Q4_K ? 0 : (QT == ARTLITE_Q4_0 ? 36 : 68) * p);
-    o_r = r * BY + 16 + 32 * p;  // (Q4_K)
+    o_w = r * BY + (QT == ARTLITE_Q4_K || QT == ARTLITE_Q5_K ? 0 : (QT == ARTLITE_Q4_0 ? 36 : 68) * p);
+    o_r = r * BY + (QT == ARTLITE_Q5_K ? 48 : 16) + 32 * p;  // (Q4_K / Q5_K: the lane's run)
   }
   // the weights of local step v of item (e, n0) into slot `slot`; !on: none (the end of the stream), counted alike
   template <int MX>
@@ -696,14 +720,15 @@ int launch_t(const GemvArgs& a, hipStream_t s) {
 }  // namespace
 
 bool gemv_supported(int qtype, int K, int N) {
-  return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0 || qtype == ARTLITE_Q4_K) && K > 0 && K % 256 == 0 &&
+  return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0 || qtype == ARTLITE_Q4_K || qtype == ARTLITE_Q5_K) && K > 0 &&
+         K % 256 == 0 &&
          N > 0 && N % 64 == 0;
 }
 
 int launch_gemv(const GemvArgs& a, hipStream_t s) {
   if (!gemv_supported(a.qtype, a.K, a.N))
     return fail(ARTLITE_EINVAL,
-                "expert GEMV: weight type %d with K %d, N %d (Q4_0 / Q8_0 / Q4_K, K a multiple of 256, N of 64)",
+                "expert GEMV: weight type %d with K %d, N %d (Q4_0 / Q8_0 / Q4_K / Q5_K, K a multiple of 256, N of 64)",
                 a.qtype, a.K, a.N);
   if (a.N <= 0 || int64_t(a.N) * a.row_bytes >= (int64_t(1) << 31))
     return fail(ARTLITE_EINVAL, "expert GEMV: %d rows of %d bytes", a.N, a.row_bytes);
@@ -715,6 +740,7 @@ int launch_gemv(const GemvArgs& a, hipStream_t s) {
   switch (a.qtype) {
     case ARTLITE_Q4_0: ART_DISPATCH(ARTLITE_Q4_0);
     case ARTLITE_Q8_0: ART_DISPATCH(ARTLITE_Q8_0);
+    case ARTLITE_Q5_K: ART_DISPATCH(ARTLITE_Q5_K);
     default: ART_DISPATCH(ARTLITE_Q4_K);
   }
 #undef ART_DISPATCH

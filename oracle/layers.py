@@ -73,6 +73,11 @@ CONFIGS = {
     # decode size: gate / up on the GEMV, the downs on the MFMA decode tiles
     "kmix": Spec("kmix", H=1024, E=32, k=4, F=512, gate_type="Q4_K", down_type="Q6_K", scale=2e-4, dmin_scale=1.5e-3,
                  shared_F=512, shared_type="Q4_K", shared_down_type="Q6_K", shared_gated=True, tokens=(16,)),
+    # test-only: Q5_K on the decode GEMV, with a Q6_K routed down (Q5_K_M files) or a Q5_K one
+    "q5km": Spec("q5km", H=1024, E=32, k=4, F=512, gate_type="Q5_K", down_type="Q6_K", scale=1e-4, dmin_scale=1e-3,
+                 shared_F=512, shared_type="Q5_K", tokens=(16,)),
+    "q5k": Spec("q5k", H=1536, E=16, k=2, F=768, gate_type="Q5_K", down_type="Q5_K", scale=1e-4, dmin_scale=1e-3,
+                x_dtype="f32", tokens=(24,)),
     "iq4": Spec("iq4", H=768, E=16, k=4, F=512, gate_type="IQ4_XS", down_type="IQ4_NL", scale=5e-5, x_dtype="f32",
                 shared_F=256, shared_type="Q4_1", shared_scale=4e-3, shared_gated=True, tokens=(24,)),
 }
