@@ -3,8 +3,9 @@
 // Persistent workgroups (as many as the device holds) take work items in turn: an item is one tile of at most
 // GEMV_BM sorted rows of A (tokens for gate / up, pairs for down) of one expert times a block of 16 RB weight rows
 // (SwiGLU: those rows of gate and of up). Plain products: 4 waves, one per 16-row block (RB 4, 64 rows). SwiGLU:
-// 8 waves, 2 row blocks (32 rows) x 4 waves that split K four ways, whose partial sums meet in LDS. Each wave
-// streams its own steps (16 rows x one K-unit of 8 groups of 32 values: Q4_0 / Q4_K 144 bytes a row, Q5_K 176, Q8_0 272)
+// 8 waves, 4 row blocks (64 rows) x 2 waves that split K in halves, whose partial sums meet in LDS. Each wave
+// streams its own steps (16 rows x one K-unit of 8 groups of 32 values: Q4_0 / Q4_K 144 bytes a row, Q5_K 176,
+// Q8_0 272)
 // with global_load_lds_dwordx4 into D LDS slots of its own, one step ahead, across item boundaries; the XQ records
 // of A's rows for a K-unit come the same way. Every load is a DMA counted as it is issued, so each wait names the
 // exact count (the compiler, which cannot order DMAs against register loads, would otherwise wait for all of them).
@@ -12,8 +13,8 @@
 // share a row. The activations are read once per K-unit into registers, one 16-byte XQ chunk per lane per row of A:
 // DPP row_newbcast:j hands every lane of 16-lane row p dword j of its groups' blocks as the broadcast operand of
 // v_dot4c_i32_i8, and the per-group words the same way. The four lanes of a row are summed at the end. The SwiGLU
-// epilogue has no barrier: the last of the four K-split waves to deliver its partial sums (an LDS counter per
-// buffer) adds them in a fixed order, forms h = silu(gate) up and writes it as XQ for the down product.
+// epilogue has no barrier: the last of the item's waves to deliver its partial sums (an LDS counter per buffer) adds
+// them in a fixed order, forms h = silu(gate) up and writes it as XQ for the down product.
 //
 // Arithmetic of one (row of A, group): A = sum_j dot4(a_j, q_j) and B = C + sum_j dot4(b_j, q_j), exactly in int32,
 // with q_j the group's codes as int8 (Q4_0 / Q4_K: nibbles 0..15, Q5_K: 0..31, Q8_0: the signed bytes) and C the code offset's
@@ -322,7 +323,9 @@ __device__ __forceinline__ float group_term(float acc, uint32_t x, uint32_t l, u
 
 template <bool SWIGLU>
 struct Shape {
-  static constexpr int RB = SWIGLU ? 2 : 4, S = SWIGLU ? 4 : 1, WAVES = RB * S, THREADS = 64 * WAVES;
+  static constexpr int RB = 4, S = SWIGLU ? 2 : 1, WAVES = RB * S, THREADS = 64 * WAVES;
+  // (SwiGLU: whole 32-row XQ groups of h per item, 8 lanes each, at most 64 lanes for GEMV_BM rows of A)
+  static_assert(!SWIGLU || (RB % 2 == 0 && 8 * RB / 2 * GEMV_BM <= 64), "SwiGLU epilogue lanes");
 };
 
 // LDS of a workgroup: each wave's D slots of 16 rows x BYTES and its XS record slots (GEMV_BM chunk rows of 1 KB;
@@ -620,9 +623,8 @@ __global__ __launch_bounds__(Shape<SWIGLU>::THREADS) __attribute__((amdgpu_waves
       // The K-ranges' partial sums through LDS, summed in a fixed order by the last wave to deliver its own (a
       // counter per buffer, no barrier: the other waves go on with their next items); RED_BUFS buffers, a wave
       // waiting before it reuses one until the epilogue RED_BUFS items back is done. Then h = silu(gate) up of
-      // the 32 rows, quantised into one group of an XQ row of N values per row of A: lanes 8 t .. 8 t + 7 take row
-      // of A t, 4 rows each. (The lane is recomputed here rather than kept from the start: the registers are
-      // needed by the steps.)
+      // the 16 RB rows, quantised into RB / 2 groups of an XQ row of N values per row of A. (The lane is recomputed
+      // here rather than kept from the start: the registers are needed by the steps.)
       const int ln = __lane_id(), b = j % RED_BUFS;
       float* rd = red + b * RED;
       if (j >= RED_BUFS) {
@@ -636,9 +638,11 @@ __global__ __launch_bounds__(Shape<SWIGLU>::THREADS) __attribute__((amdgpu_waves
       int arrived = 0;
       if (ln == 0) arrived = lds_inc(ctr + b);
       if (__builtin_amdgcn_readfirstlane(arrived) == W::WAVES - 1) {
-        if (ln < 8 * cur.m) {
-          const int t = ln >> 3, l8 = ln & 7, rbb = l8 >> 2, r0 = 4 * (l8 & 3);
-          const int UH = a.N / 256, blk = cur.n0 / 32, g = blk & 7;
+        if (ln < 8 * RB / 2 * cur.m) {
+          // lanes 8 RB / 2 t .. + 8 RB / 2 take row of A t: 8 lanes per XQ group of 32 rows, 4 rows each
+          constexpr int LPT = 8 * RB / 2;
+          const int t = ln / LPT, lt = ln % LPT, l8 = lt & 7, rbb = lt >> 2, r0 = 4 * (lt & 3);
+          const int UH = a.N / 256, blk = cur.n0 / 32 + (lt >> 3), g = blk & 7;
           float4 gsum = {0.0f, 0.0f, 0.0f, 0.0f}, usum = gsum;
 #pragma unroll
           for (int k = 0; k < S; k++) {
