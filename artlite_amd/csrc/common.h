@@ -36,7 +36,9 @@ struct QType {
   int id;
   const char* name;
   int per;    // values per block
-  int bytes;  // bytes per block
+  int bytes;  // bytes per block (in a GGUF file)
+  int dev;    // bytes per block in an uploaded layer: the same, but Q6_K's 210 padded to 224 (16-byte aligned
+              // blocks, so that the decode GEMV's 16-byte DMAs take them)
 };
 const QType* qtype_by_name(const char* name);
 const QType* qtype_by_id(int id);

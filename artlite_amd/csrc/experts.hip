@@ -93,7 +93,7 @@ struct Fmt<ARTLITE_Q4_K> : FmtT<144, 8, 32, 128, true> {};
 template <>
 struct Fmt<ARTLITE_Q5_K> : FmtT<176, 8, 24, 128, true> {};
 template <>
-struct Fmt<ARTLITE_Q6_K> : FmtT<210, 8, 16, 160, false, true> {};  // (128 + q) - (q - 32)
+struct Fmt<ARTLITE_Q6_K> : FmtT<224, 8, 16, 160, false, true> {};  // (128 + q) - (q - 32); the layer's padded blocks
 template <>
 struct Fmt<ARTLITE_IQ4_NL> : FmtT<18, 1, 32, 128> {};
 template <>

@@ -57,6 +57,11 @@ template <>
 struct Unit<ARTLITE_Q5_K> {  // (the header, the 32 high-bit bytes, the lane's 32-byte run)
   static constexpr int BYTES = 176, LW = 20;
 };
+template <>
+struct Unit<ARTLITE_Q6_K> {  // (a layer's 224-byte padded block: the lane's 64 low-bit bytes, 32 high-bit bytes, and the
+                             // 16 scales with d)
+  static constexpr int BYTES = 224, LW = 32;
+};
 
 template <typename F, int... I>
 __device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
@@ -130,6 +135,18 @@ __device__ __forceinline__ float4 lds_read_f4(const void* p) {
   "ds_read_b128 %[w3], %[pr]\n\t"             \
   "ds_read_b128 %[w4], %[pr] offset:16\n\t"
 #define ART_OW20 [w0] "=&v"(w4[0]), [w1] "=&v"(w4[1]), [w2] "=&v"(w4[2]), [w3] "=&v"(w4[3]), [w4] "=&v"(w4[4])
+#define ART_W32                                \
+  "ds_read_b128 %[w0], %[pw]\n\t"             \
+  "ds_read_b128 %[w1], %[pw] offset:16\n\t"   \
+  "ds_read_b128 %[w2], %[pw] offset:32\n\t"   \
+  "ds_read_b128 %[w3], %[pw] offset:48\n\t"   \
+  "ds_read_b128 %[w4], %[pr]\n\t"             \
+  "ds_read_b128 %[w5], %[pr] offset:16\n\t"   \
+  "ds_read_b128 %[w6], %[ps]\n\t"             \
+  "ds_read_b128 %[w7], %[ps] offset:16\n\t"
+#define ART_OW32                                                                                          \
+  [w0] "=&v"(w4[0]), [w1] "=&v"(w4[1]), [w2] "=&v"(w4[2]), [w3] "=&v"(w4[3]), [w4] "=&v"(w4[4]), [w5] "=&v"(w4[5]), \
+      [w6] "=&v"(w4[6]), [w7] "=&v"(w4[7])
 #define ART_RX(T) "ds_read_b128 %[x" #T "], %[px] offset:" #T "*1024\n\t"
 #define ART_X0
 #define ART_X1 ART_RX(0)
@@ -144,7 +161,7 @@ __device__ __forceinline__ float4 lds_read_f4(const void* p) {
 #define ART_READ(WN, MN)                                                                       \
   asm volatile("s_waitcnt vmcnt(%[n])\n\t" ART_W##WN ART_X##MN "s_waitcnt lgkmcnt(0)"       \
                : ART_OW##WN ART_OX##MN                                                          \
-               : [pw] "v"(pw), [pr] "v"(pr), [px] "v"(px), [n] "i"(N))
+               : [pw] "v"(pw), [pr] "v"(pr), [ps] "v"(ps), [px] "v"(px), [n] "i"(N))
 #define ART_READ_M(WN)                   \
   if constexpr (MX == 0) ART_READ(WN, 0); \
   if constexpr (MX == 1) ART_READ(WN, 1); \
@@ -153,7 +170,7 @@ __device__ __forceinline__ float4 lds_read_f4(const void* p) {
   if constexpr (MX == 4) ART_READ(WN, 4);
 template <int N, int QT, int MX>
 __device__ __forceinline__ void read_unit(uint32_t (&w)[Unit<QT>::LW], u32x4 (&x)[GEMV_BM], uint32_t pw, uint32_t pr,
-                                          uint32_t px) {
+                                          uint32_t ps, uint32_t px) {
   static_assert(N >= 0 && N < 64, "vmcnt");
   constexpr int LW = Unit<QT>::LW;
   if constexpr (LW == 12) {
@@ -166,6 +183,11 @@ __device__ __forceinline__ void read_unit(uint32_t (&w)[Unit<QT>::LW], u32x4 (&x
     ART_READ_M(20)
 #pragma unroll
     for (int i = 0; i < 20; i++) w[i] = w4[i >> 2][i & 3];
+  } else if constexpr (LW == 32) {
+    u32x4 w4[8];
+    ART_READ_M(32)
+#pragma unroll
+    for (int i = 0; i < 32; i++) w[i] = w4[i >> 2][i & 3];
   } else {
     u32x2 w2[LW / 2];
     uint32_t w1;
@@ -196,6 +218,8 @@ __device__ __forceinline__ void read_unit(uint32_t (&w)[Unit<QT>::LW], u32x4 (&x
 #undef ART_W12
 #undef ART_OW20
 #undef ART_W20
+#undef ART_OW32
+#undef ART_W32
 #undef ART_OW17
 #undef ART_W17
 #undef ART_OW9
@@ -231,6 +255,22 @@ __device__ __forceinline__ void codes(const uint32_t (&w)[Unit<QT>::LW], int g, 
     }
     d = o % 4 == 0 ? h2f(w[o / 4] & 0xFFFFu) : h2f(w[(o - 2) / 4] >> 16);
     mn = 0.0f;
+  } else if constexpr (QT == ARTLITE_Q6_K) {
+    // group g = 4 h + jj (h = p / 2, jj = 2 (p % 2) + H): value l's low bits are a nibble of low-bit byte 32 (jj % 2)
+    // + l of half h (w[0..15]: the high nibbles for jj >= 2), its high bits crumb jj of high-bit byte l (w[16..23]);
+    // code - 32 as int8 (the 6-bit code with bit 5 flipped, sign-extended); the scales of its two 16-value halves,
+    // int8 sub-block scales 2 g, 2 g + 1 (bytes 192.., w[24..27]) times d (bytes 208, w[28]): d in d, the second in mn
+    const int p = g >> 1, jj = 2 * (p & 1) + H, sh = 4 * (p & 1);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const uint32_t c = ((w[8 * H + j] >> sh) & 0x0F0F0F0Fu) | (((w[16 + j] >> (2 * jj)) & 0x03030303u) << 4);
+      const uint32_t y = c ^ 0x20202020u, sgn = y & 0x20202020u;
+      q[j] = y | (sgn << 1) | (sgn << 2);
+    }
+    const float dd = h2f(w[28] & 0xFFFFu);
+    const uint32_t sw = w[24 + (g >> 1)] >> (16 * (g & 1));  // (bytes 2 g, 2 g + 1 of the scales)
+    d = dd * float(int8_t(sw & 0xFFu));  // (exact: 11 x 8 significant bits)
+    mn = dd * float(int8_t((sw >> 8) & 0xFFu));
   } else {
     // a super-block: fp16 d, dmin; 12 bytes of 6-bit scales / mins (w[1..3]); the lane's 32-byte run (w[4..11]),
     // its group 2 p in the low nibbles and 2 p + 1 in the high nibbles (value order)
@@ -268,6 +308,12 @@ __device__ __forceinline__ void codes(const uint32_t (&w)[Unit<QT>::LW], int g, 
   ART_DOT(b0, q2, 10) ART_DOT(a1, q3, 3) ART_DOT(b1, q3, 11) ART_DOT(a0, q4, 4) ART_DOT(b0, q4, 12)             \
   ART_DOT(a1, q5, 5) ART_DOT(b1, q5, 13) ART_DOT(a0, q6, 6) ART_DOT(b0, q6, 14) ART_DOT(a1, q7, 7)              \
   ART_DOT(b1, q7, 15)
+// (Q6_K: the same sixteen dot4, the chains by half: a0 / b0 over dwords 0..3, a1 / b1 over 4..7, still four apart)
+#define ART_DOTS_HALVES                                                                                         \
+  ART_DOT(a0, q0, 0) ART_DOT(b0, q0, 8) ART_DOT(a1, q4, 4) ART_DOT(b1, q4, 12) ART_DOT(a0, q1, 1)                \
+  ART_DOT(b0, q1, 9) ART_DOT(a1, q5, 5) ART_DOT(b1, q5, 13) ART_DOT(a0, q2, 2) ART_DOT(b0, q2, 10)              \
+  ART_DOT(a1, q6, 6) ART_DOT(b1, q6, 14) ART_DOT(a0, q3, 3) ART_DOT(b0, q3, 11) ART_DOT(a1, q7, 7)              \
+  ART_DOT(b1, q7, 15)
 #define ART_QIN                                                                                   \
   [q0] "v"(q[0]), [q1] "v"(q[1]), [q2] "v"(q[2]), [q3] "v"(q[3]), [q4] "v"(q[4]), [q5] "v"(q[5]), \
       [q6] "v"(q[6]), [q7] "v"(q[7])
@@ -290,6 +336,21 @@ __device__ __forceinline__ float group_term(float acc, uint32_t x, uint32_t l, u
         "s_nop 1"
         : ART_ACC
         : [x] "v"(x), [l] "v"(l), [d] "v"(d), [m8] "v"(-8), ART_QIN, [l0] "i"(2 * H), [l1] "i"(2 * H + 1));
+  } else if constexpr (QT == ARTLITE_Q6_K) {
+    // the halves' sums in their own chains (a0 / b0: dwords 0..3, a1 / b1: 4..7), each scaled by its sub-block's
+    // scale (d: the first half's, mn: the second's); signed codes, no offset
+    float c1;
+    asm("s_nop 1\n\t"
+        "v_mov_b32 %[a0], 0\n\t"
+        "v_mov_b32 %[b0], 0\n\t"
+        "v_mov_b32 %[a1], 0\n\t"
+        "v_mov_b32 %[b1], 0\n\t" ART_DOTS_HALVES
+        "v_mul_f32_dpp %[c], %[l], %[d] row_newbcast:%[l0] row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[c1], %[l], %[d1] row_newbcast:%[l0] row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 0"
+        : ART_ACC, [c1] "=&v"(c1)
+        : [x] "v"(x), [l] "v"(l), [d] "v"(d), [d1] "v"(mn), ART_QIN, [l0] "i"(2 * H));
+    return __builtin_fmaf(c1, float(a1 * 256 + b1), __builtin_fmaf(coef, float(a0 * 256 + b0), acc));
   } else if constexpr (QT == ARTLITE_Q8_0) {
     asm("s_nop 1\n\t"
         "v_mov_b32 %[a0], 0\n\t"
@@ -319,6 +380,7 @@ __device__ __forceinline__ float group_term(float acc, uint32_t x, uint32_t l, u
 #undef ART_ACC
 #undef ART_DOT
 #undef ART_DOTS
+#undef ART_DOTS_HALVES
 #undef ART_QIN
 
 template <bool SWIGLU>
@@ -411,7 +473,7 @@ struct Stream {
   const GemvArgs& a;
   int wv, lane, p, r, rb, ks, u0, u1, NVw;
   u32x4* my;  // the wave's weight slots, then its record slot
-  uint32_t wbase, xbase, o_w, o_r;
+  uint32_t wbase, xbase, o_w, o_r, o_s;
   uint32_t lo[NI];   // the lane's byte offset in the 16 rows of each load instruction
   int nl = 0;        // loads issued so far
   int xend0 = 0, xend1 = 0;  // nl after each record slot's loads (two scalars: an indexed array would live in memory)
@@ -434,8 +496,15 @@ struct Stream {
     }
     wbase = lds_addr(my);
     xbase = lds_addr(my + D * WCH) + 16 * lane;
-    o_w = r * BY + (QT == ARTLITE_Q4_K || QT == ARTLITE_Q5_K ? 0 : (QT == ARTLITE_Q4_0 ? 36 : 68) * p);
-    o_r = r * BY + (QT == ARTLITE_Q5_K ? 48 : 16) + 32 * p;  // (Q4_K / Q5_K: the lane's run)
+    if constexpr (QT == ARTLITE_Q6_K) {  // (low bits of half p / 2, its high bits, the scales and d)
+      o_w = r * BY + 64 * (p >> 1);
+      o_r = r * BY + 128 + 32 * (p >> 1);
+      o_s = r * BY + 192;
+    } else {
+      o_w = r * BY + (QT == ARTLITE_Q4_K || QT == ARTLITE_Q5_K ? 0 : (QT == ARTLITE_Q4_0 ? 36 : 68) * p);
+      o_r = r * BY + (QT == ARTLITE_Q5_K ? 48 : 16) + 32 * p;  // (Q4_K / Q5_K: the lane's run)
+      o_s = o_w;
+    }
   }
   // the weights of local step v of item (e, n0) into slot `slot`; !on: none (the end of the stream), counted alike
   template <int MX>
@@ -480,7 +549,7 @@ __device__ __forceinline__ void wait_read(const Stream<QT, SWIGLU, D>& st, int n
   using SS = Stream<QT, SWIGLU, D>;
   static_for<SS::NMAX + 1>([&](auto nc) {
     constexpr int N = decltype(nc)::value;
-    if (n == N) read_unit<N, QT, MX>(w, x, sw + st.o_w, sw + st.o_r, sx);
+    if (n == N) read_unit<N, QT, MX>(w, x, sw + st.o_w, sw + st.o_r, sw + st.o_s, sx);
   });
 }
 
@@ -724,15 +793,16 @@ int launch_t(const GemvArgs& a, hipStream_t s) {
 }  // namespace
 
 bool gemv_supported(int qtype, int K, int N) {
-  return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0 || qtype == ARTLITE_Q4_K || qtype == ARTLITE_Q5_K) && K > 0 &&
-         K % 256 == 0 &&
+  return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0 || qtype == ARTLITE_Q4_K || qtype == ARTLITE_Q5_K ||
+          qtype == ARTLITE_Q6_K) &&
+         K > 0 && K % 256 == 0 &&
          N > 0 && N % 64 == 0;
 }
 
 int launch_gemv(const GemvArgs& a, hipStream_t s) {
   if (!gemv_supported(a.qtype, a.K, a.N))
     return fail(ARTLITE_EINVAL,
-                "expert GEMV: weight type %d with K %d, N %d (Q4_0 / Q8_0 / Q4_K / Q5_K, K a multiple of 256, N of 64)",
+                "expert GEMV: weight type %d with K %d, N %d (Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K, K a multiple of 256, N of 64)",
                 a.qtype, a.K, a.N);
   if (a.N <= 0 || int64_t(a.N) * a.row_bytes >= (int64_t(1) << 31))
     return fail(ARTLITE_EINVAL, "expert GEMV: %d rows of %d bytes", a.N, a.row_bytes);
@@ -745,6 +815,7 @@ int launch_gemv(const GemvArgs& a, hipStream_t s) {
     case ARTLITE_Q4_0: ART_DISPATCH(ARTLITE_Q4_0);
     case ARTLITE_Q8_0: ART_DISPATCH(ARTLITE_Q8_0);
     case ARTLITE_Q5_K: ART_DISPATCH(ARTLITE_Q5_K);
+    case ARTLITE_Q6_K: ART_DISPATCH(ARTLITE_Q6_K);
     default: ART_DISPATCH(ARTLITE_Q4_K);
   }
 #undef ART_DISPATCH

@@ -17,7 +17,7 @@ struct artlite_moe_layer {
   int device = 0;
   hipStream_t stream = nullptr;
   const QType *gq = nullptr, *dq = nullptr, *sq = nullptr, *sdq = nullptr;  // (sdq: the shared down's)
-  size_t gate_row = 0, down_row = 0, sgate_row = 0, sdown_row = 0;  // row bytes
+  size_t gate_row = 0, down_row = 0, sgate_row = 0, sdown_row = 0;  // row bytes in the layer (QType::dev blocks)
   DevBuf router, gate, up, down, sgate, sup, sdown, sinp, norm;
   bool have[9] = {};
   // activations of the staged input
@@ -40,16 +40,33 @@ struct artlite_moe_layer {
 
 namespace {
 
+// bytes of a row of cols values of type q as a GGUF file stores it
+size_t file_row(const QType* q, int cols) { return q ? size_t(cols) / q->per * q->bytes : 0; }
+
+// the block type of a weight tensor (null: the fp32 ones)
+const QType* tensor_type(const artlite_moe_layer* L, int t) {
+  switch (t) {
+    case ARTLITE_GATE_EXPS:
+    case ARTLITE_UP_EXPS: return L->gq;
+    case ARTLITE_DOWN_EXPS: return L->dq;
+    case ARTLITE_GATE_SHEXP:
+    case ARTLITE_UP_SHEXP: return L->sq;
+    case ARTLITE_DOWN_SHEXP: return L->sdq;
+    default: return nullptr;
+  }
+}
+
+// the bytes a tensor takes as uploaded (tensor_bytes, its file size)
 size_t tensor_bytes(const artlite_moe_layer* L, int t) {
   const artlite_moe_desc& d = L->d;
   switch (t) {
     case ARTLITE_ROUTER: return size_t(d.n_experts) * d.hidden * 4;
     case ARTLITE_GATE_EXPS:
-    case ARTLITE_UP_EXPS: return size_t(d.n_experts) * d.expert_ffn * L->gate_row;
-    case ARTLITE_DOWN_EXPS: return size_t(d.n_experts) * d.hidden * L->down_row;
+    case ARTLITE_UP_EXPS: return size_t(d.n_experts) * d.expert_ffn * file_row(L->gq, d.hidden);
+    case ARTLITE_DOWN_EXPS: return size_t(d.n_experts) * d.hidden * file_row(L->dq, d.expert_ffn);
     case ARTLITE_GATE_SHEXP:
-    case ARTLITE_UP_SHEXP: return size_t(d.shared_ffn) * L->sgate_row;
-    case ARTLITE_DOWN_SHEXP: return size_t(d.hidden) * L->sdown_row;
+    case ARTLITE_UP_SHEXP: return size_t(d.shared_ffn) * file_row(L->sq, d.hidden);
+    case ARTLITE_DOWN_SHEXP: return size_t(d.hidden) * file_row(L->sdq, d.shared_ffn);
     case ARTLITE_GATE_INP_SHEXP: return size_t(d.hidden) * 4;
     case ARTLITE_FFN_NORM: return d.norm_eps > 0 ? size_t(d.hidden) * 4 : 0;
     default: return 0;
@@ -475,11 +492,11 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
   L->dq = dq;
   L->sq = sq;
   L->sdq = sdq;
-  L->gate_row = size_t(d.hidden) / gq->per * gq->bytes;
-  L->down_row = size_t(d.expert_ffn) / dq->per * dq->bytes;
+  L->gate_row = size_t(d.hidden) / gq->per * gq->dev;
+  L->down_row = size_t(d.expert_ffn) / dq->per * dq->dev;
   if (sq) {
-    L->sgate_row = size_t(d.hidden) / sq->per * sq->bytes;
-    L->sdown_row = size_t(d.shared_ffn) / sdq->per * sdq->bytes;
+    L->sgate_row = size_t(d.hidden) / sq->per * sq->dev;
+    L->sdown_row = size_t(d.shared_ffn) / sdq->per * sdq->dev;
   }
   L->gemv_gu_ok = gemv_supported(d.gate_type, d.hidden, d.expert_ffn) && d.expert_ffn % 256 == 0;
   L->gemv_ok = L->gemv_gu_ok && gemv_supported(d.down_type, d.expert_ffn, d.hidden);
@@ -567,9 +584,20 @@ extern "C" int artlite_moe_layer_upload(artlite_moe_layer* L, int t, const void*
   const size_t want = tensor_bytes(L, t);
   if (!b || !want) return fail(ARTLITE_EINVAL, "moe layer upload: tensor %d not in this layer", t);
   if (nbytes != want) return fail(ARTLITE_EINVAL, "moe layer upload: tensor %d is %zu bytes, not %zu", t, nbytes, want);
-  ART_TRY(b->reserve(want + WEIGHT_TAIL));
-  ART_HIP(hipMemcpyAsync(b->p, data, want, hipMemcpyHostToDevice, L->stream));
-  ART_HIP(hipMemsetAsync(static_cast<uint8_t*>(b->p) + want, 0, WEIGHT_TAIL, L->stream));  // (the loaders' tail)
+  // blocks whose layer size differs from the file's (Q6_K) are padded with zeros, block by block, on the host
+  const QType* tq = tensor_type(L, t);
+  const size_t dev = tq && tq->dev != tq->bytes ? want / tq->bytes * tq->dev : want;
+  std::vector<uint8_t> padded;
+  const void* src = data;
+  if (dev != want) {
+    padded.assign(dev, 0);
+    const uint8_t* in = static_cast<const uint8_t*>(data);
+    for (size_t i = 0; i < want / tq->bytes; i++) std::memcpy(&padded[i * tq->dev], in + i * tq->bytes, tq->bytes);
+    src = padded.data();
+  }
+  ART_TRY(b->reserve(dev + WEIGHT_TAIL));
+  ART_HIP(hipMemcpyAsync(b->p, src, dev, hipMemcpyHostToDevice, L->stream));
+  ART_HIP(hipMemsetAsync(static_cast<uint8_t*>(b->p) + dev, 0, WEIGHT_TAIL, L->stream));  // (the loaders' tail)
   // the prefill's bound on |h| takes max |w| of the gate and up matrices
   const int wm = t == ARTLITE_GATE_EXPS ? 0 : t == ARTLITE_UP_EXPS ? 1 : t == ARTLITE_GATE_SHEXP ? 2
                : t == ARTLITE_UP_SHEXP ? 3 : -1;
