@@ -37,8 +37,8 @@ struct QType {
   const char* name;
   int per;    // values per block
   int bytes;  // bytes per block (in a GGUF file)
-  int dev;    // bytes per block in an uploaded layer: the same, but Q6_K's 210 padded to 224 (16-byte aligned
-              // blocks, so that the decode GEMV's 16-byte DMAs take them)
+  int dev;    // bytes per block in an uploaded layer: the same, but Q6_K's 210 padded to 224 and IQ4_XS's 136 to
+              // 144, its 8-byte header to 16 (16-byte aligned blocks and code runs for the decode GEMV's DMAs)
 };
 const QType* qtype_by_name(const char* name);
 const QType* qtype_by_id(int id);
@@ -80,6 +80,19 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
 }
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// four codes (bytes < 16) -> the bytes of IQ4[code] as int8 (IQ4_NL / IQ4_XS's 16 values, ggml's kvalues_iq4nl):
+// two byte permutes over the 16-byte table, one per half, the code's bit 3 choosing between them
+__device__ __forceinline__ uint32_t iq4_int8(uint32_t c) {
+  constexpr int V[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+  constexpr auto pack = [](const int* v) {
+    return uint32_t(v[0] & 0xFF) | uint32_t(v[1] & 0xFF) << 8 | uint32_t(v[2] & 0xFF) << 16 |
+           uint32_t(v[3] & 0xFF) << 24;
+  };
+  constexpr uint32_t T0 = pack(V), T1 = pack(V + 4), T2 = pack(V + 8), T3 = pack(V + 12);
+  const uint32_t s = c & 0x07070707u, hi = ((c >> 3) & 0x01010101u) * 0xFFu;
+  return (__builtin_amdgcn_perm(T3, T2, s) & hi) | (__builtin_amdgcn_perm(T1, T0, s) & ~hi);
+}
 
 constexpr int WAVE = 64;
 constexpr int LDS_BYTES = 160 * 1024;  // a gfx950 workgroup's LDS

@@ -97,7 +97,7 @@ struct Fmt<ARTLITE_Q6_K> : FmtT<224, 8, 16, 160, false, true> {};  // (128 + q) 
 template <>
 struct Fmt<ARTLITE_IQ4_NL> : FmtT<18, 1, 32, 128> {};
 template <>
-struct Fmt<ARTLITE_IQ4_XS> : FmtT<136, 8, 32, 128> {};
+struct Fmt<ARTLITE_IQ4_XS> : FmtT<144, 8, 32, 128> {};  // (the layer's padded blocks)
 
 // the 16-byte chunks of a 16-row stage: the aligned cover of each row's run; a row's LDS slot is an odd number of
 // 16-byte units, so the 16 rows' same-offset dwords fall in 16 different banks
@@ -110,17 +110,8 @@ struct Stage {
   static_assert(16 * CPR <= WEIGHT_TAIL, "a K-range's cover stays within a weight tensor's tail");
 };
 
-// four codes (bytes < 16) -> the bytes 128 + IQ4[code] (IQ4_NL / IQ4_XS's values, ggml's kvalues_iq4nl): two byte
-// permutes over the 16-byte table, one per half, the code's bit 3 choosing between them
-__device__ __forceinline__ uint32_t iq4_bytes(uint32_t c) {
-  constexpr int V[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
-  constexpr auto pack = [](const int* v) {
-    return uint32_t(128 + v[0]) | uint32_t(128 + v[1]) << 8 | uint32_t(128 + v[2]) << 16 | uint32_t(128 + v[3]) << 24;
-  };
-  constexpr uint32_t T0 = pack(V), T1 = pack(V + 4), T2 = pack(V + 8), T3 = pack(V + 12);
-  const uint32_t s = c & 0x07070707u, hi = ((c >> 3) & 0x01010101u) * 0xFFu;
-  return (__builtin_amdgcn_perm(T3, T2, s) & hi) | (__builtin_amdgcn_perm(T1, T0, s) & ~hi);
-}
+// four codes (bytes < 16) -> the bytes 128 + IQ4[code] (the int8 values with the top bit flipped)
+__device__ __forceinline__ uint32_t iq4_bytes(uint32_t c) { return iq4_int8(c) ^ 0x80808080u; }
 
 // Q4_K / Q5_K's 6-bit scale and min of group g from the 12 bytes at s6
 __device__ __forceinline__ void k_scale_min(const uint8_t* s6, int g, int& q6, int& m6) {
@@ -187,10 +178,11 @@ __device__ __forceinline__ u32x4 b_operand(const uint8_t* row, int gl, int lg, f
     const uint32_t u0 = ((lds_u32(qs) >> (2 * j)) & 0x03030303u) | (((lds_u32(hm) >> hb) & 0x01010101u) << 2);
     const uint32_t u1 = ((lds_u32(qs + 4) >> (2 * j)) & 0x03030303u) | (((lds_u32(hm + 4) >> hb) & 0x01010101u) << 2);
     return nib8(u0, u1);
-  } else {  // IQ4_XS: group g's codes at 8 + 16 g, its scale d (ls - 32)
+  } else {  // IQ4_XS (a layer's 144-byte block: the 8-byte header padded to 16): group g's codes at 16 + 16 g, its
+            // scale d (ls - 32)
     const int ls = ((blk[4 + g / 2] >> (4 * (g & 1))) & 15) | (((int(lds_u16(blk + 2)) >> (2 * g)) & 3) << 4);
     sc = __fmul_rn(h2f(lds_u16(blk)), float(ls - 32));
-    const uint8_t* qs = blk + 8 + 16 * g + 8 * (lg & 1);
+    const uint8_t* qs = blk + 16 + 16 * g + 8 * (lg & 1);
     const int sh = 4 * (lg >> 1);
     return byte8(iq4_bytes((lds_u32(qs) >> sh) & 0x0F0F0F0Fu), iq4_bytes((lds_u32(qs + 4) >> sh) & 0x0F0F0F0Fu));
   }

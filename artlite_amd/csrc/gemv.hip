@@ -50,6 +50,18 @@ struct Unit<ARTLITE_Q8_0> {
   static constexpr int BYTES = 272, LW = 17;
 };
 template <>
+struct Unit<ARTLITE_IQ4_NL> {  // (Q4_0's layout)
+  static constexpr int BYTES = 144, LW = 9;
+};
+template <>
+struct Unit<ARTLITE_Q4_1> {  // (the lane's two 20-byte blocks)
+  static constexpr int BYTES = 160, LW = 10;
+};
+template <>
+struct Unit<ARTLITE_IQ4_XS> {  // (a layer's 144-byte block: the header padded to 16 bytes, and the lane's 32-byte run)
+  static constexpr int BYTES = 144, LW = 12;
+};
+template <>
 struct Unit<ARTLITE_Q4_K> {
   static constexpr int BYTES = 144, LW = 12;
 };
@@ -119,6 +131,8 @@ __device__ __forceinline__ float4 lds_read_f4(const void* p) {
 #define ART_OW1(I) [w##I] "=&v"(w1)
 #define ART_W9 ART_R2(0, 0) ART_R2(1, 2) ART_R2(2, 4) ART_R2(3, 6) ART_R1(4, 8)
 #define ART_OW9 ART_OW2(0), ART_OW2(1), ART_OW2(2), ART_OW2(3), ART_OW1(4)
+#define ART_W10 ART_R2(0, 0) ART_R2(1, 2) ART_R2(2, 4) ART_R2(3, 6) ART_R2(4, 8)
+#define ART_OW10 ART_OW2(0), ART_OW2(1), ART_OW2(2), ART_OW2(3), ART_OW2(4)
 #define ART_W17 \
   ART_R2(0, 0) ART_R2(1, 2) ART_R2(2, 4) ART_R2(3, 6) ART_R2(4, 8) ART_R2(5, 10) ART_R2(6, 12) ART_R2(7, 14) ART_R1(8, 16)
 #define ART_OW17 \
@@ -190,15 +204,17 @@ __device__ __forceinline__ void read_unit(uint32_t (&w)[Unit<QT>::LW], u32x4 (&x
     for (int i = 0; i < 32; i++) w[i] = w4[i >> 2][i & 3];
   } else {
     u32x2 w2[LW / 2];
-    uint32_t w1;
+    uint32_t w1 = 0;
     if constexpr (LW == 9) {
       ART_READ_M(9)
+    } else if constexpr (LW == 10) {
+      ART_READ_M(10)
     } else {
       ART_READ_M(17)
     }
 #pragma unroll
     for (int i = 0; i < LW / 2; i++) w[2 * i] = w2[i][0], w[2 * i + 1] = w2[i][1];
-    w[LW - 1] = w1;
+    if constexpr (LW % 2) w[LW - 1] = w1;
   }
 }
 #undef ART_READ_M
@@ -224,6 +240,8 @@ __device__ __forceinline__ void read_unit(uint32_t (&w)[Unit<QT>::LW], u32x4 (&x
 #undef ART_W17
 #undef ART_OW9
 #undef ART_W9
+#undef ART_OW10
+#undef ART_W10
 #undef ART_OW1
 #undef ART_OW2
 #undef ART_R1
@@ -234,11 +252,12 @@ __device__ __forceinline__ void read_unit(uint32_t (&w)[Unit<QT>::LW], u32x4 (&x
 template <int QT, int H>
 __device__ __forceinline__ void codes(const uint32_t (&w)[Unit<QT>::LW], int g, uint32_t (&q)[8], float& d,
                                       float& mn) {
-  if constexpr (QT == ARTLITE_Q4_0 || QT == ARTLITE_Q8_0) {
-    // Q4_0: 18 bytes at 18 H: fp16 d, then 16 bytes whose low nibbles are values 0..15, high nibbles 16..31;
-    // Q8_0: 34 bytes at 34 H: fp16 d, then 32 signed bytes in value order
-    constexpr int o = (QT == ARTLITE_Q4_0 ? 18 : 34) * H;
-    constexpr int NQ = QT == ARTLITE_Q4_0 ? 4 : 8;
+  if constexpr (QT == ARTLITE_Q4_0 || QT == ARTLITE_Q8_0 || QT == ARTLITE_IQ4_NL) {
+    // Q4_0 / IQ4_NL: 18 bytes at 18 H: fp16 d, then 16 bytes whose low nibbles are values 0..15, high nibbles
+    // 16..31 (IQ4_NL: the codes of IQ4[] values, looked up to int8); Q8_0: 34 bytes at 34 H: fp16 d, then 32 signed
+    // bytes in value order
+    constexpr int o = (QT == ARTLITE_Q8_0 ? 34 : 18) * H;
+    constexpr int NQ = QT == ARTLITE_Q8_0 ? 8 : 4;
 #pragma unroll
     for (int j = 0; j < NQ; j++) {
       uint32_t v;
@@ -249,12 +268,38 @@ __device__ __forceinline__ void codes(const uint32_t (&w)[Unit<QT>::LW], int g, 
       if constexpr (QT == ARTLITE_Q4_0) {
         q[j] = v & 0x0F0F0F0Fu;
         q[4 + j] = (v >> 4) & 0x0F0F0F0Fu;
+      } else if constexpr (QT == ARTLITE_IQ4_NL) {
+        q[j] = iq4_int8(v & 0x0F0F0F0Fu);
+        q[4 + j] = iq4_int8((v >> 4) & 0x0F0F0F0Fu);
       } else {
         q[j] = v;
       }
     }
     d = o % 4 == 0 ? h2f(w[o / 4] & 0xFFFFu) : h2f(w[(o - 2) / 4] >> 16);
     mn = 0.0f;
+  } else if constexpr (QT == ARTLITE_Q4_1) {
+    // the lane's two 20-byte blocks: block H at 20 H, fp16 d and m, then 16 bytes of nibbles as Q4_0's (w = d q + m:
+    // mn = -m for the min term)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      q[j] = w[5 * H + 1 + j] & 0x0F0F0F0Fu;
+      q[4 + j] = (w[5 * H + 1 + j] >> 4) & 0x0F0F0F0Fu;
+    }
+    d = h2f(w[5 * H] & 0xFFFFu);
+    mn = -h2f(w[5 * H] >> 16);
+  } else if constexpr (QT == ARTLITE_IQ4_XS) {
+    // the header (fp16 d, the 16 bits of high scale crumbs, 4 bytes of low scale nibbles; w[0..1]) and the lane's
+    // 32-byte run (w[4..11]: groups 2 p, 2 p + 1, 16 bytes each in Q4_0's order of IQ4[] codes); the scale
+    // d (ls - 32), ls the 6-bit scale of group g
+    const uint32_t sh = w[0] >> 16, sl = w[1];
+    const int ls = int((sl >> (8 * (g >> 1) + 4 * (g & 1))) & 15u) | int(((sh >> (2 * g)) & 3u) << 4);
+    d = h2f(w[0] & 0xFFFFu) * float(ls - 32);  // (exact: 11 x 6 significant bits)
+    mn = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      q[j] = iq4_int8(w[4 + 4 * H + j] & 0x0F0F0F0Fu);
+      q[4 + j] = iq4_int8((w[4 + 4 * H + j] >> 4) & 0x0F0F0F0Fu);
+    }
   } else if constexpr (QT == ARTLITE_Q6_K) {
     // group g = 4 h + jj (h = p / 2, jj = 2 (p % 2) + H): value l's low bits are a nibble of low-bit byte 32 (jj % 2)
     // + l of half h (w[0..15]: the high nibbles for jj >= 2), its high bits crumb jj of high-bit byte l (w[16..23]);
@@ -351,7 +396,7 @@ __device__ __forceinline__ float group_term(float acc, uint32_t x, uint32_t l, u
         : ART_ACC, [c1] "=&v"(c1)
         : [x] "v"(x), [l] "v"(l), [d] "v"(d), [d1] "v"(mn), ART_QIN, [l0] "i"(2 * H));
     return __builtin_fmaf(c1, float(a1 * 256 + b1), __builtin_fmaf(coef, float(a0 * 256 + b0), acc));
-  } else if constexpr (QT == ARTLITE_Q8_0) {
+  } else if constexpr (QT == ARTLITE_Q8_0 || QT == ARTLITE_IQ4_NL || QT == ARTLITE_IQ4_XS) {  // (signed codes)
     asm("s_nop 1\n\t"
         "v_mov_b32 %[a0], 0\n\t"
         "v_mov_b32 %[b0], 0\n\t"
@@ -501,8 +546,10 @@ struct Stream {
       o_r = r * BY + 128 + 32 * (p >> 1);
       o_s = r * BY + 192;
     } else {
-      o_w = r * BY + (QT == ARTLITE_Q4_K || QT == ARTLITE_Q5_K ? 0 : (QT == ARTLITE_Q4_0 ? 36 : 68) * p);
-      o_r = r * BY + (QT == ARTLITE_Q5_K ? 48 : 16) + 32 * p;  // (Q4_K / Q5_K: the lane's run)
+      constexpr bool HEAD = QT == ARTLITE_Q4_K || QT == ARTLITE_Q5_K || QT == ARTLITE_IQ4_XS;  // (header + run)
+      constexpr int PB = QT == ARTLITE_Q8_0 ? 68 : QT == ARTLITE_Q4_1 ? 40 : 36;  // (the lane's two blocks)
+      o_w = r * BY + (HEAD ? 0 : PB * p);
+      o_r = r * BY + (QT == ARTLITE_Q5_K ? 48 : 16) + 32 * p;  // (Q4_K / Q5_K / IQ4_XS: the lane's run)
       o_s = o_w;
     }
   }
@@ -794,7 +841,7 @@ int launch_t(const GemvArgs& a, hipStream_t s) {
 
 bool gemv_supported(int qtype, int K, int N) {
   return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0 || qtype == ARTLITE_Q4_K || qtype == ARTLITE_Q5_K ||
-          qtype == ARTLITE_Q6_K) &&
+          qtype == ARTLITE_Q6_K || qtype == ARTLITE_Q4_1 || qtype == ARTLITE_IQ4_NL || qtype == ARTLITE_IQ4_XS) &&
          K > 0 && K % 256 == 0 &&
          N > 0 && N % 64 == 0;
 }
@@ -802,7 +849,7 @@ bool gemv_supported(int qtype, int K, int N) {
 int launch_gemv(const GemvArgs& a, hipStream_t s) {
   if (!gemv_supported(a.qtype, a.K, a.N))
     return fail(ARTLITE_EINVAL,
-                "expert GEMV: weight type %d with K %d, N %d (Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K, K a multiple of 256, N of 64)",
+                "expert GEMV: weight type %d with K %d, N %d (not Q3_K, K a multiple of 256, N of 64)",
                 a.qtype, a.K, a.N);
   if (a.N <= 0 || int64_t(a.N) * a.row_bytes >= (int64_t(1) << 31))
     return fail(ARTLITE_EINVAL, "expert GEMV: %d rows of %d bytes", a.N, a.row_bytes);
@@ -816,6 +863,9 @@ int launch_gemv(const GemvArgs& a, hipStream_t s) {
     case ARTLITE_Q8_0: ART_DISPATCH(ARTLITE_Q8_0);
     case ARTLITE_Q5_K: ART_DISPATCH(ARTLITE_Q5_K);
     case ARTLITE_Q6_K: ART_DISPATCH(ARTLITE_Q6_K);
+    case ARTLITE_Q4_1: ART_DISPATCH(ARTLITE_Q4_1);
+    case ARTLITE_IQ4_NL: ART_DISPATCH(ARTLITE_IQ4_NL);
+    case ARTLITE_IQ4_XS: ART_DISPATCH(ARTLITE_IQ4_XS);
     default: ART_DISPATCH(ARTLITE_Q4_K);
   }
 #undef ART_DISPATCH

@@ -584,7 +584,8 @@ extern "C" int artlite_moe_layer_upload(artlite_moe_layer* L, int t, const void*
   const size_t want = tensor_bytes(L, t);
   if (!b || !want) return fail(ARTLITE_EINVAL, "moe layer upload: tensor %d not in this layer", t);
   if (nbytes != want) return fail(ARTLITE_EINVAL, "moe layer upload: tensor %d is %zu bytes, not %zu", t, nbytes, want);
-  // blocks whose layer size differs from the file's (Q6_K) are padded with zeros, block by block, on the host
+  // blocks whose layer size differs from the file's are padded with zeros, block by block, on the host: Q6_K after
+  // the block, IQ4_XS after its 8-byte header (d, the scales), so that its code runs start 16-byte aligned
   const QType* tq = tensor_type(L, t);
   const size_t dev = tq && tq->dev != tq->bytes ? want / tq->bytes * tq->dev : want;
   std::vector<uint8_t> padded;
@@ -592,7 +593,13 @@ extern "C" int artlite_moe_layer_upload(artlite_moe_layer* L, int t, const void*
   if (dev != want) {
     padded.assign(dev, 0);
     const uint8_t* in = static_cast<const uint8_t*>(data);
-    for (size_t i = 0; i < want / tq->bytes; i++) std::memcpy(&padded[i * tq->dev], in + i * tq->bytes, tq->bytes);
+    const int head = tq->id == ARTLITE_IQ4_XS ? 8 : tq->bytes, gap = tq->dev - tq->bytes;
+    for (size_t i = 0; i < want / tq->bytes; i++) {
+      uint8_t* o = &padded[i * tq->dev];
+      const uint8_t* blk = in + i * tq->bytes;
+      std::memcpy(o, blk, head);
+      std::memcpy(o + head + gap, blk + head, tq->bytes - head);
+    }
     src = padded.data();
   }
   ART_TRY(b->reserve(dev + WEIGHT_TAIL));

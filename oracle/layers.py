@@ -84,7 +84,10 @@ CONFIGS = {
     "mixtile": Spec("mixtile", H=1024, E=32, k=4, F=512, gate_type="Q4_K", down_type="Q3_K", scale=2e-4,
                     dmin_scale=1.5e-3, tokens=(16,)),
     "iq4": Spec("iq4", H=768, E=16, k=4, F=512, gate_type="IQ4_XS", down_type="IQ4_NL", scale=5e-5, x_dtype="f32",
-                shared_F=256, shared_type="Q4_1", shared_scale=4e-3, shared_gated=True, tokens=(24,)),
+                shared_F=256, shared_type="Q4_1", shared_scale=4e-3, shared_gated=True, tokens=(16, 24)),
+    # test-only: Q4_1 throughout (d q + m blocks: the min term) with an IQ4_XS / IQ4_NL shared expert
+    "q41": Spec("q41", H=1024, E=16, k=2, F=512, gate_type="Q4_1", down_type="Q4_1", scale=4e-3, shared_F=256,
+                shared_type="IQ4_XS", shared_down_type="IQ4_NL", shared_scale=5e-5, tokens=(16,)),
 }
 
 ZIPF_S, ZIPF_ACTIVE, ZIPF_BETA = 1.2, 26, 0.7
