@@ -3,7 +3,8 @@
 // Persistent workgroups (as many as the device holds) take work items in turn: an item is one tile of at most
 // GEMV_BM sorted rows of A (tokens for gate / up, pairs for down) of one expert times a block of 16 RB weight rows
 // (SwiGLU: those rows of gate and of up). Plain products: 4 waves, one per 16-row block (RB 4, 64 rows). SwiGLU:
-// 8 waves, 4 row blocks (64 rows) x 2 waves that split K in halves, whose partial sums meet in LDS. Each wave
+// 8 waves, 4 row blocks (64 rows) x 2 waves that take alternate K-units (so the two read neighbouring units, which
+// share cache lines, at about the same time), whose partial sums meet in LDS. Each wave
 // streams its own steps (16 rows x one K-unit of 8 groups of 32 values: Q4_0 / Q4_K 144 bytes a row, Q5_K 176,
 // Q8_0 272)
 // with global_load_lds_dwordx4 into D LDS slots of its own, one step ahead, across item boundaries; the XQ records
@@ -516,7 +517,7 @@ struct Stream {
   static constexpr int NMAX = LA * NI + (LA + 1) * GEMV_BM;  // loads issued after a step's, at most
   static_assert(NMAX < 64, "loads in flight beyond vmcnt");
   const GemvArgs& a;
-  int wv, lane, p, r, rb, ks, u0, u1, NVw;
+  int wv, lane, p, r, rb, ks, u0, NVw;
   u32x4* my;  // the wave's weight slots, then its record slot
   uint32_t wbase, xbase, o_w, o_r, o_s;
   uint32_t lo[NI];   // the lane's byte offset in the 16 rows of each load instruction
@@ -532,8 +533,8 @@ struct Stream {
     rb = wv / S, ks = wv % S;
     my = slab + wv * (D * WCH + XS * XCH);
     const int U = a.K / 256;
-    u0 = ks * U / S, u1 = (ks + 1) * U / S;
-    NVw = (u1 - u0) * NM;
+    u0 = ks;  // (the wave's K-units: ks, ks + S, ...; the pair reads neighbouring units, which share lines, together)
+    NVw = (U - ks + S - 1) / S * NM;
 #pragma unroll
     for (int i = 0; i < NI; i++) {
       const int q = min(64 * i + lane, WCH - 1), row = q / CH;
@@ -559,7 +560,7 @@ struct Stream {
     if (on) {
       // (rows past N cannot occur: N is a multiple of the item's rows)
       const uint8_t* src = a.w[MX] + int64_t(e) * a.expert_bytes + int64_t(n0) * a.row_bytes +
-                           int64_t(u0 + v / NM) * BY;
+                           int64_t(u0 + S * (v / NM)) * BY;
       u32x4* dst = my + slot * WCH;
 #pragma unroll
       for (int i = 0; i < NI; i++)
@@ -650,7 +651,7 @@ __device__ __forceinline__ void run_item(Stream<QT, SWIGLU, D>& st, const Item& 
         const int b = SS::XS == 1 ? 0 : st.kg & 1;
         auto next_x = [&](int bn) {
           if (v0 + NM < st.NVw)
-            st.load_x(cur, st.u0 + v0 / NM + 1, bn);
+            st.load_x(cur, st.u0 + SS::S * (v0 / NM + 1), bn);
           else if (has_next)
             st.load_x(nxt, st.u0, bn);
         };
