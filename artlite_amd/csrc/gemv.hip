@@ -436,14 +436,15 @@ struct Shape {
   static_assert(!SWIGLU || (RB % 2 == 0 && 8 * RB / 2 * GEMV_BM <= 64), "SwiGLU epilogue lanes");
 };
 
-// LDS of a workgroup: each wave's D slots of 16 rows x BYTES and its XS record slots (GEMV_BM chunk rows of 1 KB;
-// SwiGLU one, plain products two), then (S > 1) RED_BUFS buffers of the K-ranges' partial sums and their counters
-// (then the item table, sized at launch)
+// LDS of a workgroup: each wave's D slots of 16 rows x BYTES and its record slot (GEMV_BM chunk rows of 1 KB;
+// one: the next K-unit's are loaded once the current ones are read, and more slots measured no faster while they
+// cost Q6_K's plain products a workgroup per CU), then (S > 1) RED_BUFS buffers of the K-ranges' partial sums and
+// their counters (then the item table, sized at launch)
 constexpr int RED_BUFS = 2;
 template <int QT, bool SWIGLU, int D>
 constexpr size_t gemv_lds() {
   using W = Shape<SWIGLU>;
-  return size_t(W::WAVES) * (D * 16 * Unit<QT>::BYTES + (SWIGLU ? 1 : 2) * GEMV_BM * 1024) +
+  return size_t(W::WAVES) * (D * 16 * Unit<QT>::BYTES + GEMV_BM * 1024) +
          (W::S > 1 ? size_t(RED_BUFS) * W::WAVES * (SWIGLU ? 2 : 1) * GEMV_BM * 16 * 4 + 32 : 0);
 }
 
@@ -513,7 +514,7 @@ struct Stream {
   static constexpr int RB = W::RB, S = W::S, BY = Unit<QT>::BYTES, CH = BY / 16, LW = Unit<QT>::LW;
   static constexpr int NM = SWIGLU ? 2 : 1, WCH = 16 * CH, NI = (WCH + 63) / 64, LAST = WCH - 64 * (NI - 1);
   static constexpr int LA = D - 1;                          // steps in flight ahead of the one being read
-  static constexpr int XS = SWIGLU ? 1 : 2, XCH = GEMV_BM * 64;  // record slots, their chunks
+  static constexpr int XCH = GEMV_BM * 64;  // chunks of the record slot
   static constexpr int NMAX = LA * NI + (LA + 1) * GEMV_BM;  // loads issued after a step's, at most
   static_assert(NMAX < 64, "loads in flight beyond vmcnt");
   const GemvArgs& a;
@@ -522,8 +523,7 @@ struct Stream {
   uint32_t wbase, xbase, o_w, o_r, o_s;
   uint32_t lo[NI];   // the lane's byte offset in the 16 rows of each load instruction
   int nl = 0;        // loads issued so far
-  int xend0 = 0, xend1 = 0;  // nl after each record slot's loads (two scalars: an indexed array would live in memory)
-  int kg = 0;         // K-units of the stream started
+  int xend = 0;       // nl after the record slot's loads
   int wend[D] = {};  // nl after the weights of the last D steps issued (wend[0]: the latest)
 
   __device__ __forceinline__ explicit Stream(const GemvArgs& args) : a(args) {
@@ -531,7 +531,7 @@ struct Stream {
     wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     lane = threadIdx.x & 63, p = lane >> 4, r = lane & 15;
     rb = wv / S, ks = wv % S;
-    my = slab + wv * (D * WCH + XS * XCH);
+    my = slab + wv * (D * WCH + XCH);
     const int U = a.K / 256;
     u0 = ks;  // (the wave's K-units: ks, ks + S, ...; the pair reads neighbouring units, which share lines, together)
     NVw = (U - ks + S - 1) / S * NM;
@@ -573,9 +573,9 @@ struct Stream {
     for (int i = D - 1; i > 0; i--) wend[i] = wend[i - 1];
     wend[0] = nl;
   }
-  // the records of K-unit ku of item I's rows of A into record slot b (lane l: chunk l of each row)
-  __device__ __forceinline__ void load_x(const Item& I, int ku, int b) {
-    u32x4* dst = my + D * WCH + b * XCH;
+  // the records of K-unit ku of item I's rows of A into the record slot (lane l: chunk l of each row)
+  __device__ __forceinline__ void load_x(const Item& I, int ku) {
+    u32x4* dst = my + D * WCH;
 #pragma unroll
     for (int t = 0; t < GEMV_BM; t++)
       if (t < I.m)
@@ -583,10 +583,7 @@ struct Stream {
             reinterpret_cast<const void*>(a.xq + int64_t(I.ar[t]) * xq_row_dwords(a.K) + ku * XQ_UNIT + 4 * lane),
             (__attribute__((address_space(3))) void*)(dst + 64 * t), 16, 0, 0);
     nl += I.m;
-    if (b)
-      xend1 = nl;
-    else
-      xend0 = nl;
+    xend = nl;
   }
 };
 
@@ -642,29 +639,17 @@ __device__ __forceinline__ void run_item(Stream<QT, SWIGLU, D>& st, const Item& 
         st.template issue_w<(MX + LA) % NM>(here || has_next, here ? cur.e : nxt.e, here ? cur.n0 : nxt.n0,
                                             here ? vi : vi - st.NVw, (gs + v + LA) % D);
       };
-      if constexpr (SWIGLU) issue();
+      issue();
       uint32_t w[LW];
       const uint32_t sw = st.wbase + ((gs + v) % D) * SS::WCH * 16;
       if constexpr (MX == 0) {
-        // the next K-unit's records: SwiGLU into the one slot once this K-unit's are read, plain products into
-        // the other slot before the wait
-        const int b = SS::XS == 1 ? 0 : st.kg & 1;
-        auto next_x = [&](int bn) {
-          if (v0 + NM < st.NVw)
-            st.load_x(cur, st.u0 + SS::S * (v0 / NM + 1), bn);
-          else if (has_next)
-            st.load_x(nxt, st.u0, bn);
-        };
-        if constexpr (SS::XS == 2) {
-          next_x(b ^ 1);
-          issue();
-        }
-        // (wend[D - 1]: this step's weights)
+        // (wend[D - 1]: this step's weights), then the next K-unit's records into the slot just read
         const int nw = st.nl - st.wend[D - 1];
-        wait_read<QT, SWIGLU, D, M>(st, min(nw, st.nl - (b ? st.xend1 : st.xend0)), sw, st.xbase + b * SS::XCH * 16,
-                                    w, xc);
-        if constexpr (SS::XS == 1) next_x(0);
-        st.kg++;
+        wait_read<QT, SWIGLU, D, M>(st, min(nw, st.nl - st.xend), sw, st.xbase, w, xc);
+        if (v0 + NM < st.NVw)
+          st.load_x(cur, st.u0 + SS::S * (v0 / NM + 1));
+        else if (has_next)
+          st.load_x(nxt, st.u0);
       } else {
         wait_read<QT, SWIGLU, D, 0>(st, st.nl - st.wend[D - 1], sw, st.xbase, w, xc);
       }
@@ -697,7 +682,7 @@ __global__ __launch_bounds__(Shape<SWIGLU>::THREADS) __attribute__((amdgpu_waves
   SS st(a);
   extern __shared__ u32x4 slab[];
   // [buffer][wave][matrix][row of A][row], after every wave's slots
-  float* red = reinterpret_cast<float*>(slab + W::WAVES * (D * SS::WCH + SS::XS * SS::XCH));
+  float* red = reinterpret_cast<float*>(slab + W::WAVES * (D * SS::WCH + SS::XCH));
 
   const int it0 = blockIdx.x, n_my = (n_items - 1 - it0) / G + 1;
   constexpr int RED = W::WAVES * NM * GEMV_BM * 16;  // floats of one partial-sum buffer
@@ -717,7 +702,7 @@ __global__ __launch_bounds__(Shape<SWIGLU>::THREADS) __attribute__((amdgpu_waves
   if (S > 1 && threadIdx.x < 8) ctr[threadIdx.x] = 0;
   __syncthreads();
   Item cur = get_item(tab, 0), nxt = cur;
-  if (st.NVw > 0) st.load_x(cur, st.u0, 0);
+  if (st.NVw > 0) st.load_x(cur, st.u0);
   int gs = 0;
   for (int j = 0; j < n_my; j++) {
     const bool has_next = j + 1 < n_my;
