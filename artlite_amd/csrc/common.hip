@@ -34,7 +34,7 @@ namespace {
 constexpr QType TYPES[] = {{ARTLITE_F32, "F32", 1, 4, 4},           {ARTLITE_F16, "F16", 1, 2, 2},
                            {ARTLITE_BF16, "BF16", 1, 2, 2},         {ARTLITE_Q4_0, "Q4_0", 32, 18, 18},
                            {ARTLITE_Q4_1, "Q4_1", 32, 20, 20},      {ARTLITE_Q8_0, "Q8_0", 32, 34, 34},
-                           {ARTLITE_Q3_K, "Q3_K", 256, 110, 110},   {ARTLITE_Q4_K, "Q4_K", 256, 144, 144},
+                           {ARTLITE_Q3_K, "Q3_K", 256, 110, 112},   {ARTLITE_Q4_K, "Q4_K", 256, 144, 144},
                            {ARTLITE_Q5_K, "Q5_K", 256, 176, 176},   {ARTLITE_Q6_K, "Q6_K", 256, 210, 224},
                            {ARTLITE_IQ4_NL, "IQ4_NL", 32, 18, 18},  {ARTLITE_IQ4_XS, "IQ4_XS", 256, 136, 144}};
 }

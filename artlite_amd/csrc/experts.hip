@@ -87,7 +87,7 @@ struct Fmt<ARTLITE_Q4_1> : FmtT<20, 1, 24, 128, true> {};
 template <>
 struct Fmt<ARTLITE_Q8_0> : FmtT<34, 1, 16, 128> {};  // (q + 128 through an unsigned byte)
 template <>
-struct Fmt<ARTLITE_Q3_K> : FmtT<110, 8, 32, 132, false, true> {};  // (128 + q) - (q - 4)
+struct Fmt<ARTLITE_Q3_K> : FmtT<112, 8, 32, 132, false, true> {};  // (128 + q) - (q - 4)
 template <>
 struct Fmt<ARTLITE_Q4_K> : FmtT<144, 8, 32, 128, true> {};
 template <>

@@ -71,6 +71,11 @@ struct Unit<ARTLITE_Q5_K> {  // (the header, the 32 high-bit bytes, the lane's 3
   static constexpr int BYTES = 176, LW = 20;
 };
 template <>
+struct Unit<ARTLITE_Q3_K> {  // (a layer's 112-byte padded block: the 32 high-bit bytes, the lane's 32 low-bit bytes, and
+                             // the 12 bytes of scales with d)
+  static constexpr int BYTES = 112, LW = 20;
+};
+template <>
 struct Unit<ARTLITE_Q6_K> {  // (a layer's 224-byte padded block: the lane's 64 low-bit bytes, 32 high-bit bytes, and the
                              // 16 scales with d)
   static constexpr int BYTES = 224, LW = 32;
@@ -150,6 +155,13 @@ __device__ __forceinline__ float4 lds_read_f4(const void* p) {
   "ds_read_b128 %[w3], %[pr]\n\t"             \
   "ds_read_b128 %[w4], %[pr] offset:16\n\t"
 #define ART_OW20 [w0] "=&v"(w4[0]), [w1] "=&v"(w4[1]), [w2] "=&v"(w4[2]), [w3] "=&v"(w4[3]), [w4] "=&v"(w4[4])
+#define ART_W20S                               \
+  "ds_read_b128 %[w0], %[pw]\n\t"             \
+  "ds_read_b128 %[w1], %[pw] offset:16\n\t"   \
+  "ds_read_b128 %[w2], %[pr]\n\t"             \
+  "ds_read_b128 %[w3], %[pr] offset:16\n\t"   \
+  "ds_read_b128 %[w4], %[ps]\n\t"
+#define ART_OW20S ART_OW20
 #define ART_W32                                \
   "ds_read_b128 %[w0], %[pw]\n\t"             \
   "ds_read_b128 %[w1], %[pw] offset:16\n\t"   \
@@ -193,6 +205,11 @@ __device__ __forceinline__ void read_unit(uint32_t (&w)[Unit<QT>::LW], u32x4 (&x
     ART_READ_M(12)
 #pragma unroll
     for (int i = 0; i < 12; i++) w[i] = w4[i >> 2][i & 3];
+  } else if constexpr (LW == 20 && QT == ARTLITE_Q3_K) {
+    u32x4 w4[5];
+    ART_READ_M(20S)
+#pragma unroll
+    for (int i = 0; i < 20; i++) w[i] = w4[i >> 2][i & 3];
   } else if constexpr (LW == 20) {
     u32x4 w4[5];
     ART_READ_M(20)
@@ -301,6 +318,24 @@ __device__ __forceinline__ void codes(const uint32_t (&w)[Unit<QT>::LW], int g, 
       q[j] = iq4_int8(w[4 + 4 * H + j] & 0x0F0F0F0Fu);
       q[4 + j] = iq4_int8((w[4 + 4 * H + j] >> 4) & 0x0F0F0F0Fu);
     }
+  } else if constexpr (QT == ARTLITE_Q3_K) {
+    // group g = 4 n + jj (n = p / 2, jj = 2 (p % 2) + H): value l's low bits are crumb jj of low-bit byte l of half n
+    // (w[8..15]), its high bit bit 4 n + jj of high-bit byte l (w[0..7]); code - 4 as int8 (the crumb, with 0xFC
+    // or'ed in where the high bit is clear); the scales of its two 16-value halves, the 6-bit sub-block scales
+    // 2 g, 2 g + 1 (low nibbles in bytes 0..7 of the scales, w[16..17]: g >= 4 the high nibbles of g - 4's bytes;
+    // crumbs in bytes 8..11, w[18]) less 32, times d (w[19], bytes 12..13): d in d, the second in mn
+    const int n = g >> 2, jj = g & 3;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const uint32_t lo = (w[8 + j] >> (2 * jj)) & 0x03030303u, hi = (w[j] >> (4 * n + jj)) & 0x01010101u;
+      q[j] = lo | ((hi ^ 0x01010101u) * 0xFCu);
+    }
+    const uint32_t lw = (w[16 + ((g & 3) >> 1)] >> (16 * (g & 1))) >> (g < 4 ? 0 : 4);
+    const uint32_t cr = w[18] >> (16 * (g & 1) + 2 * (g >> 1));
+    const int sa = int((lw & 15u) | ((cr & 3u) << 4)), sb = int(((lw >> 8) & 15u) | (((cr >> 8) & 3u) << 4));
+    const float dd = h2f(w[19] & 0xFFFFu);
+    d = dd * float(sa - 32);  // (exact: 11 x 6 significant bits)
+    mn = dd * float(sb - 32);
   } else if constexpr (QT == ARTLITE_Q6_K) {
     // group g = 4 h + jj (h = p / 2, jj = 2 (p % 2) + H): value l's low bits are a nibble of low-bit byte 32 (jj % 2)
     // + l of half h (w[0..15]: the high nibbles for jj >= 2), its high bits crumb jj of high-bit byte l (w[16..23]);
@@ -382,7 +417,7 @@ __device__ __forceinline__ float group_term(float acc, uint32_t x, uint32_t l, u
         "s_nop 1"
         : ART_ACC
         : [x] "v"(x), [l] "v"(l), [d] "v"(d), [m8] "v"(-8), ART_QIN, [l0] "i"(2 * H), [l1] "i"(2 * H + 1));
-  } else if constexpr (QT == ARTLITE_Q6_K) {
+  } else if constexpr (QT == ARTLITE_Q6_K || QT == ARTLITE_Q3_K) {
     // the halves' sums in their own chains (a0 / b0: dwords 0..3, a1 / b1: 4..7), each scaled by its sub-block's
     // scale (d: the first half's, mn: the second's); signed codes, no offset
     float c1;
@@ -546,6 +581,10 @@ struct Stream {
       o_w = r * BY + 64 * (p >> 1);
       o_r = r * BY + 128 + 32 * (p >> 1);
       o_s = r * BY + 192;
+    } else if constexpr (QT == ARTLITE_Q3_K) {  // (the high bits, low bits of half p / 2, the scales and d)
+      o_w = r * BY;
+      o_r = r * BY + 32 + 32 * (p >> 1);
+      o_s = r * BY + 96;
     } else {
       constexpr bool HEAD = QT == ARTLITE_Q4_K || QT == ARTLITE_Q5_K || QT == ARTLITE_IQ4_XS;  // (header + run)
       constexpr int PB = QT == ARTLITE_Q8_0 ? 68 : QT == ARTLITE_Q4_1 ? 40 : 36;  // (the lane's two blocks)
@@ -827,7 +866,8 @@ int launch_t(const GemvArgs& a, hipStream_t s) {
 
 bool gemv_supported(int qtype, int K, int N) {
   return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0 || qtype == ARTLITE_Q4_K || qtype == ARTLITE_Q5_K ||
-          qtype == ARTLITE_Q6_K || qtype == ARTLITE_Q4_1 || qtype == ARTLITE_IQ4_NL || qtype == ARTLITE_IQ4_XS) &&
+          qtype == ARTLITE_Q6_K || qtype == ARTLITE_Q4_1 || qtype == ARTLITE_IQ4_NL || qtype == ARTLITE_IQ4_XS ||
+          qtype == ARTLITE_Q3_K) &&
          K > 0 && K % 256 == 0 &&
          N > 0 && N % 64 == 0;
 }
@@ -835,7 +875,7 @@ bool gemv_supported(int qtype, int K, int N) {
 int launch_gemv(const GemvArgs& a, hipStream_t s) {
   if (!gemv_supported(a.qtype, a.K, a.N))
     return fail(ARTLITE_EINVAL,
-                "expert GEMV: weight type %d with K %d, N %d (not Q3_K, K a multiple of 256, N of 64)",
+                "expert GEMV: weight type %d with K %d, N %d (K a multiple of 256, N of 64)",
                 a.qtype, a.K, a.N);
   if (a.N <= 0 || int64_t(a.N) * a.row_bytes >= (int64_t(1) << 31))
     return fail(ARTLITE_EINVAL, "expert GEMV: %d rows of %d bytes", a.N, a.row_bytes);
@@ -849,6 +889,7 @@ int launch_gemv(const GemvArgs& a, hipStream_t s) {
     case ARTLITE_Q8_0: ART_DISPATCH(ARTLITE_Q8_0);
     case ARTLITE_Q5_K: ART_DISPATCH(ARTLITE_Q5_K);
     case ARTLITE_Q6_K: ART_DISPATCH(ARTLITE_Q6_K);
+    case ARTLITE_Q3_K: ART_DISPATCH(ARTLITE_Q3_K);
     case ARTLITE_Q4_1: ART_DISPATCH(ARTLITE_Q4_1);
     case ARTLITE_IQ4_NL: ART_DISPATCH(ARTLITE_IQ4_NL);
     case ARTLITE_IQ4_XS: ART_DISPATCH(ARTLITE_IQ4_XS);

@@ -78,13 +78,16 @@ CONFIGS = {
                  shared_F=512, shared_type="Q5_K", tokens=(16,)),
     "q5k": Spec("q5k", H=1536, E=16, k=2, F=768, gate_type="Q5_K", down_type="Q5_K", scale=1e-4, dmin_scale=1e-3,
                 x_dtype="f32", tokens=(24,)),
-    # test-only: Q6_K throughout on the decode GEMV; a Q3_K down after a GEMV gate / up (the down on the MFMA tiles)
+    # test-only: Q6_K throughout on the decode GEMV; a Q4_K gate / up with a Q3_K down
     "q6k": Spec("q6k", H=1024, E=16, k=2, F=512, gate_type="Q6_K", down_type="Q6_K", scale=5e-5, x_dtype="f32",
                 shared_F=256, shared_type="Q6_K", tokens=(24,)),
     "mixtile": Spec("mixtile", H=1024, E=32, k=4, F=512, gate_type="Q4_K", down_type="Q3_K", scale=2e-4,
                     dmin_scale=1.5e-3, tokens=(16,)),
     "iq4": Spec("iq4", H=768, E=16, k=4, F=512, gate_type="IQ4_XS", down_type="IQ4_NL", scale=5e-5, x_dtype="f32",
                 shared_F=256, shared_type="Q4_1", shared_scale=4e-3, shared_gated=True, tokens=(16, 24)),
+    # test-only: Q3_K throughout on the decode GEMV (16-value sub-block scales, 3-bit codes), fp32 x
+    "q3k": Spec("q3k", H=1024, E=16, k=2, F=512, gate_type="Q3_K", down_type="Q3_K", scale=1e-4, x_dtype="f32",
+                shared_F=256, shared_type="Q3_K", tokens=(16,)),
     # test-only: Q4_1 throughout (d q + m blocks: the min term) with an IQ4_XS / IQ4_NL shared expert
     "q41": Spec("q41", H=1024, E=16, k=2, F=512, gate_type="Q4_1", down_type="Q4_1", scale=4e-3, shared_F=256,
                 shared_type="IQ4_XS", shared_down_type="IQ4_NL", shared_scale=5e-5, tokens=(16,)),
