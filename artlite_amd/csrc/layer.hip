@@ -481,6 +481,12 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
       return fail(ARTLITE_EINVAL, "moe layer: shared expert types %d / %d, width %d", d.shared_type,
                   d.shared_down_type, d.shared_ffn);
   }
+  // the MFMA decode tiles (every product between the GEMV's sizes and the prefill's, and every format the other two
+  // do not take) stage an A row's whole K in LDS: K up to 32 MAX_GROUPS
+  const int kmax = 32 * MAX_GROUPS;
+  if (d.hidden > kmax || d.expert_ffn > kmax || d.shared_ffn > kmax)
+    return fail(ARTLITE_EINVAL, "moe layer: H %d, F %d, shared F %d: at most %d each", d.hidden, d.expert_ffn,
+                d.shared_ffn, kmax);
   if (d.gating != 0 && d.gating != 1) return fail(ARTLITE_EINVAL, "moe layer: gating %d", d.gating);
   if (!(d.norm_eps >= 0.0f && d.norm_eps < 1.0f) || (d.residual != 0 && d.residual != 1))
     return fail(ARTLITE_EINVAL, "moe layer: norm eps %g, residual %d", double(d.norm_eps), d.residual);
@@ -761,6 +767,12 @@ extern "C" int artlite_moe_layer_time(artlite_moe_layer** layers, int n, int64_t
       return fail(ARTLITE_EINVAL, "layer time: layers on different devices");
     ART_TRY(check_ready(layers[i]));
   }
+  // one event per kernel of the first layer's sequence: every layer must run the same sequence
+  const std::vector<std::string> names = kernel_list(L0, T);
+  for (int i = 1; i < n; i++)
+    if (kernel_list(layers[i], T) != names)
+      return fail(ARTLITE_EINVAL, "layer time: layer %d runs other kernels than layer 0 for %lld tokens", i,
+                  (long long)T);
   // every layer runs on the first layer's stream (one ordered sequence)
   std::vector<hipStream_t> own(n);
   for (int i = 0; i < n; i++) {
@@ -770,7 +782,6 @@ extern "C" int artlite_moe_layer_time(artlite_moe_layer** layers, int n, int64_t
   int rc = ARTLITE_OK;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   std::vector<hipEvent_t> ev;
-  const std::vector<std::string> names = kernel_list(L0, T);
   const int nk = int(names.size());
   auto done = [&](int code) {
     for (int i = 0; i < n; i++) layers[i]->stream = own[i];

@@ -67,10 +67,12 @@ class MoELayer:
     def from_gguf(cls, gguf: "GGUFFile", block: int, *, max_tokens: int, norm: bool = False) -> "MoELayer":
         """Block ``block``'s MoE FFN of a GGUF file (``gguf_model.GGUFFile``): its shape from the architecture's
         metadata (``embedding_length``, ``expert_count``, ``expert_used_count``, ``expert_feed_forward_length``,
-        ``expert_shared_feed_forward_length``, ``expert_gating_func``: 2 sigmoid, else softmax; the reference's
+        ``expert_shared_feed_forward_length``, ``expert_gating_func``: 1 softmax, 2 sigmoid; the reference's
         ``model_config.py:735-766``), its tensors ``blk.{block}.ffn_*`` uploaded as the file holds them (the router
         and a shared gate converted to fp32 exactly when stored as F16 / BF16). norm: with the steps either side,
-        the block's ``ffn_norm`` (RMS, eps ``attention.layer_norm_rms_epsilon``) before and the residual add after."""
+        the block's ``ffn_norm`` (RMS, eps ``attention.layer_norm_rms_epsilon``) before and the residual add after.
+        Raises ValueError for routing the layer does not compute: a gating function other than 1 or 2, a weights
+        scale other than 1, ``expert_weights_norm`` false, more than one expert group, an ``exp_probs_b`` bias."""
         b = f"blk.{block}."
         m = gguf.arch_meta
         need = [b + n + ".weight" for n in ("ffn_gate_inp", "ffn_gate_exps", "ffn_up_exps", "ffn_down_exps")]
@@ -95,7 +97,19 @@ class MoELayer:
                 raise ValueError(f"{gguf.path}: block {block} shared gate / up types {stype} / {sutype} differ")
             sF = int(m("expert_shared_feed_forward_length", sdims[1]))
         gated = b + "ffn_gate_inp_shexp.weight" in gguf
-        gating = "sigmoid" if int(m("expert_gating_func", 1)) == 2 else "softmax"
+        # routing the layer does not model is refused, not silently dropped: a weights scale, unnormalised weights,
+        # expert groups, a selection bias, gating functions other than softmax (1) and sigmoid (2) (the oracle's
+        # "no scale, no groups, no selection bias", tests/moe/ref.py:12-14; model_config.py:735-737)
+        gfunc = int(m("expert_gating_func", 1))
+        unmodelled = {"expert_gating_func": gfunc not in (1, 2),
+                      "expert_weights_scale": float(m("expert_weights_scale", 1.0)) != 1.0,
+                      "expert_weights_norm": not bool(m("expert_weights_norm", True)),
+                      "expert_group_count": int(m("expert_group_count", 1)) > 1,
+                      "exp_probs_b": b + "exp_probs_b.bias" in gguf or b + "exp_probs_b" in gguf}
+        bad = [key for key, refused in unmodelled.items() if refused]
+        if bad:
+            raise ValueError(f"{gguf.path}: block {block} routing not modelled by this layer: {', '.join(bad)}")
+        gating = "sigmoid" if gfunc == 2 else "softmax"
         eps = float(m("attention.layer_norm_rms_epsilon", 1e-6)) if norm else 0.0
         if norm and b + "ffn_norm.weight" not in gguf:
             raise ValueError(f"{gguf.path}: block {block} has no ffn_norm")

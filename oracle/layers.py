@@ -64,6 +64,9 @@ CONFIGS = {
     # the prefill tiles)
     "mix_pf": Spec("mix_pf", H=1024, E=16, k=2, F=512, gate_type="Q8_0", down_type="Q4_0", scale=0.01,
                    x_dtype="f32", shared_F=512, shared_type="Q8_0", shared_gated=True, tokens=(256,)),
+    # test-only: Q4_0 with about 128 pairs per expert (T = 512), so the prefill tiles' 8-row-block form runs
+    "q4_rows": Spec("q4_rows", H=1024, E=8, k=2, F=512, gate_type="Q4_0", down_type="Q4_0", scale=0.02,
+                    router="uniform", tokens=(512,)),
     # test-only: the other block formats of real GGUF files, on the MFMA decode tiles -- K-quants (Q5_K gate / up,
     # Q6_K down, a Q4_K / Q3_K shared expert: 16-value sub-block scales) with bf16 x, and IQ4_XS / IQ4_NL with a
     # Q4_1 shared expert and fp32 x
@@ -185,12 +188,13 @@ def shared_out(layer: Layer, x: np.ndarray) -> np.ndarray:
                                  gguf_ref.dequantize(s.sdown_type, d, s.shared_F), layer.shared_inp)
 
 
-def forward(layer: Layer, x: np.ndarray, ids: np.ndarray | None = None, w: np.ndarray | None = None) -> dict:
+def forward(layer: Layer, x: np.ndarray, ids: np.ndarray | None = None, w: np.ndarray | None = None,
+            gating: str = "softmax") -> dict:
     """The oracle's layer: logits (``logits``), the routing of ``moe_ref.moe_route`` (or the given ids / w), the routed
     sum ``moe_ref.moe_ffn`` plus the shared expert. Returns logits, ids, w, y (T, H) fp32."""
     lg = logits(layer, x)
     if ids is None:
-        ids, w = moe_ref.moe_route(lg, layer.spec.k)
+        ids, w = moe_ref.moe_route(lg, layer.spec.k, gating)
     y = moe_ref.moe_ffn(x, ids, w, expert(layer)) + shared_out(layer, x)
     return {"logits": lg, "ids": ids, "w": w, "y": y}
 
@@ -219,18 +223,19 @@ def forward_f64(layer: Layer, x: np.ndarray, ids: np.ndarray, w: np.ndarray) -> 
     return y
 
 
-def route_host(layer: Layer, lg: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+def route_host(layer: Layer, lg: np.ndarray, gating: str = "softmax") -> tuple[np.ndarray, np.ndarray]:
     """The C++ host routing (``host_ref.moe_route``) of plain (T, E) logits."""
     T, E = lg.shape
-    return host_ref.moe_route(lg.reshape(-1), T, E, E, 0, E, layer.spec.k)
+    return host_ref.moe_route(lg.reshape(-1), T, E, E, 0, E, layer.spec.k, sigmoid=gating == "sigmoid")
 
 
-def tie_collapsed(lg: np.ndarray, k: int) -> np.ndarray:
+def tie_collapsed(lg: np.ndarray, k: int, gating: str = "softmax") -> np.ndarray:
     """Tokens whose probability ranking can differ from their logit ranking: two of their k + 1 largest logits are
-    distinct but have equal fp32 softmax probabilities (the oracle ranks by p, the host step by logit)."""
-    from .np_ops import softmax
+    distinct but have equal fp32 probabilities, softmax or (gating "sigmoid") sigmoid (the oracle ranks by p, the host
+    step by logit)."""
+    from .np_ops import sigmoid, softmax
 
-    p = softmax(lg)
+    p = softmax(lg) if gating == "softmax" else sigmoid(lg)
     order = np.argsort(-host_ref.ordered_keys(lg).astype(np.int64), axis=1, kind="stable")[:, :k + 1]
     lt = np.take_along_axis(lg, order, 1)
     pt = np.take_along_axis(p, order, 1)

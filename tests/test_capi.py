@@ -13,6 +13,8 @@ from artlite_amd import _hip
 from artlite_amd.moe import COLS
 from artlite_amd.moe import route as MR
 
+from . import known_answers
+
 HEADER = Path(__file__).resolve().parents[1] / "include" / "artlite_moe.h"
 
 
@@ -59,19 +61,12 @@ def test_no_gpu_fails_loudly() -> None:
         plan.route(np.zeros((2, 8), np.float32), 2)
 
 
-@pytest.mark.parametrize("u", [8, 13, 17, 21, 31, 32])
+@pytest.mark.parametrize("u", [0, 1, 8, 13, 17, 21, 31, 32])
 def test_deal(u: int) -> None:
-    """The reference's test_deal: a union of u experts over the columns: every half once, whole experts first, at
-    most MAX_ITEMS items and ceil(2 u / 8) halves per column."""
-    union = sorted(np.random.default_rng(u).choice(256, u, replace=False).tolist())
-    items = MR.deal(union, COLS)
-    halves = [(e, h) for col in items for e, h0, h1 in col for h in range(h0, h1 + 1)]
-    assert sorted(halves) == sorted((e, h) for e in union for h in (0, 1))
-    assert max(len(col) for col in items) <= MR.MAX_ITEMS
-    assert max(sum(h1 - h0 + 1 for _, h0, h1 in col) for col in items) == -(-2 * u // COLS)
-    for col in items:
-        whole = [h1 - h0 == 1 for _, h0, h1 in col]
-        assert whole == sorted(whole, reverse=True)
+    """Unions of u chosen experts (the reference test_deal's sizes, plus 0 and 1) dealt over the 8 columns: the deal
+    invariants."""
+    union = np.sort(np.random.default_rng(u).permutation(256)[:u]).tolist()
+    known_answers.check_deal(MR.deal(union, COLS), union, COLS, MR.MAX_ITEMS)
 
 
 def test_item_weights() -> None:
@@ -79,3 +74,13 @@ def test_item_weights() -> None:
     w = np.array([[0.75, 0.25], [0.5, 0.5]])
     assert MR.item_weights(ids, w, 5).tolist() == [0.25, 0.5]
     assert MR.item_weights(ids, w, 9).tolist() == [0.0, 0.0]
+
+
+def test_layer_shape_limits_before_any_device() -> None:
+    """A layer whose products the MFMA decode tiles cannot stage (K beyond 4096) is refused at create."""
+    from artlite_amd.moe.layer import MoELayer
+
+    for H, F, sF in ((8192, 512, 0), (1024, 6144, 0), (1024, 512, 8192)):
+        with pytest.raises(_hip.Error, match="at most 4096 each"):
+            MoELayer(hidden=H, n_experts=8, top_k=2, expert_ffn=F, gate_type="Q4_0", down_type="Q4_0", max_tokens=4,
+                     shared_ffn=sF, shared_type="Q4_0" if sF else "")

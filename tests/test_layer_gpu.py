@@ -9,14 +9,14 @@
 - experts: h = silu(x G^T) (x U^T) of each sorted pair and each pair's expert output against float64 math;
 - output: within 1e-3 relative L2 of the fp32 oracle (``moe_ffn`` + ``shared_expert``) and of float64 math for the
   same routing; bitwise identical on a second run (deterministic kernels, no float atomics).
-Config sizes are reduced where the oracle would take long; the full sizes follow in test_layer_full_gpu.py."""
+Config sizes are reduced here; test_layer_full_gpu.py runs configs 3, 4 and 5 at their stated sizes."""
 
 import numpy as np
 import pytest
 
 from oracle import gguf_ref, host_ref, layers, moe_ref
 
-from .helpers import gpu_input, gpu_layer, rel_l2, ulp_diff
+from .helpers import check_against_oracle, gpu_input, gpu_layer, near_tie, rel_l2, ulp_diff
 
 pytestmark = pytest.mark.gpu
 
@@ -129,3 +129,21 @@ def test_layer_errors() -> None:
     with pytest.raises(Error, match="5 tokens of at most 4"):
         g.stage(np.zeros((5, 64), np.float32))
     g.close()
+
+
+@pytest.mark.parametrize(("name", "T"), [("decode", 16), ("mix_pf", 256), ("kquants", 32), ("q4_rows", 512)])
+def test_layer_sigmoid_gating(name: str, T: int) -> None:
+    """Sigmoid gating over the whole layer (the GEMV, the prefill tiles, the MFMA decode tiles) against the oracle's
+    ``moe_route(gating="sigmoid")`` and the C++ host routing's sigmoid mode."""
+    spec = layers.CONFIGS[name]
+    layer = layers.make_layer(spec, 11)
+    x = layers.make_x(spec, T, 11)
+    with gpu_layer(layer, max_tokens=T, gating="sigmoid") as g:
+        y = g(gpu_input(spec, x))
+        taps = check_against_oracle(g, layer, x, y, gating="sigmoid")
+    lg = layers.logits(layer, x)
+    want = layers.forward(layer, x, gating="sigmoid")
+    near = near_tie(lg, spec.k, "sigmoid")
+    assert np.array_equal(taps["ids"][~near], want["ids"][~near])
+    s = 1 / (1 + np.exp(-np.take_along_axis(lg, taps["ids"], 1).astype(np.float64)))
+    np.testing.assert_allclose(taps["weights"], s / np.maximum(s.sum(1, keepdims=True), 2.0 ** -14), rtol=3e-7)

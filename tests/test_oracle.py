@@ -11,6 +11,8 @@ import pytest
 
 from oracle import gguf_ref, host_ref, layers, moe_ref, np_ops, ref_lib, tensors
 
+from . import known_answers
+
 GOLDEN = Path(__file__).resolve().parent / "golden" / "dequant_golden.npz"
 QTYPES = ("Q4_0", "Q4_1", "Q8_0", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "IQ4_NL", "IQ4_XS")
 
@@ -129,22 +131,11 @@ def test_dequant_subnormal_scales() -> None:
 # ---- the layer oracle's routing (tests/moe/ref.py:11-18) and the C++ host routing (moe_host.cpp:45-73)
 
 
-def _test_route_logits() -> np.ndarray:
-    """The logits of the reference's test_route (tests/moe/test_plan.py:18-33): ties at the top, all tied, -0 / +0."""
-    rng = np.random.default_rng(0)
-    lg = rng.standard_normal((1024, 256)).astype(np.float32) * 2
-    lg[0, [3, 9, 200]] = lg[0].max() + 1
-    lg[1, :] = 0.5
-    lg[2, :8], lg[2, 8:] = -0.0, -1
-    lg[2, 5] = 0.0
-    return lg
-
-
 def test_moe_route_known_answers() -> None:
-    """The reference tests' known answers: a three-way tie at the top in id order, all-tied rows the lowest ids,
-    -0 and +0 tied."""
-    ids, w = moe_ref.moe_route(_test_route_logits(), 8)
-    assert ids[0, :3].tolist() == [3, 9, 200] and ids[1].tolist() == ids[2].tolist() == list(range(8))
+    """The planted rows: equal maxima in id order, an all-equal row the lowest ids, +0 and -0 tied; int64 ids."""
+    lg, planted = known_answers.planted_logits(1024)
+    ids, w = moe_ref.moe_route(lg, 8)
+    known_answers.assert_planted(ids, planted)
     assert np.allclose(w[1], 1 / 8) and ids.dtype == np.int64
 
 
@@ -187,10 +178,9 @@ def test_host_route_matches_oracle() -> None:
     """The reference's test_route: the C++ host routing (by logit) equals the oracle (by probability), weights within
     2e-7, from plain (T, E) rows and from the router GEMM's layout (32 experts per column at a pitch of 64, NaN in
     the gaps)."""
-    lg = _test_route_logits()
+    lg, _ = known_answers.planted_logits(1024)
     rids, rw = moe_ref.moe_route(lg, 8)
-    rows = np.full((1024, 8, 64), np.nan, np.float32)
-    rows[:, :, :32] = lg.reshape(1024, 8, 32)
+    rows = known_answers.router_gemm_rows(lg)
     for args in ((lg.reshape(-1), 1024, 256, 256, 0, 256, 8), (rows.reshape(-1), 1024, 512, 32, 64, 256, 8)):
         ids, w = host_ref.moe_route(*args)
         assert np.array_equal(ids, rids) and ids.dtype == np.int32
@@ -225,27 +215,18 @@ def test_tie_collapse_detector() -> None:
 
 @pytest.mark.parametrize("T", [24, 2048])
 def test_plan_invariants(T: int) -> None:
-    """The reference's test_plan (tests/moe/test_plan.py:36-67) on the oracle's plan."""
+    """The reference test_plan's invariants on the oracle's plan of its routings."""
+    from types import SimpleNamespace
+
     rng = np.random.default_rng(T)
     lg = rng.standard_normal((T, 256)).astype(np.float32) + np.linspace(0, 3, 256, dtype=np.float32)
     ids, _ = host_ref.moe_route(lg.reshape(-1), T, 256, 256, 0, 256, 8)
-    chunk, cols = 192, 8
-    cap = -(-(256 + -(-T * 8 // chunk)) // cols)
-    p = host_ref.moe_plan(ids, 256, cols, cap, chunk)
-    counts = p["counts"]
-    assert max(counts) - min(counts) <= 1
-    assert sum(counts) == sum(-(-r // chunk) for r in np.bincount(ids.ravel()))
-    g, j = np.divmod(p["pos"], chunk)
-    c, k = np.divmod(g, cap)
-    assert len(set(p["pos"].ravel().tolist())) == ids.size
-    for t in range(T):
-        for i in range(8):
-            assert p["experts"][c[t, i], k[t, i]] == ids[t, i] and p["rows"][c[t, i], k[t, i], j[t, i]] == t
-    for col in range(cols):
-        for kk in range(counts[col]):
-            r = p["rows"][col, kk]
-            n = int(((c == col) & (k == kk)).sum())
-            assert (r[n:] == r[0]).all() and (np.diff(r[:n]) > 0).all()
+    cap = -(-(256 + -(-T * 8 // 192)) // 8)
+    p = host_ref.moe_plan(ids, 256, 8, cap, 192)
+    n = p["counts"]
+    plan = SimpleNamespace(experts=[p["experts"][c, :n[c]] for c in range(8)], sizes=[p["sizes"][c, :n[c]] for c in range(8)],
+                           rows=[p["rows"][c, :n[c]] for c in range(8)], pos=p["pos"], counts=n.tolist())
+    known_answers.check_plan(plan, ids, cap)
 
 
 def test_plan_errors() -> None:
@@ -325,3 +306,120 @@ def test_rms_norm_pins() -> None:
         d = np.sqrt(ms + 1e-6)
         for i in range(96):
             assert got[t, i] == np.float32(np.float32(np.float64(x[t, i]) / d) * w[i])
+
+
+# ---- closed-form pins of the fp32 ops and the layer formulas (tests/np_ops.py:10-17, tests/moe/ref.py:11-24,55-60):
+# each case has an answer the mathematics fixes independently of the oracle's own formula, chosen so that swapping
+# gate and up, taking silu for sigmoid, dropping the gate of the shared expert or transposing down fails
+
+
+def _f32_close(got: object, want: float, ulps: int = 1) -> bool:
+    g = np.float32(got)
+    w = np.float32(want)
+    return abs(int(np.array(g).view(np.int32)) - int(np.array(w).view(np.int32))) <= ulps
+
+
+def test_sigmoid_closed_forms() -> None:
+    """sigmoid(0) = 1/2 exactly; sigmoid(ln 3) = 3/4, sigmoid(-ln 3) = 1/4; sigmoid(x) + sigmoid(-x) = 1; the
+    saturated ends exactly 0 and 1."""
+    assert np_ops.sigmoid(np.float32(0.0)) == np.float32(0.5)
+    ln3 = np.float32(np.log(3.0))
+    assert _f32_close(np_ops.sigmoid(ln3), 0.75) and _f32_close(np_ops.sigmoid(-ln3), 0.25)
+    x = np.linspace(-12, 12, 97, dtype=np.float32)
+    assert np.abs(np_ops.sigmoid(x).astype(np.float64) + np_ops.sigmoid(-x) - 1).max() < 2 ** -23
+    assert np_ops.sigmoid(np.float32(-100.0)) == 0.0 and np_ops.sigmoid(np.float32(100.0)) == 1.0
+    assert np.all(np.diff(np_ops.sigmoid(x)) >= 0)  # (monotone)
+
+
+def test_silu_closed_forms() -> None:
+    """silu(0) = 0; silu(2) = 2 / (1 + e^-2) (not sigmoid(2)); silu(x) - silu(-x) = x; silu(x) = x for large x and -0
+    for very negative x (e^-x overflows: x / inf); the minimum near x = -1.278 at about -0.2785."""
+    assert np_ops.silu(np.float32(0.0)) == 0.0
+    assert _f32_close(np_ops.silu(np.float32(2.0)), 2.0 / (1.0 + np.exp(-2.0)))
+    assert not _f32_close(np_ops.silu(np.float32(2.0)), 1.0 / (1.0 + np.exp(-2.0)), 1000)
+    x = np.linspace(-9, 9, 73, dtype=np.float32)
+    assert np.abs(np_ops.silu(x).astype(np.float64) - np_ops.silu(-x) - x).max() < 4e-6
+    assert np_ops.silu(np.float32(30.0)) == np.float32(30.0)
+    r = np_ops.silu(np.float32(-100.0))
+    assert r == 0.0 and np.signbit(r)
+    t = np.linspace(-3, 0, 3001, dtype=np.float32)
+    assert abs(float(np_ops.silu(t).min()) + 0.27846) < 1e-4 and abs(float(t[np_ops.silu(t).argmin()]) + 1.2785) < 2e-3
+
+
+def test_swiglu_closed_form() -> None:
+    """A one-hot FFN (H = 3, F = 2): gate row 0 picks x0, up row 0 picks 2 x1, down column 0 lands in output 2, so
+    y = [0, 0, silu(x0) 2 x1] exactly up to fp32 rounding; swapping gate and up would give silu(2 x1) x0."""
+    gate = np.array([[1, 0, 0], [0, 0, 0]], np.float32)
+    up = np.array([[0, 2, 0], [0, 0, 0]], np.float32)
+    down = np.zeros((3, 2), np.float32)
+    down[2, 0] = 1.0
+    x = np.array([[2.0, 3.0, 5.0], [-1.0, 0.5, 7.0]], np.float32)
+    y = moe_ref.swiglu(x, gate, up, down)
+    for t in range(2):
+        x0, x1 = float(x[t, 0]), float(x[t, 1])
+        want = x0 / (1 + np.exp(-x0)) * 2 * x1
+        assert y[t, 0] == 0 and y[t, 1] == 0 and _f32_close(y[t, 2], want, 2)
+        assert not _f32_close(y[t, 2], 2 * x1 / (1 + np.exp(-2 * x1)) * x0, 1000)
+    # a diagonal FFN: y_i = silu(a_i x_i) b_i x_i c_i for diagonal gate a, up b, down c
+    a, b, c = (np.array(v, np.float32) for v in ([0.5, -2.0, 1.5], [3.0, 0.25, -1.0], [2.0, 1.0, -0.5]))
+    x = np.array([[1.0, 2.0, -3.0]], np.float32)
+    y = moe_ref.swiglu(x, np.diag(a), np.diag(b), np.diag(c))[0]
+    for i in range(3):
+        g = float(a[i] * x[0, i])
+        assert _f32_close(y[i], g / (1 + np.exp(-g)) * float(b[i] * x[0, i]) * float(c[i]), 3)
+
+
+def test_shared_expert_gate() -> None:
+    """The shared expert: without gate_inp exactly swiglu(x); with a gate_inp orthogonal to x, sigmoid(0) = 1/2, so
+    exactly half of it; with x . gate_inp = ln 3, three quarters."""
+    rng = np.random.default_rng(4)
+    H, F = 8, 6
+    g, u = rng.standard_normal((F, H)).astype(np.float32), rng.standard_normal((F, H)).astype(np.float32)
+    d = rng.standard_normal((H, F)).astype(np.float32)
+    x = np.zeros((2, H), np.float32)
+    x[0, :4] = [1.0, -2.0, 0.5, 3.0]
+    x[1, 4:] = [0.25, 1.0, -1.0, 2.0]
+    full = moe_ref.swiglu(x, g, u, d)
+    assert np.array_equal(moe_ref.shared_expert(x, g, u, d, None), full)
+    gi = np.zeros(H, np.float32)  # x0 . gi = 1 (-1) + 0.5 (2) = 0; x1 has nothing at 0 or 2
+    gi[2] = 2.0
+    gi[0] = -1.0
+    assert np.array_equal(moe_ref.shared_expert(x, g, u, d, gi), np.float32(0.5) * full)
+    gi = np.zeros(H, np.float32)
+    gi[3] = np.float32(np.log(3.0)) / np.float32(3.0)  # (x0 . gi = ln 3)
+    s = moe_ref.shared_expert(x, g, u, d, gi)
+    assert np.allclose(s[0], 0.75 * full[0], rtol=2e-7, atol=0) and np.array_equal(s[1], 0.5 * full[1])
+
+
+def test_moe_route_closed_forms() -> None:
+    """Softmax gating: logits ln(1, 2, 3, 4) have p = (0.1, 0.2, 0.3, 0.4), so top 2 is (3, 2) with weights 4/7, 3/7.
+    Sigmoid gating: logits (0, ln 3, -ln 3, 2) have sigmoids (1/2, 3/4, 1/4, 0.8808), so top 2 is (3, 1) with weights
+    s3 / (s3 + 3/4) and 3/4 / (s3 + 3/4); ties to the lower id; a sum below 2^-14 is clamped to it."""
+    lg = np.log(np.array([[1.0, 2.0, 3.0, 4.0]])).astype(np.float32)
+    ids, w = moe_ref.moe_route(lg, 2)
+    assert ids.tolist() == [[3, 2]] and _f32_close(w[0, 0], 4 / 7, 2) and _f32_close(w[0, 1], 3 / 7, 2)
+    ln3 = float(np.float32(np.log(3.0)))
+    lg = np.array([[0.0, ln3, -ln3, 2.0], [1.0, 1.0, 1.0, -1.0], [-30.0, -30.0, -31.0, -32.0]], np.float32)
+    ids, w = moe_ref.moe_route(lg, 2, gating="sigmoid")
+    s3 = 1 / (1 + np.exp(-2.0))
+    assert ids[0].tolist() == [3, 1]
+    assert _f32_close(w[0, 0], s3 / (s3 + 0.75), 2) and _f32_close(w[0, 1], 0.75 / (s3 + 0.75), 2)
+    assert ids[1].tolist() == [0, 1] and w[1, 0] == w[1, 1] == np.float32(0.5)
+    tiny = 1 / (1 + np.exp(30.0))
+    assert ids[2].tolist() == [0, 1] and _f32_close(w[2, 0], tiny / 2.0 ** -14, 4)  # (the clamp, not 1/2)
+    with pytest.raises(AssertionError):
+        assert _f32_close(w[2, 0], 0.5, 1000)
+
+
+def test_router_logits_closed_form() -> None:
+    """The router logits x W^T (float64, one rounding): a one-hot token picks a router column exactly; a token of
+    2^-j weights sums exactly representable terms, the float64 sum then rounded once."""
+    spec = layers.CONFIGS["cpu"]
+    layer = layers.make_layer(spec, 0)
+    x = np.zeros((2, spec.H), np.float32)
+    x[0, 17] = 1.0
+    x[1, :3] = [0.5, 0.25, -2.0]
+    lg = layers.logits(layer, x)
+    assert np.array_equal(lg[0], layer.router[:, 17])
+    r = layer.router.astype(np.float64)
+    assert np.array_equal(lg[1], (0.5 * r[:, 0] + 0.25 * r[:, 1] - 2.0 * r[:, 2]).astype(np.float32))

@@ -1,5 +1,6 @@
-"""The GPU chunk plan (artlite_moe_plan) against the oracle's restatement of artlite::moe_plan, element for element,
-and the reference's test_plan invariants (tests/moe/test_plan.py:36-67); its errors; multi-block dispatches."""
+"""The GPU chunk plan (``artlite_moe_plan``) element for element against the oracle's restatement of
+``artlite::moe_plan``, plus the plan invariants of the reference's test_plan (tests/moe/test_plan.py:36-67), for the
+reference's routings, multi-block dispatches and skewed popularity; its argument errors."""
 
 import numpy as np
 import pytest
@@ -8,6 +9,8 @@ from artlite_amd import Error
 from artlite_amd.moe import CHUNK, COLS
 from artlite_amd.moe import plan as MP
 from oracle import host_ref
+
+from . import known_answers
 
 pytestmark = pytest.mark.gpu
 
@@ -27,25 +30,13 @@ def _compare(ids: np.ndarray, E: int, cap: int) -> MP.Plan:
 
 @pytest.mark.parametrize("T", [24, 2048])
 def test_plan(T: int) -> None:
-    """A routing's chunks: every pair once at its pos row of its expert's chunk, pairs in token order, ceil(r / CHUNK)
-    chunks, columns within one chunk of each other, padding rows the chunk's first token."""
+    """The reference test_plan's routings (experts biased by a ramp, top 8 of 256): the oracle's plan element for
+    element, and the plan invariants."""
     rng = np.random.default_rng(T)
-    ids, _ = MP.route(rng.standard_normal((T, 256)).astype(np.float32) + np.linspace(0, 3, 256, dtype=np.float32), 8)
+    ramp = np.linspace(0, 3, 256, dtype=np.float32)
+    ids, _ = MP.route(rng.standard_normal((T, 256)).astype(np.float32) + ramp, 8)
     cap = -(-(256 + -(-T * 8 // CHUNK)) // COLS)
-    plan = _compare(ids, 256, cap)
-    counts = plan.counts
-    assert max(counts) - min(counts) <= 1 and sum(counts) == sum(-(-r // CHUNK) for r in np.bincount(ids.ravel()))
-    g, j = np.divmod(plan.pos, CHUNK)
-    c, k = np.divmod(g, cap)
-    assert len(set(plan.pos.ravel().tolist())) == ids.size
-    for t in range(T):
-        for i in range(8):
-            assert plan.experts[c[t, i]][k[t, i]] == ids[t, i] and plan.rows[c[t, i]][k[t, i], j[t, i]] == t
-    for col in range(COLS):
-        for kk in range(counts[col]):
-            r = plan.rows[col][kk]
-            n = int(((c == col) & (k == kk)).sum())
-            assert (r[n:] == r[0]).all() and (np.diff(r[:n]) > 0).all()
+    known_answers.check_plan(_compare(ids, 256, cap), ids, cap)
 
 
 @pytest.mark.parametrize(("T", "k", "E"), [(4096, 8, 128), (3000, 6, 64), (1, 1, 1), (5000, 4, 1024)])
@@ -55,7 +46,7 @@ def test_plan_large_and_skewed(T: int, k: int, E: int) -> None:
     p = 1.0 / np.arange(1, E + 1) ** 1.2
     ids = np.stack([rng.choice(E, k, replace=False, p=p / p.sum()) for _ in range(T)]).astype(np.int32)
     cap = -(-(E + -(-T * k // CHUNK)) // COLS)
-    _compare(ids, E, cap)
+    known_answers.check_plan(_compare(ids, E, cap), ids, cap)
 
 
 def test_plan_errors() -> None:

@@ -1,6 +1,7 @@
-"""GPU routing (artlite_moe_route / artlite_moe_top_k) against the oracle: the reference's test_top_k
-(tests/moe/test_route.py:16-26) and test_route (tests/moe/test_plan.py:18-33), bit-exact ids against the C++ host
-routing's restatement for every supported E / k shape, NaN logits, sigmoid gating, the empty case."""
+"""GPU routing (``artlite_moe_route``, ``artlite_moe_top_k``) against the oracle: the known answers of the reference's
+routing tests (tests/moe/test_route.py:16-26, tests/moe/test_plan.py:18-33), the decode ``route.route`` (GPU top k
+then the deal), ids bit-exact against the C++ host routing's restatement over many E / k shapes, NaN logits, sigmoid
+gating, no tokens."""
 
 import numpy as np
 import pytest
@@ -10,41 +11,55 @@ from artlite_amd.moe import plan as MP
 from artlite_amd.moe import route as MR
 from oracle import host_ref, moe_ref
 
+from . import known_answers
 from .helpers import ulp_diff
 
 pytestmark = pytest.mark.gpu
 
 
 def test_top_k() -> None:
-    """The cores' top 8 (ties to the lower id) and weights against moe_ref.moe_route, ties included."""
-    rng = np.random.default_rng(0)
-    lg = rng.standard_normal((64, 256)).astype(np.float32) * 2
-    lg[0, [3, 9, 200]] = lg[0].max() + 1
-    lg[1, :] = 0.5
+    """The decode cores' top 8 on the planted rows (equal maxima in id order, an all-equal row) and 61 random ones:
+    the layer oracle's ids; its weights within 2e-6; the weights are the float64 softmax of the chosen logits."""
+    lg, planted = known_answers.planted_logits(64)
     ids, w = MR.top_k(lg, 8)
-    rids, rw = moe_ref.moe_route(lg, 8)
-    assert np.array_equal(ids, rids)
-    assert np.abs(w - rw).max() < 2e-6
-    assert ids[0, :3].tolist() == [3, 9, 200] and ids[1].tolist() == list(range(8))
-    e = np.exp(np.take_along_axis(lg, ids, 1).astype(np.float64) - lg.max(1, keepdims=True))
-    assert np.abs(w - e / e.sum(1, keepdims=True)).max() < 1e-15
+    known_answers.assert_planted(ids, {r: planted[r] for r in (0, 1)})
+    want_ids, want_w = moe_ref.moe_route(lg, 8)
+    np.testing.assert_array_equal(ids, want_ids)
+    np.testing.assert_allclose(w, want_w, rtol=0, atol=2e-6)
+    chosen = np.take_along_axis(lg, ids, 1).astype(np.float64)
+    soft = np.exp(chosen - chosen[:, :1])
+    np.testing.assert_allclose(w, soft / soft.sum(1, keepdims=True), rtol=0, atol=1e-15)
 
 
 def test_route() -> None:
-    """The reference's test_route: both layouts, 1024 tokens; the oracle's ids, weights within 2e-7."""
-    rng = np.random.default_rng(0)
-    lg = rng.standard_normal((1024, 256)).astype(np.float32) * 2
-    lg[0, [3, 9, 200]] = lg[0].max() + 1
-    lg[1, :] = 0.5
-    lg[2, :8], lg[2, 8:] = -0.0, -1
-    lg[2, 5] = 0.0
-    rids, rw = moe_ref.moe_route(lg, 8)
-    rows = np.full((1024, COLS, 64), np.nan, np.float32)
-    rows[:, :, :32] = lg.reshape(1024, COLS, 32)
-    for ids, w in (MP.route(lg, 8), MP.route(rows.reshape(1024, -1), 8, E=256, per_col=32, pitch=64)):
-        assert np.array_equal(ids, rids)
-        assert np.abs(w - rw).max() < 2e-7
-    assert rids[0, :3].tolist() == [3, 9, 200] and rids[1].tolist() == rids[2].tolist() == list(range(8))
+    """1024 tokens with the planted rows (equal maxima, all equal, +0 / -0), as plain rows and in the router GEMM's
+    layout (NaN gaps never read): the layer oracle's ids, weights within 2e-7."""
+    lg, planted = known_answers.planted_logits(1024)
+    want_ids, want_w = moe_ref.moe_route(lg, 8)
+    known_answers.assert_planted(want_ids, planted)
+    for ids, w in (MP.route(lg, 8), MP.route(known_answers.router_gemm_rows(lg), 8, E=256, per_col=32, pitch=64)):
+        np.testing.assert_array_equal(ids, want_ids)
+        np.testing.assert_allclose(w, want_w, rtol=0, atol=2e-7)
+
+
+def test_decode_route() -> None:
+    """``route.route``: the GPU top k, then the deal of every chosen expert over the columns; against the layer
+    oracle's ids and the deal invariants, and the per-item weights against a per-slot lookup."""
+    for S, E, k in ((4, 256, 8), (3, 128, 8), (1, 64, 6), (5, 96, 4)):  # (unions of at most 32: the deal's range)
+        lg = (np.random.default_rng(S * E + k).standard_normal((S, E)) * 1.5).astype(np.float32)
+        ids, w, items = MR.route(lg, k, COLS)
+        want_ids, want_w = moe_ref.moe_route(lg, k)
+        np.testing.assert_array_equal(ids, want_ids)
+        np.testing.assert_allclose(w, want_w, rtol=0, atol=2e-6)
+        union = sorted(set(ids.ravel().tolist()))
+        known_answers.check_deal(items, union, COLS, MR.MAX_ITEMS)
+        for e in union:
+            per_slot = [float(w[s, list(ids[s]).index(e)]) if e in ids[s] else 0.0 for s in range(S)]
+            assert MR.item_weights(ids, w, e).tolist() == per_slot
+    ids, w, items = MR.route(lg, k, COLS, gating="sigmoid")
+    hids, hw = host_ref.moe_route(lg.reshape(-1), lg.shape[0], E, E, 0, E, k, sigmoid=True)
+    np.testing.assert_array_equal(ids, hids)
+    np.testing.assert_allclose(w, hw, rtol=2e-7, atol=0)
 
 
 @pytest.mark.parametrize(("E", "k"), [(8, 2), (60, 4), (64, 6), (65, 1), (128, 8), (256, 8), (256, 16), (512, 8),
