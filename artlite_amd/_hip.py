@@ -46,6 +46,8 @@ SIGNATURES = {
                                          c_f64p]),
     "artlite_moe_plan": (ctypes.c_int, [c_i32p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                         ctypes.c_int, ctypes.c_int, c_i32p, c_i32p, c_i32p, c_i32p, c_i64p]),
+    "artlite_moe_plan_static": (ctypes.c_int, [c_i32p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                               ctypes.c_int, ctypes.c_int, c_i32p, c_i32p, c_i32p, c_i32p, c_i64p]),
     "artlite_dequant_supported": (ctypes.c_int, [ctypes.c_char_p]),
     "artlite_dequant_rows": (ctypes.c_int, [ctypes.c_char_p, c_u8p, ctypes.c_size_t, ctypes.c_size_t,
                                             ctypes.c_size_t, c_f32p]),

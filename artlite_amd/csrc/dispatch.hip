@@ -11,7 +11,15 @@
 //  2. k_scatter: each pair's rank among the earlier pairs of its block with the same expert (wave ballots over the
 //     id bits give the peers and the in-wave rank; a per-wave count table orders the waves) plus its block's base:
 //     its position in the sorted order. Stable by construction: no atomics decide any position.
+#include <mutex>
+
 #include "route.h"
+
+// The device memory of artlite_moe_plan_static (the entry point that allocates nothing): one array per GPU, held until
+// the process ends. Kernels never name it: host code looks its per-device address up with hipGetSymbolAddress and
+// passes that address, as it passes the buffers of artlite_moe_plan.
+constexpr size_t PLAN_SCRATCH_BYTES = size_t(8) << 20;
+static __device__ __align__(256) uint8_t scratch[PLAN_SCRATCH_BYTES];
 
 namespace artlite {
 
@@ -250,60 +258,152 @@ int launch_plan(const DispatchBufs& d, const PlanBufs& pl, hipStream_t s) {
   return ARTLITE_OK;
 }
 
+namespace {
+
+// The device memory of one host-pointer plan call: the staged ids, the per-block histogram table, counts / offsets /
+// chunk prefix, order / slot, pos, the plan's rows / experts / sizes / column counts, the control words.
+struct PlanMem {
+  int32_t *ids, *table, *o2, *o3, *o5, *ctrl;
+  int64_t* pos;
+};
+
+// bytes of each PlanMem region, in order (each followed by a 256-byte tail the vector loads may touch)
+void plan_sizes(int64_t P, int E, int cols, int cap, int chunk, size_t (&b)[7]) {
+  const size_t slots = size_t(cols) * cap;
+  b[0] = size_t(P) * 4;
+  b[1] = size_t(dispatch_blocks(P)) * E * 4;
+  b[2] = size_t(3 * E + 3) * 4;
+  b[3] = size_t(2 * P) * 4;
+  b[4] = size_t(P) * 8;
+  b[5] = (slots * chunk + 2 * slots + cols) * 4;
+  b[6] = CTRL_WORDS * 4;
+}
+
+__global__ void k_zero_words(int32_t* p, int n) {
+  if (int(threadIdx.x) < n) p[threadIdx.x] = 0;
+}
+static_assert(CTRL_WORDS <= 64, "k_zero_words: one 64-thread block");
+
+int check_plan_args(const char* who, const int32_t* ids, int64_t n, int k, int E, int cols, int cap, int chunk,
+                    const int32_t* experts, const int32_t* counts, const int32_t* sizes, const int32_t* rows,
+                    const int64_t* pos) {
+  if (n < 0 || k < 1 || E < 1 || cols < 1 || cap < 0 || chunk < 1)
+    return fail(ARTLITE_EINVAL, "%s: n %lld, k %d, E %d, cols %d, cap %d, chunk %d", who, (long long)n, k, E, cols,
+                cap, chunk);
+  if (E > MAX_EXPERTS) return fail(ARTLITE_EINVAL, "%s: E %d beyond this build's %d", who, E, MAX_EXPERTS);
+  if (!counts || (n && (!ids || !pos)) || (cap && (!experts || !sizes || !rows)))
+    return fail(ARTLITE_EINVAL, "%s: null array", who);
+  return ARTLITE_OK;
+}
+
+// The plan of n x k ids on stream s in the device memory m, the results copied to the caller's host arrays.
+int plan_run(const int32_t* ids, int64_t n, int k, int E, int cols, int cap, int chunk, int32_t* experts,
+             int32_t* counts, int32_t* sizes, int32_t* rows, int64_t* pos, const PlanMem& m, hipStream_t s) {
+  const int64_t P = n * k;
+  const size_t slots = size_t(cols) * cap;
+  if (P) ART_HIP(hipMemcpyAsync(m.ids, ids, size_t(P) * 4, hipMemcpyHostToDevice, s));
+  k_zero_words<<<1, 64, 0, s>>>(m.ctrl, CTRL_WORDS);  // (a fill kernel: no memset node if a caller captures)
+  ART_HIP(hipGetLastError());
+  DispatchBufs d{m.ids, P, E, k, m.table, m.ctrl, m.o2, m.o2 + E, m.o3, m.o3 + P, nullptr, 0, m.o2 + 2 * E + 1, chunk};
+  PlanBufs pl{cols, cap, m.o5 + slots * chunk, m.o5 + slots * chunk + 2 * slots, m.o5 + slots * chunk + slots, m.o5,
+              m.pos};
+  ART_TRY(launch_plan(d, pl, s));
+  int32_t ctrl[CTRL_WORDS];
+  ART_HIP(hipMemcpyAsync(ctrl, m.ctrl, sizeof ctrl, hipMemcpyDeviceToHost, s));
+  ART_HIP(hipStreamSynchronize(s));
+  if (ctrl[CTRL_BAD]) return fail(ARTLITE_EINVAL, "moe_plan: expert id %d of %d", ids[P - ctrl[CTRL_BAD_FIRST]], E);
+  if (ctrl[CTRL_OVER_CAP]) return fail(ARTLITE_EINVAL, "moe_plan: more than %d chunks in a column", cap);
+  const int total = ctrl[CTRL_CHUNKS];
+  ART_HIP(hipMemcpyAsync(counts, pl.ccounts, size_t(cols) * 4, hipMemcpyDeviceToHost, s));
+  // (only the dealt slots are written: the reference's arrays keep their other entries)
+  for (int col = 0; col < cols; col++) {
+    const int mc = total > col ? (total - 1 - col) / cols + 1 : 0;
+    if (!mc) continue;
+    ART_HIP(hipMemcpyAsync(experts + size_t(col) * cap, pl.experts + size_t(col) * cap, size_t(mc) * 4,
+                           hipMemcpyDeviceToHost, s));
+    ART_HIP(hipMemcpyAsync(sizes + size_t(col) * cap, pl.sizes + size_t(col) * cap, size_t(mc) * 4,
+                           hipMemcpyDeviceToHost, s));
+    ART_HIP(hipMemcpyAsync(rows + size_t(col) * cap * chunk, pl.rows + size_t(col) * cap * chunk,
+                           size_t(mc) * chunk * 4, hipMemcpyDeviceToHost, s));
+  }
+  if (P) ART_HIP(hipMemcpyAsync(pos, pl.pos, size_t(P) * 8, hipMemcpyDeviceToHost, s));
+  ART_HIP(hipStreamSynchronize(s));
+  return ARTLITE_OK;
+}
+
+// ---- the no-allocation variant's device memory: one static array per GPU, its address looked up once per device
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[MAX_DEVICES] = {};
+
+// the current device's copy of scratch (hipGetSymbolAddress on its first use on each device, that device current);
+// host code uses this address, never the array's name
+int scratch_of_device(uint8_t** out) {
+  int dev = 0;
+  ART_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= MAX_DEVICES) return fail(ARTLITE_EINVAL, "moe_plan_static: device %d beyond %d", dev, MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(ARTLITE_EHIP, "moe_plan_static: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch[dev] = p;
+  }
+  *out = static_cast<uint8_t*>(g_scratch[dev]);
+  return ARTLITE_OK;
+}
+
+}  // namespace
+
 }  // namespace artlite
 
 using namespace artlite;
 
 extern "C" int artlite_moe_plan(const int32_t* ids, int64_t n, int k, int E, int cols, int cap, int chunk,
                                 int32_t* experts, int32_t* counts, int32_t* sizes, int32_t* rows, int64_t* pos) {
-  if (n < 0 || k < 1 || E < 1 || cols < 1 || cap < 0 || chunk < 1)
-    return fail(ARTLITE_EINVAL, "moe_plan: n %lld, k %d, E %d, cols %d, cap %d, chunk %d", (long long)n, k, E, cols,
-                cap, chunk);
-  if (E > MAX_EXPERTS) return fail(ARTLITE_EINVAL, "moe_plan: E %d beyond this build's %d", E, MAX_EXPERTS);
-  if (!counts || (n && (!ids || !pos)) || (cap && (!experts || !sizes || !rows)))
-    return fail(ARTLITE_EINVAL, "moe_plan: null array");
-  const int64_t P = n * k;
+  ART_TRY(check_plan_args("moe_plan", ids, n, k, E, cols, cap, chunk, experts, counts, sizes, rows, pos));
   HostCtx* c;
   ART_TRY(host_ctx(&c));
-  const int64_t nb = dispatch_blocks(P);
-  const size_t slots = size_t(cols) * cap;
+  size_t b[7];
+  plan_sizes(n * k, E, cols, cap, chunk, b);
   // in: ids | out: table | out2: counts, offsets, cstart | out3: order, slot | out4: pos | out5: rows, experts, sizes,
   // column counts | flag: ctrl
-  ART_TRY(c->in.reserve(size_t(P) * 4));
-  ART_TRY(c->out.reserve(size_t(nb) * E * 4));
-  ART_TRY(c->out2.reserve(size_t(3 * E + 3) * 4));
-  ART_TRY(c->out3.reserve(size_t(2 * P) * 4));
-  ART_TRY(c->out4.reserve(size_t(P) * 8));
-  ART_TRY(c->out5.reserve((slots * chunk + 2 * slots + cols) * 4));
-  ART_TRY(c->flag.reserve(CTRL_WORDS * 4));
-  if (P) ART_HIP(hipMemcpyAsync(c->in.p, ids, size_t(P) * 4, hipMemcpyHostToDevice, c->stream));
-  ART_HIP(hipMemsetAsync(c->flag.p, 0, CTRL_WORDS * 4, c->stream));
-  int32_t* o2 = c->out2.as<int32_t>();
-  int32_t* o5 = c->out5.as<int32_t>();
-  DispatchBufs d{c->in.as<int32_t>(), P, E, k, c->out.as<int32_t>(), c->flag.as<int32_t>(), o2, o2 + E,
-                 c->out3.as<int32_t>(), c->out3.as<int32_t>() + P, nullptr, 0, o2 + 2 * E + 1, chunk};
-  PlanBufs pl{cols, cap, o5 + slots * chunk, o5 + slots * chunk + 2 * slots, o5 + slots * chunk + slots, o5,
-              c->out4.as<int64_t>()};
-  ART_TRY(launch_plan(d, pl, c->stream));
-  int32_t ctrl[CTRL_WORDS];
-  ART_HIP(hipMemcpyAsync(ctrl, c->flag.p, sizeof ctrl, hipMemcpyDeviceToHost, c->stream));
-  ART_HIP(hipStreamSynchronize(c->stream));
-  if (ctrl[CTRL_BAD]) return fail(ARTLITE_EINVAL, "moe_plan: expert id %d of %d", ids[P - ctrl[CTRL_BAD_FIRST]], E);
-  if (ctrl[CTRL_OVER_CAP]) return fail(ARTLITE_EINVAL, "moe_plan: more than %d chunks in a column", cap);
-  const int total = ctrl[CTRL_CHUNKS];
-  ART_HIP(hipMemcpyAsync(counts, pl.ccounts, size_t(cols) * 4, hipMemcpyDeviceToHost, c->stream));
-  // (only the dealt slots are written: the reference's arrays keep their other entries)
-  for (int col = 0; col < cols; col++) {
-    const int m = total > col ? (total - 1 - col) / cols + 1 : 0;
-    if (!m) continue;
-    ART_HIP(hipMemcpyAsync(experts + size_t(col) * cap, pl.experts + size_t(col) * cap, size_t(m) * 4,
-                           hipMemcpyDeviceToHost, c->stream));
-    ART_HIP(hipMemcpyAsync(sizes + size_t(col) * cap, pl.sizes + size_t(col) * cap, size_t(m) * 4,
-                           hipMemcpyDeviceToHost, c->stream));
-    ART_HIP(hipMemcpyAsync(rows + size_t(col) * cap * chunk, pl.rows + size_t(col) * cap * chunk,
-                           size_t(m) * chunk * 4, hipMemcpyDeviceToHost, c->stream));
+  ART_TRY(c->in.reserve(b[0]));
+  ART_TRY(c->out.reserve(b[1]));
+  ART_TRY(c->out2.reserve(b[2]));
+  ART_TRY(c->out3.reserve(b[3]));
+  ART_TRY(c->out4.reserve(b[4]));
+  ART_TRY(c->out5.reserve(b[5]));
+  ART_TRY(c->flag.reserve(b[6]));
+  const PlanMem m{c->in.as<int32_t>(), c->out.as<int32_t>(), c->out2.as<int32_t>(), c->out3.as<int32_t>(),
+                  c->out5.as<int32_t>(), c->flag.as<int32_t>(), c->out4.as<int64_t>()};
+  return plan_run(ids, n, k, E, cols, cap, chunk, experts, counts, sizes, rows, pos, m, c->stream);
+}
+
+extern "C" int artlite_moe_plan_static(const int32_t* ids, int64_t n, int k, int E, int cols, int cap, int chunk,
+                                       int32_t* experts, int32_t* counts, int32_t* sizes, int32_t* rows,
+                                       int64_t* pos) {
+  ART_TRY(check_plan_args("moe_plan_static", ids, n, k, E, cols, cap, chunk, experts, counts, sizes, rows, pos));
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) return fail(ARTLITE_EHIP, "moe_plan_static: no HIP device");
+  size_t b[7], at[7], total = 0;
+  plan_sizes(n * k, E, cols, cap, chunk, b);
+  for (int i = 0; i < 7; i++) {
+    at[i] = total;
+    total += (b[i] + 255) / 256 * 256 + 256;
   }
-  if (P) ART_HIP(hipMemcpyAsync(pos, pl.pos, size_t(P) * 8, hipMemcpyDeviceToHost, c->stream));
-  ART_HIP(hipStreamSynchronize(c->stream));
-  return ARTLITE_OK;
+  if (total > PLAN_SCRATCH_BYTES)
+    return fail(ARTLITE_EINVAL,
+                "moe_plan_static: n %lld x k %d, E %d, %d x %d chunks of %d need %zu bytes of device scratch, beyond "
+                "its %zu (use artlite_moe_plan)",
+                (long long)n, k, E, cols, cap, chunk, total, PLAN_SCRATCH_BYTES);
+  uint8_t* base = nullptr;
+  ART_TRY(scratch_of_device(&base));
+  const PlanMem m{reinterpret_cast<int32_t*>(base + at[0]), reinterpret_cast<int32_t*>(base + at[1]),
+                  reinterpret_cast<int32_t*>(base + at[2]), reinterpret_cast<int32_t*>(base + at[3]),
+                  reinterpret_cast<int32_t*>(base + at[5]), reinterpret_cast<int32_t*>(base + at[6]),
+                  reinterpret_cast<int64_t*>(base + at[4])};
+  // the null stream: nothing is created (a stream's creation may allocate)
+  return plan_run(ids, n, k, E, cols, cap, chunk, experts, counts, sizes, rows, pos, m, nullptr);
 }

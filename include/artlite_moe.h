@@ -59,6 +59,16 @@ int artlite_moe_top_k(const float* logits, int64_t n, int E, int k, int sigmoid,
 int artlite_moe_plan(const int32_t* ids, int64_t n, int k, int E, int cols, int cap, int chunk, int32_t* experts,
                      int32_t* counts, int32_t* sizes, int32_t* rows, int64_t* pos);
 
+/* ---- the chunk plan without allocating: no counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): artlite_moe_plan's
+ * arguments and results, with every device buffer it needs (the staged ids, the per-block histograms, counters,
+ * the results before their copy back) carved from one static 8 MiB array per GPU, held until the process ends, and
+ * the null stream. It calls no hipMalloc / hipFree. A call needing more than that array returns ARTLITE_EINVAL
+ * (about 250000 pairs at E = 128). Calls share the GPU's array: calls that overlap on one GPU (other threads) race;
+ * each call clears the counters it needs. */
+int artlite_moe_plan_static(const int32_t* ids, int64_t n, int k, int E, int cols, int cap, int chunk,
+                            int32_t* experts, int32_t* counts, int32_t* sizes, int32_t* rows, int64_t* pos);
+
 /* ---- dequantization: replaces _native.dequant_supported / dequant_rows (reference csrc/bindings/gguf.cpp:62-76 ->
  * artlite::dequant_rows, csrc/artlite/dequant.h:12-17). n rows of qtype (the reference's native types: "F32", "F16",
  * "BF16", "Q4_0", "Q4_1", "Q8_0", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "IQ4_NL", "IQ4_XS"), row_bytes apart in raw, into
