@@ -18,8 +18,11 @@ ARCH = "gfx950"
 # all device code: gfx950 only; packed fp32 instructions off (they are not trusted on the target pool)
 COMMON = ["-std=c++17", "-O3", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
           "-packed-fp32-ops", "-Wall", "-Wno-unused-result"]
-# per-file extra flags: the dequantizer's fp32 operations in the reference's order, unfused
-EXTRA = {"dequant.hip": ["-ffp-contract=off"], "route.hip": ["-ffp-contract=off"]}
+# per-file extra flags: the dequantizer's fp32 operations in the reference's order, unfused; the prefill tiles with the
+# machine scheduler's ILP strategy (it issues a stage's LDS reads ahead of the MFMAs that use them, where the default
+# strategy, chasing an occupancy these one-wave-per-SIMD kernels cannot have, reads each operand right before its use)
+EXTRA = {"dequant.hip": ["-ffp-contract=off"], "route.hip": ["-ffp-contract=off"],
+         "prefill.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]}
 
 
 def hipcc() -> str:

@@ -44,13 +44,14 @@ __device__ void count_tail(const DispatchBufs& d, int c, int start, int total) {
     d.offsets[e] = start;
   }
   if (e == 0) d.offsets[d.E] = total;
-  if (d.BM > 0) {  // the expert GEMMs' tiles: experts ascending, BM sorted rows each
-    const int nt = e < d.E ? (c + d.BM - 1) / d.BM : 0;
+  if (d.BM > 0) {  // the expert GEMMs' tiles: experts ascending, BM sorted rows each (balanced: balanced_rows)
+    const int rows = d.balanced ? balanced_rows(c, d.BM) : d.BM;
+    const int nt = e < d.E ? (c + rows - 1) / rows : 0;
     int nt_total;
     const int t0 = block_scan(nt, &nt_total);
     for (int m = 0; m < nt; m++) {
       d.tiles[2 * (t0 + m)] = e;
-      d.tiles[2 * (t0 + m) + 1] = start + m * d.BM;
+      d.tiles[2 * (t0 + m) + 1] = start + m * rows;
     }
     if (e == 0) d.ctrl[CTRL_TILES] = nt_total;
   }

@@ -30,14 +30,15 @@ struct GemmArgs {
   float* y;                // plain output (row stride N)
 };
 
-// rows of A (tokens / pairs) per tile of the decode (GEMV-like) kernel, and of the prefill tiling
+// rows of A (tokens / pairs) per tile of the MFMA decode tiles, and the most of a prefill tile (an expert's rows in
+// tiles of balanced_rows(count, PREFILL_BM) rows)
 constexpr int DECODE_BM = 8;
-constexpr int PREFILL_BM = 128;
+constexpr int PREFILL_BM = 256;
 
-// One prefill launch (fp16 MFMA tiles of PREFILL_BM rows): for each tile and each block of output rows,
-// out[s][n] = sum_k A[row(s)][k] W_e[n][k] with A in fp16, its rows scaled by 2^-in_exp[token], and W_e's rows raw
-// GGUF blocks. SwiGLU launches (w[1] set) write h = silu(A W_gate^T) * (A W_up^T) in fp16 scaled by
-// 2^-out_exp[token]; plain launches write fp32 (the A scale undone).
+// One prefill launch (prefill.hip: fp16 MFMA tiles of at most PREFILL_BM rows): for each tile and each block of output
+// rows, out[s][n] = sum_k A[row_a(s)][k] W_e[n][k] with A in fp16 (its rows scaled by powers of two) and W_e's rows
+// raw GGUF blocks; row_scale[s] = (x, y) undoes the scales: plain launches write fp32 x y sum (y set) or fp16 y sum
+// (y16 set: the row's true values are x times these), SwiGLU launches (w[1] set) write h = silu(x g) (x u) y in fp16.
 struct PrefillArgs {
   const uint8_t* w[2];     // weight tensors: (gate, up) or (down, null); expert e at w + e expert_bytes
   int64_t expert_bytes;
@@ -45,18 +46,16 @@ struct PrefillArgs {
   int N, K;                // output rows per expert, values per row
   int qtype;               // ARTLITE_Q4_0 / Q8_0
   const uint16_t* a;       // A: fp16 rows of K values
-  int a_gather;            // 1: A row of sorted row s = token(s); 0: A row = s
-  const int32_t* order;    // token(s) = order[s] / topk (null: token(s) = s)
-  int topk;
+  const int32_t* row_a;    // per output row s: its A row (a token); null: A row s
+  const float2* row_scale; // per output row s: (x, y) as above
   const int32_t* tiles;    // (expert, first sorted row) per tile; null: dense rows 0 .. dense_rows of expert 0
   const int32_t* n_tiles;  // the tile count (device)
   const int32_t* offsets;  // E + 1 expert offsets in the sorted order
   int dense_rows;
   int64_t max_tiles;       // grid bound
-  const int32_t* in_exp;   // per token: the exponent of A's row scale
-  const int32_t* out_exp;  // SwiGLU: per token, the exponent of h's scale
-  uint16_t* h;             // SwiGLU output: fp16 h 2^-out_exp[token(s)] (row stride N)
+  uint16_t* h;             // SwiGLU output: fp16 (row stride N)
   float* y;                // plain output: fp32 (row stride N)
+  uint16_t* y16;           // or fp16 (row stride N)
 };
 
 // whether the prefill tiling takes N rows of K values of weights of this type
@@ -64,11 +63,18 @@ bool prefill_supported(int qtype, int K, int N);
 
 int launch_prefill(const PrefillArgs& a, hipStream_t s);
 
-// x (T rows of H fp32 / bf16 values) -> the prefill's fp16 rows x16 scaled by 2^-x_exp[t], and per token the
-// exponents h_exp (h_exp2) of the h scale from the bound on |h| that wmax[0], wmax[1] (wmax[2], wmax[3]) give: max
-// |w| of the gate and up matrices (pairs: 1 or 2)
-int launch_prefill_x(const void* x, int x_dtype, int64_t T, int H, const float* wmax, int pairs, uint16_t* x16,
-                     int32_t* x_exp, int32_t* h_exp, int32_t* h_exp2, hipStream_t s);
+// x (T rows of H fp32 / bf16 values) -> the prefill's fp16 rows x16 = x 2^-xe[t] (each token's largest |x| into
+// [2^14, 2^15)), and per token the row factors of the expert products: gu[t] = (2^xe, 2^-he) for the gate / up
+// launch (he: the exponent of h's scale, from the bound on |h| that wmax[0], wmax[1] give: max |w| of the gate and up
+// matrices) and dn[t] = (2^(he + ye), 2^-ye) for the down launch's fp16 output (ye from the bound on its sums that F
+// and wmax[4], max |w| of the down matrix, give: |sum| 2^-ye < 2^15); pairs 2: the same for a second (shared)
+// expert's matrices wmax[2], wmax[3] into gu2, and dn2 = (2^he, 1) for its fp32 down output
+int launch_prefill_x(const void* x, int x_dtype, int64_t T, int H, const float* wmax, int pairs, int F, uint16_t* x16,
+                     float2* gu, float2* dn, float2* gu2, float2* dn2, hipStream_t s);
+
+// per sorted pair row s (P of them): its token t = order[s] / k into row_a, gu[t] into gu_row, dn[t] into dn_row
+int launch_prefill_rows(const int32_t* order, int64_t P, int k, const float2* gu, const float2* dn, int32_t* row_a,
+                        float2* gu_row, float2* dn_row, hipStream_t s);
 
 // *out = max |w| over a tensor's nblocks GGUF blocks (Q4_0, Q8_0)
 int launch_weight_max(const uint8_t* w, int qtype, int64_t nblocks, float* out, hipStream_t s);
@@ -81,6 +87,10 @@ int launch_expert_gemm(const GemmArgs& a, hipStream_t s);
 // res (optional; x_dtype res_dtype): added last, y[t] += res[t] (the block's residual)
 int launch_combine(const float* Y, const int32_t* slot, const float* w, int k, const float* ys, const float* ws_logit,
                    int ws_sigmoid, int64_t T, int H, const void* res, int res_dtype, float* y, hipStream_t s);
+// the same over fp16 pair outputs: Y[s] = Y16[s] yf[s].x (the down launch's row factors; H a multiple of 8)
+int launch_combine16(const uint16_t* Y16, const float2* yf, const int32_t* slot, const float* w, int k,
+                     const float* ys, const float* ws_logit, int ws_sigmoid, int64_t T, int H, const void* res,
+                     int res_dtype, float* y, hipStream_t s);
 
 // fp32 activations -> bf16 hi + lo planes (x = hi + lo to 2^-16 relative)
 int launch_split(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, hipStream_t s);

@@ -415,464 +415,36 @@ int launch_decode(const GemmArgs& a, hipStream_t s) {
   return ARTLITE_OK;
 }
 
-// ---- Prefill tiling (k_prefill): fp16 products on v_mfma_f32_16x16x32_f16. A is fp16 rows, each token's row
-// scaled by a power of two (2^-in_exp[token]) into [2^14, 2^15) at its largest, so bf16 activations convert
-// exactly and fp32 ones round once (2^-11). The weights' blocks are decoded in registers to fp16 d (q - 8) (Q4_0)
-// or d q (Q8_0): the code exactly, the product with the fp16 scale rounded once (2^-11 relative), so the MFMA's
-// fp32 sums need no per-group scale FMA. The SwiGLU launch writes h in fp16 scaled by 2^-out_exp[token], where
-// out_exp bounds |h| <= (sum |x|)^2 max|w_gate| max|w_up| below 2^15; the plain launch scales its fp32 outputs back
-// by 2^in_exp[token].
-// A workgroup is one tile of PREFILL_BM sorted rows of one expert times 256 staged weight rows (SwiGLU: 128 of gate
-// and the same 128 of up; plain: 256), as 8 waves: wave w takes all 128 rows (MB = 8 MFMA row blocks) and two
-// 16-row column blocks (SwiGLU: gate and up rows 16 w .. + 16, so h forms in the wave; plain: rows 32 w .. + 32), so
-// each lane's decode of a block's codes feeds 8 MFMAs. K streams in stages of two 32-value groups through a ring of
-// R LDS stages filled by DMA (global_load_lds, issued by asm so that the compiler, which would wait for every DMA
-// in flight before any LDS read it sees, does not know of them): every wave issues the same number of loads per
-// stage (past the last stage, loads of stage 0 again), so each wait is a fixed count of this wave's loads, and
-// R - 1 stages are in flight while one computes. The operands of the next group are read from LDS while the
-// current group computes; stage st + 1's wait and barrier sit between stage st's two groups, after which the slot
-// of stage st (both groups in registers by then) takes stage st + R.
-// A rows sit in LDS as 16-byte chunks of 8 values, XOR-swizzled by row, so the 16 rows of an operand read fall in
-// different banks; a weight row's stage bytes (two blocks) sit packed, read as aligned dwords (a block's codes start
-// 2 bytes into it: the first block's are shifted into place with alignbit). MFMA layout (16x16x32): lane l holds A
-// row l % 16 and B column l % 16, both with K values 8 (l / 16) .. + 8; C column l % 16, rows 4 (l / 16) .. + 4.
-template <int QT>
-struct PStage {
-  static constexpr int GB = Fmt<QT>::GROUP_BYTES;
-  static constexpr int ROW = 2 * GB;  // weight bytes of a row per stage
-  static constexpr int DW = ROW / 4;  // its dwords (9 / 17)
-};
-static_assert(PStage<ARTLITE_Q4_0>::ROW % 4 == 0 && PStage<ARTLITE_Q8_0>::ROW % 4 == 0, "stage rows in dwords");
-
-template <int QT>
-struct PLayout {
-  static constexpr int WAVES = 8, THREADS = 64 * WAVES;
-  static constexpr int WROWS = 256;                             // staged weight rows of a workgroup
-  static constexpr int ACH = 8;                                 // 16-byte chunks of an A row per stage
-  static constexpr int ABYTES = PREFILL_BM * ACH * 16;          // one stage of A
-  static constexpr int AI = PREFILL_BM * ACH / 64 / WAVES;      // A DMA instructions per wave per stage
-  static constexpr int BI = (WROWS * PStage<QT>::DW + 64 * WAVES - 1) / (64 * WAVES);  // weight dword DMAs per wave
-  static constexpr int BBYTES = WAVES * BI * 256;               // one stage of weights (padded)
-  static constexpr int SBYTES = ABYTES + BBYTES;
-  static constexpr int R = (150 * 1024 / SBYTES) < 5 ? (150 * 1024 / SBYTES) : 5;  // stages in the ring
-  static constexpr int LOADS = AI + BI;                         // DMA instructions per wave per stage
-  static_assert(R >= 3, "ring");
-  static_assert((R - 1) * LOADS < 64, "vmcnt");
-  static_assert(AI * 64 * WAVES == PREFILL_BM * ACH, "A stage in whole instructions");
-};
-
-template <int N>
-__device__ __forceinline__ void pf_wait() {
-  static_assert(N >= 0 && N < 64, "vmcnt");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory");
-}
-
-// every wave's LDS reads done, then the workgroup barrier
-__device__ __forceinline__ void pf_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-__device__ __forceinline__ uint32_t pf_lds_addr(const void* p) {
-  return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
-}
-
-// one DMA of SIZE bytes per lane from g into LDS at lds (wave-uniform) + SIZE lane. M0 carries the LDS address; no
-// compiler-generated code in these kernels uses M0 (the asm sets it before each load, with the one wait state a
-// load after an M0 write needs).
-template <int SIZE>
-__device__ __forceinline__ void pf_dma(const void* g, uint32_t lds) {
-  if constexpr (SIZE == 16)
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
-  else
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
-}
-
-// the same from a uniform base (SGPRs) plus the lane's 32-bit byte offset (no 64-bit address arithmetic per load)
-template <int SIZE>
-__device__ __forceinline__ void pf_dma_s(const void* base, uint32_t off, uint32_t lds) {
-  if constexpr (SIZE == 16)
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
-                 : "memory", "m0");
-  else
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds)
-                 : "memory", "m0");
-}
-
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-
-// the operands of one 32-value group: per row block, the lane's 8 fp16 of A; per column block, the weight row's
-// fp16 scale and 8 of its code bytes (Q4_0: 16 nibbles, 8 of them the lane's)
-template <int MB>
-struct POps {
-  u32x4 a[MB];
-  uint32_t sc[2];
-  uint32_t cw[2][2];
-};
-
-// Decode of a lane's 8 weights to fp16: the code bytes spread into fp16 1024 + c (c < 256 exact, one perm per two),
-// the offset taken off exactly by one packed FMA (Q4_0's high nibbles, kept in place as 16 q, are scaled by 1/16 in
-// it), then the product with the block's scale, rounded once.
-template <int QT>
-struct PDecode {
-  uint32_t msk;
-  f16x2 mul, add;
-  __device__ __forceinline__ explicit PDecode(int lg) {
-    if constexpr (QT == ARTLITE_Q4_0) {
-      const bool hi = lg >= 2;  // (lane groups 2, 3 hold K values 16 .. 31: the high nibbles)
-      msk = hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
-      mul = hi ? f16x2{_Float16(0.0625f), _Float16(0.0625f)} : f16x2{_Float16(1.0f), _Float16(1.0f)};
-      add = hi ? f16x2{_Float16(-72.0f), _Float16(-72.0f)} : f16x2{_Float16(-1032.0f), _Float16(-1032.0f)};
+// ---- the prefill's activations: per token t, x's row in fp16 scaled by 2^-xe (its largest |x| into [2^14, 2^15);
+// exact for bf16 x unless below 2^-14 of that), and the factors of the expert products' rows: gu[t] = (2^xe, 2^-he),
+// he the exponent of h's scale from the bound B = 2 (sum |x|)^2 (max |w_gate|) (max |w_up|) >= |silu(g) u| >= |h|
+// (|g| <= sum |x| max |w_gate|, |silu(g)| <= |g|): he = ilogb(B) - 14, so |h| 2^-he < 2^15 (fp16 holds it). wmax[j]:
+// max |w| of the bound's two matrices (pair j: wmax[2 j], wmax[2 j + 1]). The down launch's sums over F fp16 values
+// of h 2^-he (below 2^15) times weights (below max |w_down| = wmax[4], up to fp16 rounding) stay below
+// 2^15 F wmax[4] (1 + 2^-11): with ye = ilogb(F wmax[4]) + 1 they stay below 2^15 (1 + 2^-11) < 65504 after the
+// factor 2^-ye, so the expert launch writes fp16 sums times 2^-ye and the true output is that times 2^(he + ye):
+// dn[t] = (2^(he + ye), 2^-ye). The shared expert's down writes fp32: dn2[t] = (2^he, 1). One workgroup per token.
+__device__ __forceinline__ void prefill_x_factors(int64_t t, int tid, int xe, float l1, const float* wmax, int pairs,
+                                                  int F, float2* gu, float2* dn, float2* gu2, float2* dn2) {
+  if (tid < pairs) {
+    // (in double: the square of a large sum stays finite)
+    const double b = 2.0 * double(l1) * double(l1) * double(wmax[2 * tid]) * double(wmax[2 * tid + 1]);
+    const int he = max(-126, min(126, (b > 0.0 && b < 1e300) ? ilogb(b) - 14 : 0));
+    (tid ? gu2 : gu)[t] = make_float2(__builtin_ldexpf(1.0f, xe), __builtin_ldexpf(1.0f, -he));
+    if (tid) {
+      dn2[t] = make_float2(__builtin_ldexpf(1.0f, he), 1.0f);
     } else {
-      msk = 0x80808080u;  // (Q8_0: the sign bits flipped, c = q + 128)
-      mul = f16x2{_Float16(1.0f), _Float16(1.0f)};
-      add = f16x2{_Float16(-1152.0f), _Float16(-1152.0f)};
+      const double bd = double(F) * double(wmax[4]);
+      const int ye = (bd > 0.0 && bd < 1e300) ? min(min(126, 126 - he), max(max(-126, -126 - he), ilogb(bd) + 1)) : 0;
+      dn[t] = make_float2(__builtin_ldexpf(1.0f, he + ye), __builtin_ldexpf(1.0f, -ye));
     }
   }
-  __device__ __forceinline__ u32x4 operator()(const uint32_t (&cw)[2], uint32_t sc) const {
-    const uint32_t v0 = QT == ARTLITE_Q4_0 ? cw[0] & msk : cw[0] ^ msk;
-    const uint32_t v1 = QT == ARTLITE_Q4_0 ? cw[1] & msk : cw[1] ^ msk;
-    const uint32_t w[4] = {__builtin_amdgcn_perm(0x64646464u, v0, 0x04010400u),
-                           __builtin_amdgcn_perm(0x64646464u, v0, 0x04030402u),
-                           __builtin_amdgcn_perm(0x64646464u, v1, 0x04010400u),
-                           __builtin_amdgcn_perm(0x64646464u, v1, 0x04030402u)};
-    const f16x2 d = __builtin_bit_cast(f16x2, sc | (sc << 16));
-    u32x4 b;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const f16x2 c = __builtin_bit_cast(f16x2, w[j]) * mul + add;  // (exact: the code less its offset)
-      b[j] = __builtin_bit_cast(uint32_t, c * d);
-    }
-    return b;
-  }
-};
-
-__device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, const f32x4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
-                                                 0);
 }
 
-// The items (tile, column block) of a launch, in tile-major order, dealt to the 8 XCDs in contiguous runs: workgroup
-// b runs on XCD b % 8 (the dispatcher's round robin), and the G = grid / 8 workgroups of an XCD take its run's items
-// in turn, so the column blocks of a tile, and the tiles of an expert, run close in time on one XCD and share its L2
-// (the tile's A rows, the expert's weights).
-struct PItem {
-  int e, s0, m_valid, n0;
-};
-
-template <bool SWIGLU>
-__device__ __forceinline__ PItem prefill_item(const PrefillArgs& a, int64_t w, int nbk) {
-  constexpr int WN = SWIGLU ? 128 : 256;
-  const int tl = int(w / nbk);
-  PItem I;
-  I.n0 = int(w % nbk) * WN;
-  if (a.tiles) {
-    I.e = a.tiles[2 * tl];
-    I.s0 = a.tiles[2 * tl + 1];
-    I.m_valid = min(PREFILL_BM, a.offsets[I.e + 1] - I.s0);
-  } else {
-    I.e = 0;
-    I.s0 = tl * PREFILL_BM;
-    I.m_valid = min(PREFILL_BM, a.dense_rows - I.s0);
-  }
-  return I;
-}
-
-// The lane's DMA sources of an item. A: instruction i writes chunks (wv AI + i) 64 + lane of a stage's A region;
-// chunk p holds row r = p / ACH, physical chunk c = p % ACH, which is logical chunk c ^ swz(r) (K values 8 c .. + 8
-// of the stage); rows past the tile repeat its last (their outputs are not stored). Weights: instruction j writes
-// dwords (wv BI + j) 64 + lane of the stage's weight region, staged row q / DW (SwiGLU: gate rows n0 .. + 128, then
-// up's; plain: rows n0 .. + 256), dword q % DW of the row's stage bytes; dwords past the rows load the last one
-// again (padding), rows past N the last row. Held as 32-bit byte offsets (A: from a.a; weights: from the
-// instruction's matrix, which is uniform: 128 rows of gate are a whole number of instructions).
-template <int QT, bool SWIGLU>
-struct PSrc {
-  using L = PLayout<QT>;
-  static constexpr int GATE_INSTS = 128 * PStage<QT>::DW / 64;  // (SwiGLU: instructions of the gate rows)
-  static_assert(128 * PStage<QT>::DW % 64 == 0, "matrix-uniform weight instructions");
-  uint32_t a[L::AI];
-  uint32_t w[L::BI];
-  __device__ __forceinline__ static int swz(int r) { return (r >> 1) & 7; }
-  __device__ __forceinline__ static const uint8_t* wbase(const PrefillArgs& g, int wv, int j) {
-    return SWIGLU && wv * L::BI + j >= GATE_INSTS ? g.w[1] : g.w[0];
-  }
-  __device__ __forceinline__ void set(const PrefillArgs& g, const PItem& I, int wv, int lane) {
-#pragma unroll
-    for (int i = 0; i < L::AI; i++) {
-      const int p = (wv * L::AI + i) * 64 + lane, r = p / L::ACH, c = (p % L::ACH) ^ swz(r);
-      const int s = I.s0 + min(r, I.m_valid - 1);
-      const int ar = g.a_gather ? (g.order ? g.order[s] / g.topk : s) : s;
-      a[i] = (uint32_t(ar) * uint32_t(g.K) + 8 * c) * 2;  // (bytes)
-    }
-#pragma unroll
-    for (int j = 0; j < L::BI; j++) {
-      const int q = min((wv * L::BI + j) * 64 + lane, L::WROWS * PStage<QT>::DW - 1);
-      const int row = q / PStage<QT>::DW, dw = q % PStage<QT>::DW;
-      const int n = min(I.n0 + (SWIGLU ? row % 128 : row), g.N - 1);
-      w[j] = uint32_t(I.e) * uint32_t(g.expert_bytes) + uint32_t(n) * uint32_t(g.row_bytes) + 4 * dw;
-    }
-  }
-};
-
-// The K loop of one item over MBN row blocks of A (the tile's rows, rounded up to 16-row blocks that hold any), in
-// the workgroup's continuous stream of stages: the item's stage st is global step g0 + st in ring slot
-// (g0 + st) % R; the R steps issued ahead reach into the next item's first stages (or, after the last item, load
-// stage 0 again). On entry cur holds group 0 of stage 0 (read from LDS); on exit, group 0 of the next item's stage 0.
-// The loads of stage st of an item (sources src) into the ring slot at byte offset so: A from a.a + 128 st, the
-// weights from their matrix + ROW st (uniform bases), each lane at its own offset.
-template <int QT, bool SWIGLU>
-__device__ __forceinline__ void prefill_issue(const PrefillArgs& a, uint32_t lds_base, int wv,
-                                              const PSrc<QT, SWIGLU>& src, int st, uint32_t so) {
-  using L = PLayout<QT>;
-  const uint32_t adst = lds_base + so + wv * L::AI * 1024, bdst = lds_base + so + L::ABYTES + wv * L::BI * 256;
-  const uint8_t* ab = reinterpret_cast<const uint8_t*>(a.a) + 128 * st;
-#pragma unroll
-  for (int i = 0; i < L::AI; i++) pf_dma_s<16>(ab, src.a[i], adst + i * 1024);
-#pragma unroll
-  for (int i = 0; i < L::BI; i++)
-    pf_dma_s<4>(PSrc<QT, SWIGLU>::wbase(a, wv, i) + st * PStage<QT>::ROW, src.w[i], bdst + i * 256);
-}
-
-// The K loop of one item over MBN row blocks of A (the tile's rows, rounded up to 16-row blocks that hold any), in
-// the workgroup's continuous stream of stages through the ring: the item's stage st sits in slot (so0 + st SBYTES)
-// mod R SBYTES; the step issued as stage st completes (into stage st's slot) is stage st + R, which past the item's
-// last stage is the next item's stage st + R - stages (or, after the last item, stage 0 again). On entry cur holds
-// group 0 of stage 0; on exit, group 0 of the next item's stage 0 (all 8 row blocks), and the slot it came from is
-// returned.
-template <int QT, bool SWIGLU, int MBN>
-__device__ __forceinline__ uint32_t prefill_loop(const PrefillArgs& a, uint8_t* lds, uint32_t so,
-                                                 const PSrc<QT, SWIGLU>& src, const PSrc<QT, SWIGLU>& nsrc,
-                                                 bool has_next, POps<8>& cur, POps<8>& nxt, f32x4 (&acc)[8][2]) {
-  using F = Fmt<QT>;
-  using L = PLayout<QT>;
-  constexpr int R = L::R, ROW = PStage<QT>::ROW, GB = F::GROUP_BYTES;
-  const int lane = threadIdx.x & (WAVE - 1), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
-  const int lg = lane >> 4, lr = lane & 15;
-  const int stages = a.K / 64;
-  const uint32_t lbase = pf_lds_addr(lds);
-  // the lane's LDS read offsets in a slot: A row lr (row block mb at + 16 mb rows), group gl: the chunk of K
-  // 8 lg .. + 8; B: the staged row of column block nb, its block gl
-  constexpr int AMB = 16 * L::ACH * 16;
-  const uint32_t aof[2] = {uint32_t(lr * L::ACH * 16 + ((0 + lg) ^ PSrc<QT, SWIGLU>::swz(lr)) * 16),
-                           uint32_t(lr * L::ACH * 16 + ((4 + lg) ^ PSrc<QT, SWIGLU>::swz(lr)) * 16)};
-  const uint32_t bof[2] = {uint32_t(L::ABYTES + (SWIGLU ? 16 * wv + lr : 32 * wv + lr) * ROW),
-                           uint32_t(L::ABYTES + (SWIGLU ? 128 + 16 * wv + lr : 32 * wv + 16 + lr) * ROW)};
-  // the code bytes of lane group lg at the block + 2 + cb: Q4_0 bytes 8 (lg & 1) .. + 8 (lane groups 0, 1 take the
-  // low nibbles, 2, 3 the high ones), Q8_0 bytes 8 lg .. + 8
-  const int cb = QT == ARTLITE_Q4_0 ? 8 * (lg & 1) : 8 * lg;
-  auto read = [&](POps<8>& o, uint32_t sl, int gl, auto nr) {
-    const uint8_t* ap = lds + sl + aof[gl];
-#pragma unroll
-    for (int mb = 0; mb < decltype(nr)::value; mb++) o.a[mb] = *reinterpret_cast<const u32x4*>(ap + mb * AMB);
-#pragma unroll
-    for (int nb = 0; nb < 2; nb++) {
-      const uint8_t* b = lds + sl + bof[nb] + gl * GB;  // (4-byte aligned: gl GB is 0 or 2 mod 4)
-      o.sc[nb] = *reinterpret_cast<const uint16_t*>(b);
-      if (gl == 0) {
-        const uint32_t* d = reinterpret_cast<const uint32_t*>(b + cb);
-        const uint32_t d0 = d[0], d1 = d[1], d2 = d[2];
-        o.cw[nb][0] = __builtin_amdgcn_alignbit(d1, d0, 16);
-        o.cw[nb][1] = __builtin_amdgcn_alignbit(d2, d1, 16);
-      } else {
-        const uint32_t* d = reinterpret_cast<const uint32_t*>(b + 2 + cb);
-        o.cw[nb][0] = d[0];
-        o.cw[nb][1] = d[1];
-      }
-    }
-  };
-  const PDecode<QT> dec(lg);
-  auto compute = [&](const POps<8>& o) {
-#pragma unroll
-    for (int nb = 0; nb < 2; nb++) {
-      const u32x4 b = dec(o.cw[nb], o.sc[nb]);
-#pragma unroll
-      for (int mb = 0; mb < MBN; mb++) acc[mb][nb] = mfma16(o.a[mb], b, acc[mb][nb]);
-    }
-  };
-  using NR = std::integral_constant<int, MBN>;
-  using N8 = std::integral_constant<int, 8>;
-  auto next_slot = [](uint32_t x) { return x + L::SBYTES == R * L::SBYTES ? 0u : x + L::SBYTES; };
-  // one stage: group 1 read while group 0 computes; the wait for the next stage, the barrier, the step into this
-  // stage's slot; the next stage's group 0 read while group 1 computes
-  auto step = [&](const PSrc<QT, SWIGLU>& isrc, int ist, auto nr) {
-    read(nxt, so, 1, NR{});
-    compute(cur);
-    pf_wait<(R - 2) * L::LOADS>();  // (the next stage: the R - 2 steps after it issued)
-    pf_barrier();
-    prefill_issue<QT, SWIGLU>(a, lbase, wv, isrc, ist, so);  // (into the slot every wave is past)
-    so = next_slot(so);
-    read(cur, so, 0, nr);
-    compute(nxt);
-  };
-  int st = 0;
-  for (; st < stages - R; st++) step(src, st + R, NR{});
-  for (; st + 1 < stages; st++) step(has_next ? nsrc : src, has_next ? st + R - stages : 0, NR{});
-  step(has_next ? nsrc : src, has_next ? st + R - stages : 0, N8{});
-  return so;
-}
-
-template <int QT, bool SWIGLU>
-__global__ __launch_bounds__(512) void k_prefill(const PrefillArgs a) {
-  using L = PLayout<QT>;
-  constexpr int R = L::R;
-  constexpr int WN = SWIGLU ? 128 : 256;  // output columns per item
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  // per row of an item: (2^in_exp, 2^-out_exp), in three buffers: item q's in buffer q % 3, filled while item q - 1
-  // computes (waves 0, 1); item q - 2's epilogue, the last reader of that buffer, is behind every wave by then
-  // (item q - 1's barriers), while item q - 1's may still be running in other waves (two buffers would race)
-  float2* rowf = reinterpret_cast<float2*>(lds + R * L::SBYTES);
-  const int lane = threadIdx.x & (WAVE - 1), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
-  const int lg = lane >> 4, lr = lane & 15;
-  const int nbk = (a.N + WN - 1) / WN;
-  const int64_t ntl = a.tiles ? int64_t(*a.n_tiles) : (a.dense_rows + PREFILL_BM - 1) / PREFILL_BM;
-  const int64_t items = ntl * nbk, per = (items + 7) / 8;
-  const int G = gridDim.x / 8, x = blockIdx.x % 8, j0 = blockIdx.x / 8;
-  const int64_t first = x * per + j0, end = min(items, (x + 1) * per);
-  if (first >= end) return;
-  const int nq = int((end - first + G - 1) / G);  // this workgroup's items: first + q G
-  // the row scales of item I into buffer b
-  auto row_info = [&](const PItem& I, int b) {
-    if (threadIdx.x < PREFILL_BM) {
-      const int m = threadIdx.x;
-      float2 f = {1.0f, 1.0f};
-      if (m < I.m_valid) {
-        const int s = I.s0 + m, t = a.order ? a.order[s] / a.topk : s;
-        f.x = __builtin_ldexpf(1.0f, a.in_exp[t]);
-        if (SWIGLU) f.y = __builtin_ldexpf(1.0f, -a.out_exp[t]);
-      }
-      rowf[b * PREFILL_BM + m] = f;
-    }
-  };
-
-  PItem I = prefill_item<SWIGLU>(a, first, nbk);
-  PSrc<QT, SWIGLU> src, nsrc;
-  src.set(a, I, wv, lane);
-  row_info(I, 0);
-  // the first item's first R stages (stages >= R: the launch checks), then its stage 0 read
-#pragma unroll
-  for (int j = 0; j < R; j++) prefill_issue<QT, SWIGLU>(a, pf_lds_addr(lds), wv, src, j, j * L::SBYTES);
-  pf_wait<(R - 1) * L::LOADS>();  // (stage 0: R - 1 stages issued after it)
-  __syncthreads();                // (and the row scales)
-  POps<8> cur, nxt;
-  {
-    using F = Fmt<QT>;
-    constexpr int AMB = 16 * L::ACH * 16, ROW = PStage<QT>::ROW;
-    const uint32_t aof0 = uint32_t(lr * L::ACH * 16 + (lg ^ PSrc<QT, SWIGLU>::swz(lr)) * 16);
-#pragma unroll
-    for (int mb = 0; mb < 8; mb++) cur.a[mb] = *reinterpret_cast<const u32x4*>(lds + aof0 + mb * AMB);
-    const int cb = QT == ARTLITE_Q4_0 ? 8 * (lg & 1) : 8 * lg;
-#pragma unroll
-    for (int nb = 0; nb < 2; nb++) {
-      const uint8_t* b = lds + L::ABYTES + (SWIGLU ? 128 * nb + 16 * wv + lr : 32 * wv + 16 * nb + lr) * ROW;
-      cur.sc[nb] = *reinterpret_cast<const uint16_t*>(b);
-      const uint32_t* d = reinterpret_cast<const uint32_t*>(b + cb);
-      cur.cw[nb][0] = __builtin_amdgcn_alignbit(d[1], d[0], 16);
-      cur.cw[nb][1] = __builtin_amdgcn_alignbit(d[2], d[1], 16);
-      (void)F::OFF;
-    }
-  }
-
-  uint32_t so = 0;  // the ring slot (byte offset) of the current item's stage 0
-  for (int q = 0; q < nq; q++) {
-    const bool has_next = q + 1 < nq;
-    PItem J{};
-    if (has_next) {
-      J = prefill_item<SWIGLU>(a, first + int64_t(q + 1) * G, nbk);
-      nsrc.set(a, J, wv, lane);
-      row_info(J, (q + 1) % 3);  // (read after this item's barriers)
-    }
-    f32x4 acc[8][2];
-#pragma unroll
-    for (int mb = 0; mb < 8; mb++) acc[mb][0] = acc[mb][1] = f32x4{0, 0, 0, 0};
-    const int mbn = (I.m_valid + 15) / 16;
-    if (mbn <= 2)
-      so = prefill_loop<QT, SWIGLU, 2>(a, lds, so, src, nsrc, has_next, cur, nxt, acc);
-    else if (mbn <= 4)
-      so = prefill_loop<QT, SWIGLU, 4>(a, lds, so, src, nsrc, has_next, cur, nxt, acc);
-    else
-      so = prefill_loop<QT, SWIGLU, 8>(a, lds, so, src, nsrc, has_next, cur, nxt, acc);
-
-    // epilogue: lane output i of block (mb, nb): row 16 mb + 4 lg + i of the tile; column (SwiGLU) n0 + 16 wv + lr
-    // of gate (nb 0) and up (nb 1), (plain) n0 + 32 wv + 16 nb + lr
-    const float2* rf = rowf + (q % 3) * PREFILL_BM;
-#pragma unroll
-    for (int mb = 0; mb < 8; mb++) {
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int m = 16 * mb + 4 * lg + i;
-        if (m >= I.m_valid) continue;
-        const int64_t o = int64_t(I.s0 + m) * a.N;
-        const float2 f = rf[m];
-        if constexpr (SWIGLU) {
-          const int n = I.n0 + 16 * wv + lr;
-          if (n >= a.N) continue;
-          const float g = acc[mb][0][i] * f.x, u = acc[mb][1][i] * f.x;
-          const float h = g / (1.0f + expf(-g)) * u;
-          a.h[o + n] = __builtin_bit_cast(uint16_t, _Float16(h * f.y));
-        } else {
-#pragma unroll
-          for (int nb = 0; nb < 2; nb++) {
-            const int n = I.n0 + 32 * wv + 16 * nb + lr;
-            if (n < a.N) a.y[o + n] = acc[mb][nb][i] * f.x;
-          }
-        }
-      }
-    }
-    I = J;
-    src = nsrc;
-  }
-  pf_wait<0>();  // (the loads past the last stage land before the workgroup's LDS is released)
-}
-
-template <int QT, bool SWIGLU>
-int launch_prefill_t(const PrefillArgs& a, hipStream_t s) {
-  using L = PLayout<QT>;
-  const int64_t tiles = a.tiles ? a.max_tiles : (a.dense_rows + PREFILL_BM - 1) / PREFILL_BM;
-  const int64_t items = tiles * ((a.N + (SWIGLU ? 127 : 255)) / (SWIGLU ? 128 : 256));
-  if (items <= 0) return ARTLITE_OK;
-  if (items >= (int64_t(1) << 31)) return fail(ARTLITE_EINVAL, "prefill GEMM: %lld work items", (long long)items);
-  if (a.K / 64 < L::R) return fail(ARTLITE_EINVAL, "prefill GEMM: K %d below %d", a.K, 64 * L::R);
-  constexpr size_t lds = size_t(L::R) * L::SBYTES + 3 * PREFILL_BM * 8;
-  // persistent workgroups: as many as the device holds at once (a multiple of 8, the XCDs), at most the items
-  static const int resident = [] {
-    const void* f = reinterpret_cast<const void*>(k_prefill<QT, SWIGLU>);
-    int dev = 0, cus = 0, per_cu = 0;
-    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess ||
-        hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, L::THREADS, lds) != hipSuccess)
-      return 0;
-    return cus * std::max(1, per_cu);
-  }();
-  if (resident < 8) return fail(ARTLITE_EHIP, "prefill GEMM: kernel set-up failed");
-  const unsigned grid = unsigned(std::min<int64_t>((items + 7) / 8 * 8, resident / 8 * 8));
-  k_prefill<QT, SWIGLU><<<grid, L::THREADS, lds, s>>>(a);
-  ART_HIP(hipGetLastError());
-  return ARTLITE_OK;
-}
-
-bool prefill_supported(int qtype, int K, int N) {
-  const int r = qtype == ARTLITE_Q4_0 ? PLayout<ARTLITE_Q4_0>::R : PLayout<ARTLITE_Q8_0>::R;
-  return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0) && K >= 64 * r && K % 64 == 0 && N > 0 && N % 16 == 0;
-}
-
-int launch_prefill(const PrefillArgs& a, hipStream_t s) {
-  if (!prefill_supported(a.qtype, a.K, a.N))
-    return fail(ARTLITE_EINVAL, "prefill GEMM: weight type %d, K %d, N %d", a.qtype, a.K, a.N);
-  if (!a.a || !a.in_exp || (a.w[1] ? !a.h || !a.out_exp : !a.y) || (a.tiles && (!a.n_tiles || !a.offsets)))
-    return fail(ARTLITE_EINVAL, "prefill GEMM: null argument");
-  const bool swiglu = a.w[1] != nullptr;
-  if (a.qtype == ARTLITE_Q4_0) return swiglu ? launch_prefill_t<ARTLITE_Q4_0, true>(a, s) : launch_prefill_t<ARTLITE_Q4_0, false>(a, s);
-  return swiglu ? launch_prefill_t<ARTLITE_Q8_0, true>(a, s) : launch_prefill_t<ARTLITE_Q8_0, false>(a, s);
-}
-
-// ---- the prefill's activations: per token t, x's row in fp16 scaled by 2^-x_exp[t] (its largest |x| into
-// [2^14, 2^15); exact for bf16 x unless below 2^-14 of that), and the exponents h_exp[t] of h's scale: the bound
-// B = 2 (sum |x|)^2 (max |w_gate|) (max |w_up|) >= |silu(g) u| >= |h| (|g| <= sum |x| max |w_gate|, |silu(g)| <=
-// |g|), h_exp = ilogb(B) - 14, so |h| 2^-h_exp < 2^15 (fp16 holds it). wmax[j]: max |w| of the bound's two matrices
-// (pair j: wmax[2 j], wmax[2 j + 1]). One workgroup per token.
 __global__ __launch_bounds__(256) void k_prefill_x(const void* __restrict__ x, int x_dtype, int H,
-                                                   const float* __restrict__ wmax, int pairs,
-                                                   uint16_t* __restrict__ x16, int32_t* __restrict__ x_exp,
-                                                   int32_t* __restrict__ h_exp, int32_t* __restrict__ h_exp2) {
+                                                   const float* __restrict__ wmax, int pairs, int F,
+                                                   uint16_t* __restrict__ x16, float2* gu, float2* dn, float2* gu2,
+                                                   float2* dn2) {
   __shared__ float red[2][8];
   const int64_t t = blockIdx.x;
   auto at = [&](int i) -> float {
@@ -896,22 +468,16 @@ __global__ __launch_bounds__(256) void k_prefill_x(const void* __restrict__ x, i
   const int xe = (mx > 0.0f && mx <= 3.4e38f) ? ilogbf(mx) - 14 : 0;
   for (int i = threadIdx.x; i < H; i += 256)
     x16[t * H + i] = __builtin_bit_cast(uint16_t, _Float16(__builtin_ldexpf(at(i), -xe)));
-  if (threadIdx.x < pairs) {
-    // (in double: the square of a large sum stays finite)
-    const double b = 2.0 * double(l1) * double(l1) * double(wmax[2 * threadIdx.x]) * double(wmax[2 * threadIdx.x + 1]);
-    const int he = (b > 0.0 && b < 1e300) ? ilogb(b) - 14 : 0;
-    (threadIdx.x ? h_exp2 : h_exp)[t] = max(-126, min(126, he));
-  }
-  if (threadIdx.x == 0) x_exp[t] = xe;
+  prefill_x_factors(t, threadIdx.x, xe, l1, wmax, pairs, F, gu, dn, gu2, dn2);
 }
 
 // The same for H a multiple of 8 up to 2048 NP: the row read once, 8 values per thread per piece (one 16-byte load for
 // bf16, two for fp32), kept in registers for the fp16 pass, written as 16-byte pieces.
 template <int XT, int NP>
 __global__ __launch_bounds__(256) void k_prefill_x_rows(const void* __restrict__ x, int H,
-                                                        const float* __restrict__ wmax, int pairs,
-                                                        uint16_t* __restrict__ x16, int32_t* __restrict__ x_exp,
-                                                        int32_t* __restrict__ h_exp, int32_t* __restrict__ h_exp2) {
+                                                        const float* __restrict__ wmax, int pairs, int F,
+                                                        uint16_t* __restrict__ x16, float2* gu, float2* dn, float2* gu2,
+                                                        float2* dn2) {
   __shared__ float red[2][4];
   const int64_t t = blockIdx.x;
   const int n8 = H / 8;
@@ -960,21 +526,16 @@ __global__ __launch_bounds__(256) void k_prefill_x_rows(const void* __restrict__
       reinterpret_cast<uint4*>(x16 + t * H)[i] = make_uint4(w[0], w[1], w[2], w[3]);
     }
   }
-  if (threadIdx.x < pairs) {
-    const double b = 2.0 * double(l1) * double(l1) * double(wmax[2 * threadIdx.x]) * double(wmax[2 * threadIdx.x + 1]);
-    const int he = (b > 0.0 && b < 1e300) ? ilogb(b) - 14 : 0;
-    (threadIdx.x ? h_exp2 : h_exp)[t] = max(-126, min(126, he));
-  }
-  if (threadIdx.x == 0) x_exp[t] = xe;
+  prefill_x_factors(t, threadIdx.x, xe, l1, wmax, pairs, F, gu, dn, gu2, dn2);
 }
 
-int launch_prefill_x(const void* x, int x_dtype, int64_t T, int H, const float* wmax, int pairs, uint16_t* x16,
-                     int32_t* x_exp, int32_t* h_exp, int32_t* h_exp2, hipStream_t s) {
+int launch_prefill_x(const void* x, int x_dtype, int64_t T, int H, const float* wmax, int pairs, int F, uint16_t* x16,
+                     float2* gu, float2* dn, float2* gu2, float2* dn2, hipStream_t s) {
   if (T <= 0) return ARTLITE_OK;
-  if (pairs < 1 || pairs > 2 || (pairs == 2 && !h_exp2)) return fail(ARTLITE_EINVAL, "prefill x: %d bounds", pairs);
+  if (pairs < 1 || pairs > 2 || (pairs == 2 && (!gu2 || !dn2))) return fail(ARTLITE_EINVAL, "prefill x: %d bounds", pairs);
   if (H % 8 == 0 && H <= 4 * 2048) {
     const bool f32 = x_dtype == ARTLITE_X_F32;
-#define ART_PX(XT, NP) k_prefill_x_rows<XT, NP><<<unsigned(T), 256, 0, s>>>(x, H, wmax, pairs, x16, x_exp, h_exp, h_exp2)
+#define ART_PX(XT, NP) k_prefill_x_rows<XT, NP><<<unsigned(T), 256, 0, s>>>(x, H, wmax, pairs, F, x16, gu, dn, gu2, dn2)
     if (H <= 2048) {
       if (f32) ART_PX(ARTLITE_X_F32, 1); else ART_PX(ARTLITE_X_BF16, 1);
     } else if (H <= 4096) {
@@ -986,7 +547,27 @@ int launch_prefill_x(const void* x, int x_dtype, int64_t T, int H, const float* 
     ART_HIP(hipGetLastError());
     return ARTLITE_OK;
   }
-  k_prefill_x<<<unsigned(T), 256, 0, s>>>(x, x_dtype, H, wmax, pairs, x16, x_exp, h_exp, h_exp2);
+  k_prefill_x<<<unsigned(T), 256, 0, s>>>(x, x_dtype, H, wmax, pairs, F, x16, gu, dn, gu2, dn2);
+  ART_HIP(hipGetLastError());
+  return ARTLITE_OK;
+}
+
+// per sorted pair row: its token and that token's row factors, so that the prefill tiles read them with plain DMAs
+__global__ void k_prefill_rows(const int32_t* __restrict__ order, int64_t P, int k, const float2* __restrict__ gu,
+                               const float2* __restrict__ dn, int32_t* __restrict__ row_a, float2* __restrict__ gu_row,
+                               float2* __restrict__ dn_row) {
+  const int64_t s = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (s >= P) return;
+  const int t = order[s] / k;
+  row_a[s] = t;
+  gu_row[s] = gu[t];
+  dn_row[s] = dn[t];
+}
+
+int launch_prefill_rows(const int32_t* order, int64_t P, int k, const float2* gu, const float2* dn, int32_t* row_a,
+                        float2* gu_row, float2* dn_row, hipStream_t s) {
+  if (P <= 0) return ARTLITE_OK;
+  k_prefill_rows<<<unsigned((P + 255) / 256), 256, 0, s>>>(order, P, k, gu, dn, row_a, gu_row, dn_row);
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
 }
@@ -1086,6 +667,66 @@ int launch_combine(const float* Y, const int32_t* slot, const float* w, int k, c
   if (H % 4) return fail(ARTLITE_EINVAL, "combine: H %d not a multiple of 4", H);
   const dim3 grid(unsigned((H / 4 + 255) / 256), unsigned(T)), block(256);
   k_combine<<<grid, block, 0, s>>>(Y, slot, w, k, ys, ws_logit, ws_sigmoid, T, H, res, res_dtype, y);
+  ART_HIP(hipGetLastError());
+  return ARTLITE_OK;
+}
+
+// The same over fp16 pair outputs, 8 columns per thread (16-byte loads): Y[s] = Y16[s] yf[s].x, the factor folded
+// into the weight (a power of two: (w f) v = w (f v) exactly), so the sum is the fp32 one over those values.
+__global__ void k_combine16(const uint16_t* __restrict__ Y16, const float2* __restrict__ yf,
+                            const int32_t* __restrict__ slot, const float* __restrict__ w, int k,
+                            const float* __restrict__ ys, const float* __restrict__ ws_logit, int ws_sigmoid, int64_t T,
+                            int H, const void* __restrict__ res, int res_dtype, float* __restrict__ y) {
+  const int64_t t = blockIdx.y;
+  const int h8 = blockIdx.x * blockDim.x + threadIdx.x;
+  if (h8 * 8 >= H) return;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (ys) {
+    float ws = 1.0f;
+    if (ws_logit) ws = ws_sigmoid ? 1.0f / (1.0f + expf(-ws_logit[t])) : ws_logit[t];
+    const float4* p = reinterpret_cast<const float4*>(ys + t * H) + 2 * h8;
+    const float4 a = p[0], b = p[1];
+    acc[0] = ws * a.x, acc[1] = ws * a.y, acc[2] = ws * a.z, acc[3] = ws * a.w;
+    acc[4] = ws * b.x, acc[5] = ws * b.y, acc[6] = ws * b.z, acc[7] = ws * b.w;
+  }
+  for (int i = 0; i < k; i++) {
+    const int64_t r = slot[t * k + i];
+    const float wi = w[t * k + i] * yf[r].x;
+    const uint4 v = reinterpret_cast<const uint4*>(Y16 + r * H)[h8];
+    const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      acc[2 * j] = __builtin_fmaf(wi, h2f(q[j] & 0xFFFFu), acc[2 * j]);
+      acc[2 * j + 1] = __builtin_fmaf(wi, h2f(q[j] >> 16), acc[2 * j + 1]);
+    }
+  }
+  if (res) {
+    float r[8];
+    if (res_dtype == ARTLITE_X_F32) {
+      const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(res) + t * H) + 2 * h8;
+      const float4 a = p[0], b = p[1];
+      r[0] = a.x, r[1] = a.y, r[2] = a.z, r[3] = a.w, r[4] = b.x, r[5] = b.y, r[6] = b.z, r[7] = b.w;
+    } else {
+      const uint4 v = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(res) + t * H)[h8];
+      const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) r[2 * j] = bf16_to_f32(q[j] & 0xFFFFu), r[2 * j + 1] = bf16_to_f32(q[j] >> 16);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[j] = acc[j] + r[j];
+  }
+  float4* o = reinterpret_cast<float4*>(y + t * H) + 2 * h8;
+  o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+}
+
+int launch_combine16(const uint16_t* Y16, const float2* yf, const int32_t* slot, const float* w, int k,
+                     const float* ys, const float* ws_logit, int ws_sigmoid, int64_t T, int H, const void* res,
+                     int res_dtype, float* y, hipStream_t s) {
+  if (T <= 0) return ARTLITE_OK;
+  if (H % 8) return fail(ARTLITE_EINVAL, "combine: H %d not a multiple of 8", H);
+  const dim3 grid(unsigned((H / 8 + 255) / 256), unsigned(T)), block(256);
+  k_combine16<<<grid, block, 0, s>>>(Y16, yf, slot, w, k, ys, ws_logit, ws_sigmoid, T, H, res, res_dtype, y);
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
 }

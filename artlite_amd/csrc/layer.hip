@@ -25,8 +25,10 @@ struct artlite_moe_layer {
   int64_t staged = -1;  // tokens staged, -1: none
   DevBuf x, xhi, xlo;
   DevBuf xn;  // the RMS-normalised x (norm_eps > 0)
-  DevBuf x16, xexp, hexp, shexp;  // the prefill's fp16 activations and their per-token scale exponents
-  DevBuf wmax;                    // max |w| of gate, up, shared gate, shared up (the bound on |h|)
+  DevBuf x16;                     // the prefill's fp16 activations (each token's row scaled by a power of two)
+  DevBuf gu_tok, dn_tok, sgu_tok, sdn_tok;  // per token, the row factors of the prefill's products (float2)
+  DevBuf row_a, gu_row, dn_row;   // per sorted pair row: its token and its factors
+  DevBuf wmax;                    // max |w| of gate, up, shared gate, shared up (the bounds on |h|), down
   DevBuf logits, ids, w, sg;
   DevBuf table, ctrl, counts, offsets, order, slot, tiles;
   DevBuf hhi, hlo, ypairs, shhi, shlo, ys, y;
@@ -106,7 +108,7 @@ int check_ready(const artlite_moe_layer* L) {
 
 // The kernels a forward pass of T tokens takes. Decode-sized passes (at most GEMV_BM pairs per expert on
 // average) run the experts on the VALU GEMV over XQ activations; prefill-sized ones (16 pairs per expert on
-// average, enough to fill PREFILL_BM tiles) on the fp16 MFMA prefill tiles; those between on the MFMA decode tiles
+// average) on the fp16 MFMA prefill tiles; those between on the MFMA decode tiles
 // over bf16 planes. A decode-sized pass whose down format the GEMV does not take (a Q6_K down after Q4_K gate / up,
 // as mixed GGUF quantisations store them) runs gate / up on the GEMV and the down on the decode tiles, h turned from
 // XQ into bf16 planes between them.
@@ -127,7 +129,7 @@ Path path_of(const artlite_moe_layer* L, int64_t T) {
   p.gemv = p.gemv_gu && L->gemv_ok;
   p.shared_gemv = L->d.shared_ffn && p.gemv_gu && L->shared_gemv_ok;
   p.prefill = !p.gemv_gu && L->prefill_ok && T * L->d.top_k >= int64_t(16) * L->d.n_experts;
-  p.shared_prefill = L->d.shared_ffn && p.prefill && L->shared_prefill_ok && T >= PREFILL_BM / 2;
+  p.shared_prefill = L->d.shared_ffn && p.prefill && L->shared_prefill_ok && T >= 64;
   const bool planes = (!p.gemv_gu && !p.prefill) || (L->d.shared_ffn && !p.shared_gemv && !p.shared_prefill);
   p.split = planes && (L->x_dtype == ARTLITE_X_F32 || L->d.norm_eps > 0);  // (the normalised x is fp32)
   p.quant = p.gemv_gu;
@@ -151,6 +153,7 @@ std::vector<std::string> kernel_list(const artlite_moe_layer* L, int64_t T) {
     k.push_back("dispatch_count");
     k.push_back("dispatch_scatter");
   }
+  if (p.prefill) k.push_back("prefill_rows");
   k.push_back("gate_up");
   if (p.gemv_gu && !p.gemv) k.push_back("h_planes");
   k.push_back("down");
@@ -187,9 +190,9 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
   const uint16_t *ahi = static_cast<const uint16_t*>(xin), *alo = nullptr;
   if (path.prefill) {
     ART_TRY(mark());
-    ART_TRY(launch_prefill_x(xin, xdt, T, H, L->wmax.as<float>(), path.shared_prefill ? 2 : 1,
-                             L->x16.as<uint16_t>(), L->xexp.as<int32_t>(), L->hexp.as<int32_t>(),
-                             L->shexp.as<int32_t>(), s));
+    ART_TRY(launch_prefill_x(xin, xdt, T, H, L->wmax.as<float>(), path.shared_prefill ? 2 : 1, F,
+                             L->x16.as<uint16_t>(), L->gu_tok.as<float2>(), L->dn_tok.as<float2>(),
+                             L->sgu_tok.as<float2>(), L->sdn_tok.as<float2>(), s));
   }
   if (path.split) {
     ART_TRY(mark());
@@ -207,7 +210,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
   const int BM = path.gemv_gu ? GEMV_BM : path.prefill ? PREFILL_BM : DECODE_BM;
   DispatchBufs db{L->ids.as<int32_t>(), P, E, k, L->table.as<int32_t>(), L->ctrl.as<int32_t>(),
                   L->counts.as<int32_t>(), L->offsets.as<int32_t>(), L->order.as<int32_t>(), L->slot.as<int32_t>(),
-                  L->tiles.as<int32_t>(), BM, nullptr, 0};
+                  L->tiles.as<int32_t>(), BM, nullptr, 0, path.prefill ? 1 : 0};
   if (path.small) {
     ART_TRY(mark());
     ART_TRY(launch_route_small(L->logits.as<float>(), T, E, k, d.gating, L->ids.as<int32_t>(), L->w.as<float>(), db,
@@ -221,6 +224,11 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     ART_TRY(launch_dispatch_count(db, nb, s));
     ART_TRY(mark());
     ART_TRY(launch_dispatch_scatter(db, nb, s));
+  }
+  if (path.prefill) {
+    ART_TRY(mark());
+    ART_TRY(launch_prefill_rows(L->order.as<int32_t>(), P, k, L->gu_tok.as<float2>(), L->dn_tok.as<float2>(),
+                                L->row_a.as<int32_t>(), L->gu_row.as<float2>(), L->dn_row.as<float2>(), s));
   }
   if (path.gemv_gu) {
     GemvArgs g{};
@@ -292,15 +300,12 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     g.K = H;
     g.qtype = d.gate_type;
     g.a = L->x16.as<uint16_t>();
-    g.a_gather = 1;
-    g.order = L->order.as<int32_t>();
-    g.topk = k;
+    g.row_a = L->row_a.as<int32_t>();
+    g.row_scale = L->gu_row.as<float2>();
     g.tiles = L->tiles.as<int32_t>();
     g.n_tiles = L->ctrl.as<int32_t>() + CTRL_TILES;
     g.offsets = L->offsets.as<int32_t>();
     g.max_tiles = tile_bound(P, E, BM);
-    g.in_exp = L->xexp.as<int32_t>();
-    g.out_exp = L->hexp.as<int32_t>();
     g.h = L->h16.as<uint16_t>();
     ART_TRY(mark());
     ART_TRY(launch_prefill(g, s));
@@ -313,11 +318,10 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     dn.K = F;
     dn.qtype = d.down_type;
     dn.a = L->h16.as<uint16_t>();
-    dn.a_gather = 0;
-    dn.in_exp = L->hexp.as<int32_t>();
-    dn.out_exp = nullptr;
+    dn.row_a = nullptr;
+    dn.row_scale = L->dn_row.as<float2>();
     dn.h = nullptr;
-    dn.y = L->ypairs.as<float>();
+    dn.y16 = L->ypairs.as<uint16_t>();  // (fp16 pair outputs, their rows' true values dn_row[s].x times these)
     ART_TRY(mark());
     ART_TRY(launch_prefill(dn, s));
   } else {
@@ -395,8 +399,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     sg.qtype = d.shared_type;
     sg.a = L->x16.as<uint16_t>();
     sg.dense_rows = int(T);
-    sg.in_exp = L->xexp.as<int32_t>();
-    sg.out_exp = L->shexp.as<int32_t>();
+    sg.row_scale = L->sgu_tok.as<float2>();
     sg.h = L->sh16.as<uint16_t>();
     ART_TRY(mark());
     ART_TRY(launch_prefill(sg, s));
@@ -408,8 +411,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     sd.K = d.shared_ffn;
     sd.qtype = L->sdq->id;
     sd.a = L->sh16.as<uint16_t>();
-    sd.in_exp = L->shexp.as<int32_t>();
-    sd.out_exp = nullptr;
+    sd.row_scale = L->sdn_tok.as<float2>();
     sd.h = nullptr;
     sd.y = L->ys.as<float>();
     ART_TRY(mark());
@@ -446,9 +448,14 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     ys = L->ys.as<float>();
   }
   ART_TRY(mark());
-  ART_TRY(launch_combine(L->ypairs.as<float>(), L->slot.as<int32_t>(), L->w.as<float>(), k, ys,
-                         d.shared_gated ? L->sg.as<float>() : nullptr, 1, T, H, d.residual ? L->x.p : nullptr,
-                         L->x_dtype, L->y.as<float>(), s));
+  if (path.prefill)
+    ART_TRY(launch_combine16(L->ypairs.as<uint16_t>(), L->dn_row.as<float2>(), L->slot.as<int32_t>(), L->w.as<float>(),
+                             k, ys, d.shared_gated ? L->sg.as<float>() : nullptr, 1, T, H,
+                             d.residual ? L->x.p : nullptr, L->x_dtype, L->y.as<float>(), s));
+  else
+    ART_TRY(launch_combine(L->ypairs.as<float>(), L->slot.as<int32_t>(), L->w.as<float>(), k, ys,
+                           d.shared_gated ? L->sg.as<float>() : nullptr, 1, T, H, d.residual ? L->x.p : nullptr,
+                           L->x_dtype, L->y.as<float>(), s));
   ART_TRY(mark());
   L->last_T = T;
   L->last_gemv = path.gemv_gu;
@@ -543,14 +550,18 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
   res(L->hlo, size_t(P * F) * 2);
   res(L->ypairs, size_t(P * H) * 4);
   res(L->y, size_t(T * H) * 4);
-  res(L->wmax, 4 * 4);
+  res(L->wmax, 5 * 4);
   if (L->prefill_ok) {
     res(L->x16, size_t(T * H) * 2);
-    res(L->xexp, size_t(T) * 4);
-    res(L->hexp, size_t(T) * 4);
+    res(L->gu_tok, size_t(T) * 8);
+    res(L->dn_tok, size_t(T) * 8);
+    res(L->row_a, size_t(P) * 4);
+    res(L->gu_row, size_t(P) * 8);
+    res(L->dn_row, size_t(P) * 8);
     res(L->h16, size_t(P * F) * 2);
     if (L->shared_prefill_ok) {
-      res(L->shexp, size_t(T) * 4);
+      res(L->sgu_tok, size_t(T) * 8);
+      res(L->sdn_tok, size_t(T) * 8);
       res(L->sh16, size_t(T) * d.shared_ffn * 2);
     }
   }
@@ -611,12 +622,12 @@ extern "C" int artlite_moe_layer_upload(artlite_moe_layer* L, int t, const void*
   ART_TRY(b->reserve(dev + WEIGHT_TAIL));
   ART_HIP(hipMemcpyAsync(b->p, src, dev, hipMemcpyHostToDevice, L->stream));
   ART_HIP(hipMemsetAsync(static_cast<uint8_t*>(b->p) + dev, 0, WEIGHT_TAIL, L->stream));  // (the loaders' tail)
-  // the prefill's bound on |h| takes max |w| of the gate and up matrices
+  // the prefill's bounds on |h| take max |w| of the gate and up matrices, the one on the down's sums that of down
   const int wm = t == ARTLITE_GATE_EXPS ? 0 : t == ARTLITE_UP_EXPS ? 1 : t == ARTLITE_GATE_SHEXP ? 2
-               : t == ARTLITE_UP_SHEXP ? 3 : -1;
-  const bool pre = wm < 2 ? L->prefill_ok : L->shared_prefill_ok;
+               : t == ARTLITE_UP_SHEXP ? 3 : t == ARTLITE_DOWN_EXPS ? 4 : -1;
+  const bool pre = wm < 2 || wm == 4 ? L->prefill_ok : L->shared_prefill_ok;
   if (wm >= 0 && pre) {
-    const QType* q = wm < 2 ? L->gq : L->sq;
+    const QType* q = wm < 2 ? L->gq : wm == 4 ? L->dq : L->sq;
     ART_TRY(launch_weight_max(static_cast<const uint8_t*>(b->p), q->id, int64_t(want / q->bytes),
                               L->wmax.as<float>() + wm, L->stream));
   }
@@ -691,7 +702,24 @@ extern "C" int artlite_moe_layer_tap(artlite_moe_layer* L, int tap, void* out, s
     case ARTLITE_TAP_OFFSETS: src = L->offsets.p, bytes = size_t(E + 1) * 4; break;
     case ARTLITE_TAP_ORDER: src = L->order.p, bytes = size_t(P) * 4; break;
     case ARTLITE_TAP_SLOT: src = L->slot.p, bytes = size_t(P) * 4; break;
-    case ARTLITE_TAP_Y: src = L->ypairs.p, bytes = size_t(P) * L->d.hidden * 4; break;
+    case ARTLITE_TAP_Y:
+      if (L->last_prefill) {  // (fp16 pair outputs: row s's true values are dn_row[s].x times them)
+        const int H = L->d.hidden;
+        const size_t n = size_t(P) * H;
+        if (nbytes < n * 4) return fail(ARTLITE_EINVAL, "moe layer tap: %zu bytes, need %zu", nbytes, n * 4);
+        ART_HIP(hipStreamSynchronize(L->stream));
+        std::vector<uint16_t> y(n);
+        std::vector<float2> dn(static_cast<size_t>(P));
+        if (n) ART_HIP(hipMemcpy(y.data(), L->ypairs.p, n * 2, hipMemcpyDeviceToHost));
+        if (P) ART_HIP(hipMemcpy(dn.data(), L->dn_row.p, size_t(P) * 8, hipMemcpyDeviceToHost));
+        float* o = static_cast<float*>(out);
+        for (int64_t r = 0; r < P; r++)
+          for (int c = 0; c < H; c++)
+            o[size_t(r) * H + c] = float(__builtin_bit_cast(_Float16, y[size_t(r) * H + c])) * dn[size_t(r)].x;
+        return ARTLITE_OK;
+      }
+      src = L->ypairs.p, bytes = size_t(P) * L->d.hidden * 4;
+      break;
     case ARTLITE_TAP_XN:
       if (!(L->d.norm_eps > 0)) return fail(ARTLITE_EINVAL, "moe layer tap: no norm in this layer");
       src = L->xn.p, bytes = size_t(T) * L->d.hidden * 4;
@@ -713,16 +741,15 @@ extern "C" int artlite_moe_layer_tap(artlite_moe_layer* L, int tap, void* out, s
         return ARTLITE_OK;
       }
       if (L->last_prefill) {
-        // fp16 h, scaled by 2^-hexp[token]: token(s) = order[s] / k
+        // fp16 h, its row scaled by 2^-he: the down launch's factors dn_row[s] multiply to 2^he
         const int F = L->d.expert_ffn;
         std::vector<uint16_t> h(n);
-        std::vector<int32_t> order(static_cast<size_t>(P)), he(static_cast<size_t>(T));
+        std::vector<float2> dn(static_cast<size_t>(P));
         ART_HIP(hipMemcpy(h.data(), L->h16.p, n * 2, hipMemcpyDeviceToHost));
-        ART_HIP(hipMemcpy(order.data(), L->order.p, size_t(P) * 4, hipMemcpyDeviceToHost));
-        ART_HIP(hipMemcpy(he.data(), L->hexp.p, size_t(T) * 4, hipMemcpyDeviceToHost));
+        ART_HIP(hipMemcpy(dn.data(), L->dn_row.p, size_t(P) * 8, hipMemcpyDeviceToHost));
         for (int64_t r = 0; r < P; r++)
           for (int c = 0; c < F; c++)
-            o[r * F + c] = std::ldexp(float(__builtin_bit_cast(_Float16, h[size_t(r) * F + c])), he[order[r] / L->d.top_k]);
+            o[r * F + c] = float(__builtin_bit_cast(_Float16, h[size_t(r) * F + c])) * (dn[size_t(r)].x * dn[size_t(r)].y);
         return ARTLITE_OK;
       }
       std::vector<uint16_t> hi(n), lo(n);

@@ -1,0 +1,582 @@
+// The prefill tiles: the experts' grouped GEMMs at prefill sizes (tens to hundreds of rows per expert) over raw GGUF
+// Q4_0 / Q8_0 blocks, on gfx950's fp16 MFMA (v_mfma_f32_16x16x32_f16).
+//
+// Numerics. A is fp16 rows, each token's row scaled by a power of two (2^-in_exp[token]) so that its largest |x| sits
+// in [2^14, 2^15): bf16 activations convert exactly, fp32 ones round once (2^-11). Each lane decodes its 8 codes of a
+// block to fp16 d (q - 8) (Q4_0) or d q (Q8_0): the code exactly, the product with the block's fp16 scale rounded
+// once (2^-11 relative); the MFMA accumulates all of K in fp32, so no per-group scale work is left. The SwiGLU launch
+// writes h = silu(g) u in fp16 scaled by 2^-out_exp[token] (out_exp bounds |h| below 2^15); the plain launch writes
+// fp32, the A scale undone.
+//
+// Shape of the work. An expert's sorted rows are cut into tiles of at most 256 rows of nearly equal size
+// (balanced_rows: 270 rows are two tiles of 144 and 126, not 256 and 14). An item is one tile times 256 staged
+// weight rows (SwiGLU: 128 rows of gate and the same 128 of up; plain: 256 rows). A workgroup is 4 waves, one per
+// SIMD, each with the full 512 registers: wave w takes all of the tile's rows (up to 16 MFMA row blocks) times 64
+// weight rows (4 column blocks: SwiGLU gate rows 32 w .. + 32 and the same up rows, so h forms in the wave; plain
+// rows 64 w .. + 64), 256 fp32 accumulators per lane. Per 32-value group a wave reads 16 A operands from LDS (1 KB
+// per 64 MFMA flops... 256 B of LDS per 16-cycle MFMA: half the LDS bandwidth at full MFMA rate) and decodes 4 B
+// operands (about 13 VALU each, reused by 16 row blocks: under one VALU per MFMA, the budget that matters, since on
+// gfx950 every VALU instruction delays the MFMA stream by about 2.5 cycles).
+//
+// Data movement. K streams in stages of 64 values (two groups) through a ring of R = 3 LDS slots filled by DMA
+// (global_load_lds, issued by asm from uniform bases with 32-bit lane offsets, so that the compiler, which would wait
+// for every DMA in flight before any LDS read it sees, does not know of them). Every wave issues the same loads per
+// stage, so each wait is a fixed count of this wave's loads: at step st, stage st must have landed and stage st + 1
+// may still be in flight; after the barrier (every wave past its reads of the previous slot) stage st + 2 is issued
+// into that slot, two steps ahead. The issue side runs on across items (the next item's first stages load while the
+// current one finishes and writes its epilogue) and, past the last item, reloads a stage of it (dummies keep the
+// counts fixed).
+// A rows sit in LDS as 16-byte chunks of 8 values, XOR-swizzled by row (16 rows of an operand read in different
+// banks); a weight row's stage bytes (two blocks, 36 / 68 B) sit packed, read as aligned dwords (the first block's
+// codes start 2 bytes into it: shifted into place with alignbit).
+// MFMA layout (16x16x32): lane l holds A row l % 16 and B column l % 16, both with K values 8 (l / 16) .. + 8;
+// C column l % 16, rows 4 (l / 16) .. + 4. The decoded weights are the A operand and the activations B, so C is the
+// output transposed: a lane holds one tile row's 4 consecutive output columns, stored as one 8 / 16 B write.
+#include "experts.h"
+#include "route.h"
+
+namespace artlite {
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int TILE_ROWS = 256;  // A rows of a tile, at most
+
+template <int QT>
+struct PG {
+  static constexpr int GB = QT == ARTLITE_Q4_0 ? 18 : 34;  // bytes of a 32-value block
+  static constexpr int WN = 256;                          // weight rows staged per item
+  static constexpr int WROW = 2 * GB;                     // stage bytes of a staged weight row (two blocks)
+  static constexpr int WDW = WROW / 4;                    // its dwords (9 / 17)
+  static constexpr int THREADS = 512;                     // 8 waves, two per SIMD
+  static constexpr int ABYTES = TILE_ROWS * 128;          // a stage of A: 64 fp16 per row
+  static constexpr int AI = ABYTES / 16 / THREADS;        // A DMAs (16 B) per lane per stage
+  static constexpr int BI = (WN * WDW + THREADS - 1) / THREADS;  // weight DMAs (4 B) per lane per stage
+  static constexpr int WBYTES = BI * THREADS * 4;         // (the last dwords: padding the dummies fill)
+  static constexpr int SBYTES = ABYTES + WBYTES;
+  static constexpr int MI = 2;           // item metadata DMAs (4 B) per lane per stage
+  static constexpr int META = MI * THREADS * 4;  // an item's metadata: 256 row tokens (int), 256 row factors (float2),
+                                                 // padding
+  static constexpr int LOADS = AI + BI + MI;
+  static constexpr int R = 3;
+  static constexpr int MAXQ = 128;  // items of a workgroup the item table holds
+  static constexpr int LDS = R * SBYTES + 2 * META + MAXQ * 16;
+  static_assert(AI * 16 * THREADS == ABYTES, "whole A DMAs");
+  static_assert(META >= 3 * 1024, "metadata");
+  static_assert(128 * WDW % 64 == 0, "a wave's weight DMA reads one matrix (gate or up)");
+  static_assert(LDS <= LDS_BYTES, "LDS");
+  static_assert((R - 1) * LOADS < 64, "vmcnt");
+};
+
+template <int N>
+__device__ __forceinline__ void pg_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory");
+}
+
+// every wave's LDS reads done, then the workgroup barrier
+__device__ __forceinline__ void pg_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+__device__ __forceinline__ uint32_t pg_lds_addr(const void* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
+
+// One DMA of SIZE bytes per lane from base (uniform) + off (the lane's 32-bit byte offset) into LDS at lds (uniform) +
+// SIZE lane. M0 carries the LDS address; no compiler-generated code in this kernel uses M0 (the asm sets it before
+// each load, with the one wait state a load after an M0 write needs).
+template <int SIZE>
+__device__ __forceinline__ void pg_dma(const void* base, uint32_t off, uint32_t lds) {
+  if constexpr (SIZE == 16)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                 0);
+}
+
+// Decode of a lane's 8 weights to fp16: the code bytes spread into fp16 1024 + c (c < 256 exact, one perm per two),
+// the offset taken off exactly by one packed FMA (Q4_0's high nibbles, kept in place as 16 q, are scaled by 1/16 in
+// it), then the product with the block's scale, rounded once.
+template <int QT>
+struct PGDecode {
+  uint32_t msk;
+  f16x2 mul, add;
+  __device__ __forceinline__ explicit PGDecode(int lg) {
+    if constexpr (QT == ARTLITE_Q4_0) {
+      const bool hi = lg >= 2;  // (lane groups 2, 3 hold K values 16 .. 31 of a block: the high nibbles)
+      msk = hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+      mul = hi ? f16x2{_Float16(0.0625f), _Float16(0.0625f)} : f16x2{_Float16(1.0f), _Float16(1.0f)};
+      add = hi ? f16x2{_Float16(-72.0f), _Float16(-72.0f)} : f16x2{_Float16(-1032.0f), _Float16(-1032.0f)};
+    } else {
+      msk = 0x80808080u;  // (Q8_0: the sign bits flipped, c = q + 128)
+      mul = f16x2{_Float16(1.0f), _Float16(1.0f)};
+      add = f16x2{_Float16(-1152.0f), _Float16(-1152.0f)};
+    }
+  }
+  __device__ __forceinline__ u32x4 operator()(uint32_t c0, uint32_t c1, uint32_t sc) const {
+    const uint32_t v0 = QT == ARTLITE_Q4_0 ? c0 & msk : c0 ^ msk;
+    const uint32_t v1 = QT == ARTLITE_Q4_0 ? c1 & msk : c1 ^ msk;
+    const uint32_t w[4] = {__builtin_amdgcn_perm(0x64646464u, v0, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, v0, 0x04030402u),
+                           __builtin_amdgcn_perm(0x64646464u, v1, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, v1, 0x04030402u)};
+    const f16x2 d = __builtin_bit_cast(f16x2, sc | (sc << 16));
+    u32x4 b;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const f16x2 c = __builtin_bit_cast(f16x2, w[j]) * mul + add;  // (exact: the code less its offset)
+      b[j] = __builtin_bit_cast(uint32_t, c * d);
+    }
+    return b;
+  }
+};
+
+// An item: expert e, its sorted rows s0 .. s0 + m_valid, output columns n0 .. (SwiGLU: + 128 of gate and up; plain:
+// + 256)
+struct PGItem {
+  int e, s0, m_valid, n0;
+};
+
+// item w of a launch (tile w / nbk, column block w % nbk); global loads: read once per workgroup, at its start
+template <bool SWIGLU>
+__device__ __forceinline__ PGItem pg_item(const PrefillArgs& a, int64_t w, int nbk) {
+  constexpr int WN = SWIGLU ? 128 : 256;
+  const int tl = int(w / nbk);
+  PGItem I;
+  I.n0 = int(w % nbk) * WN;
+  if (a.tiles) {
+    I.e = a.tiles[2 * tl];
+    I.s0 = a.tiles[2 * tl + 1];
+    const int lo = a.offsets[I.e], hi = a.offsets[I.e + 1];
+    I.m_valid = min(balanced_rows(hi - lo, TILE_ROWS), hi - I.s0);
+  } else {
+    const int rows = balanced_rows(a.dense_rows, TILE_ROWS);
+    I.e = 0;
+    I.s0 = tl * rows;
+    I.m_valid = min(rows, a.dense_rows - I.s0);
+  }
+  return I;
+}
+
+// The lane's DMA sources of an item at stage 0. A: instruction i of wave w writes chunks (4 i + w) 64 + lane of a
+// stage's A region; chunk p holds row r = p / 8, physical chunk c = p % 8, which is logical chunk c ^ swz(r) (K values
+// 8 c .. + 8 of the stage); rows past the tile's valid ones repeat its last (their outputs are not stored); a row's A
+// row comes from the item's metadata in LDS (tok). Weights: instruction j of wave w writes dwords (4 j + w) 64 + lane
+// of the stage's weight region: staged row q / WDW (SwiGLU: gate rows n0 .. + 128, then the same rows of up; plain:
+// rows n0 .. + 256), dword q % WDW of the row's stage bytes; rows past N load the last row. Offsets in bytes (A: from
+// a.a; weights: from the instruction's matrix).
+template <int QT, bool SWIGLU>
+struct PGSrc {
+  using L = PG<QT>;
+  uint32_t a[L::AI];
+  uint32_t w[L::BI];
+  __device__ __forceinline__ static int swz(int r) { return (r >> 1) & 7; }
+  __device__ __forceinline__ void set(const PrefillArgs& g, const PGItem& I, const int32_t* tok, int tid) {
+#pragma unroll
+    for (int i = 0; i < L::AI; i++) {
+      const int p = i * L::THREADS + tid, r = p >> 3, c = (p & 7) ^ swz(r);
+      const int row = min(r, I.m_valid - 1);
+      const int ar = g.row_a ? tok[row] : I.s0 + row;
+      a[i] = (uint32_t(ar) * uint32_t(g.K) + 8 * c) * 2;
+    }
+#pragma unroll
+    for (int j = 0; j < L::BI; j++) {  // (dwords past the staged rows: padding, loading the last dword again)
+      const int q = min(j * L::THREADS + tid, L::WN * L::WDW - 1), row = q / L::WDW, dw = q % L::WDW;
+      const int n = min(I.n0 + (SWIGLU ? row % 128 : row), g.N - 1);
+      w[j] = uint32_t(I.e) * uint32_t(g.expert_bytes) + uint32_t(n) * uint32_t(g.row_bytes) + 4 * dw;
+    }
+  }
+};
+
+// The lane's metadata DMA sources of an item: dword u = j 512 + tid of the item's metadata (u < 256: the A row of
+// tile row u, from row_a (without it, from row_scale: unread); u < 768: the row factors, float2 per row, as dwords,
+// from row_scale; past that, padding: a reload of row 0's first dword), tile rows past the valid ones repeating the
+// last. Offsets in bytes.
+struct PGMeta {
+  uint32_t m[2];
+  __device__ __forceinline__ void set(const PrefillArgs& g, const PGItem& I, int tid) {
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int u = j * 512 + tid;
+      if (u < 256) {
+        m[j] = uint32_t(I.s0 + min(u, I.m_valid - 1)) * 4;
+      } else if (u < 768) {
+        const int row = (u - 256) >> 1;
+        m[j] = (uint32_t(I.s0 + min(row, I.m_valid - 1)) * 2 + (u & 1)) * 4;
+      } else {
+        m[j] = uint32_t(I.s0) * 4;
+      }
+    }
+  }
+};
+
+// the issue side: the item whose stages are being issued, its next stage, the ring slot they go to
+template <int QT, bool SWIGLU>
+struct PGIssue {
+  PGSrc<QT, SWIGLU> src;
+  int st;    // its next stage
+  int q;     // its index among this workgroup's items (nq: past the last, dummies)
+  int slot;  // the ring slot of the next issue
+};
+
+// The codes of one block of the lane's weight row (row: its stage bytes in LDS): block g (0, 1) of the stage; cb the
+// lane group's code byte offset (Q4_0: 8 (lg & 1), both nibbles of those 8 bytes; Q8_0: 8 lg).
+template <int QT>
+__device__ __forceinline__ void pg_codes(const uint8_t* row, int g, int cb, uint32_t& sc, uint32_t& c0, uint32_t& c1) {
+  constexpr int GB = PG<QT>::GB;
+  if (g == 0) {  // codes at + 2 + cb: two bytes past a dword boundary
+    const uint32_t* d = reinterpret_cast<const uint32_t*>(row + cb);
+    const uint32_t d0 = d[0], d1 = d[1], d2 = d[2];
+    c0 = __builtin_amdgcn_alignbit(d1, d0, 16);
+    c1 = __builtin_amdgcn_alignbit(d2, d1, 16);
+    sc = *reinterpret_cast<const uint16_t*>(row);
+  } else {  // codes at GB + 2 + cb: dword-aligned (GB + 2 is 20 or 36)
+    const uint32_t* d = reinterpret_cast<const uint32_t*>(row + GB + 2 + cb);
+    c0 = d[0];
+    c1 = d[1];
+    sc = *reinterpret_cast<const uint16_t*>(row + GB);
+  }
+}
+
+// The DMA sources of one issue (one stage of the issue item plus the metadata of the item after the compute item):
+// uniform base pointers (at that stage) and destination slots; the lanes' offsets are in PGSrc and PGMeta.
+struct PGBases {
+  const uint8_t *ab, *wb0, *wb1, *mt, *ms;
+  uint32_t dst, mdst;
+};
+
+// One DMA of an issue: n < AI an A chunk, then the weights' dwords, then the metadata's (instruction i of wave w
+// writes the region's bytes (8 i + w) 64 + lane times the DMA's size).
+template <int QT, bool SWIGLU>
+__device__ __forceinline__ void pg_dma_n(int n, const PGBases& b, const PGSrc<QT, SWIGLU>& src, const PGMeta& meta,
+                                         int wv) {
+  using L = PG<QT>;
+  if (n < L::AI) {
+    pg_dma<16>(b.ab, src.a[n], b.dst + (8 * n + wv) * 1024);
+  } else if (n < L::AI + L::BI) {
+    const int j = n - L::AI;
+    pg_dma<4>(SWIGLU && (j * L::THREADS + 64 * wv) >= 128 * L::WDW ? b.wb1 : b.wb0, src.w[j],
+              b.dst + L::ABYTES + (8 * j + wv) * 256);
+  } else {
+    const int j = n - L::AI - L::BI;
+    pg_dma<4>(j == 0 && wv < 4 ? b.mt : b.ms, meta.m[j], b.mdst + (8 * j + wv) * 256);
+  }
+}
+
+// One step: stage st's products (two groups) -- MBN row blocks of the tile times the wave's 2 column blocks -- with
+// one issue's DMAs spread among them. The work is laid out as IT = 2 MBN iterations (group 0's row blocks, then group
+// 1's), pinned in order by scheduling barriers; an iteration issues its row block's 2 MFMAs, reads the A operand of the
+// iteration PF ahead and issues its share of the DMAs, and the first two decode a column block of group 1's weights.
+// aof: the lane's A chunk offset in a slot for group 0 (aof1: group 1); bof: its weight row's offset per column block.
+template <int QT, bool SWIGLU, int MBN>
+__device__ __forceinline__ void pg_step(const uint8_t* slot, uint32_t aof0, uint32_t aof1, const uint32_t (&bof)[2],
+                                        int cb, const PGDecode<QT>& dec, f32x4 (&acc)[MBN][2],
+                                        const PGSrc<QT, SWIGLU>& src, const PGMeta& meta, const PGBases& b, int wv) {
+  using L = PG<QT>;
+  constexpr int IT = 2 * MBN, PF = MBN < 4 ? MBN : 4;
+  auto a_addr = [&](int it) { return slot + (it < MBN ? aof0 : aof1) + (it % MBN) * 2048; };
+  uint32_t sc0[2], c00[2], c01[2], sc1[2], c10[2], c11[2];
+#pragma unroll
+  for (int nb = 0; nb < 2; nb++) pg_codes<QT>(slot + bof[nb], 0, cb, sc0[nb], c00[nb], c01[nb]);
+  u32x4 av[PF + 1];
+#pragma unroll
+  for (int it = 0; it < PF; it++) av[it] = *reinterpret_cast<const u32x4*>(a_addr(it));
+#pragma unroll
+  for (int nb = 0; nb < 2; nb++) pg_codes<QT>(slot + bof[nb], 1, cb, sc1[nb], c10[nb], c11[nb]);
+  u32x4 b0[2], b1[2];
+#pragma unroll
+  for (int nb = 0; nb < 2; nb++) b0[nb] = dec(c00[nb], c01[nb], sc0[nb]);
+#pragma unroll
+  for (int it = 0; it < IT; it++) {
+    if (it + PF < IT) av[(it + PF) % (PF + 1)] = *reinterpret_cast<const u32x4*>(a_addr(it + PF));
+    const u32x4 x = av[it % (PF + 1)];
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) {
+      if (it < MBN)
+        acc[it][nb] = mfma16(b0[nb], x, acc[it][nb]);
+      else
+        acc[it - MBN][nb] = mfma16(b1[nb], x, acc[it - MBN][nb]);
+    }
+    if (it < 2) b1[it] = dec(c10[it], c11[it], sc1[it]);  // (group 1's weights, a column block per iteration)
+#pragma unroll
+    for (int n = it * L::LOADS / IT; n < (it + 1) * L::LOADS / IT; n++) pg_dma_n<QT, SWIGLU>(n, b, src, meta, wv);
+    __builtin_amdgcn_sched_barrier(0);  // (nothing moves from one iteration to another)
+  }
+}
+
+// silu(g) u with the hardware's exp2 and reciprocal (each within an ulp or two of fp32; the fp16 rounding of h,
+// 2^-11, dominates)
+__device__ __forceinline__ float pg_swiglu(float g, float u) {
+  const float e = __builtin_amdgcn_exp2f(-1.4426950408889634f * g);
+  return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
+}
+
+// The workgroup's state shared by its items.
+struct PGCtx {
+  uint8_t* lds;
+  uint32_t lbase;
+  int tid, wv, lane, lg, lr;
+  int stages, nq;
+  const int4* table;  // (in LDS) the items: (e, s0, m_valid, n0)
+};
+
+template <int QT>
+__device__ __forceinline__ const int32_t* pg_tok(const PGCtx& c, int q) {
+  return reinterpret_cast<const int32_t*>(c.lds + PG<QT>::R * PG<QT>::SBYTES + (q & 1) * PG<QT>::META);
+}
+
+template <int QT>
+__device__ __forceinline__ const float2* pg_rowf(const PGCtx& c, int q) {  // (after the 256 row tokens)
+  return reinterpret_cast<const float2*>(c.lds + PG<QT>::R * PG<QT>::SBYTES + (q & 1) * PG<QT>::META + 1024);
+}
+
+__device__ __forceinline__ PGItem pg_table(const PGCtx& c, int q) {
+  const int4 v = c.table[q];
+  return PGItem{__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
+                __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w)};
+}
+
+// The bases of the next issue: the issue item's next stage (past the last item, a reload of stage 0: dummies keep the
+// counts fixed), and the metadata DMAs of item mq into its buffer.
+template <int QT, bool SWIGLU>
+__device__ __forceinline__ PGBases pg_bases(const PrefillArgs& a, const PGCtx& c, const PGIssue<QT, SWIGLU>& is,
+                                            int mq) {
+  using L = PG<QT>;
+  const int st = __builtin_amdgcn_readfirstlane(is.q < c.nq ? is.st : 0);
+  PGBases b;
+  b.ab = static_cast<const uint8_t*>(static_cast<const void*>(a.a)) + 128 * st;
+  b.wb0 = a.w[0] + st * L::WROW;
+  b.wb1 = (SWIGLU ? a.w[1] : a.w[0]) + st * L::WROW;
+  b.ms = reinterpret_cast<const uint8_t*>(a.row_scale);
+  b.mt = a.row_a ? reinterpret_cast<const uint8_t*>(a.row_a) : b.ms;
+  b.dst = __builtin_amdgcn_readfirstlane(c.lbase + is.slot * L::SBYTES);
+  b.mdst = __builtin_amdgcn_readfirstlane(c.lbase + L::R * L::SBYTES + (mq & 1) * L::META);
+  return b;
+}
+
+// The issue side moves on: the next slot; past an item's last stage, the next item (its sources from its metadata,
+// which the DMAs of the compute item's first steps brought into LDS).
+template <int QT, bool SWIGLU>
+__device__ __forceinline__ void pg_advance(const PrefillArgs& a, const PGCtx& c, PGIssue<QT, SWIGLU>& is) {
+  using L = PG<QT>;
+  is.slot = is.slot + 1 == L::R ? 0 : is.slot + 1;
+  if (is.q < c.nq && ++is.st == c.stages) {
+    is.st = 0;
+    if (++is.q < c.nq) is.src.set(a, pg_table(c, is.q), pg_tok<QT>(c, is.q), c.tid);
+  }
+}
+
+// One item: its K loop (stage by stage through the ring) and its epilogue. cslot: the slot of its stage 0; meta / mq:
+// the metadata DMAs every step issues (of item mq).
+template <int QT, bool SWIGLU, int MBN>
+__device__ __forceinline__ int pg_run(const PrefillArgs& a, const PGCtx& c, PGIssue<QT, SWIGLU>& is,
+                                      const PGMeta& meta, int mq, const PGItem& I, int q, int cslot) {
+  using L = PG<QT>;
+  const int lr = c.lr, lg = c.lg, wv = c.wv;
+  const int sz = PGSrc<QT, SWIGLU>::swz(lr);
+  const uint32_t aof0 = uint32_t(lr * 128 + ((0 + lg) ^ sz) * 16), aof1 = uint32_t(lr * 128 + ((4 + lg) ^ sz) * 16);
+  // the wave's weight rows: SwiGLU gate rows 16 wv .. + 16 (column block 0) and the same rows of up (staged at + 128);
+  // plain rows 32 wv .. + 32
+  uint32_t bof[2];
+#pragma unroll
+  for (int nb = 0; nb < 2; nb++)
+    bof[nb] = uint32_t(L::ABYTES + (SWIGLU ? 128 * nb + 16 * wv + lr : 32 * wv + 16 * nb + lr) * L::WROW);
+  const int cb = QT == ARTLITE_Q4_0 ? 8 * (lg & 1) : 8 * lg;
+  const PGDecode<QT> dec(lg);
+  f32x4 acc[MBN][2];
+#pragma unroll
+  for (int mb = 0; mb < MBN; mb++) acc[mb][0] = acc[mb][1] = f32x4{0, 0, 0, 0};
+  for (int st = 0; st < c.stages; st++) {
+    pg_wait<L::LOADS>();  // (stage st: only the issue after it may be in flight)
+    pg_barrier();         // (every wave's stage st landed; every wave past its reads of the previous slot)
+    const PGBases b = pg_bases<QT, SWIGLU>(a, c, is, mq);
+    const PGSrc<QT, SWIGLU> src = is.src;
+    pg_advance<QT, SWIGLU>(a, c, is);
+    pg_step<QT, SWIGLU, MBN>(c.lds + cslot * L::SBYTES, aof0, aof1, bof, cb, dec, acc, src, meta, b, wv);
+    cslot = __builtin_amdgcn_readfirstlane(cslot + 1 == L::R ? 0 : cslot + 1);
+  }
+  // epilogue: lane output i of block (mb, nb): row 16 mb + lr of the tile; column (SwiGLU) n0 + 16 wv + 4 lg + i, gate
+  // in nb 0 and up in nb 1; (plain) n0 + 32 wv + 16 nb + 4 lg + i. A lane stores its row's 4 columns at once.
+  const float2* rf = pg_rowf<QT>(c, q);
+#pragma unroll
+  for (int mb = 0; mb < MBN; mb++) {
+    const int m = 16 * mb + lr;
+    if (m >= I.m_valid) continue;
+    const int64_t o = int64_t(I.s0 + m) * a.N;
+    const float2 f = rf[m];
+    if constexpr (SWIGLU) {
+      const int n = I.n0 + 16 * wv + 4 * lg;
+      if (n < a.N) {
+        uint32_t v[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+          const f16x2 h = {_Float16(pg_swiglu(acc[mb][0][2 * i] * f.x, acc[mb][1][2 * i] * f.x) * f.y),
+                           _Float16(pg_swiglu(acc[mb][0][2 * i + 1] * f.x, acc[mb][1][2 * i + 1] * f.x) * f.y)};
+          v[i] = __builtin_bit_cast(uint32_t, h);
+        }
+        *reinterpret_cast<uint2*>(a.h + o + n) = make_uint2(v[0], v[1]);
+      }
+    } else if (a.y16) {  // (fp16: the sums times f.y)
+#pragma unroll
+      for (int nb = 0; nb < 2; nb++) {
+        const int n = I.n0 + 32 * wv + 16 * nb + 4 * lg;
+        if (n < a.N) {
+          const f16x2 v0 = {_Float16(acc[mb][nb][0] * f.y), _Float16(acc[mb][nb][1] * f.y)};
+          const f16x2 v1 = {_Float16(acc[mb][nb][2] * f.y), _Float16(acc[mb][nb][3] * f.y)};
+          *reinterpret_cast<uint2*>(a.y16 + o + n) =
+              make_uint2(__builtin_bit_cast(uint32_t, v0), __builtin_bit_cast(uint32_t, v1));
+        }
+      }
+    } else {  // (fp32: the sums times f.x f.y, a power of two)
+      const float fs = f.x * f.y;
+#pragma unroll
+      for (int nb = 0; nb < 2; nb++) {
+        const int n = I.n0 + 32 * wv + 16 * nb + 4 * lg;
+        if (n < a.N) *reinterpret_cast<float4*>(a.y + o + n) = make_float4(acc[mb][nb][0] * fs, acc[mb][nb][1] * fs,
+                                                                            acc[mb][nb][2] * fs, acc[mb][nb][3] * fs);
+      }
+    }
+  }
+  return cslot;
+}
+
+template <int QT, bool SWIGLU>
+__global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_pgemm(const PrefillArgs a) {
+  using L = PG<QT>;
+  constexpr int WN = SWIGLU ? 128 : 256;  // output columns per item
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  PGCtx c;
+  c.lds = lds;
+  c.lbase = pg_lds_addr(lds);
+  c.tid = threadIdx.x;
+  c.lane = c.tid & (WAVE - 1);
+  c.wv = __builtin_amdgcn_readfirstlane(c.tid / WAVE);
+  c.lg = c.lane >> 4;
+  c.lr = c.lane & 15;
+  c.stages = a.K / 64;
+  int4* table = reinterpret_cast<int4*>(lds + L::R * L::SBYTES + 2 * L::META);
+  c.table = table;
+  const int nbk = (a.N + WN - 1) / WN;
+  const int drows = a.tiles ? 0 : balanced_rows(a.dense_rows, TILE_ROWS);
+  const int64_t ntl = a.tiles ? int64_t(*a.n_tiles) : (a.dense_rows + drows - 1) / drows;
+  const int64_t items = ntl * nbk, per = (items + 7) / 8;
+  // items dealt to the 8 XCDs in contiguous runs (workgroup b runs on XCD b % 8): the column blocks of a tile, and an
+  // expert's tiles, run close in time on one XCD and share its L2 (the tile's A rows, the expert's weights)
+  const int G = gridDim.x / 8, x = blockIdx.x % 8, j0 = blockIdx.x / 8;
+  const int64_t first = x * per + j0, end = min(items, (x + 1) * per);
+  if (first >= end) return;
+  c.nq = int((end - first + G - 1) / G);  // this workgroup's items: first + q G (at most MAXQ: the launch checks)
+  // the item table: every global load of the tiles and offsets, once, before any DMA is in flight
+  if (c.tid < c.nq) {
+    const PGItem I = pg_item<SWIGLU>(a, first + int64_t(c.tid) * G, nbk);
+    table[c.tid] = make_int4(I.e, I.s0, I.m_valid, I.n0);
+  }
+  __syncthreads();
+  // item 0's metadata, landed before its sources are made; then the first R - 1 issues (stages >= R + 1:
+  // prefill_supported), each with the metadata of item 1 (item 0's again when there is none)
+  PGMeta meta;
+  PGItem I = pg_table(c, 0);
+  meta.set(a, I, c.tid);
+  PGIssue<QT, SWIGLU> is;
+  is.q = 0;
+  is.st = 0;
+  is.slot = 0;
+  {
+    PGBases b = pg_bases<QT, SWIGLU>(a, c, is, 0);
+#pragma unroll
+    for (int j = 0; j < L::MI; j++) pg_dma_n<QT, SWIGLU>(L::AI + L::BI + j, b, is.src, meta, c.wv);
+    pg_wait<0>();
+    __syncthreads();
+  }
+  is.src.set(a, I, pg_tok<QT>(c, 0), c.tid);
+  int mq = c.nq > 1 ? 1 : 0;
+  meta.set(a, pg_table(c, mq), c.tid);
+#pragma unroll
+  for (int j = 0; j < L::R - 1; j++) {
+    const PGBases b = pg_bases<QT, SWIGLU>(a, c, is, mq);
+    const PGSrc<QT, SWIGLU> src = is.src;
+    pg_advance<QT, SWIGLU>(a, c, is);
+#pragma unroll
+    for (int n = 0; n < L::LOADS; n++) pg_dma_n<QT, SWIGLU>(n, b, src, meta, c.wv);
+  }
+
+  int cslot = 0;
+  for (int q = 0; q < c.nq; q++) {
+    I = pg_table(c, q);
+    // the tile's row blocks, rounded up to an even count (an instance of the K loop per count)
+    switch ((I.m_valid + 31) / 32) {
+      case 1: cslot = pg_run<QT, SWIGLU, 2>(a, c, is, meta, mq, I, q, cslot); break;
+      case 2: cslot = pg_run<QT, SWIGLU, 4>(a, c, is, meta, mq, I, q, cslot); break;
+      case 3: cslot = pg_run<QT, SWIGLU, 6>(a, c, is, meta, mq, I, q, cslot); break;
+      case 4: cslot = pg_run<QT, SWIGLU, 8>(a, c, is, meta, mq, I, q, cslot); break;
+      case 5: cslot = pg_run<QT, SWIGLU, 10>(a, c, is, meta, mq, I, q, cslot); break;
+      case 6: cslot = pg_run<QT, SWIGLU, 12>(a, c, is, meta, mq, I, q, cslot); break;
+      case 7: cslot = pg_run<QT, SWIGLU, 14>(a, c, is, meta, mq, I, q, cslot); break;
+      default: cslot = pg_run<QT, SWIGLU, 16>(a, c, is, meta, mq, I, q, cslot); break;
+    }
+    // the metadata the next item's steps issue: item q + 2's into the buffer item q's epilogue just read (past the
+    // next item's first barrier, every wave is done with it), else item q + 1's again (the same bytes)
+    mq = q + 2 < c.nq ? q + 2 : min(q + 1, c.nq - 1);
+    meta.set(a, pg_table(c, mq), c.tid);
+  }
+  pg_wait<0>();  // (the dummy loads past the last stage land before the workgroup's LDS is released)
+}
+
+template <int QT, bool SWIGLU>
+int launch_pgemm(const PrefillArgs& a, hipStream_t s) {
+  using L = PG<QT>;
+  const int rows = a.tiles ? TILE_ROWS : balanced_rows(a.dense_rows, TILE_ROWS);
+  const int64_t tiles = a.tiles ? a.max_tiles : (a.dense_rows + rows - 1) / rows;
+  const int64_t items = tiles * ((a.N + (SWIGLU ? 127 : 255)) / (SWIGLU ? 128 : 256));
+  if (items <= 0) return ARTLITE_OK;
+  // persistent workgroups: as many as the device holds at once (a multiple of 8, the XCDs), at most the items
+  static const int resident = [] {
+    const void* f = reinterpret_cast<const void*>(k_pgemm<QT, SWIGLU>);
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, L::LDS) != hipSuccess ||
+        hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, L::THREADS, L::LDS) != hipSuccess)
+      return 0;
+    return cus * std::max(1, per_cu);
+  }();
+  if (resident < 8) return fail(ARTLITE_EHIP, "prefill GEMM: kernel set-up failed");
+  const int64_t grid = std::min<int64_t>((items + 7) / 8 * 8, resident / 8 * 8);
+  // a workgroup's items (an XCD's run of ceil(items / 8), dealt over its grid / 8 workgroups) fit its item table
+  if (((items + 7) / 8 + grid / 8 - 1) / (grid / 8) > L::MAXQ)
+    return fail(ARTLITE_EINVAL, "prefill GEMM: %lld work items, more than %d per workgroup", (long long)items, L::MAXQ);
+  k_pgemm<QT, SWIGLU><<<unsigned(grid), L::THREADS, L::LDS, s>>>(a);
+  ART_HIP(hipGetLastError());
+  return ARTLITE_OK;
+}
+
+}  // namespace
+
+bool prefill_supported(int qtype, int K, int N) {
+  // (K: whole stages of 64, at least R + 1 of them: the issue side, R - 1 stages ahead, switches to the next item at
+  // an item's step stages - R + 1 >= 2, after the metadata the item's first step issued has landed)
+  return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0) && K >= 64 * (PG<ARTLITE_Q4_0>::R + 1) && K % 64 == 0 &&
+         N > 0 && N % 16 == 0;
+}
+
+int launch_prefill(const PrefillArgs& a, hipStream_t s) {
+  if (!prefill_supported(a.qtype, a.K, a.N))
+    return fail(ARTLITE_EINVAL, "prefill GEMM: weight type %d, K %d, N %d", a.qtype, a.K, a.N);
+  if (!a.a || !a.row_scale || (a.w[1] ? !a.h : !a.y && !a.y16) || (a.tiles && (!a.n_tiles || !a.offsets)))
+    return fail(ARTLITE_EINVAL, "prefill GEMM: null argument");
+  const bool swiglu = a.w[1] != nullptr;
+  if (a.qtype == ARTLITE_Q4_0)
+    return swiglu ? launch_pgemm<ARTLITE_Q4_0, true>(a, s) : launch_pgemm<ARTLITE_Q4_0, false>(a, s);
+  return swiglu ? launch_pgemm<ARTLITE_Q8_0, true>(a, s) : launch_pgemm<ARTLITE_Q8_0, false>(a, s);
+}
+
+}  // namespace artlite

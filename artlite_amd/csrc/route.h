@@ -160,7 +160,16 @@ struct DispatchBufs {
   int BM;            // rows per tile (0: no tile list)
   int32_t* cstart;   // E + 1 chunk prefix (plan only; may be null)
   int chunk;         // plan chunk size (0: no plan)
+  int balanced = 0;  // 1: an expert's c rows in tiles of balanced_rows(c, BM) rows (the last one shorter)
 };
+
+// rows per tile when an expert's c rows are split into tiles of at most bm rows of nearly equal size: the fewest
+// tiles, their size rounded up to a multiple of 16 (whole MFMA row blocks); the tiles are ceil(c / that)
+__host__ __device__ inline int balanced_rows(int c, int bm) {
+  if (c <= 0) return bm;
+  const int nt = (c + bm - 1) / bm, r = ((c + nt - 1) / nt + 15) / 16 * 16;
+  return r < bm ? r : bm;
+}
 
 // blocks of a dispatch of P pairs
 inline int64_t dispatch_blocks(int64_t P) { return P > 0 ? (P + DISPATCH_BLOCK - 1) / DISPATCH_BLOCK : 1; }

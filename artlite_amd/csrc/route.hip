@@ -406,7 +406,8 @@ __global__ __launch_bounds__(DISPATCH_BLOCK) void k_route_small(const float* __r
   // both sums stay below 2^16: at most DISPATCH_BLOCK pairs)
   const int e = tid;
   const int c = e < E ? base[e] : 0;
-  const int nt = e < E && d.BM > 0 ? (c + d.BM - 1) / d.BM : 0;
+  const int rows = d.balanced ? balanced_rows(c, d.BM) : d.BM;
+  const int nt = e < E && d.BM > 0 ? (c + rows - 1) / rows : 0;
   int packed_total;
   const int packed = block_scan(c | (nt << 16), &packed_total);
   const int start = packed & 0xFFFF, total = packed_total & 0xFFFF;
@@ -420,7 +421,7 @@ __global__ __launch_bounds__(DISPATCH_BLOCK) void k_route_small(const float* __r
     const int t0 = packed >> 16;
     for (int m = 0; m < nt; m++) {
       d.tiles[2 * (t0 + m)] = e;
-      d.tiles[2 * (t0 + m) + 1] = start + m * d.BM;
+      d.tiles[2 * (t0 + m) + 1] = start + m * rows;
     }
     if (e == 0) d.ctrl[CTRL_TILES] = packed_total >> 16;
   }
