@@ -218,74 +218,114 @@ __global__ __launch_bounds__(4 * WAVE) void k_router_small(const void* __restric
 }
 
 // Router logits for prefill-sized batches on the fp64 MFMA (v_mfma_f64_16x16x4_f64; fp32 x fp32 products are exact
-// in fp64, the sums in fp64, rounded once to fp32 like the other router kernels): a workgroup is 16 tokens times all
-// experts, a wave per 16 experts. Layout: lane l holds A row l % 16 (token) and B column l % 16 (expert), both at K
-// position l / 16 of the step; result element i of lane l is row 4 i + l / 16, column l % 16. The K values of a
-// 16-value block are dealt as step s, lane group g -> k0 + 4 g + s, so each lane's four steps are one 16-byte load of
-// its W row and one 8 / 16-byte load of its x row.
-template <int XT>
-__global__ __launch_bounds__(1024) void k_router_mfma(const void* __restrict__ xv, const float* __restrict__ W, int H,
-                                                      int E, int64_t T, float* __restrict__ out, int64_t out_row) {
+// in fp64, the sums in fp64, rounded once to fp32 like the other router kernels). A workgroup is a tile of 32 tokens
+// times TE experts, waves of 16 x 16 (wave w: token block w & 1, expert block w / 2). K streams in stages of 64
+// values through two LDS buffers (x and W rows as fp32, rows padded to 68 values so that a wave's 16 rows read
+// different banks), each thread loading 16-byte pieces of x and W, two stages ahead in registers. MFMA layout: lane l holds A row l % 16 (token) and B column l % 16 (expert), both at K position l / 16 of
+// the step; result element i of lane l is row 4 i + l / 16, column l % 16. The K values of a 16-value block are dealt
+// as step s, lane group g -> k0 + 4 g + s, so each lane's four steps are one 16-byte LDS read of its x row and one of
+// its W row; step s accumulates into acc[s] (consecutive MFMAs independent), the four summed at the end. Rows past T,
+// experts past E load the last one (not stored); K past H loads zeros.
+template <int XT, int TE>
+__global__ __launch_bounds__(2 * TE / 16 * WAVE) void k_router_mfma(const void* __restrict__ xv,
+                                                                    const float* __restrict__ W, int H, int E,
+                                                                    int64_t T, float* __restrict__ out,
+                                                                    int64_t out_row) {
   typedef double d4 __attribute__((ext_vector_type(4)));
-  const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE;
-  const int g = lane >> 4, r = lane & 15;
-  const int64_t t0 = int64_t(blockIdx.x) * 16;
-  const int e0 = 16 * wv;
-  const int64_t t = min(t0 + r, T - 1);  // (rows past T and experts past E load the last one; not stored)
-  const float* wr = W + int64_t(min(e0 + r, E - 1)) * H + 4 * g;
-  d4 c = {0, 0, 0, 0};
-  auto x4 = [&](int k0) -> float4 {
-    if (XT == ARTLITE_X_F32) return *reinterpret_cast<const float4*>(static_cast<const float*>(xv) + t * H + k0 + 4 * g);
-    const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(xv) + t * H + k0 + 4 * g);
-    return make_float4(bf16_to_f32(v.x & 0xFFFFu), bf16_to_f32(v.x >> 16), bf16_to_f32(v.y & 0xFFFFu),
-                       bf16_to_f32(v.y >> 16));
+  constexpr int TM = 32, KS = 64, PAD = 68, THREADS = 2 * TE / 16 * WAVE;
+  constexpr int NX = TM * 16 / THREADS, NW = TE * 16 / THREADS;  // 16-byte pieces per thread per stage
+  __shared__ __attribute__((aligned(16))) float xs[2][TM][PAD];
+  __shared__ __attribute__((aligned(16))) float ws[2][TE][PAD];
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), wv = tid / WAVE;
+  const int tb = wv & 1, eb = wv >> 1, g = lane >> 4, r = lane & 15;
+  const int64_t t0 = int64_t(blockIdx.x) * TM;
+  const int e0 = int(blockIdx.y) * TE;
+  // the thread's loads: piece i is row (tid + i THREADS) / 16 of x (or W), values 4 lq .. + 4 of each stage
+  const int lq = tid & 15;
+  const void* xp[NX];
+  const float* wp[NW];
+#pragma unroll
+  for (int i = 0; i < NX; i++) {
+    const int64_t xt = min(t0 + (tid + i * THREADS) / 16, T - 1);
+    xp[i] = XT == ARTLITE_X_F32 ? static_cast<const void*>(static_cast<const float*>(xv) + xt * H)
+                                : static_cast<const void*>(static_cast<const uint16_t*>(xv) + xt * H);
+  }
+#pragma unroll
+  for (int i = 0; i < NW; i++) wp[i] = W + int64_t(min(e0 + (tid + i * THREADS) / 16, E - 1)) * H;
+  struct Piece {
+    float4 x[NX], w[NW];
   };
-  // 64 values of K per step, the next step's loads issued before this step's products; two accumulators (even and
-  // odd 16-value blocks), summed at the end
-  d4 c1 = {0, 0, 0, 0};
-  float4 xa[4], wa[4], xb[4], wb[4];
-  auto load = [&](int k, float4(&xs)[4], float4(&ws)[4]) {
+  // (loads past H read the last piece again, unconditionally, so that no branch makes the compiler wait for loads in
+  // flight; the store into LDS puts zeros in their place)
+  auto gload = [&](int k0) -> Piece {
+    const int k = min(k0 + 4 * lq, H - 4);
+    Piece p;
+#pragma unroll
+    for (int i = 0; i < NX; i++) {
+      if (XT == ARTLITE_X_F32) {
+        p.x[i] = *reinterpret_cast<const float4*>(static_cast<const float*>(xp[i]) + k);
+      } else {
+        const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(xp[i]) + k);
+        p.x[i] = make_float4(bf16_to_f32(v.x & 0xFFFFu), bf16_to_f32(v.x >> 16), bf16_to_f32(v.y & 0xFFFFu),
+                             bf16_to_f32(v.y >> 16));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NW; i++) p.w[i] = *reinterpret_cast<const float4*>(wp[i] + k);
+    return p;
+  };
+  // (values, not references or lvalue selects, which the compiler turns into pointer selects over scratch copies)
+  auto sstore = [&](int st, Piece p) {
+    const float m = st * KS + 4 * lq < H ? 1.0f : 0.0f;  // (x 1 exact; x 0 gives +-0, adding nothing)
+#pragma unroll
+    for (int i = 0; i < NX; i++)
+      *reinterpret_cast<float4*>(&xs[st & 1][(tid + i * THREADS) / 16][4 * lq]) =
+          make_float4(p.x[i].x * m, p.x[i].y * m, p.x[i].z * m, p.x[i].w * m);
+#pragma unroll
+    for (int i = 0; i < NW; i++)
+      *reinterpret_cast<float4*>(&ws[st & 1][(tid + i * THREADS) / 16][4 * lq]) =
+          make_float4(p.w[i].x * m, p.w[i].y * m, p.w[i].z * m, p.w[i].w * m);
+  };
+  d4 acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) acc[i] = d4{0, 0, 0, 0};
+  const int S = (H + KS - 1) / KS;
+  // stage st: its products from buffer st & 1, then the next stage's piece (loaded two stages before) into the other
+  // buffer (whose reads ended before the last barrier), then a barrier; the loop is unrolled by two so that the two
+  // pieces in flight keep their registers (a copy would wait for the loads)
+  auto products = [&](int st) {
+    const float* xrow = &xs[st & 1][16 * tb + r][4 * g];
+    const float* wrow = &ws[st & 1][16 * eb + r][4 * g];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      xs[j] = x4(k + 16 * j);
-      ws[j] = *reinterpret_cast<const float4*>(wr + k + 16 * j);
+      const float4 a = *reinterpret_cast<const float4*>(xrow + 16 * j);
+      const float4 b = *reinterpret_cast<const float4*>(wrow + 16 * j);
+      acc[0] = __builtin_amdgcn_mfma_f64_16x16x4f64(double(a.x), double(b.x), acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f64_16x16x4f64(double(a.y), double(b.y), acc[1], 0, 0, 0);
+      acc[2] = __builtin_amdgcn_mfma_f64_16x16x4f64(double(a.z), double(b.z), acc[2], 0, 0, 0);
+      acc[3] = __builtin_amdgcn_mfma_f64_16x16x4f64(double(a.w), double(b.w), acc[3], 0, 0, 0);
     }
   };
-  auto products = [&](const float4(&xs)[4], const float4(&ws)[4]) {
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      d4& acc = (j & 1) ? c1 : c;
-      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xs[j].x), double(ws[j].x), acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xs[j].y), double(ws[j].y), acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xs[j].z), double(ws[j].z), acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xs[j].w), double(ws[j].w), acc, 0, 0, 0);
-    }
-  };
-  const int steps = H / 64;
-  if (steps > 0) load(0, xa, wa);
-  int k0 = 0;
-  for (int st = 0; st < steps; st += 2, k0 += 128) {
-    if (st + 1 < steps) load(k0 + 64, xb, wb);
-    products(xa, wa);
-    if (st + 1 >= steps) {
-      k0 += 64;
-      break;
-    }
-    if (st + 2 < steps) load(k0 + 128, xa, wa);
-    products(xb, wb);
+  Piece pa = gload(0);
+  sstore(0, pa);
+  Piece pb = gload(KS);
+  __syncthreads();
+  for (int st = 0; st < S; st += 2) {
+    pa = gload((st + 2) * KS);  // (past the last stage: never stored)
+    products(st);
+    if (st + 1 < S) sstore(st + 1, pb);
+    __syncthreads();
+    if (st + 1 >= S) break;
+    pb = gload((st + 3) * KS);
+    products(st + 1);
+    if (st + 2 < S) sstore(st + 2, pa);
+    __syncthreads();
   }
-  c += c1;
-  for (; k0 < H; k0 += 16) {
-    const float4 xv4 = x4(k0), wv4 = *reinterpret_cast<const float4*>(wr + k0);
-    c = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xv4.x), double(wv4.x), c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xv4.y), double(wv4.y), c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xv4.z), double(wv4.z), c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f64_16x16x4f64(double(xv4.w), double(wv4.w), c, 0, 0, 0);
-  }
-  const int e = e0 + r;
+  const d4 c = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  const int e = e0 + 16 * eb + r;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    const int64_t tt = t0 + 4 * i + g;
+    const int64_t tt = t0 + 16 * tb + 4 * i + g;
     if (tt < T && e < E) out[tt * out_row + e] = float(c[i]);
   }
 }
@@ -334,12 +374,13 @@ int launch_router(const void* x, int x_dtype, const float* W, int H, int E, int6
   const int tt = int(std::min<int64_t>(ROUTER_TG, std::max<int64_t>(1, ROUTER_LDS / (int64_t(H) * xb))));
   if (int64_t(H) * xb > ROUTER_LDS) return fail(ARTLITE_EINVAL, "router: H %d too wide", H);
   const size_t lds = size_t(tt) * H * xb;
-  if (!xq && T >= 64 && E >= 16 && E <= 16 * 16 && H % 16 == 0) {  // (prefill-sized: the fp64 MFMA)
-    const dim3 g(unsigned((T + 15) / 16)), b(unsigned((E + 15) / 16) * WAVE);
+  if (!xq && T >= 64 && E >= 16 && H % 16 == 0) {  // (prefill-sized: the fp64 MFMA)
+    constexpr int TE = 64;  // (tiles of 32 x 64, 8 waves: measured faster than 32 x 32 with two workgroups per CU)
+    const dim3 g(unsigned((T + 31) / 32), unsigned((E + TE - 1) / TE)), b(2 * TE / 16 * WAVE);
     if (x_dtype == ARTLITE_X_F32)
-      k_router_mfma<ARTLITE_X_F32><<<g, b, 0, s>>>(x, W, H, E, T, out, out_row);
+      k_router_mfma<ARTLITE_X_F32, TE><<<g, b, 0, s>>>(x, W, H, E, T, out, out_row);
     else
-      k_router_mfma<ARTLITE_X_BF16><<<g, b, 0, s>>>(x, W, H, E, T, out, out_row);
+      k_router_mfma<ARTLITE_X_BF16, TE><<<g, b, 0, s>>>(x, W, H, E, T, out, out_row);
     ART_HIP(hipGetLastError());
     return ARTLITE_OK;
   }
