@@ -62,7 +62,8 @@ SIGNATURES = {
     "artlite_moe_layer_output": (ctypes.c_int, [ctypes.c_void_p, c_f32p, ctypes.c_int64]),
     "artlite_moe_layer_tap": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t]),
     "artlite_moe_layer_time": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int, ctypes.c_int64,
-                                              ctypes.c_int, ctypes.c_int, c_f64p, c_f64p, ctypes.c_int, c_i32p]),
+                                              ctypes.c_int, ctypes.c_int, c_f64p, c_f64p, c_f64p, ctypes.c_int,
+                                              c_i32p]),
     "artlite_moe_kernel_names": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_char_p, ctypes.c_size_t]),
     "artlite_hbm_copy": (ctypes.c_int, [ctypes.c_size_t, ctypes.c_int, c_f64p]),
 }

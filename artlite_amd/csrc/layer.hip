@@ -783,7 +783,8 @@ extern "C" int artlite_moe_kernel_names(artlite_moe_layer* L, int64_t T, char* b
 }
 
 extern "C" int artlite_moe_layer_time(artlite_moe_layer** layers, int n, int64_t T, int warmup, int iters,
-                                      double* ms_per_run, double* kernel_ms, int kernel_cap, int* n_kernels) {
+                                      double* ms_per_run, double* run_ms, double* kernel_ms, int kernel_cap,
+                                      int* n_kernels) {
   if (!layers || n < 1 || iters < 1 || warmup < 0 || !ms_per_run) return fail(ARTLITE_EINVAL, "layer time: arguments");
   artlite_moe_layer* L0 = layers[0];
   for (int i = 0; i < n; i++) {
@@ -808,29 +809,45 @@ extern "C" int artlite_moe_layer_time(artlite_moe_layer** layers, int n, int64_t
   }
   int rc = ARTLITE_OK;
   hipEvent_t e0 = nullptr, e1 = nullptr;
-  std::vector<hipEvent_t> ev;
+  std::vector<hipEvent_t> ev, er;
   const int nk = int(names.size());
   auto done = [&](int code) {
     for (int i = 0; i < n; i++) layers[i]->stream = own[i];
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
     for (hipEvent_t x : ev) (void)hipEventDestroy(x);
+    for (hipEvent_t x : er) (void)hipEventDestroy(x);
     return code;
   };
   if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
     return done(fail(ARTLITE_EHIP, "layer time: events"));
+  if (run_ms) {  // (an event before each run past the first; e0 and e1 bound the region)
+    er.resize(size_t(iters > 1 ? iters - 1 : 0), nullptr);
+    for (hipEvent_t& x : er)
+      if (hipEventCreate(&x) != hipSuccess) return done(fail(ARTLITE_EHIP, "layer time: events"));
+  }
   hipStream_t s = L0->stream;
   for (int i = 0; i < warmup; i++)
     if ((rc = run(layers[i % n], T, nullptr)) != ARTLITE_OK) return done(rc);
   if (hipStreamSynchronize(s) != hipSuccess) return done(fail(ARTLITE_EHIP, "layer time: sync"));
   if (hipEventRecord(e0, s) != hipSuccess) return done(fail(ARTLITE_EHIP, "layer time: record"));
-  for (int i = 0; i < iters; i++)
+  for (int i = 0; i < iters; i++) {
+    if (run_ms && i > 0 && hipEventRecord(er[size_t(i - 1)], s) != hipSuccess)
+      return done(fail(ARTLITE_EHIP, "layer time: record"));
     if ((rc = run(layers[i % n], T, nullptr)) != ARTLITE_OK) return done(rc);
+  }
   if (hipEventRecord(e1, s) != hipSuccess || hipEventSynchronize(e1) != hipSuccess)
     return done(fail(ARTLITE_EHIP, "layer time: record"));
   float ms = 0;
   if (hipEventElapsedTime(&ms, e0, e1) != hipSuccess) return done(fail(ARTLITE_EHIP, "layer time: elapsed"));
   *ms_per_run = double(ms) / iters;
+  if (run_ms)
+    for (int i = 0; i < iters; i++) {
+      float t = 0;
+      if (hipEventElapsedTime(&t, i ? er[size_t(i - 1)] : e0, i + 1 < iters ? er[size_t(i)] : e1) != hipSuccess)
+        return done(fail(ARTLITE_EHIP, "layer time: elapsed"));
+      run_ms[i] = t;
+    }
   if (n_kernels) *n_kernels = nk;
   if (kernel_ms) {
     // a second timed region with an event before each kernel and after the last

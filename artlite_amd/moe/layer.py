@@ -192,18 +192,20 @@ class MoELayer:
 
 
 def time_layers(layers: list[MoELayer], *, warmup: int, iters: int, per_kernel: bool = True
-                ) -> tuple[float, dict[str, float]]:
-    """(ms per run over ``iters`` runs cycling through ``layers`` after ``warmup``; per kernel average ms, from a second
-    timed region with an event before each kernel) with HIP events on the layers' stream."""
+                ) -> tuple[float, list[float], dict[str, float]]:
+    """(ms per run over ``iters`` runs cycling through ``layers`` after ``warmup``; each run's ms, from an event
+    before each run of that region; per kernel average ms, from a second timed region with an event before each
+    kernel) with HIP events on the layers' stream."""
     T = layers[0].T
     hs = (ctypes.c_void_p * len(layers))(*[ly.handle.value for ly in layers])
     ms = ctypes.c_double(0)
+    runs = (ctypes.c_double * iters)()
     names = layers[0].kernel_names()
     kms = (ctypes.c_double * len(names))()
     nk = ctypes.c_int32(0)
-    _hip.check(_hip.lib().artlite_moe_layer_time(hs, len(layers), T, warmup, iters, ctypes.byref(ms),
+    _hip.check(_hip.lib().artlite_moe_layer_time(hs, len(layers), T, warmup, iters, ctypes.byref(ms), runs,
                                                  kms if per_kernel else None, len(names), ctypes.byref(nk)))
-    return ms.value, ({n: kms[i] for i, n in enumerate(names)} if per_kernel else {})
+    return ms.value, list(runs), ({n: kms[i] for i, n in enumerate(names)} if per_kernel else {})
 
 
 def hbm_copy_ms(nbytes: int, iters: int = 20) -> float:
