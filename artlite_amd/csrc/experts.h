@@ -76,7 +76,8 @@ int launch_prefill_x(const void* x, int x_dtype, int64_t T, int H, const float* 
 int launch_prefill_rows(const int32_t* order, int64_t P, int k, const float2* gu, const float2* dn, int32_t* row_a,
                         float2* gu_row, float2* dn_row, hipStream_t s);
 
-// *out = max |w| over a tensor's nblocks GGUF blocks (Q4_0, Q8_0)
+// *out = a bound on max |w| over a tensor's nblocks GGUF blocks (Q4_0, Q8_0: exact; Q4_K: from d, dmin and the
+// largest 6-bit scale and min)
 int launch_weight_max(const uint8_t* w, int qtype, int64_t nblocks, float* out, hipStream_t s);
 // the most 32-value groups of a row (K <= 32 MAX_GROUPS)
 constexpr int MAX_GROUPS = 128;

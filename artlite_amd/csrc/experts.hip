@@ -572,28 +572,32 @@ int launch_prefill_rows(const int32_t* order, int64_t P, int k, const float2* gu
   return ARTLITE_OK;
 }
 
-// ---- max |w| of a weight tensor's blocks: the fp16 scale's magnitude times the format's largest code (Q4_0: 8,
-// Q8_0: 128), by an atomic max on the float's bits (non-negative floats order as their bits)
-__global__ void k_weight_max(const uint8_t* __restrict__ w, int block_bytes, float code_max, int64_t nblocks,
-                             uint32_t* __restrict__ out) {
+// ---- a bound on max |w| of a weight tensor's blocks: the fp16 scale's magnitude times the format's largest code
+// (Q4_0: 8, Q8_0: 128; Q4_K: |d| 63 15 + |dmin| 63, its 6-bit scale and min at their largest), by an atomic max on the
+// float's bits (non-negative floats order as their bits)
+__global__ void k_weight_max(const uint8_t* __restrict__ w, int block_bytes, float code_max, float min_max,
+                             int64_t nblocks, uint32_t* __restrict__ out) {
   float mx = 0.0f;
   for (int64_t b = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; b < nblocks; b += int64_t(gridDim.x) * blockDim.x) {
-    uint16_t d;
+    uint16_t d, dm;
     __builtin_memcpy(&d, w + b * block_bytes, 2);
-    mx = fmaxf(mx, fabsf(f16_to_f32(d)));
+    __builtin_memcpy(&dm, w + b * block_bytes + 2, 2);
+    mx = fmaxf(mx, fabsf(f16_to_f32(d)) + (min_max > 0.0f ? fabsf(f16_to_f32(dm)) * min_max : 0.0f));
   }
   for (int o = 32; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-  if ((threadIdx.x & 63) == 0) atomicMax(out, __float_as_uint(mx * code_max));
+  if ((threadIdx.x & 63) == 0) atomicMax(out, __float_as_uint(mx * code_max));  // (min_max: already over code_max)
 }
 
 int launch_weight_max(const uint8_t* w, int qtype, int64_t nblocks, float* out, hipStream_t s) {
-  if (qtype != ARTLITE_Q4_0 && qtype != ARTLITE_Q8_0) return fail(ARTLITE_EINVAL, "weight max: type %d", qtype);
+  if (qtype != ARTLITE_Q4_0 && qtype != ARTLITE_Q8_0 && qtype != ARTLITE_Q4_K)
+    return fail(ARTLITE_EINVAL, "weight max: type %d", qtype);
   ART_HIP(hipMemsetAsync(out, 0, 4, s));
   if (nblocks <= 0) return ARTLITE_OK;
-  const int bb = qtype == ARTLITE_Q4_0 ? 18 : 34;
+  const int bb = qtype == ARTLITE_Q4_0 ? 18 : qtype == ARTLITE_Q8_0 ? 34 : 144;
+  const float code = qtype == ARTLITE_Q4_0 ? 8.0f : qtype == ARTLITE_Q8_0 ? 128.0f : 945.0f;
+  const float mins = qtype == ARTLITE_Q4_K ? 63.0f / 945.0f * 1.0001f : 0.0f;  // (a bound: rounded up)
   const unsigned grid = unsigned(std::min<int64_t>((nblocks + 255) / 256, 1024));
-  k_weight_max<<<grid, 256, 0, s>>>(w, bb, qtype == ARTLITE_Q4_0 ? 8.0f : 128.0f, nblocks,
-                                    reinterpret_cast<uint32_t*>(out));
+  k_weight_max<<<grid, 256, 0, s>>>(w, bb, code, mins, nblocks, reinterpret_cast<uint32_t*>(out));
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
 }

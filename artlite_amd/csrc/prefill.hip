@@ -48,14 +48,19 @@ constexpr int TILE_ROWS = 256;  // A rows of a tile, at most
 
 template <int QT>
 struct PG {
-  static constexpr int GB = QT == ARTLITE_Q4_0 ? 18 : 34;  // bytes of a 32-value block
+  // Q4_K: a stage is a quarter of a 256-value super-block (144 B: d, dmin, 12 bytes of 6-bit scales and mins, 128
+  // code bytes); a row's stage bytes are its super-block's 16-byte header and the quarter's 32 code bytes, staged in
+  // two regions (the headers of the item's 256 rows, then their codes), each DMA instruction reading one of them
+  static constexpr bool K4 = QT == ARTLITE_Q4_K;
+  static constexpr int GB = QT == ARTLITE_Q4_0 ? 18 : 34;  // bytes of a 32-value block (Q4_0, Q8_0)
   static constexpr int WN = 256;                          // weight rows staged per item
-  static constexpr int WROW = 2 * GB;                     // stage bytes of a staged weight row (two blocks)
-  static constexpr int WDW = WROW / 4;                    // its dwords (9 / 17)
+  static constexpr int WROW = K4 ? 48 : 2 * GB;           // stage bytes of a staged weight row (two blocks)
+  static constexpr int WDW = WROW / 4;                    // its dwords (9 / 17 / 12)
   static constexpr int THREADS = 512;                     // 8 waves, two per SIMD
   static constexpr int ABYTES = TILE_ROWS * 128;          // a stage of A: 64 fp16 per row
   static constexpr int AI = ABYTES / 16 / THREADS;        // A DMAs (16 B) per lane per stage
   static constexpr int BI = (WN * WDW + THREADS - 1) / THREADS;  // weight DMAs (4 B) per lane per stage
+  static constexpr int KHDR = WN * 16;                    // Q4_K: the header region's bytes (the codes follow)
   static constexpr int WBYTES = BI * THREADS * 4;         // (the last dwords: padding the dummies fill)
   static constexpr int SBYTES = ABYTES + WBYTES;
   static constexpr int MI = 2;           // item metadata DMAs (4 B) per lane per stage
@@ -67,7 +72,8 @@ struct PG {
   static constexpr int LDS = R * SBYTES + 2 * META + MAXQ * 16;
   static_assert(AI * 16 * THREADS == ABYTES, "whole A DMAs");
   static_assert(META >= 3 * 1024, "metadata");
-  static_assert(128 * WDW % 64 == 0, "a wave's weight DMA reads one matrix (gate or up)");
+  static_assert(K4 || 128 * WDW % 64 == 0, "a wave's weight DMA reads one matrix (gate or up)");
+  static_assert(!K4 || (BI == 6 && WN * WDW == BI * THREADS), "Q4_K: two header and four code DMAs, no padding");
   static_assert(LDS <= LDS_BYTES, "LDS");
   static_assert((R - 1) * LOADS < 64, "vmcnt");
 };
@@ -140,6 +146,44 @@ struct PGDecode {
   }
 };
 
+// Q4_K: the scale and min of the lane's two sub-blocks of stage quarter qi (sub-blocks 2 qi, 2 qi + 1) from its row's
+// super-block header h (d, dmin; 12 bytes of 6-bit scales and mins, packed as the format packs them: sub-blocks 0-3
+// in the low 6 bits of bytes 0-3 (scales) and 4-7 (mins), sub-blocks 4-7 in the nibbles of bytes 8-11 with their top
+// 2 bits in the top bits of bytes 0-7), as fp32: s = d sc and o = dmin m, both exact.
+__device__ __forceinline__ void pg_k4_scales(const u32x4& h, int qi, float (&s)[2], float (&o)[2]) {
+  const float d = float(__builtin_bit_cast(_Float16, uint16_t(h[0] & 0xFFFFu)));
+  const float dm = float(__builtin_bit_cast(_Float16, uint16_t(h[0] >> 16)));
+#pragma unroll
+  for (int g = 0; g < 2; g++) {
+    const int sh = 8 * (2 * (qi & 1) + g);  // (the sub-block's byte within each 4-byte run)
+    uint32_t sc, m;
+    if (qi < 2) {
+      sc = (h[1] >> sh) & 63;
+      m = (h[2] >> sh) & 63;
+    } else {
+      sc = ((h[3] >> sh) & 0xF) | (((h[1] >> (sh + 6)) & 3) << 4);
+      m = ((h[3] >> (sh + 4)) & 0xF) | (((h[2] >> (sh + 6)) & 3) << 4);
+    }
+    s[g] = d * float(sc);
+    o[g] = dm * float(m);
+  }
+}
+
+// Q4_K: the lane's 8 weights of one sub-block from its 8 codes (the bytes of m0, m1, each < 16): q s - o in fp32
+// (the product exact, one rounding), then rounded to fp16.
+__device__ __forceinline__ u32x4 pg_k4_decode(uint32_t m0, uint32_t m1, float s, float o) {
+  u32x4 b;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t v = i < 2 ? m0 : m1;
+    const int sh = 16 * (i & 1);
+    const f16x2 h = {_Float16(__builtin_fmaf(float((v >> sh) & 0xFF), s, -o)),
+                     _Float16(__builtin_fmaf(float((v >> (sh + 8)) & 0xFF), s, -o))};
+    b[i] = __builtin_bit_cast(uint32_t, h);
+  }
+  return b;
+}
+
 // An item: expert e, its sorted rows s0 .. s0 + m_valid, output columns n0 .. (SwiGLU: + 128 of gate and up; plain:
 // + 256)
 struct PGItem {
@@ -190,7 +234,16 @@ struct PGSrc {
     }
 #pragma unroll
     for (int j = 0; j < L::BI; j++) {  // (dwords past the staged rows: padding, loading the last dword again)
-      const int q = min(j * L::THREADS + tid, L::WN * L::WDW - 1), row = q / L::WDW, dw = q % L::WDW;
+      int row, dw;
+      if constexpr (L::K4) {  // (instructions 0, 1: the headers, 4 dwords a row; 2 .. 5: the codes, 8 a row)
+        const int q = (j < 2 ? j : j - 2) * L::THREADS + tid;
+        row = j < 2 ? q >> 2 : q >> 3;
+        dw = j < 2 ? q & 3 : q & 7;
+      } else {
+        const int q = min(j * L::THREADS + tid, L::WN * L::WDW - 1);
+        row = q / L::WDW;
+        dw = q % L::WDW;
+      }
       const int n = min(I.n0 + (SWIGLU ? row % 128 : row), g.N - 1);
       w[j] = uint32_t(I.e) * uint32_t(g.expert_bytes) + uint32_t(n) * uint32_t(g.row_bytes) + 4 * dw;
     }
@@ -251,6 +304,7 @@ __device__ __forceinline__ void pg_codes(const uint8_t* row, int g, int cb, uint
 // uniform base pointers (at that stage) and destination slots; the lanes' offsets are in PGSrc and PGMeta.
 struct PGBases {
   const uint8_t *ab, *wb0, *wb1, *mt, *ms;
+  const uint8_t *wq0, *wq1;  // (Q4_K: the stage's code bytes; wb0, wb1 its super-block headers)
   uint32_t dst, mdst;
 };
 
@@ -264,8 +318,12 @@ __device__ __forceinline__ void pg_dma_n(int n, const PGBases& b, const PGSrc<QT
     pg_dma<16>(b.ab, src.a[n], b.dst + (8 * n + wv) * 1024);
   } else if (n < L::AI + L::BI) {
     const int j = n - L::AI;
-    pg_dma<4>(SWIGLU && (j * L::THREADS + 64 * wv) >= 128 * L::WDW ? b.wb1 : b.wb0, src.w[j],
-              b.dst + L::ABYTES + (8 * j + wv) * 256);
+    const uint8_t* base;
+    if constexpr (L::K4)  // (headers: instruction 1 reads up's; codes: instructions 4, 5)
+      base = j < 2 ? (SWIGLU && j == 1 ? b.wb1 : b.wb0) : (SWIGLU && j >= 4 ? b.wq1 : b.wq0);
+    else
+      base = SWIGLU && (j * L::THREADS + 64 * wv) >= 128 * L::WDW ? b.wb1 : b.wb0;
+    pg_dma<4>(base, src.w[j], b.dst + L::ABYTES + (8 * j + wv) * 256);
   } else {
     const int j = n - L::AI - L::BI;
     pg_dma<4>(j == 0 && wv < 4 ? b.mt : b.ms, meta.m[j], b.mdst + (8 * j + wv) * 256);
@@ -279,22 +337,47 @@ __device__ __forceinline__ void pg_dma_n(int n, const PGBases& b, const PGSrc<QT
 // aof: the lane's A chunk offset in a slot for group 0 (aof1: group 1); bof: its weight row's offset per column block.
 template <int QT, bool SWIGLU, int MBN>
 __device__ __forceinline__ void pg_step(const uint8_t* slot, uint32_t aof0, uint32_t aof1, const uint32_t (&bof)[2],
-                                        int cb, const PGDecode<QT>& dec, f32x4 (&acc)[MBN][2],
+                                        int cb, int qi, const PGDecode<QT>& dec, f32x4 (&acc)[MBN][2],
                                         const PGSrc<QT, SWIGLU>& src, const PGMeta& meta, const PGBases& b, int wv) {
   using L = PG<QT>;
   constexpr int IT = 2 * MBN, PF = MBN < 4 ? MBN : 4;
   auto a_addr = [&](int it) { return slot + (it < MBN ? aof0 : aof1) + (it % MBN) * 2048; };
+  // group 1's codes and scales (Q4_K: the same code bytes' high nibbles, the second sub-block's scale and min)
   uint32_t sc0[2], c00[2], c01[2], sc1[2], c10[2], c11[2];
-#pragma unroll
-  for (int nb = 0; nb < 2; nb++) pg_codes<QT>(slot + bof[nb], 0, cb, sc0[nb], c00[nb], c01[nb]);
+  float ks1[2], ko1[2];
   u32x4 av[PF + 1];
-#pragma unroll
-  for (int it = 0; it < PF; it++) av[it] = *reinterpret_cast<const u32x4*>(a_addr(it));
-#pragma unroll
-  for (int nb = 0; nb < 2; nb++) pg_codes<QT>(slot + bof[nb], 1, cb, sc1[nb], c10[nb], c11[nb]);
   u32x4 b0[2], b1[2];
+  if constexpr (L::K4) {  // (bof: the lane's weight row in the item; cb: its code bytes' offset, 8 lg)
+    u32x4 h[2];
 #pragma unroll
-  for (int nb = 0; nb < 2; nb++) b0[nb] = dec(c00[nb], c01[nb], sc0[nb]);
+    for (int nb = 0; nb < 2; nb++) {
+      h[nb] = *reinterpret_cast<const u32x4*>(slot + L::ABYTES + bof[nb] * 16);
+      const uint32_t* c = reinterpret_cast<const uint32_t*>(slot + L::ABYTES + L::KHDR + bof[nb] * 32 + cb);
+      c00[nb] = c[0];
+      c01[nb] = c[1];
+    }
+#pragma unroll
+    for (int it = 0; it < PF; it++) av[it] = *reinterpret_cast<const u32x4*>(a_addr(it));
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) {
+      float ks[2], ko[2];
+      pg_k4_scales(h[nb], qi, ks, ko);
+      ks1[nb] = ks[1];
+      ko1[nb] = ko[1];
+      c10[nb] = (c00[nb] >> 4) & 0x0F0F0F0Fu;
+      c11[nb] = (c01[nb] >> 4) & 0x0F0F0F0Fu;
+      b0[nb] = pg_k4_decode(c00[nb] & 0x0F0F0F0Fu, c01[nb] & 0x0F0F0F0Fu, ks[0], ko[0]);
+    }
+  } else {
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) pg_codes<QT>(slot + bof[nb], 0, cb, sc0[nb], c00[nb], c01[nb]);
+#pragma unroll
+    for (int it = 0; it < PF; it++) av[it] = *reinterpret_cast<const u32x4*>(a_addr(it));
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) pg_codes<QT>(slot + bof[nb], 1, cb, sc1[nb], c10[nb], c11[nb]);
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) b0[nb] = dec(c00[nb], c01[nb], sc0[nb]);
+  }
 #pragma unroll
   for (int it = 0; it < IT; it++) {
     if (it + PF < IT) av[(it + PF) % (PF + 1)] = *reinterpret_cast<const u32x4*>(a_addr(it + PF));
@@ -306,7 +389,12 @@ __device__ __forceinline__ void pg_step(const uint8_t* slot, uint32_t aof0, uint
       else
         acc[it - MBN][nb] = mfma16(b1[nb], x, acc[it - MBN][nb]);
     }
-    if (it < 2) b1[it] = dec(c10[it], c11[it], sc1[it]);  // (group 1's weights, a column block per iteration)
+    if (it < 2) {  // (group 1's weights, a column block per iteration)
+      if constexpr (L::K4)
+        b1[it] = pg_k4_decode(c10[it], c11[it], ks1[it], ko1[it]);
+      else
+        b1[it] = dec(c10[it], c11[it], sc1[it]);
+    }
 #pragma unroll
     for (int n = it * L::LOADS / IT; n < (it + 1) * L::LOADS / IT; n++) pg_dma_n<QT, SWIGLU>(n, b, src, meta, wv);
     __builtin_amdgcn_sched_barrier(0);  // (nothing moves from one iteration to another)
@@ -354,8 +442,16 @@ __device__ __forceinline__ PGBases pg_bases(const PrefillArgs& a, const PGCtx& c
   const int st = __builtin_amdgcn_readfirstlane(is.q < c.nq ? is.st : 0);
   PGBases b;
   b.ab = static_cast<const uint8_t*>(static_cast<const void*>(a.a)) + 128 * st;
-  b.wb0 = a.w[0] + st * L::WROW;
-  b.wb1 = (SWIGLU ? a.w[1] : a.w[0]) + st * L::WROW;
+  if constexpr (L::K4) {  // (super-block st / 4, its quarter st % 4)
+    b.wb0 = a.w[0] + (st >> 2) * 144;
+    b.wb1 = (SWIGLU ? a.w[1] : a.w[0]) + (st >> 2) * 144;
+    b.wq0 = b.wb0 + 16 + 32 * (st & 3);
+    b.wq1 = b.wb1 + 16 + 32 * (st & 3);
+  } else {
+    b.wb0 = a.w[0] + st * L::WROW;
+    b.wb1 = (SWIGLU ? a.w[1] : a.w[0]) + st * L::WROW;
+    b.wq0 = b.wq1 = nullptr;
+  }
   b.ms = reinterpret_cast<const uint8_t*>(a.row_scale);
   b.mt = a.row_a ? reinterpret_cast<const uint8_t*>(a.row_a) : b.ms;
   b.dst = __builtin_amdgcn_readfirstlane(c.lbase + is.slot * L::SBYTES);
@@ -386,10 +482,13 @@ __device__ __forceinline__ int pg_run(const PrefillArgs& a, const PGCtx& c, PGIs
   const uint32_t aof0 = uint32_t(lr * 128 + ((0 + lg) ^ sz) * 16), aof1 = uint32_t(lr * 128 + ((4 + lg) ^ sz) * 16);
   // the wave's weight rows: SwiGLU gate rows 16 wv .. + 16 (column block 0) and the same rows of up (staged at + 128);
   // plain rows 32 wv .. + 32
+  // (Q4_K: bof the row itself, its header and codes in their regions)
   uint32_t bof[2];
 #pragma unroll
-  for (int nb = 0; nb < 2; nb++)
-    bof[nb] = uint32_t(L::ABYTES + (SWIGLU ? 128 * nb + 16 * wv + lr : 32 * wv + 16 * nb + lr) * L::WROW);
+  for (int nb = 0; nb < 2; nb++) {
+    const int row = SWIGLU ? 128 * nb + 16 * wv + lr : 32 * wv + 16 * nb + lr;
+    bof[nb] = L::K4 ? uint32_t(row) : uint32_t(L::ABYTES + row * L::WROW);
+  }
   const int cb = QT == ARTLITE_Q4_0 ? 8 * (lg & 1) : 8 * lg;
   const PGDecode<QT> dec(lg);
   f32x4 acc[MBN][2];
@@ -401,7 +500,7 @@ __device__ __forceinline__ int pg_run(const PrefillArgs& a, const PGCtx& c, PGIs
     const PGBases b = pg_bases<QT, SWIGLU>(a, c, is, mq);
     const PGSrc<QT, SWIGLU> src = is.src;
     pg_advance<QT, SWIGLU>(a, c, is);
-    pg_step<QT, SWIGLU, MBN>(c.lds + cslot * L::SBYTES, aof0, aof1, bof, cb, dec, acc, src, meta, b, wv);
+    pg_step<QT, SWIGLU, MBN>(c.lds + cslot * L::SBYTES, aof0, aof1, bof, cb, st & 3, dec, acc, src, meta, b, wv);
     cslot = __builtin_amdgcn_readfirstlane(cslot + 1 == L::R ? 0 : cslot + 1);
   }
   // epilogue: lane output i of block (mb, nb): row 16 mb + lr of the tile; column (SwiGLU) n0 + 16 wv + 4 lg + i, gate
@@ -564,8 +663,9 @@ int launch_pgemm(const PrefillArgs& a, hipStream_t s) {
 bool prefill_supported(int qtype, int K, int N) {
   // (K: whole stages of 64, at least R + 1 of them: the issue side, R - 1 stages ahead, switches to the next item at
   // an item's step stages - R + 1 >= 2, after the metadata the item's first step issued has landed)
-  return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0) && K >= 64 * (PG<ARTLITE_Q4_0>::R + 1) && K % 64 == 0 &&
-         N > 0 && N % 16 == 0;
+  // (Q4_K: whole super-blocks)
+  return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0 || qtype == ARTLITE_Q4_K) &&
+         K >= 64 * (PG<ARTLITE_Q4_0>::R + 1) && K % (qtype == ARTLITE_Q4_K ? 256 : 64) == 0 && N > 0 && N % 16 == 0;
 }
 
 int launch_prefill(const PrefillArgs& a, hipStream_t s) {
@@ -576,6 +676,8 @@ int launch_prefill(const PrefillArgs& a, hipStream_t s) {
   const bool swiglu = a.w[1] != nullptr;
   if (a.qtype == ARTLITE_Q4_0)
     return swiglu ? launch_pgemm<ARTLITE_Q4_0, true>(a, s) : launch_pgemm<ARTLITE_Q4_0, false>(a, s);
+  if (a.qtype == ARTLITE_Q4_K)
+    return swiglu ? launch_pgemm<ARTLITE_Q4_K, true>(a, s) : launch_pgemm<ARTLITE_Q4_K, false>(a, s);
   return swiglu ? launch_pgemm<ARTLITE_Q8_0, true>(a, s) : launch_pgemm<ARTLITE_Q8_0, false>(a, s);
 }
 

@@ -67,6 +67,9 @@ CONFIGS = {
     # test-only: Q4_0 with about 128 pairs per expert (T = 512), so the prefill tiles' 8-row-block form runs
     "q4_rows": Spec("q4_rows", H=1024, E=8, k=2, F=512, gate_type="Q4_0", down_type="Q4_0", scale=0.02,
                     router="uniform", tokens=(512,)),
+    # the same with Q4_K gate / up and down (the prefill tiles' super-block staging in both launches)
+    "k4_rows": Spec("k4_rows", H=1024, E=8, k=2, F=512, gate_type="Q4_K", down_type="Q4_K", scale=2e-4,
+                    dmin_scale=1.5e-3, router="uniform", tokens=(512,)),
     # test-only: the other block formats of real GGUF files, on the MFMA decode tiles -- K-quants (Q5_K gate / up,
     # Q6_K down, a Q4_K / Q3_K shared expert: 16-value sub-block scales) with bf16 x, and IQ4_XS / IQ4_NL with a
     # Q4_1 shared expert and fp32 x

@@ -71,6 +71,13 @@ def test_full_q4_rows() -> None:
     assert "prefill_x" in r["kernels"] and r["counts"].min() > 64
 
 
+def test_full_k4_rows() -> None:
+    """The same small layer in Q4_K (gate / up and down): the prefill tiles' super-block staging (headers and code
+    quarters) and in-register decode in both launches, every expert over 64 rows."""
+    r = run_full("k4_rows", 512)
+    assert "prefill_x" in r["kernels"] and r["counts"].min() > 64
+
+
 def test_full_decode_cfg2_t64() -> None:
     """Config 2 at its largest decode batch (64 tokens) with a second seed."""
     r = run_full("decode", 64, seed=7)
