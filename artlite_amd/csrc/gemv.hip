@@ -492,13 +492,22 @@ struct Item {
   int ar[GEMV_BM];  // the A rows (XQ rows) of the tile's rows of A
 };
 
-// wave 0: items it0, it0 + G, ... (n of them) into tab, 64 at a time, lane j one item
+// The items of workgroup w of G, dealt back and forth: round j holds items j G .. j G + G - 1, forward in even rounds
+// and backward in odd ones (the tiles come heaviest first, so a workgroup's items even out); item j of w, and how
+// many of n_items it has.
+__device__ __forceinline__ int snake_item(int w, int j, int G) { return j * G + ((j & 1) ? G - 1 - w : w); }
+__device__ __forceinline__ int snake_count(int w, int G, int n_items) {
+  const int full = n_items / G, r = n_items - full * G;
+  return full + (r && ((full & 1) ? w >= G - r : w < r));
+}
+
+// wave 0: items snake_item(it0, 0, G), ... (n of them) into tab, 64 at a time, lane j one item
 __device__ __forceinline__ void fill_items(const GemvArgs& a, int it0, int G, int n, int NB, int rows, int4* tab,
                                            int lane) {
   for (int j0 = 0; j0 < n; j0 += 64) {
     const int j = j0 + lane;
     if (j < n) {
-      const int it = it0 + j * G, tile = it / NB;
+      const int it = snake_item(it0, j, G), tile = it / NB;
       int e = 0, s0 = tile * GEMV_BM, end = a.dense_rows;
       if (a.tiles) {
         e = a.tiles[2 * tile];
@@ -707,7 +716,7 @@ __device__ __forceinline__ void run_item(Stream<QT, SWIGLU, D>& st, const Item& 
     }
 }
 
-// A persistent workgroup: items blockIdx.x, blockIdx.x + gridDim.x, ... of (tile, block of 16 RB rows), tile-major.
+// A persistent workgroup: items snake_item(blockIdx.x, j, gridDim.x) of (tile, block of 16 RB rows), tile-major.
 template <int QT, bool SWIGLU, int D>
 __global__ __launch_bounds__(Shape<SWIGLU>::THREADS) __attribute__((amdgpu_waves_per_eu(QT == ARTLITE_Q4_0 ? 4 : 2))) void k_gemv(
     const GemvArgs a) {
@@ -723,7 +732,7 @@ __global__ __launch_bounds__(Shape<SWIGLU>::THREADS) __attribute__((amdgpu_waves
   // [buffer][wave][matrix][row of A][row], after every wave's slots
   float* red = reinterpret_cast<float*>(slab + W::WAVES * (D * SS::WCH + SS::XCH));
 
-  const int it0 = blockIdx.x, n_my = (n_items - 1 - it0) / G + 1;
+  const int it0 = blockIdx.x, n_my = snake_count(it0, G, n_items);
   constexpr int RED = W::WAVES * NM * GEMV_BM * 16;  // floats of one partial-sum buffer
   int* ctr = reinterpret_cast<int*>(red + (S > 1 ? RED_BUFS * RED : 0));  // [b]: arrivals, [4 + b]: epilogues done
   int4* tab = reinterpret_cast<int4*>(ctr + (S > 1 ? 8 : 0));

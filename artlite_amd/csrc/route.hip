@@ -458,14 +458,35 @@ __global__ __launch_bounds__(DISPATCH_BLOCK) void k_route_small(const float* __r
     base[e] = start;
   }
   if (e == 0) d.offsets[E] = total;
-  if (d.BM > 0) {  // the expert GEMMs' tiles: experts ascending, BM sorted rows each
+  if (d.BM > 0 && (d.balanced || d.BM > 4)) {  // the expert GEMMs' tiles: experts ascending, BM sorted rows each
     const int t0 = packed >> 16;
     for (int m = 0; m < nt; m++) {
       d.tiles[2 * (t0 + m)] = e;
       d.tiles[2 * (t0 + m) + 1] = start + m * rows;
     }
-    if (e == 0) d.ctrl[CTRL_TILES] = packed_total >> 16;
+  } else if (d.BM > 0) {
+    // the GEMV's tiles by rows, most first: every expert's full tiles of BM rows, then the last tiles of BM - 1
+    // rows, ..., of 1 row (experts ascending within each class), so that a persistent launch dealing its items back
+    // and forth hands each workgroup items of about equal total rows
+    const int full = e < E ? c / rows : 0, rem = e < E ? c % rows : 0;
+    int nfull, rtot;
+    const int pf = block_scan(full, &nfull);
+    // (11-bit fields: a class holds at most MAX_EXPERTS tiles; the last field's prefix stays below 2^10 and its total,
+    // which may reach 2^10 and carry out of the word, is not read)
+    const int pr = block_scan((rem == 3) | (rem == 2) << 11 | (rem == 1) << 22, &rtot);
+    for (int m = 0; m < full; m++) {
+      d.tiles[2 * (pf + m)] = e;
+      d.tiles[2 * (pf + m) + 1] = start + m * rows;
+    }
+    if (rem) {  // (class base: the full tiles, then the classes of more rows)
+      const uint32_t up = uint32_t(pr), ut = uint32_t(rtot);
+      const int n3 = int(ut & 0x7FF), n2 = int((ut >> 11) & 0x7FF);
+      const int t = nfull + (rem == 3 ? int(up & 0x7FF) : rem == 2 ? n3 + int((up >> 11) & 0x7FF) : n3 + n2 + int(up >> 22));
+      d.tiles[2 * t] = e;
+      d.tiles[2 * t + 1] = start + full * rows;
+    }
   }
+  if (d.BM > 0 && e == 0) d.ctrl[CTRL_TILES] = packed_total >> 16;
   // each pair's rank among the earlier pairs of its expert: the lanes of its wave with the same expert (ballots over
   // the id bits), then the earlier waves' counts
   uint64_t peers = __ballot(valid);
