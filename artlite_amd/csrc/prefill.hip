@@ -1,34 +1,37 @@
 // The prefill tiles: the experts' grouped GEMMs at prefill sizes (tens to hundreds of rows per expert) over raw GGUF
-// Q4_0 / Q8_0 blocks, on gfx950's fp16 MFMA (v_mfma_f32_16x16x32_f16).
+// Q4_0 / Q8_0 / Q4_K blocks, on gfx950's fp16 MFMA (v_mfma_f32_16x16x32_f16).
 //
 // Numerics. A is fp16 rows, each token's row scaled by a power of two (2^-in_exp[token]) so that its largest |x| sits
 // in [2^14, 2^15): bf16 activations convert exactly, fp32 ones round once (2^-11). Each lane decodes its 8 codes of a
 // block to fp16 d (q - 8) (Q4_0) or d q (Q8_0): the code exactly, the product with the block's fp16 scale rounded
-// once (2^-11 relative); the MFMA accumulates all of K in fp32, so no per-group scale work is left. The SwiGLU launch
-// writes h = silu(g) u in fp16 scaled by 2^-out_exp[token] (out_exp bounds |h| below 2^15); the plain launch writes
-// fp32, the A scale undone.
+// once (2^-11 relative); Q4_K: q (d sc) - dmin m in fp32 (the products exact), rounded once to fp16. The MFMA
+// accumulates all of K in fp32, so no per-group scale work is left. Each row's factors (x, y) undo the scales: the
+// SwiGLU launch writes h = silu(x g) (x u) y in fp16 (y bounds |h| below 2^15); the plain launch writes fp16 y sum
+// (y bounds it below 2^15; the row's true values are x times these) or fp32 x y sum.
 //
 // Shape of the work. An expert's sorted rows are cut into tiles of at most 256 rows of nearly equal size
 // (balanced_rows: 270 rows are two tiles of 144 and 126, not 256 and 14). An item is one tile times 256 staged
-// weight rows (SwiGLU: 128 rows of gate and the same 128 of up; plain: 256 rows). A workgroup is 4 waves, one per
-// SIMD, each with the full 512 registers: wave w takes all of the tile's rows (up to 16 MFMA row blocks) times 64
-// weight rows (4 column blocks: SwiGLU gate rows 32 w .. + 32 and the same up rows, so h forms in the wave; plain
-// rows 64 w .. + 64), 256 fp32 accumulators per lane. Per 32-value group a wave reads 16 A operands from LDS (1 KB
-// per 64 MFMA flops... 256 B of LDS per 16-cycle MFMA: half the LDS bandwidth at full MFMA rate) and decodes 4 B
-// operands (about 13 VALU each, reused by 16 row blocks: under one VALU per MFMA, the budget that matters, since on
-// gfx950 every VALU instruction delays the MFMA stream by about 2.5 cycles).
+// weight rows (SwiGLU: 128 rows of gate and the same 128 of up; plain: 256 rows). A workgroup is 8 waves, two per
+// SIMD: wave w takes all of the tile's rows (up to 16 MFMA row blocks) times 32 weight rows (2 column blocks: SwiGLU
+// gate rows 16 w .. + 16 and the same up rows, so h forms in the wave; plain rows 32 w .. + 32), 128 fp32
+// accumulators per lane; the K loop is instantiated per even row-block count so that they stay in registers.
+// Per 32-value group a wave reads an A operand from LDS per row block and decodes 2 B operands (Q4_0: about 13
+// VALU each; Q4_K: about 25, in fp32).
 //
 // Data movement. K streams in stages of 64 values (two groups) through a ring of R = 3 LDS slots filled by DMA
 // (global_load_lds, issued by asm from uniform bases with 32-bit lane offsets, so that the compiler, which would wait
-// for every DMA in flight before any LDS read it sees, does not know of them). Every wave issues the same loads per
-// stage, so each wait is a fixed count of this wave's loads: at step st, stage st must have landed and stage st + 1
-// may still be in flight; after the barrier (every wave past its reads of the previous slot) stage st + 2 is issued
-// into that slot, two steps ahead. The issue side runs on across items (the next item's first stages load while the
-// current one finishes and writes its epilogue) and, past the last item, reloads a stage of it (dummies keep the
-// counts fixed).
+// for every DMA in flight before any LDS read it sees, does not know of them), the stage's loads spread over the
+// step's MFMA iterations. Every wave issues the same loads per stage, so each wait is a fixed count of this wave's
+// loads: at step st, stage st must have landed and stage st + 1 may still be in flight; after the barrier (every
+// wave past its reads of the previous slot) stage st + 2 is issued into that slot, two steps ahead. Each item's row
+// metadata (tokens, scale factors) arrives by DMA too, and the workgroup's item table is read once at its start, so
+// no global load is waited for in the K loop. The issue side runs on across items (the next item's first stages load
+// while the current one finishes and writes its epilogue) and, past the last item, reloads a stage of it (dummies
+// keep the counts fixed).
 // A rows sit in LDS as 16-byte chunks of 8 values, XOR-swizzled by row (16 rows of an operand read in different
-// banks); a weight row's stage bytes (two blocks, 36 / 68 B) sit packed, read as aligned dwords (the first block's
-// codes start 2 bytes into it: shifted into place with alignbit).
+// banks); a weight row's stage bytes (two blocks, 36 / 68 B; Q4_K: the super-block header and the quarter's 32
+// code bytes, in two regions) sit packed, read as aligned dwords (Q4_0 / Q8_0: the first block's codes start 2 bytes
+// into it, shifted into place with alignbit).
 // MFMA layout (16x16x32): lane l holds A row l % 16 and B column l % 16, both with K values 8 (l / 16) .. + 8;
 // C column l % 16, rows 4 (l / 16) .. + 4. The decoded weights are the A operand and the activations B, so C is the
 // output transposed: a lane holds one tile row's 4 consecutive output columns, stored as one 8 / 16 B write.
