@@ -361,6 +361,7 @@ __device__ __forceinline__ void pg_step(const uint8_t* slot, uint32_t aof0, uint
     }
 #pragma unroll
     for (int it = 0; it < PF; it++) av[it] = *reinterpret_cast<const u32x4*>(a_addr(it));
+    __builtin_amdgcn_sched_barrier(0);  // (the A reads issue before the decode, so that their latency overlaps it)
 #pragma unroll
     for (int nb = 0; nb < 2; nb++) {
       float ks[2], ko[2];
@@ -378,6 +379,7 @@ __device__ __forceinline__ void pg_step(const uint8_t* slot, uint32_t aof0, uint
     for (int it = 0; it < PF; it++) av[it] = *reinterpret_cast<const u32x4*>(a_addr(it));
 #pragma unroll
     for (int nb = 0; nb < 2; nb++) pg_codes<QT>(slot + bof[nb], 1, cb, sc1[nb], c10[nb], c11[nb]);
+    __builtin_amdgcn_sched_barrier(0);  // (the A reads issue before the decode, so that their latency overlaps it)
 #pragma unroll
     for (int nb = 0; nb < 2; nb++) b0[nb] = dec(c00[nb], c01[nb], sc0[nb]);
   }
@@ -571,16 +573,51 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   const int drows = a.tiles ? 0 : balanced_rows(a.dense_rows, TILE_ROWS);
   const int64_t ntl = a.tiles ? int64_t(*a.n_tiles) : (a.dense_rows + drows - 1) / drows;
   const int64_t items = ntl * nbk, per = (items + 7) / 8;
-  // items dealt to the 8 XCDs in contiguous runs (workgroup b runs on XCD b % 8): the column blocks of a tile, and an
-  // expert's tiles, run close in time on one XCD and share its L2 (the tile's A rows, the expert's weights)
+  // Items are dealt to the 8 XCDs in contiguous runs (workgroup b runs on XCD b % 8): the column blocks of a tile, and
+  // an expert's tiles, run close in time on one XCD and share its L2 (the tile's A rows, the expert's weights). Within
+  // a run, an item costs about its tile's row blocks, so the XCD's G workgroups take the run's items ranked by row
+  // blocks (most first, then by index), dealt back and forth: position q G + j0 in even rounds, q G + G - 1 - j0 in
+  // odd ones. Every workgroup of the XCD ranks the same way, so each item is taken once (any assignment gives the
+  // same results: each item writes its own outputs).
   const int G = gridDim.x / 8, x = blockIdx.x % 8, j0 = blockIdx.x / 8;
-  const int64_t first = x * per + j0, end = min(items, (x + 1) * per);
-  if (first >= end) return;
-  c.nq = int((end - first + G - 1) / G);  // this workgroup's items: first + q G (at most MAXQ: the launch checks)
-  // the item table: every global load of the tiles and offsets, once, before any DMA is in flight
+  const int64_t lo = x * per, hi = min(items, (x + 1) * per);
+  const int n_run = hi > lo ? int(hi - lo) : 0, full = n_run / G, rem = n_run - full * G;
+  c.nq = full + (rem && ((full & 1) ? j0 >= G - rem : j0 < rem));  // (at most MAXQ: the launch checks)
+  if (c.nq == 0) return;
+  // the ranking and the item table: every global load of the tiles and offsets, once, before any DMA is in flight
+  // (the ranking's keys and order in the ring's memory, not yet in use: n_run <= MAXQ G <= 4096)
+  uint8_t* key = lds;
+  uint16_t* order = reinterpret_cast<uint16_t*>(lds + 4096);
+  for (int i = c.tid; i < n_run; i += L::THREADS)
+    key[i] = uint8_t((pg_item<SWIGLU>(a, lo + i, nbk).m_valid + 31) / 32);  // (the K loop's even row-block count / 2)
+  __syncthreads();
+  if (c.wv == 0) {  // (one wave: per key, ballots over runs of 64 items)
+    constexpr int KM = TILE_ROWS / 32;  // (keys 1 .. KM)
+    int tot[KM + 1] = {}, start[KM + 1];
+    for (int i0 = 0; i0 < n_run; i0 += WAVE) {
+      const int k = i0 + c.lane < n_run ? key[i0 + c.lane] : 0;
+#pragma unroll
+      for (int kk = 1; kk <= KM; kk++) tot[kk] += __popcll(__ballot(k == kk));
+    }
+    start[KM] = 0;  // (key KM first)
+#pragma unroll
+    for (int kk = KM - 1; kk >= 1; kk--) start[kk] = start[kk + 1] + tot[kk + 1];
+    const uint64_t below = (uint64_t(1) << c.lane) - 1;
+    for (int i0 = 0; i0 < n_run; i0 += WAVE) {
+      const int i = i0 + c.lane, k = i < n_run ? key[i] : 0;
+#pragma unroll
+      for (int kk = 1; kk <= KM; kk++) {
+        const uint64_t m = __ballot(k == kk);
+        if (k == kk) order[start[kk] + __popcll(m & below)] = uint16_t(i);
+        start[kk] += __popcll(m);
+      }
+    }
+  }
+  __syncthreads();
   if (c.tid < c.nq) {
-    const PGItem I = pg_item<SWIGLU>(a, first + int64_t(c.tid) * G, nbk);
-    table[c.tid] = make_int4(I.e, I.s0, I.m_valid, I.n0);
+    const int q = c.tid, pos = q * G + ((q & 1) ? G - 1 - j0 : j0);
+    const PGItem I = pg_item<SWIGLU>(a, lo + order[pos], nbk);
+    table[q] = make_int4(I.e, I.s0, I.m_valid, I.n0);
   }
   __syncthreads();
   // item 0's metadata, landed before its sources are made; then the first R - 1 issues (stages >= R + 1:
@@ -654,7 +691,8 @@ int launch_pgemm(const PrefillArgs& a, hipStream_t s) {
   if (resident < 8) return fail(ARTLITE_EHIP, "prefill GEMM: kernel set-up failed");
   const int64_t grid = std::min<int64_t>((items + 7) / 8 * 8, resident / 8 * 8);
   // a workgroup's items (an XCD's run of ceil(items / 8), dealt over its grid / 8 workgroups) fit its item table
-  if (((items + 7) / 8 + grid / 8 - 1) / (grid / 8) > L::MAXQ)
+  // (and an XCD's run fits the ranking's 4096 entries)
+  if (((items + 7) / 8 + grid / 8 - 1) / (grid / 8) > L::MAXQ || (items + 7) / 8 > 4096)
     return fail(ARTLITE_EINVAL, "prefill GEMM: %lld work items, more than %d per workgroup", (long long)items, L::MAXQ);
   k_pgemm<QT, SWIGLU><<<unsigned(grid), L::THREADS, L::LDS, s>>>(a);
   ART_HIP(hipGetLastError());
