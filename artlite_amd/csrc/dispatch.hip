@@ -186,6 +186,12 @@ __global__ __launch_bounds__(DISPATCH_BLOCK) void k_scatter(DispatchBufs d, Plan
   const int dest = d.table[int64_t(blockIdx.x) * d.E + id] + rank;
   d.order[dest] = int32_t(p);
   d.slot[p] = dest;
+  if (d.row_a) {  // (the prefill's per-row token and factors, gathered here rather than by a launch of their own)
+    const int t = int(p / d.k);
+    d.row_a[dest] = t;
+    d.row_out[0][dest] = d.row_f[0][t];
+    d.row_out[1][dest] = d.row_f[1][t];
+  }
   if (pl.pos) {  // the plan's row of this pair
     const int o = dest - d.offsets[id];
     const int j = d.cstart[id] + o / d.chunk, i = o % d.chunk;

@@ -44,7 +44,7 @@ struct PrefillArgs {
   int64_t expert_bytes;
   int row_bytes;
   int N, K;                // output rows per expert, values per row
-  int qtype;               // ARTLITE_Q4_0 / Q8_0
+  int qtype;               // ARTLITE_Q4_0 / Q8_0 / Q4_K
   const uint16_t* a;       // A: fp16 rows of K values
   const int32_t* row_a;    // per output row s: its A row (a token); null: A row s
   const float2* row_scale; // per output row s: (x, y) as above
@@ -71,10 +71,6 @@ int launch_prefill(const PrefillArgs& a, hipStream_t s);
 // expert's matrices wmax[2], wmax[3] into gu2, and dn2 = (2^he, 1) for its fp32 down output
 int launch_prefill_x(const void* x, int x_dtype, int64_t T, int H, const float* wmax, int pairs, int F, uint16_t* x16,
                      float2* gu, float2* dn, float2* gu2, float2* dn2, hipStream_t s);
-
-// per sorted pair row s (P of them): its token t = order[s] / k into row_a, gu[t] into gu_row, dn[t] into dn_row
-int launch_prefill_rows(const int32_t* order, int64_t P, int k, const float2* gu, const float2* dn, int32_t* row_a,
-                        float2* gu_row, float2* dn_row, hipStream_t s);
 
 // *out = a bound on max |w| over a tensor's nblocks GGUF blocks (Q4_0, Q8_0: exact; Q4_K: from d, dmin and the
 // largest 6-bit scale and min)

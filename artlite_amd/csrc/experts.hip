@@ -552,26 +552,6 @@ int launch_prefill_x(const void* x, int x_dtype, int64_t T, int H, const float* 
   return ARTLITE_OK;
 }
 
-// per sorted pair row: its token and that token's row factors, so that the prefill tiles read them with plain DMAs
-__global__ void k_prefill_rows(const int32_t* __restrict__ order, int64_t P, int k, const float2* __restrict__ gu,
-                               const float2* __restrict__ dn, int32_t* __restrict__ row_a, float2* __restrict__ gu_row,
-                               float2* __restrict__ dn_row) {
-  const int64_t s = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (s >= P) return;
-  const int t = order[s] / k;
-  row_a[s] = t;
-  gu_row[s] = gu[t];
-  dn_row[s] = dn[t];
-}
-
-int launch_prefill_rows(const int32_t* order, int64_t P, int k, const float2* gu, const float2* dn, int32_t* row_a,
-                        float2* gu_row, float2* dn_row, hipStream_t s) {
-  if (P <= 0) return ARTLITE_OK;
-  k_prefill_rows<<<unsigned((P + 255) / 256), 256, 0, s>>>(order, P, k, gu, dn, row_a, gu_row, dn_row);
-  ART_HIP(hipGetLastError());
-  return ARTLITE_OK;
-}
-
 // ---- a bound on max |w| of a weight tensor's blocks: the fp16 scale's magnitude times the format's largest code
 // (Q4_0: 8, Q8_0: 128; Q4_K: |d| 63 15 + |dmin| 63, its 6-bit scale and min at their largest), by an atomic max on the
 // float's bits (non-negative floats order as their bits)

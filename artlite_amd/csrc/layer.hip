@@ -153,7 +153,6 @@ std::vector<std::string> kernel_list(const artlite_moe_layer* L, int64_t T) {
     k.push_back("dispatch_count");
     k.push_back("dispatch_scatter");
   }
-  if (p.prefill) k.push_back("prefill_rows");
   k.push_back("gate_up");
   if (p.gemv_gu && !p.gemv) k.push_back("h_planes");
   k.push_back("down");
@@ -211,6 +210,13 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
   DispatchBufs db{L->ids.as<int32_t>(), P, E, k, L->table.as<int32_t>(), L->ctrl.as<int32_t>(),
                   L->counts.as<int32_t>(), L->offsets.as<int32_t>(), L->order.as<int32_t>(), L->slot.as<int32_t>(),
                   L->tiles.as<int32_t>(), BM, nullptr, 0, path.prefill ? 1 : 0};
+  if (path.prefill) {  // (the scatter also writes each sorted row's token and factors)
+    db.row_a = L->row_a.as<int32_t>();
+    db.row_f[0] = L->gu_tok.as<float2>();
+    db.row_f[1] = L->dn_tok.as<float2>();
+    db.row_out[0] = L->gu_row.as<float2>();
+    db.row_out[1] = L->dn_row.as<float2>();
+  }
   if (path.small) {
     ART_TRY(mark());
     ART_TRY(launch_route_small(L->logits.as<float>(), T, E, k, d.gating, L->ids.as<int32_t>(), L->w.as<float>(), db,
@@ -224,11 +230,6 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     ART_TRY(launch_dispatch_count(db, nb, s));
     ART_TRY(mark());
     ART_TRY(launch_dispatch_scatter(db, nb, s));
-  }
-  if (path.prefill) {
-    ART_TRY(mark());
-    ART_TRY(launch_prefill_rows(L->order.as<int32_t>(), P, k, L->gu_tok.as<float2>(), L->dn_tok.as<float2>(),
-                                L->row_a.as<int32_t>(), L->gu_row.as<float2>(), L->dn_row.as<float2>(), s));
   }
   if (path.gemv_gu) {
     GemvArgs g{};

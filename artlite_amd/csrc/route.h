@@ -161,6 +161,11 @@ struct DispatchBufs {
   int32_t* cstart;   // E + 1 chunk prefix (plan only; may be null)
   int chunk;         // plan chunk size (0: no plan)
   int balanced = 0;  // 1: an expert's c rows in tiles of balanced_rows(c, BM) rows (the last one shorter)
+  // (optional, the prefill path) per sorted row s, filled by the scatter: its token t = order[s] / k into row_a, and
+  // that token's row factors row_f[0][t], row_f[1][t] into row_out[0][s], row_out[1][s]
+  int32_t* row_a = nullptr;
+  const float2* row_f[2] = {nullptr, nullptr};
+  float2* row_out[2] = {nullptr, nullptr};
 };
 
 // rows per tile when an expert's c rows are split into tiles of at most bm rows of nearly equal size: the fewest
