@@ -38,6 +38,8 @@
 #include "experts.h"
 #include "route.h"
 
+#include <utility>
+
 namespace artlite {
 
 namespace {
@@ -110,6 +112,24 @@ __device__ __forceinline__ void pg_dma(const void* base, uint32_t off, uint32_t 
 __device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
                                                  0);
+}
+
+// v as a value the compiler cannot hoist: what the rare paths (item switches, epilogues) compute from a lane's index
+// is computed there, not kept in registers (or spilled) throughout the K loop
+__device__ __forceinline__ int pg_fresh(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// f(std::integral_constant<int, i>{}) for i = 0 .. N - 1, expanded at compile time (loops this long and this large
+// are not always unrolled, and their registers, accumulators included, must be indexed by constants)
+template <typename F, int... I>
+__device__ __forceinline__ void pg_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void pg_for(F&& f) {
+  pg_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 // Decode of a lane's 8 weights to fp16: the code bytes spread into fp16 1024 + c (c < 256 exact, one perm per two),
@@ -228,6 +248,7 @@ struct PGSrc {
   uint32_t w[L::BI];
   __device__ __forceinline__ static int swz(int r) { return (r >> 1) & 7; }
   __device__ __forceinline__ void set(const PrefillArgs& g, const PGItem& I, const int32_t* tok, int tid) {
+    tid = pg_fresh(tid);
 #pragma unroll
     for (int i = 0; i < L::AI; i++) {
       const int p = i * L::THREADS + tid, r = p >> 3, c = (p & 7) ^ swz(r);
@@ -260,6 +281,7 @@ struct PGSrc {
 struct PGMeta {
   uint32_t m[2];
   __device__ __forceinline__ void set(const PrefillArgs& g, const PGItem& I, int tid) {
+    tid = pg_fresh(tid);
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const int u = j * 512 + tid;
@@ -275,134 +297,144 @@ struct PGMeta {
   }
 };
 
-// the issue side: the item whose stages are being issued, its next stage, the ring slot they go to
-template <int QT, bool SWIGLU>
-struct PGIssue {
-  PGSrc<QT, SWIGLU> src;
-  int st;    // its next stage
-  int q;     // its index among this workgroup's items (nq: past the last, dummies)
-  int slot;  // the ring slot of the next issue
-};
-
-// The codes of one block of the lane's weight row (row: its stage bytes in LDS): block g (0, 1) of the stage; cb the
-// lane group's code byte offset (Q4_0: 8 (lg & 1), both nibbles of those 8 bytes; Q8_0: 8 lg).
-template <int QT>
-__device__ __forceinline__ void pg_codes(const uint8_t* row, int g, int cb, uint32_t& sc, uint32_t& c0, uint32_t& c1) {
-  constexpr int GB = PG<QT>::GB;
-  if (g == 0) {  // codes at + 2 + cb: two bytes past a dword boundary
-    const uint32_t* d = reinterpret_cast<const uint32_t*>(row + cb);
-    const uint32_t d0 = d[0], d1 = d[1], d2 = d[2];
-    c0 = __builtin_amdgcn_alignbit(d1, d0, 16);
-    c1 = __builtin_amdgcn_alignbit(d2, d1, 16);
-    sc = *reinterpret_cast<const uint16_t*>(row);
-  } else {  // codes at GB + 2 + cb: dword-aligned (GB + 2 is 20 or 36)
-    const uint32_t* d = reinterpret_cast<const uint32_t*>(row + GB + 2 + cb);
-    c0 = d[0];
-    c1 = d[1];
-    sc = *reinterpret_cast<const uint16_t*>(row + GB);
-  }
-}
-
-// The DMA sources of one issue (one stage of the issue item plus the metadata of the item after the compute item):
-// uniform base pointers (at that stage) and destination slots; the lanes' offsets are in PGSrc and PGMeta.
+// The DMA sources of the open window (one stage of the issue item plus the metadata of item mq): uniform base pointers
+// (at that stage) and destination slots; the lanes' offsets are in PGSrc and PGMeta.
 struct PGBases {
   const uint8_t *ab, *wb0, *wb1, *mt, *ms;
   const uint8_t *wq0, *wq1;  // (Q4_K: the stage's code bytes; wb0, wb1 its super-block headers)
   uint32_t dst, mdst;
 };
 
-// One DMA of an issue: n < AI an A chunk, then the weights' dwords, then the metadata's (instruction i of wave w
-// writes the region's bytes (8 i + w) 64 + lane times the DMA's size).
+// The issue side: the item whose stages are being issued, the stage and ring slot of the window last opened, the item
+// whose metadata the windows carry (mq), and the open window's bases.
 template <int QT, bool SWIGLU>
-__device__ __forceinline__ void pg_dma_n(int n, const PGBases& b, const PGSrc<QT, SWIGLU>& src, const PGMeta& meta,
-                                         int wv) {
+struct PGIssue {
+  PGSrc<QT, SWIGLU> src;
+  PGMeta meta;
+  PGBases b;
+  int st;    // the window's stage of item q
+  int q;     // its index among this workgroup's items (nq: past the last, dummies)
+  int slot;  // its ring slot
+  int mq;
+};
+
+// One DMA of the open window: n < BI the weights' dwords (first: they come from HBM), then the A chunks, then the
+// metadata's dwords (instruction i of wave w writes the region's bytes (8 i + w) 64 + lane times the DMA's size).
+template <int QT, bool SWIGLU>
+__device__ __forceinline__ void pg_dma_n(int n, const PGIssue<QT, SWIGLU>& is, int wv) {
   using L = PG<QT>;
-  if (n < L::AI) {
-    pg_dma<16>(b.ab, src.a[n], b.dst + (8 * n + wv) * 1024);
-  } else if (n < L::AI + L::BI) {
-    const int j = n - L::AI;
+  const PGBases& b = is.b;
+  if (n < L::BI) {
+    const int j = n;
     const uint8_t* base;
     if constexpr (L::K4)  // (headers: instruction 1 reads up's; codes: instructions 4, 5)
       base = j < 2 ? (SWIGLU && j == 1 ? b.wb1 : b.wb0) : (SWIGLU && j >= 4 ? b.wq1 : b.wq0);
     else
       base = SWIGLU && (j * L::THREADS + 64 * wv) >= 128 * L::WDW ? b.wb1 : b.wb0;
-    pg_dma<4>(base, src.w[j], b.dst + L::ABYTES + (8 * j + wv) * 256);
+    pg_dma<4>(base, is.src.w[j], b.dst + L::ABYTES + (8 * j + wv) * 256);
+  } else if (n < L::BI + L::AI) {
+    const int i = n - L::BI;
+    pg_dma<16>(b.ab, is.src.a[i], b.dst + (8 * i + wv) * 1024);
   } else {
-    const int j = n - L::AI - L::BI;
-    pg_dma<4>(j == 0 && wv < 4 ? b.mt : b.ms, meta.m[j], b.mdst + (8 * j + wv) * 256);
+    const int j = n - L::BI - L::AI;
+    pg_dma<4>(j == 0 && wv < 4 ? b.mt : b.ms, is.meta.m[j], b.mdst + (8 * j + wv) * 256);
   }
 }
 
-// One step: stage st's products (two groups) -- MBN row blocks of the tile times the wave's 2 column blocks -- with
-// one issue's DMAs spread among them. The work is laid out as IT = 2 MBN iterations (group 0's row blocks, then group
-// 1's), pinned in order by scheduling barriers; an iteration issues its row block's 2 MFMAs, reads the A operand of the
-// iteration PF ahead and issues its share of the DMAs, and the first two decode a column block of group 1's weights.
-// aof: the lane's A chunk offset in a slot for group 0 (aof1: group 1); bof: its weight row's offset per column block.
-template <int QT, bool SWIGLU, int MBN>
-__device__ __forceinline__ void pg_step(const uint8_t* slot, uint32_t aof0, uint32_t aof1, const uint32_t (&bof)[2],
-                                        int cb, int qi, const PGDecode<QT>& dec, f32x4 (&acc)[MBN][2],
-                                        const PGSrc<QT, SWIGLU>& src, const PGMeta& meta, const PGBases& b, int wv) {
-  using L = PG<QT>;
-  constexpr int IT = 2 * MBN, PF = MBN < 4 ? MBN : 4;
-  auto a_addr = [&](int it) { return slot + (it < MBN ? aof0 : aof1) + (it % MBN) * 2048; };
-  // group 1's codes and scales (Q4_K: the same code bytes' high nibbles, the second sub-block's scale and min)
-  uint32_t sc0[2], c00[2], c01[2], sc1[2], c10[2], c11[2];
-  float ks1[2], ko1[2];
-  u32x4 av[PF + 1];
-  u32x4 b0[2], b1[2];
-  if constexpr (L::K4) {  // (bof: the lane's weight row in the item; cb: its code bytes' offset, 8 lg)
-    u32x4 h[2];
+// The lane's fixed places: its A chunk in a slot for row block 0 of group 0 (aof0) and of group 1 (aof1); its weight
+// row per column block (bof: the row's stage bytes in a slot; Q4_K: the row itself, its header and codes in their
+// regions): SwiGLU gate rows 16 wv .. + 16 (column block 0) and the same rows of up (staged at + 128), plain rows
+// 32 wv .. + 32; cb its code bytes' offset in a block (Q4_K: in the quarter's 32 bytes, 8 lg).
+template <int QT>
+struct PGLane {
+  uint32_t aof0, aof1, bof[2];
+  int cb;
+  PGDecode<QT> dec;
+  __device__ __forceinline__ PGLane(int lr, int lg, int wv, bool swiglu) : dec(lg) {
+    const int sz = (lr >> 1) & 7;  // (the A rows' chunk swizzle, PGSrc::swz)
+    aof0 = uint32_t(lr * 128 + ((0 + lg) ^ sz) * 16);
+    aof1 = uint32_t(lr * 128 + ((4 + lg) ^ sz) * 16);
 #pragma unroll
     for (int nb = 0; nb < 2; nb++) {
-      h[nb] = *reinterpret_cast<const u32x4*>(slot + L::ABYTES + bof[nb] * 16);
-      const uint32_t* c = reinterpret_cast<const uint32_t*>(slot + L::ABYTES + L::KHDR + bof[nb] * 32 + cb);
-      c00[nb] = c[0];
-      c01[nb] = c[1];
+      const int row = swiglu ? 128 * nb + 16 * wv + lr : 32 * wv + 16 * nb + lr;
+      bof[nb] = PG<QT>::K4 ? uint32_t(row) : uint32_t(PG<QT>::ABYTES + row * PG<QT>::WROW);
     }
-#pragma unroll
-    for (int it = 0; it < PF; it++) av[it] = *reinterpret_cast<const u32x4*>(a_addr(it));
-    __builtin_amdgcn_sched_barrier(0);  // (the A reads issue before the decode, so that their latency overlaps it)
-#pragma unroll
-    for (int nb = 0; nb < 2; nb++) {
-      float ks[2], ko[2];
-      pg_k4_scales(h[nb], qi, ks, ko);
-      ks1[nb] = ks[1];
-      ko1[nb] = ko[1];
-      c10[nb] = (c00[nb] >> 4) & 0x0F0F0F0Fu;
-      c11[nb] = (c01[nb] >> 4) & 0x0F0F0F0Fu;
-      b0[nb] = pg_k4_decode(c00[nb] & 0x0F0F0F0Fu, c01[nb] & 0x0F0F0F0Fu, ks[0], ko[0]);
-    }
-  } else {
-#pragma unroll
-    for (int nb = 0; nb < 2; nb++) pg_codes<QT>(slot + bof[nb], 0, cb, sc0[nb], c00[nb], c01[nb]);
-#pragma unroll
-    for (int it = 0; it < PF; it++) av[it] = *reinterpret_cast<const u32x4*>(a_addr(it));
-#pragma unroll
-    for (int nb = 0; nb < 2; nb++) pg_codes<QT>(slot + bof[nb], 1, cb, sc1[nb], c10[nb], c11[nb]);
-    __builtin_amdgcn_sched_barrier(0);  // (the A reads issue before the decode, so that their latency overlaps it)
-#pragma unroll
-    for (int nb = 0; nb < 2; nb++) b0[nb] = dec(c00[nb], c01[nb], sc0[nb]);
+    cb = QT == ARTLITE_Q4_0 ? 8 * (lg & 1) : 8 * lg;
   }
+};
+
+// The weight operands a step starts with: group 0's weights decoded, group 1's codes and scale (Q4_K: the code bytes'
+// high nibbles, the second sub-block's scale and min). The previous step reads and decodes them in its last
+// iterations, past the barrier that certifies their stage, so that a step's MFMAs start as soon as the last ones of
+// the previous step. (Its first 4 A operands come the same way, through the ring of A operands.)
+template <int QT>
+struct PGOps {
+  u32x4 b0[2];
+  uint32_t c10[2], c11[2], sc1[2];  // (Q4_0 / Q8_0: the scale in sc1's high half)
+  float ks1[2], ko1[2];
+};
+
+// What the decode of group 0 takes, as read from LDS: its code dwords and scale (Q4_0 / Q8_0: the codes start two bytes
+// into d[0], and the scale is sc0's low half; shifted and masked at the decode, not at the read, so that the read's
+// iteration does not wait for the data; Q4_K: d[0], d[1] the code bytes, h the super-block headers).
+template <int QT>
+struct PGRaw {
+  uint32_t d[3][2], sc0[2];
+  u32x4 h[2];
+};
+
+// The LDS reads of a step's weight codes from its slot s, all aligned dwords: per column block, group 0's from the lane
+// group's code byte offset cb (Q4_0: 8 (lg & 1), both nibbles of those 8 bytes; Q8_0: 8 lg) two bytes past the
+// block's scale (the row's first dword: the scale in its low half); group 1's from GB + 2 + cb (20 or 36), its scale
+// the high half of the dword at GB - 2.
+template <int QT>
+__device__ __forceinline__ void pg_read_codes(const uint8_t* s, const PGLane<QT>& ln, PGOps<QT>& o, PGRaw<QT>& r) {
+  using L = PG<QT>;
 #pragma unroll
-  for (int it = 0; it < IT; it++) {
-    if (it + PF < IT) av[(it + PF) % (PF + 1)] = *reinterpret_cast<const u32x4*>(a_addr(it + PF));
-    const u32x4 x = av[it % (PF + 1)];
-#pragma unroll
-    for (int nb = 0; nb < 2; nb++) {
-      if (it < MBN)
-        acc[it][nb] = mfma16(b0[nb], x, acc[it][nb]);
-      else
-        acc[it - MBN][nb] = mfma16(b1[nb], x, acc[it - MBN][nb]);
+  for (int nb = 0; nb < 2; nb++) {
+    if constexpr (L::K4) {
+      r.h[nb] = *reinterpret_cast<const u32x4*>(s + L::ABYTES + ln.bof[nb] * 16);
+      const uint32_t* c = reinterpret_cast<const uint32_t*>(s + L::ABYTES + L::KHDR + ln.bof[nb] * 32 + ln.cb);
+      r.d[0][nb] = c[0];
+      r.d[1][nb] = c[1];
+    } else {
+      const uint8_t* row = s + ln.bof[nb];
+      const uint32_t* d = reinterpret_cast<const uint32_t*>(row + ln.cb);
+      r.d[0][nb] = d[0];
+      r.d[1][nb] = d[1];
+      r.d[2][nb] = d[2];
+      r.sc0[nb] = *reinterpret_cast<const uint32_t*>(row);
+      const uint32_t* e = reinterpret_cast<const uint32_t*>(row + L::GB + 2 + ln.cb);
+      o.c10[nb] = e[0];
+      o.c11[nb] = e[1];
+      o.sc1[nb] = *reinterpret_cast<const uint32_t*>(row + L::GB - 2);
     }
-    if (it < 2) {  // (group 1's weights, a column block per iteration)
-      if constexpr (L::K4)
-        b1[it] = pg_k4_decode(c10[it], c11[it], ks1[it], ko1[it]);
-      else
-        b1[it] = dec(c10[it], c11[it], sc1[it]);
-    }
-#pragma unroll
-    for (int n = it * L::LOADS / IT; n < (it + 1) * L::LOADS / IT; n++) pg_dma_n<QT, SWIGLU>(n, b, src, meta, wv);
-    __builtin_amdgcn_sched_barrier(0);  // (nothing moves from one iteration to another)
+  }
+}
+
+// A operand j < 4 of a step from its slot s: iteration j's (group j < MBN ? 0 : 1, row block j % MBN; small: the
+// step's tile has 2 row blocks, so operands 2, 3 are group 1's row blocks 0, 1)
+template <int QT>
+__device__ __forceinline__ u32x4 pg_read_a0(const uint8_t* s, const PGLane<QT>& ln, bool small, int j) {
+  const uint32_t o = j < 2 ? ln.aof0 + j * 2048 : small ? ln.aof1 + (j - 2) * 2048 : ln.aof0 + j * 2048;
+  return *reinterpret_cast<const u32x4*>(s + o);
+}
+
+// group 0's weights of column block nb (Q4_K: also group 1's scale, min and codes; qi the stage's quarter of its
+// super-block)
+template <int QT>
+__device__ __forceinline__ void pg_decode0(PGOps<QT>& o, const PGRaw<QT>& r, const PGLane<QT>& ln, int qi, int nb) {
+  if constexpr (PG<QT>::K4) {
+    float ks[2], ko[2];
+    pg_k4_scales(r.h[nb], qi, ks, ko);
+    o.ks1[nb] = ks[1];
+    o.ko1[nb] = ko[1];
+    o.c10[nb] = (r.d[0][nb] >> 4) & 0x0F0F0F0Fu;
+    o.c11[nb] = (r.d[1][nb] >> 4) & 0x0F0F0F0Fu;
+    o.b0[nb] = pg_k4_decode(r.d[0][nb] & 0x0F0F0F0Fu, r.d[1][nb] & 0x0F0F0F0Fu, ks[0], ko[0]);
+  } else {
+    o.b0[nb] = ln.dec(__builtin_amdgcn_alignbit(r.d[1][nb], r.d[0][nb], 16),
+                      __builtin_amdgcn_alignbit(r.d[2][nb], r.d[1][nb], 16), r.sc0[nb] & 0xFFFFu);
   }
 }
 
@@ -438,14 +470,23 @@ __device__ __forceinline__ PGItem pg_table(const PGCtx& c, int q) {
                 __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w)};
 }
 
-// The bases of the next issue: the issue item's next stage (past the last item, a reload of stage 0: dummies keep the
-// counts fixed), and the metadata DMAs of item mq into its buffer.
+// Opens the next window: the next stage of the issue item (past its last, the next item, its sources from its
+// metadata, which landed two windows after the first that carried it) into the next ring slot, with the metadata of
+// item mq (>= 0: a new one) into its buffer; past the last item, a reload of stage 0 (dummies keep the counts fixed).
 template <int QT, bool SWIGLU>
-__device__ __forceinline__ PGBases pg_bases(const PrefillArgs& a, const PGCtx& c, const PGIssue<QT, SWIGLU>& is,
-                                            int mq) {
+__device__ __forceinline__ void pg_open(const PrefillArgs& a, const PGCtx& c, PGIssue<QT, SWIGLU>& is, int mq) {
   using L = PG<QT>;
+  if (mq >= 0 && mq != is.mq) {
+    is.mq = mq;
+    is.meta.set(a, pg_table(c, mq), c.tid);
+  }
+  is.slot = is.slot + 1 == L::R ? 0 : is.slot + 1;
+  if (is.q < c.nq && ++is.st == c.stages) {
+    is.st = 0;
+    if (++is.q < c.nq) is.src.set(a, pg_table(c, is.q), pg_tok<QT>(c, is.q), c.tid);
+  }
   const int st = __builtin_amdgcn_readfirstlane(is.q < c.nq ? is.st : 0);
-  PGBases b;
+  PGBases& b = is.b;
   b.ab = static_cast<const uint8_t*>(static_cast<const void*>(a.a)) + 128 * st;
   if constexpr (L::K4) {  // (super-block st / 4, its quarter st % 4)
     b.wb0 = a.w[0] + (st >> 2) * 144;
@@ -460,57 +501,100 @@ __device__ __forceinline__ PGBases pg_bases(const PrefillArgs& a, const PGCtx& c
   b.ms = reinterpret_cast<const uint8_t*>(a.row_scale);
   b.mt = a.row_a ? reinterpret_cast<const uint8_t*>(a.row_a) : b.ms;
   b.dst = __builtin_amdgcn_readfirstlane(c.lbase + is.slot * L::SBYTES);
-  b.mdst = __builtin_amdgcn_readfirstlane(c.lbase + L::R * L::SBYTES + (mq & 1) * L::META);
-  return b;
+  b.mdst = __builtin_amdgcn_readfirstlane(c.lbase + L::R * L::SBYTES + (is.mq & 1) * L::META);
 }
 
-// The issue side moves on: the next slot; past an item's last stage, the next item (its sources from its metadata,
-// which the DMAs of the compute item's first steps brought into LDS).
-template <int QT, bool SWIGLU>
-__device__ __forceinline__ void pg_advance(const PrefillArgs& a, const PGCtx& c, PGIssue<QT, SWIGLU>& is) {
+// One step: the products of the stage in slot s (two groups) -- MBN row blocks of the tile times the wave's 2 column
+// blocks -- laid out as IT = 2 MBN iterations (group 0's row blocks, then group 1's) pinned in order by scheduling
+// barriers. Iteration it issues its row block's 2 MFMAs on A operand av[it % 4] and then reads into that register the
+// operand of iteration it + 4 (IT is a multiple of 4, so the ring runs on from step to step: the last 4 iterations
+// read the next step's first 4 operands); the first two decode a column block of group 1's weights. Four iterations
+// before the end comes the workgroup's barrier: this wave's reads of slot s are all issued by then, and the stage in
+// the next slot ns has landed (vmcnt: only the window opened at the previous barrier may be in flight). Past it the
+// wave reads the next step's operands from ns (nqi: that stage's quarter; nsmall: its tile has 2 row blocks) and
+// decodes its group 0 weights in the last two iterations, opens the next window (into slot s: every wave is done
+// reading it) and issues that window's weight DMAs; its other DMAs go out in the next step's iterations before the
+// barrier (2 row blocks: none, so at the step's start). nmq >= 0: the item whose metadata the windows carry from now
+// on.
+template <int QT, bool SWIGLU, int MBN>
+__device__ __forceinline__ void pg_step(const PrefillArgs& a, const PGCtx& c, PGIssue<QT, SWIGLU>& is,
+                                        const PGLane<QT>& ln, PGOps<QT>& ops, u32x4 (&av)[4], const uint8_t* s,
+                                        const uint8_t* ns, int nqi, bool nsmall, int nmq, f32x4 (&acc)[MBN][2]) {
   using L = PG<QT>;
-  is.slot = is.slot + 1 == L::R ? 0 : is.slot + 1;
-  if (is.q < c.nq && ++is.st == c.stages) {
-    is.st = 0;
-    if (++is.q < c.nq) is.src.set(a, pg_table(c, is.q), pg_tok<QT>(c, is.q), c.tid);
+  constexpr int IT = 2 * MBN, HEAD = IT - 4, HS = L::LOADS - L::BI;
+  auto a_addr = [&](int it) { return s + (it < MBN ? ln.aof0 : ln.aof1) + (it % MBN) * 2048; };
+  u32x4 b1[2];
+  PGOps<QT> nx;
+  PGRaw<QT> raw;
+  if constexpr (HEAD == 0) {
+#pragma unroll
+    for (int n = L::BI; n < L::LOADS; n++) pg_dma_n<QT, SWIGLU>(n, is, c.wv);
   }
+  pg_for<IT>([&](auto itc) __attribute__((always_inline)) {
+    constexpr int it = decltype(itc)::value;
+    if constexpr (it == HEAD) {
+      pg_wait<L::LOADS>();
+      pg_barrier();
+    }
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) {
+      if constexpr (it < MBN)
+        acc[it][nb] = mfma16(ops.b0[nb], av[it % 4], acc[it][nb]);
+      else
+        acc[it - MBN][nb] = mfma16(b1[nb], av[it % 4], acc[it - MBN][nb]);
+    }
+    if constexpr (it == HEAD) pg_read_codes<QT>(ns, ln, nx, raw);
+    if constexpr (it < HEAD)
+      av[it % 4] = *reinterpret_cast<const u32x4*>(a_addr(it + 4));
+    else
+      av[it % 4] = pg_read_a0<QT>(ns, ln, nsmall, it - HEAD);
+    if constexpr (it == HEAD) pg_open<QT, SWIGLU>(a, c, is, nmq);
+    if constexpr (it < 2) {  // (group 1's weights, a column block per iteration)
+      if constexpr (L::K4)
+        b1[it] = pg_k4_decode(ops.c10[it], ops.c11[it], ops.ks1[it], ops.ko1[it]);
+      else
+        b1[it] = ln.dec(ops.c10[it], ops.c11[it], ops.sc1[it] >> 16);
+    }
+    if constexpr (it >= IT - 2) pg_decode0<QT>(nx, raw, ln, nqi, it - (IT - 2));
+    if constexpr (it < HEAD) {  // (the window opened at the previous barrier: A and metadata)
+#pragma unroll
+      for (int n = L::BI + it * HS / HEAD; n < L::BI + (it + 1) * HS / HEAD; n++) pg_dma_n<QT, SWIGLU>(n, is, c.wv);
+    } else {  // (the window just opened: weights)
+      constexpr int j = it - HEAD;
+#pragma unroll
+      for (int n = j * L::BI / 4; n < (j + 1) * L::BI / 4; n++) pg_dma_n<QT, SWIGLU>(n, is, c.wv);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // (nothing moves from one iteration to another)
+  });
+  ops = nx;
 }
 
-// One item: its K loop (stage by stage through the ring) and its epilogue. cslot: the slot of its stage 0; meta / mq:
-// the metadata DMAs every step issues (of item mq).
+// One item: its K loop (stage by stage through the ring; cslot: the slot of its stage 0) and its epilogue. Its first
+// step's operands are read already (ops, av), and its last step reads those of the next item's first.
 template <int QT, bool SWIGLU, int MBN>
 __device__ __forceinline__ int pg_run(const PrefillArgs& a, const PGCtx& c, PGIssue<QT, SWIGLU>& is,
-                                      const PGMeta& meta, int mq, const PGItem& I, int q, int cslot) {
+                                      const PGLane<QT>& ln, PGOps<QT>& ops, u32x4 (&av)[4], const PGItem& I, int q,
+                                      int cslot) {
   using L = PG<QT>;
-  const int lr = c.lr, lg = c.lg, wv = c.wv;
-  const int sz = PGSrc<QT, SWIGLU>::swz(lr);
-  const uint32_t aof0 = uint32_t(lr * 128 + ((0 + lg) ^ sz) * 16), aof1 = uint32_t(lr * 128 + ((4 + lg) ^ sz) * 16);
-  // the wave's weight rows: SwiGLU gate rows 16 wv .. + 16 (column block 0) and the same rows of up (staged at + 128);
-  // plain rows 32 wv .. + 32
-  // (Q4_K: bof the row itself, its header and codes in their regions)
-  uint32_t bof[2];
-#pragma unroll
-  for (int nb = 0; nb < 2; nb++) {
-    const int row = SWIGLU ? 128 * nb + 16 * wv + lr : 32 * wv + 16 * nb + lr;
-    bof[nb] = L::K4 ? uint32_t(row) : uint32_t(L::ABYTES + row * L::WROW);
-  }
-  const int cb = QT == ARTLITE_Q4_0 ? 8 * (lg & 1) : 8 * lg;
-  const PGDecode<QT> dec(lg);
+  const int wv = c.wv;
   f32x4 acc[MBN][2];
 #pragma unroll
   for (int mb = 0; mb < MBN; mb++) acc[mb][0] = acc[mb][1] = f32x4{0, 0, 0, 0};
+  // From the item's first barrier on the windows carry the metadata of item q + 1 (into the buffer of item q - 1,
+  // whose epilogue every wave is past by then), else item q's again. The last step's reads are for the next item.
+  const int nmq = q + 1 < c.nq ? q + 1 : q;
+  bool nsmall = false;
+  if (q + 1 < c.nq) nsmall = pg_table(c, q + 1).m_valid <= 32;
   for (int st = 0; st < c.stages; st++) {
-    pg_wait<L::LOADS>();  // (stage st: only the issue after it may be in flight)
-    pg_barrier();         // (every wave's stage st landed; every wave past its reads of the previous slot)
-    const PGBases b = pg_bases<QT, SWIGLU>(a, c, is, mq);
-    const PGSrc<QT, SWIGLU> src = is.src;
-    pg_advance<QT, SWIGLU>(a, c, is);
-    pg_step<QT, SWIGLU, MBN>(c.lds + cslot * L::SBYTES, aof0, aof1, bof, cb, st & 3, dec, acc, src, meta, b, wv);
-    cslot = __builtin_amdgcn_readfirstlane(cslot + 1 == L::R ? 0 : cslot + 1);
+    const int ns = cslot + 1 == L::R ? 0 : cslot + 1;
+    pg_step<QT, SWIGLU, MBN>(a, c, is, ln, ops, av, c.lds + cslot * L::SBYTES, c.lds + ns * L::SBYTES, (st + 1) & 3,
+                             st + 1 < c.stages ? MBN == 2 : nsmall, st == 0 ? nmq : -1, acc);
+    cslot = __builtin_amdgcn_readfirstlane(ns);
   }
   // epilogue: lane output i of block (mb, nb): row 16 mb + lr of the tile; column (SwiGLU) n0 + 16 wv + 4 lg + i, gate
   // in nb 0 and up in nb 1; (plain) n0 + 32 wv + 16 nb + 4 lg + i. A lane stores its row's 4 columns at once.
   const float2* rf = pg_rowf<QT>(c, q);
+  const int lr = pg_fresh(c.lr), lg = pg_fresh(c.lg);
 #pragma unroll
   for (int mb = 0; mb < MBN; mb++) {
     const int m = 16 * mb + lr;
@@ -620,32 +704,49 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     table[q] = make_int4(I.e, I.s0, I.m_valid, I.n0);
   }
   __syncthreads();
-  // item 0's metadata, landed before its sources are made; then the first R - 1 issues (stages >= R + 1:
-  // prefill_supported), each with the metadata of item 1 (item 0's again when there is none)
-  PGMeta meta;
-  PGItem I = pg_table(c, 0);
-  meta.set(a, I, c.tid);
+  // item 0's metadata, landed before its sources are made (buffer 0)
   PGIssue<QT, SWIGLU> is;
-  is.q = 0;
-  is.st = 0;
-  is.slot = 0;
+  PGItem I = pg_table(c, 0);
+  is.meta.set(a, I, c.tid);
   {
-    PGBases b = pg_bases<QT, SWIGLU>(a, c, is, 0);
+    const uint8_t* ms = reinterpret_cast<const uint8_t*>(a.row_scale);
+    const uint8_t* mt = a.row_a ? reinterpret_cast<const uint8_t*>(a.row_a) : ms;
+    const uint32_t mdst = __builtin_amdgcn_readfirstlane(c.lbase + L::R * L::SBYTES);
 #pragma unroll
-    for (int j = 0; j < L::MI; j++) pg_dma_n<QT, SWIGLU>(L::AI + L::BI + j, b, is.src, meta, c.wv);
+    for (int j = 0; j < L::MI; j++) pg_dma<4>(j == 0 && c.wv < 4 ? mt : ms, is.meta.m[j], mdst + (8 * j + c.wv) * 256);
     pg_wait<0>();
     __syncthreads();
   }
+  // the windows of stages 0 and 1 (stages >= R + 2: prefill_supported), carrying item 1's metadata (item 0's again
+  // when there is none); the barrier that certifies stage 0; the window of stage 2, its weights now, the rest in
+  // the first step; the first step's operands
   is.src.set(a, I, pg_tok<QT>(c, 0), c.tid);
-  int mq = c.nq > 1 ? 1 : 0;
-  meta.set(a, pg_table(c, mq), c.tid);
+  is.q = 0;
+  is.st = -1;
+  is.slot = -1;
+  is.mq = 0;
+  const int mq = c.nq > 1 ? 1 : 0;
 #pragma unroll
-  for (int j = 0; j < L::R - 1; j++) {
-    const PGBases b = pg_bases<QT, SWIGLU>(a, c, is, mq);
-    const PGSrc<QT, SWIGLU> src = is.src;
-    pg_advance<QT, SWIGLU>(a, c, is);
+  for (int w = 0; w < 2; w++) {
+    pg_open<QT, SWIGLU>(a, c, is, mq);
 #pragma unroll
-    for (int n = 0; n < L::LOADS; n++) pg_dma_n<QT, SWIGLU>(n, b, src, meta, c.wv);
+    for (int n = 0; n < L::LOADS; n++) pg_dma_n<QT, SWIGLU>(n, is, c.wv);
+  }
+  pg_wait<L::LOADS>();
+  pg_barrier();
+  pg_open<QT, SWIGLU>(a, c, is, mq);
+#pragma unroll
+  for (int n = 0; n < L::BI; n++) pg_dma_n<QT, SWIGLU>(n, is, c.wv);
+  const PGLane<QT> ln(c.lr, c.lg, c.wv, SWIGLU);
+  PGOps<QT> ops;
+  u32x4 av[4];
+  {
+    PGRaw<QT> raw;
+    pg_read_codes<QT>(c.lds, ln, ops, raw);
+#pragma unroll
+    for (int j = 0; j < 4; j++) av[j] = pg_read_a0<QT>(c.lds, ln, I.m_valid <= 32, j);
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) pg_decode0<QT>(ops, raw, ln, 0, nb);
   }
 
   int cslot = 0;
@@ -653,19 +754,15 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     I = pg_table(c, q);
     // the tile's row blocks, rounded up to an even count (an instance of the K loop per count)
     switch ((I.m_valid + 31) / 32) {
-      case 1: cslot = pg_run<QT, SWIGLU, 2>(a, c, is, meta, mq, I, q, cslot); break;
-      case 2: cslot = pg_run<QT, SWIGLU, 4>(a, c, is, meta, mq, I, q, cslot); break;
-      case 3: cslot = pg_run<QT, SWIGLU, 6>(a, c, is, meta, mq, I, q, cslot); break;
-      case 4: cslot = pg_run<QT, SWIGLU, 8>(a, c, is, meta, mq, I, q, cslot); break;
-      case 5: cslot = pg_run<QT, SWIGLU, 10>(a, c, is, meta, mq, I, q, cslot); break;
-      case 6: cslot = pg_run<QT, SWIGLU, 12>(a, c, is, meta, mq, I, q, cslot); break;
-      case 7: cslot = pg_run<QT, SWIGLU, 14>(a, c, is, meta, mq, I, q, cslot); break;
-      default: cslot = pg_run<QT, SWIGLU, 16>(a, c, is, meta, mq, I, q, cslot); break;
+      case 1: cslot = pg_run<QT, SWIGLU, 2>(a, c, is, ln, ops, av, I, q, cslot); break;
+      case 2: cslot = pg_run<QT, SWIGLU, 4>(a, c, is, ln, ops, av, I, q, cslot); break;
+      case 3: cslot = pg_run<QT, SWIGLU, 6>(a, c, is, ln, ops, av, I, q, cslot); break;
+      case 4: cslot = pg_run<QT, SWIGLU, 8>(a, c, is, ln, ops, av, I, q, cslot); break;
+      case 5: cslot = pg_run<QT, SWIGLU, 10>(a, c, is, ln, ops, av, I, q, cslot); break;
+      case 6: cslot = pg_run<QT, SWIGLU, 12>(a, c, is, ln, ops, av, I, q, cslot); break;
+      case 7: cslot = pg_run<QT, SWIGLU, 14>(a, c, is, ln, ops, av, I, q, cslot); break;
+      default: cslot = pg_run<QT, SWIGLU, 16>(a, c, is, ln, ops, av, I, q, cslot); break;
     }
-    // the metadata the next item's steps issue: item q + 2's into the buffer item q's epilogue just read (past the
-    // next item's first barrier, every wave is done with it), else item q + 1's again (the same bytes)
-    mq = q + 2 < c.nq ? q + 2 : min(q + 1, c.nq - 1);
-    meta.set(a, pg_table(c, mq), c.tid);
   }
   pg_wait<0>();  // (the dummy loads past the last stage land before the workgroup's LDS is released)
 }
@@ -702,11 +799,12 @@ int launch_pgemm(const PrefillArgs& a, hipStream_t s) {
 }  // namespace
 
 bool prefill_supported(int qtype, int K, int N) {
-  // (K: whole stages of 64, at least R + 1 of them: the issue side, R - 1 stages ahead, switches to the next item at
-  // an item's step stages - R + 1 >= 2, after the metadata the item's first step issued has landed)
+  // (K: whole stages of 64, at least R + 2 of them: the window of an item's stage 0 opens at the previous item's step
+  // stages - R, which must come at least two windows after that item's first step opened the first window carrying
+  // the next item's metadata: stages - R >= 2)
   // (Q4_K: whole super-blocks)
   return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0 || qtype == ARTLITE_Q4_K) &&
-         K >= 64 * (PG<ARTLITE_Q4_0>::R + 1) && K % (qtype == ARTLITE_Q4_K ? 256 : 64) == 0 && N > 0 && N % 16 == 0;
+         K >= 64 * (PG<ARTLITE_Q4_0>::R + 2) && K % (qtype == ARTLITE_Q4_K ? 256 : 64) == 0 && N > 0 && N % 16 == 0;
 }
 
 int launch_prefill(const PrefillArgs& a, hipStream_t s) {
