@@ -132,9 +132,19 @@ __device__ __forceinline__ void pg_for(F&& f) {
   pg_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// Decode of a lane's 8 weights to fp16: the code bytes spread into fp16 1024 + c (c < 256 exact, one perm per two),
-// the offset taken off exactly by one packed FMA (Q4_0's high nibbles, kept in place as 16 q, are scaled by 1/16 in
-// it), then the product with the block's scale, rounded once.
+// A column block's operand (a lane's 8 weights of a group, as 4 words of fp16 pairs) is decoded in 5 tasks that a step
+// spreads over its iterations (the matrix cores take only a few other instructions per MFMA for free): the
+// preparation, then the 4 words. PGPrep holds what the words take: the code dwords (Q4_0: masked to its nibbles;
+// Q8_0: sign bits flipped; Q4_K: each byte < 16), and the scale (Q4_0 / Q8_0: as an fp16 pair; Q4_K: the sub-block's
+// scale s and min o in fp32).
+struct PGPrep {
+  uint32_t v0, v1, d;
+  float s, o;
+};
+
+// Q4_0 / Q8_0 decode of a lane's 8 weights to fp16: the code bytes spread into fp16 1024 + c (c < 256 exact, one perm
+// per two), the offset taken off exactly by one packed FMA (Q4_0's high nibbles, kept in place as 16 q, are scaled by
+// 1/16 in it), then the product with the block's scale, rounded once.
 template <int QT>
 struct PGDecode {
   uint32_t msk;
@@ -151,21 +161,17 @@ struct PGDecode {
       add = f16x2{_Float16(-1152.0f), _Float16(-1152.0f)};
     }
   }
-  __device__ __forceinline__ u32x4 operator()(uint32_t c0, uint32_t c1, uint32_t sc) const {
-    const uint32_t v0 = QT == ARTLITE_Q4_0 ? c0 & msk : c0 ^ msk;
-    const uint32_t v1 = QT == ARTLITE_Q4_0 ? c1 & msk : c1 ^ msk;
-    const uint32_t w[4] = {__builtin_amdgcn_perm(0x64646464u, v0, 0x04010400u),
-                           __builtin_amdgcn_perm(0x64646464u, v0, 0x04030402u),
-                           __builtin_amdgcn_perm(0x64646464u, v1, 0x04010400u),
-                           __builtin_amdgcn_perm(0x64646464u, v1, 0x04030402u)};
-    const f16x2 d = __builtin_bit_cast(f16x2, sc | (sc << 16));
-    u32x4 b;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const f16x2 c = __builtin_bit_cast(f16x2, w[j]) * mul + add;  // (exact: the code less its offset)
-      b[j] = __builtin_bit_cast(uint32_t, c * d);
-    }
-    return b;
+  __device__ __forceinline__ PGPrep prep(uint32_t c0, uint32_t c1, uint32_t sc) const {
+    PGPrep p;
+    p.v0 = QT == ARTLITE_Q4_0 ? c0 & msk : c0 ^ msk;
+    p.v1 = QT == ARTLITE_Q4_0 ? c1 & msk : c1 ^ msk;
+    p.d = sc | (sc << 16);
+    return p;
+  }
+  __device__ __forceinline__ uint32_t word(const PGPrep& p, int j) const {
+    const uint32_t w = __builtin_amdgcn_perm(0x64646464u, j < 2 ? p.v0 : p.v1, j & 1 ? 0x04030402u : 0x04010400u);
+    const f16x2 c = __builtin_bit_cast(f16x2, w) * mul + add;  // (exact: the code less its offset)
+    return __builtin_bit_cast(uint32_t, c * __builtin_bit_cast(f16x2, p.d));
   }
 };
 
@@ -192,19 +198,14 @@ __device__ __forceinline__ void pg_k4_scales(const u32x4& h, int qi, float (&s)[
   }
 }
 
-// Q4_K: the lane's 8 weights of one sub-block from its 8 codes (the bytes of m0, m1, each < 16): q s - o in fp32
-// (the product exact, one rounding), then rounded to fp16.
-__device__ __forceinline__ u32x4 pg_k4_decode(uint32_t m0, uint32_t m1, float s, float o) {
-  u32x4 b;
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const uint32_t v = i < 2 ? m0 : m1;
-    const int sh = 16 * (i & 1);
-    const f16x2 h = {_Float16(__builtin_fmaf(float((v >> sh) & 0xFF), s, -o)),
-                     _Float16(__builtin_fmaf(float((v >> (sh + 8)) & 0xFF), s, -o))};
-    b[i] = __builtin_bit_cast(uint32_t, h);
-  }
-  return b;
+// Q4_K: word j of the lane's 8 weights of one sub-block from its 8 codes (the bytes of v0, v1, each < 16): q s - o in
+// fp32 (the product exact, one rounding), then rounded to fp16.
+__device__ __forceinline__ uint32_t pg_k4_word(const PGPrep& p, int j) {
+  const uint32_t v = j < 2 ? p.v0 : p.v1;
+  const int sh = 16 * (j & 1);
+  const f16x2 h = {_Float16(__builtin_fmaf(float((v >> sh) & 0xFF), p.s, -p.o)),
+                   _Float16(__builtin_fmaf(float((v >> (sh + 8)) & 0xFF), p.s, -p.o))};
+  return __builtin_bit_cast(uint32_t, h);
 }
 
 // An item: expert e, its sorted rows s0 .. s0 + m_valid, output columns n0 .. (SwiGLU: + 128 of gate and up; plain:
@@ -237,17 +238,19 @@ __device__ __forceinline__ PGItem pg_item(const PrefillArgs& a, int64_t w, int n
 // The lane's DMA sources of an item at stage 0. A: instruction i of wave w writes chunks (4 i + w) 64 + lane of a
 // stage's A region; chunk p holds row r = p / 8, physical chunk c = p % 8, which is logical chunk c ^ swz(r) (K values
 // 8 c .. + 8 of the stage); rows past the tile's valid ones repeat its last (their outputs are not stored); a row's A
-// row comes from the item's metadata in LDS (tok). Weights: instruction j of wave w writes dwords (4 j + w) 64 + lane
+// row comes from the item's metadata in LDS (tok). Weights: instruction j of wave w writes dwords (8 j + w) 64 + lane
 // of the stage's weight region: staged row q / WDW (SwiGLU: gate rows n0 .. + 128, then the same rows of up; plain:
-// rows n0 .. + 256), dword q % WDW of the row's stage bytes; rows past N load the last row. Offsets in bytes (A: from
-// a.a; weights: from the instruction's matrix).
+// rows n0 .. + 256), dword q % WDW of the row's stage bytes (q = 512 j + tid: consecutive lanes read consecutive
+// dwords of a row); rows past N load the last row. Offsets in bytes (A: from a.a; weights: from the instruction's
+// matrix).
 template <int QT, bool SWIGLU>
 struct PGSrc {
   using L = PG<QT>;
   uint32_t a[L::AI];
   uint32_t w[L::BI];
   __device__ __forceinline__ static int swz(int r) { return (r >> 1) & 7; }
-  __device__ __forceinline__ void set(const PrefillArgs& g, const PGItem& I, const int32_t* tok, int tid) {
+  // the A sources (a's row tokens from its metadata in LDS)
+  __device__ __forceinline__ void set_a(const PrefillArgs& g, const PGItem& I, const int32_t* tok, int tid) {
     tid = pg_fresh(tid);
 #pragma unroll
     for (int i = 0; i < L::AI; i++) {
@@ -256,6 +259,10 @@ struct PGSrc {
       const int ar = g.row_a ? tok[row] : I.s0 + row;
       a[i] = (uint32_t(ar) * uint32_t(g.K) + 8 * c) * 2;
     }
+  }
+  // the weight sources
+  __device__ __forceinline__ void set_w(const PrefillArgs& g, const PGItem& I, int tid) {
+    tid = pg_fresh(tid);
 #pragma unroll
     for (int j = 0; j < L::BI; j++) {  // (dwords past the staged rows: padding, loading the last dword again)
       int row, dw;
@@ -297,24 +304,26 @@ struct PGMeta {
   }
 };
 
-// The DMA sources of the open window (one stage of the issue item plus the metadata of item mq): uniform base pointers
-// (at that stage) and destination slots; the lanes' offsets are in PGSrc and PGMeta.
+// The DMA sources of the open window (an A stage, the weight stage after it, the metadata of item mq): uniform base
+// pointers (at those stages) and destinations (dst: the A stage's slot; dstw: the weight region of the next slot);
+// the lanes' offsets are in PGSrc and PGMeta.
 struct PGBases {
   const uint8_t *ab, *wb0, *wb1, *mt, *ms;
   const uint8_t *wq0, *wq1;  // (Q4_K: the stage's code bytes; wb0, wb1 its super-block headers)
-  uint32_t dst, mdst;
+  uint32_t dst, dstw, mdst;
 };
 
-// The issue side: the item whose stages are being issued, the stage and ring slot of the window last opened, the item
-// whose metadata the windows carry (mq), and the open window's bases.
+// The issue side: the A stream (item qa, stage sta of the window last opened, its ring slot) and the weight stream one
+// stage ahead of it (item qw, stage stw: its stage index runs one ahead, and so does its slot), the item whose
+// metadata the windows carry (mq), and the open window's bases. Past the last item a stream reloads stage 0 of it
+// (dummies keep the counts fixed).
 template <int QT, bool SWIGLU>
 struct PGIssue {
   PGSrc<QT, SWIGLU> src;
   PGMeta meta;
   PGBases b;
-  int st;    // the window's stage of item q
-  int q;     // its index among this workgroup's items (nq: past the last, dummies)
-  int slot;  // its ring slot
+  int sta, qa, stw, qw;
+  int slot;
   int mq;
 };
 
@@ -331,7 +340,7 @@ __device__ __forceinline__ void pg_dma_n(int n, const PGIssue<QT, SWIGLU>& is, i
       base = j < 2 ? (SWIGLU && j == 1 ? b.wb1 : b.wb0) : (SWIGLU && j >= 4 ? b.wq1 : b.wq0);
     else
       base = SWIGLU && (j * L::THREADS + 64 * wv) >= 128 * L::WDW ? b.wb1 : b.wb0;
-    pg_dma<4>(base, is.src.w[j], b.dst + L::ABYTES + (8 * j + wv) * 256);
+    pg_dma<4>(base, is.src.w[j], b.dstw + (8 * j + wv) * 256);
   } else if (n < L::BI + L::AI) {
     const int i = n - L::BI;
     pg_dma<16>(b.ab, is.src.a[i], b.dst + (8 * i + wv) * 1024);
@@ -341,10 +350,12 @@ __device__ __forceinline__ void pg_dma_n(int n, const PGIssue<QT, SWIGLU>& is, i
   }
 }
 
-// The lane's fixed places: its A chunk in a slot for row block 0 of group 0 (aof0) and of group 1 (aof1); its weight
-// row per column block (bof: the row's stage bytes in a slot; Q4_K: the row itself, its header and codes in their
-// regions): SwiGLU gate rows 16 wv .. + 16 (column block 0) and the same rows of up (staged at + 128), plain rows
-// 32 wv .. + 32; cb its code bytes' offset in a block (Q4_K: in the quarter's 32 bytes, 8 lg).
+// The lane's fixed places: its A chunk in a slot for row block 0 of group 0 (aof0) and of group 1 (aof1); its staged
+// weight row per column block (bof: the row's stage bytes in a slot; Q4_K: the row itself, its header and codes in
+// their regions): SwiGLU gate rows 16 wv .. + 16 (column block 0) and the same rows of up (staged
+// at + 128); plain: of rows 32 wv .. + 32, MFMA row i of block nb is row 32 wv + 8 (i / 4) + 4 nb + i % 4, so that a
+// lane's outputs of the two blocks are 8 consecutive columns; cb its code bytes' offset in a block (Q4_K: in the
+// quarter's 32 bytes, 8 lg).
 template <int QT>
 struct PGLane {
   uint32_t aof0, aof1, bof[2];
@@ -356,7 +367,7 @@ struct PGLane {
     aof1 = uint32_t(lr * 128 + ((4 + lg) ^ sz) * 16);
 #pragma unroll
     for (int nb = 0; nb < 2; nb++) {
-      const int row = swiglu ? 128 * nb + 16 * wv + lr : 32 * wv + 16 * nb + lr;
+      const int row = swiglu ? 128 * nb + 16 * wv + lr : 32 * wv + 8 * (lr >> 2) + 4 * nb + (lr & 3);
       bof[nb] = PG<QT>::K4 ? uint32_t(row) : uint32_t(PG<QT>::ABYTES + row * PG<QT>::WROW);
     }
     cb = QT == ARTLITE_Q4_0 ? 8 * (lg & 1) : 8 * lg;
@@ -386,28 +397,27 @@ struct PGRaw {
 // The LDS reads of a step's weight codes from its slot s, all aligned dwords: per column block, group 0's from the lane
 // group's code byte offset cb (Q4_0: 8 (lg & 1), both nibbles of those 8 bytes; Q8_0: 8 lg) two bytes past the
 // block's scale (the row's first dword: the scale in its low half); group 1's from GB + 2 + cb (20 or 36), its scale
-// the high half of the dword at GB - 2.
+// the high half of the dword at GB - 2. Q4_K: the header, the code dwords 2 lg, 2 lg + 1.
 template <int QT>
 __device__ __forceinline__ void pg_read_codes(const uint8_t* s, const PGLane<QT>& ln, PGOps<QT>& o, PGRaw<QT>& r) {
   using L = PG<QT>;
+  auto dw = [](const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); };
 #pragma unroll
   for (int nb = 0; nb < 2; nb++) {
     if constexpr (L::K4) {
       r.h[nb] = *reinterpret_cast<const u32x4*>(s + L::ABYTES + ln.bof[nb] * 16);
-      const uint32_t* c = reinterpret_cast<const uint32_t*>(s + L::ABYTES + L::KHDR + ln.bof[nb] * 32 + ln.cb);
-      r.d[0][nb] = c[0];
-      r.d[1][nb] = c[1];
+      const uint8_t* c = s + L::ABYTES + L::KHDR + ln.bof[nb] * 32 + ln.cb;
+      r.d[0][nb] = dw(c);
+      r.d[1][nb] = dw(c + 4);
     } else {
       const uint8_t* row = s + ln.bof[nb];
-      const uint32_t* d = reinterpret_cast<const uint32_t*>(row + ln.cb);
-      r.d[0][nb] = d[0];
-      r.d[1][nb] = d[1];
-      r.d[2][nb] = d[2];
-      r.sc0[nb] = *reinterpret_cast<const uint32_t*>(row);
-      const uint32_t* e = reinterpret_cast<const uint32_t*>(row + L::GB + 2 + ln.cb);
-      o.c10[nb] = e[0];
-      o.c11[nb] = e[1];
-      o.sc1[nb] = *reinterpret_cast<const uint32_t*>(row + L::GB - 2);
+      r.d[0][nb] = dw(row + ln.cb);
+      r.d[1][nb] = dw(row + ln.cb + 4);
+      r.d[2][nb] = dw(row + ln.cb + 8);
+      r.sc0[nb] = dw(row);
+      o.c10[nb] = dw(row + L::GB + 2 + ln.cb);
+      o.c11[nb] = dw(row + L::GB + 6 + ln.cb);
+      o.sc1[nb] = dw(row + L::GB - 2);
     }
   }
 }
@@ -420,10 +430,10 @@ __device__ __forceinline__ u32x4 pg_read_a0(const uint8_t* s, const PGLane<QT>& 
   return *reinterpret_cast<const u32x4*>(s + o);
 }
 
-// group 0's weights of column block nb (Q4_K: also group 1's scale, min and codes; qi the stage's quarter of its
-// super-block)
+// The preparation of group 0's operand of column block nb from what was read (Q4_K: also group 1's codes, scale and
+// min into o; qi the stage's quarter of its super-block), and a word of an operand.
 template <int QT>
-__device__ __forceinline__ void pg_decode0(PGOps<QT>& o, const PGRaw<QT>& r, const PGLane<QT>& ln, int qi, int nb) {
+__device__ __forceinline__ PGPrep pg_prep0(PGOps<QT>& o, const PGRaw<QT>& r, const PGLane<QT>& ln, int qi, int nb) {
   if constexpr (PG<QT>::K4) {
     float ks[2], ko[2];
     pg_k4_scales(r.h[nb], qi, ks, ko);
@@ -431,11 +441,47 @@ __device__ __forceinline__ void pg_decode0(PGOps<QT>& o, const PGRaw<QT>& r, con
     o.ko1[nb] = ko[1];
     o.c10[nb] = (r.d[0][nb] >> 4) & 0x0F0F0F0Fu;
     o.c11[nb] = (r.d[1][nb] >> 4) & 0x0F0F0F0Fu;
-    o.b0[nb] = pg_k4_decode(r.d[0][nb] & 0x0F0F0F0Fu, r.d[1][nb] & 0x0F0F0F0Fu, ks[0], ko[0]);
+    PGPrep p;
+    p.v0 = r.d[0][nb] & 0x0F0F0F0Fu;
+    p.v1 = r.d[1][nb] & 0x0F0F0F0Fu;
+    p.s = ks[0];
+    p.o = ko[0];
+    return p;
   } else {
-    o.b0[nb] = ln.dec(__builtin_amdgcn_alignbit(r.d[1][nb], r.d[0][nb], 16),
-                      __builtin_amdgcn_alignbit(r.d[2][nb], r.d[1][nb], 16), r.sc0[nb] & 0xFFFFu);
+    return ln.dec.prep(__builtin_amdgcn_alignbit(r.d[1][nb], r.d[0][nb], 16),
+                       __builtin_amdgcn_alignbit(r.d[2][nb], r.d[1][nb], 16), r.sc0[nb] & 0xFFFFu);
   }
+}
+
+// the preparation of group 1's operand of column block nb (its codes read a step before)
+template <int QT>
+__device__ __forceinline__ PGPrep pg_prep1(const PGOps<QT>& o, const PGLane<QT>& ln, int nb) {
+  if constexpr (PG<QT>::K4) {
+    PGPrep p;
+    p.v0 = o.c10[nb];
+    p.v1 = o.c11[nb];
+    p.s = o.ks1[nb];
+    p.o = o.ko1[nb];
+    return p;
+  } else {
+    return ln.dec.prep(o.c10[nb], o.c11[nb], o.sc1[nb] >> 16);
+  }
+}
+
+template <int QT>
+__device__ __forceinline__ uint32_t pg_word(const PGPrep& p, const PGLane<QT>& ln, int j) {
+  if constexpr (PG<QT>::K4)
+    return pg_k4_word(p, j);
+  else
+    return ln.dec.word(p, j);
+}
+
+// group 0's whole operand of column block nb (the set-up's, for the first step)
+template <int QT>
+__device__ __forceinline__ void pg_decode0(PGOps<QT>& o, const PGRaw<QT>& r, const PGLane<QT>& ln, int qi, int nb) {
+  const PGPrep p = pg_prep0<QT>(o, r, ln, qi, nb);
+#pragma unroll
+  for (int j = 0; j < 4; j++) o.b0[nb][j] = pg_word<QT>(p, ln, j);
 }
 
 // silu(g) u with the hardware's exp2 and reciprocal (each within an ulp or two of fp32; the fp16 rounding of h,
@@ -470,9 +516,26 @@ __device__ __forceinline__ PGItem pg_table(const PGCtx& c, int q) {
                 __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w)};
 }
 
-// Opens the next window: the next stage of the issue item (past its last, the next item, its sources from its
-// metadata, which landed two windows after the first that carried it) into the next ring slot, with the metadata of
-// item mq (>= 0: a new one) into its buffer; past the last item, a reload of stage 0 (dummies keep the counts fixed).
+// the weight bases of stage sw (Q4_K: super-block sw / 4, its quarter sw % 4)
+template <int QT, bool SWIGLU>
+__device__ __forceinline__ void pg_wbases(const PrefillArgs& a, int sw, PGBases& b) {
+  using L = PG<QT>;
+  if constexpr (L::K4) {
+    b.wb0 = a.w[0] + (sw >> 2) * 144;
+    b.wb1 = (SWIGLU ? a.w[1] : a.w[0]) + (sw >> 2) * 144;
+    b.wq0 = b.wb0 + 16 + 32 * (sw & 3);
+    b.wq1 = b.wb1 + 16 + 32 * (sw & 3);
+  } else {
+    b.wb0 = a.w[0] + sw * L::WROW;
+    b.wb1 = (SWIGLU ? a.w[1] : a.w[0]) + sw * L::WROW;
+    b.wq0 = b.wq1 = nullptr;
+  }
+}
+
+// Opens the next window: the A stream's next stage and the weight stream's (past an item's last stage, the next item:
+// the A sources from its metadata, which landed two windows after the first that carried it; the weight sources from
+// its table entry), into the next ring slot (weights: the slot after it), with the metadata of item mq (>= 0: a new one)
+// into its buffer.
 template <int QT, bool SWIGLU>
 __device__ __forceinline__ void pg_open(const PrefillArgs& a, const PGCtx& c, PGIssue<QT, SWIGLU>& is, int mq) {
   using L = PG<QT>;
@@ -481,57 +544,62 @@ __device__ __forceinline__ void pg_open(const PrefillArgs& a, const PGCtx& c, PG
     is.meta.set(a, pg_table(c, mq), c.tid);
   }
   is.slot = is.slot + 1 == L::R ? 0 : is.slot + 1;
-  if (is.q < c.nq && ++is.st == c.stages) {
-    is.st = 0;
-    if (++is.q < c.nq) is.src.set(a, pg_table(c, is.q), pg_tok<QT>(c, is.q), c.tid);
+  if (is.qa < c.nq && ++is.sta == c.stages) {
+    is.sta = 0;
+    if (++is.qa < c.nq) is.src.set_a(a, pg_table(c, is.qa), pg_tok<QT>(c, is.qa), c.tid);
   }
-  const int st = __builtin_amdgcn_readfirstlane(is.q < c.nq ? is.st : 0);
+  if (is.qw < c.nq && ++is.stw == c.stages) {
+    is.stw = 0;
+    if (++is.qw < c.nq) is.src.set_w(a, pg_table(c, is.qw), c.tid);
+  }
+  const int sa = __builtin_amdgcn_readfirstlane(is.qa < c.nq ? is.sta : 0);
   PGBases& b = is.b;
-  b.ab = static_cast<const uint8_t*>(static_cast<const void*>(a.a)) + 128 * st;
-  if constexpr (L::K4) {  // (super-block st / 4, its quarter st % 4)
-    b.wb0 = a.w[0] + (st >> 2) * 144;
-    b.wb1 = (SWIGLU ? a.w[1] : a.w[0]) + (st >> 2) * 144;
-    b.wq0 = b.wb0 + 16 + 32 * (st & 3);
-    b.wq1 = b.wb1 + 16 + 32 * (st & 3);
-  } else {
-    b.wb0 = a.w[0] + st * L::WROW;
-    b.wb1 = (SWIGLU ? a.w[1] : a.w[0]) + st * L::WROW;
-    b.wq0 = b.wq1 = nullptr;
-  }
+  b.ab = static_cast<const uint8_t*>(static_cast<const void*>(a.a)) + 128 * sa;
+  pg_wbases<QT, SWIGLU>(a, __builtin_amdgcn_readfirstlane(is.qw < c.nq ? is.stw : 0), b);
   b.ms = reinterpret_cast<const uint8_t*>(a.row_scale);
   b.mt = a.row_a ? reinterpret_cast<const uint8_t*>(a.row_a) : b.ms;
+  const int ws = is.slot + 1 == L::R ? 0 : is.slot + 1;
   b.dst = __builtin_amdgcn_readfirstlane(c.lbase + is.slot * L::SBYTES);
+  b.dstw = __builtin_amdgcn_readfirstlane(c.lbase + ws * L::SBYTES + L::ABYTES);
   b.mdst = __builtin_amdgcn_readfirstlane(c.lbase + L::R * L::SBYTES + (is.mq & 1) * L::META);
 }
 
-// One step: the products of the stage in slot s (two groups) -- MBN row blocks of the tile times the wave's 2 column
+// One step g: the products of the stage in slot s (two groups) -- MBN row blocks of the tile times the wave's 2 column
 // blocks -- laid out as IT = 2 MBN iterations (group 0's row blocks, then group 1's) pinned in order by scheduling
 // barriers. Iteration it issues its row block's 2 MFMAs on A operand av[it % 4] and then reads into that register the
 // operand of iteration it + 4 (IT is a multiple of 4, so the ring runs on from step to step: the last 4 iterations
-// read the next step's first 4 operands); the first two decode a column block of group 1's weights. Four iterations
-// before the end comes the workgroup's barrier: this wave's reads of slot s are all issued by then, and the stage in
-// the next slot ns has landed (vmcnt: only the window opened at the previous barrier may be in flight). Past it the
-// wave reads the next step's operands from ns (nqi: that stage's quarter; nsmall: its tile has 2 row blocks) and
-// decodes its group 0 weights in the last two iterations, opens the next window (into slot s: every wave is done
-// reading it) and issues that window's weight DMAs; its other DMAs go out in the next step's iterations before the
-// barrier (2 row blocks: none, so at the step's start). nmq >= 0: the item whose metadata the windows carry from now
-// on.
+// read the next step's first 4 operands). The step opens a window at its start and issues its DMAs over the
+// iterations before its barrier: A stage g + 2 into the slot the previous barrier freed, weight stage g + 3 into the
+// slot whose codes the previous step read. The weights run a stage ahead: the first two iterations decode a column
+// block each of this stage's group 1 (from codes read a step ago); iteration RD, 8 before the end (or the third; 2 row
+// blocks: the first, ahead of its barrier), reads the next stage's codes from the next slot ns (certified by the
+// previous step's barrier), so that the last two decode the next stage's group 0 (nqi: that stage's quarter) from
+// data long landed. Four iterations before the end comes the workgroup's barrier: this wave's reads of the A stage in
+// slot s are all issued by then (the next step's window may overwrite it), and the A stage in ns has landed (vmcnt:
+// only this step's window may be in flight); past it the wave reads the next step's first A operands from ns
+// (nsmall: its tile has 2 row blocks). 2 row blocks: the window, its DMAs and the codes' read come before the barrier
+// at the step's start. nmq >= 0: the item whose metadata the windows carry from now on.
 template <int QT, bool SWIGLU, int MBN>
 __device__ __forceinline__ void pg_step(const PrefillArgs& a, const PGCtx& c, PGIssue<QT, SWIGLU>& is,
                                         const PGLane<QT>& ln, PGOps<QT>& ops, u32x4 (&av)[4], const uint8_t* s,
                                         const uint8_t* ns, int nqi, bool nsmall, int nmq, f32x4 (&acc)[MBN][2]) {
   using L = PG<QT>;
-  constexpr int IT = 2 * MBN, HEAD = IT - 4, HS = L::LOADS - L::BI;
+  constexpr int IT = 2 * MBN, HEAD = IT - 4, RD = MBN > 4 ? MBN - 4 : 0;
   auto a_addr = [&](int it) { return s + (it < MBN ? ln.aof0 : ln.aof1) + (it % MBN) * 2048; };
   u32x4 b1[2];
   PGOps<QT> nx;
   PGRaw<QT> raw;
-  if constexpr (HEAD == 0) {
+  PGPrep p1[2], p0[2];
+  if constexpr (HEAD == 0) {  // (2 row blocks: the window and the codes' read before the step's barrier)
+    pg_open<QT, SWIGLU>(a, c, is, nmq);
 #pragma unroll
-    for (int n = L::BI; n < L::LOADS; n++) pg_dma_n<QT, SWIGLU>(n, is, c.wv);
+    for (int n = 0; n < L::LOADS; n++) pg_dma_n<QT, SWIGLU>(n, is, c.wv);
+    pg_read_codes<QT>(ns, ln, nx, raw);
   }
+  static_assert(HEAD == 0 || RD < HEAD, "the next stage's codes are read before the barrier that frees their slot");
   pg_for<IT>([&](auto itc) __attribute__((always_inline)) {
     constexpr int it = decltype(itc)::value;
+    if constexpr (it == 0 && HEAD > 0) pg_open<QT, SWIGLU>(a, c, is, nmq);
     if constexpr (it == HEAD) {
       pg_wait<L::LOADS>();
       pg_barrier();
@@ -543,26 +611,31 @@ __device__ __forceinline__ void pg_step(const PrefillArgs& a, const PGCtx& c, PG
       else
         acc[it - MBN][nb] = mfma16(b1[nb], av[it % 4], acc[it - MBN][nb]);
     }
-    if constexpr (it == HEAD) pg_read_codes<QT>(ns, ln, nx, raw);
+    if constexpr (it == RD && HEAD > 0) pg_read_codes<QT>(ns, ln, nx, raw);
     if constexpr (it < HEAD)
       av[it % 4] = *reinterpret_cast<const u32x4*>(a_addr(it + 4));
     else
       av[it % 4] = pg_read_a0<QT>(ns, ln, nsmall, it - HEAD);
-    if constexpr (it == HEAD) pg_open<QT, SWIGLU>(a, c, is, nmq);
-    if constexpr (it < 2) {  // (group 1's weights, a column block per iteration)
-      if constexpr (L::K4)
-        b1[it] = pg_k4_decode(ops.c10[it], ops.c11[it], ops.ks1[it], ops.ko1[it]);
-      else
-        b1[it] = ln.dec(ops.c10[it], ops.c11[it], ops.sc1[it] >> 16);
-    }
-    if constexpr (it >= IT - 2) pg_decode0<QT>(nx, raw, ln, nqi, it - (IT - 2));
-    if constexpr (it < HEAD) {  // (the window opened at the previous barrier: A and metadata)
+    // the decodes, each a column block's preparation and 4 words (10 tasks), dealt over group 0's iterations (this
+    // stage's group 1) and group 1's (the next stage's group 0)
+    pg_for<10>([&](auto tc) __attribute__((always_inline)) {
+      constexpr int t = decltype(tc)::value, nb = t / 5, k = t % 5;
+      if constexpr (t * MBN / 10 == it) {
+        if constexpr (k == 0)
+          p1[nb] = pg_prep1<QT>(ops, ln, nb);
+        else
+          b1[nb][k - 1] = pg_word<QT>(p1[nb], ln, k - 1);
+      }
+      if constexpr (MBN + t * MBN / 10 == it) {
+        if constexpr (k == 0)
+          p0[nb] = pg_prep0<QT>(nx, raw, ln, nqi, nb);
+        else
+          nx.b0[nb][k - 1] = pg_word<QT>(p0[nb], ln, k - 1);
+      }
+    });
+    if constexpr (it < HEAD) {  // (the window's DMAs: weights first)
 #pragma unroll
-      for (int n = L::BI + it * HS / HEAD; n < L::BI + (it + 1) * HS / HEAD; n++) pg_dma_n<QT, SWIGLU>(n, is, c.wv);
-    } else {  // (the window just opened: weights)
-      constexpr int j = it - HEAD;
-#pragma unroll
-      for (int n = j * L::BI / 4; n < (j + 1) * L::BI / 4; n++) pg_dma_n<QT, SWIGLU>(n, is, c.wv);
+      for (int n = it * L::LOADS / HEAD; n < (it + 1) * L::LOADS / HEAD; n++) pg_dma_n<QT, SWIGLU>(n, is, c.wv);
     }
     __builtin_amdgcn_sched_barrier(0);  // (nothing moves from one iteration to another)
   });
@@ -580,30 +653,35 @@ __device__ __forceinline__ int pg_run(const PrefillArgs& a, const PGCtx& c, PGIs
   f32x4 acc[MBN][2];
 #pragma unroll
   for (int mb = 0; mb < MBN; mb++) acc[mb][0] = acc[mb][1] = f32x4{0, 0, 0, 0};
-  // From the item's first barrier on the windows carry the metadata of item q + 1 (into the buffer of item q - 1,
-  // whose epilogue every wave is past by then), else item q's again. The last step's reads are for the next item.
+  // From the item's second step on (past its first barrier) the windows carry the metadata of item q + 1 (into the
+  // buffer of item q - 1, whose epilogue every wave is past by then), else item q's again. The last step's reads are
+  // for the next item.
   const int nmq = q + 1 < c.nq ? q + 1 : q;
   bool nsmall = false;
   if (q + 1 < c.nq) nsmall = pg_table(c, q + 1).m_valid <= 32;
+#pragma clang loop unroll(disable)  // (one copy of the step: none peeled for the first)
   for (int st = 0; st < c.stages; st++) {
     const int ns = cslot + 1 == L::R ? 0 : cslot + 1;
     pg_step<QT, SWIGLU, MBN>(a, c, is, ln, ops, av, c.lds + cslot * L::SBYTES, c.lds + ns * L::SBYTES, (st + 1) & 3,
-                             st + 1 < c.stages ? MBN == 2 : nsmall, st == 0 ? nmq : -1, acc);
+                             st + 1 < c.stages ? MBN == 2 : nsmall, st == 1 ? nmq : -1, acc);
     cslot = __builtin_amdgcn_readfirstlane(ns);
   }
   // epilogue: lane output i of block (mb, nb): row 16 mb + lr of the tile; column (SwiGLU) n0 + 16 wv + 4 lg + i, gate
-  // in nb 0 and up in nb 1; (plain) n0 + 32 wv + 16 nb + 4 lg + i. A lane stores its row's 4 columns at once.
+  // in nb 0 and up in nb 1; (plain) n0 + 32 wv + 8 lg + 4 nb + i. A lane stores its row's 4 (8) columns at once.
   const float2* rf = pg_rowf<QT>(c, q);
   const int lr = pg_fresh(c.lr), lg = pg_fresh(c.lg);
-#pragma unroll
-  for (int mb = 0; mb < MBN; mb++) {
+  float2 fr[3];  // (the row factors, read two row blocks ahead; rows past the valid ones hold the last one's)
+  fr[0] = rf[lr];
+  fr[1] = rf[16 + lr];
+  pg_for<MBN>([&](auto mbc) __attribute__((always_inline)) {
+    constexpr int mb = decltype(mbc)::value;
+    if constexpr (mb + 2 < MBN) fr[(mb + 2) % 3] = rf[16 * (mb + 2) + lr];
     const int m = 16 * mb + lr;
-    if (m >= I.m_valid) continue;
+    const float2 f = fr[mb % 3];
     const int64_t o = int64_t(I.s0 + m) * a.N;
-    const float2 f = rf[m];
     if constexpr (SWIGLU) {
       const int n = I.n0 + 16 * wv + 4 * lg;
-      if (n < a.N) {
+      if (m < I.m_valid && n < a.N) {
         uint32_t v[2];
 #pragma unroll
         for (int i = 0; i < 2; i++) {
@@ -613,27 +691,28 @@ __device__ __forceinline__ int pg_run(const PrefillArgs& a, const PGCtx& c, PGIs
         }
         *reinterpret_cast<uint2*>(a.h + o + n) = make_uint2(v[0], v[1]);
       }
-    } else if (a.y16) {  // (fp16: the sums times f.y)
+    } else {
+      const int n = I.n0 + 32 * wv + 8 * lg;  // (the lane's 8 columns: 4 of each column block)
+      if (m < I.m_valid && n < a.N) {
+        if (a.y16) {  // (fp16: the sums times f.y)
+          uint32_t v[4];
 #pragma unroll
-      for (int nb = 0; nb < 2; nb++) {
-        const int n = I.n0 + 32 * wv + 16 * nb + 4 * lg;
-        if (n < a.N) {
-          const f16x2 v0 = {_Float16(acc[mb][nb][0] * f.y), _Float16(acc[mb][nb][1] * f.y)};
-          const f16x2 v1 = {_Float16(acc[mb][nb][2] * f.y), _Float16(acc[mb][nb][3] * f.y)};
-          *reinterpret_cast<uint2*>(a.y16 + o + n) =
-              make_uint2(__builtin_bit_cast(uint32_t, v0), __builtin_bit_cast(uint32_t, v1));
+          for (int i = 0; i < 4; i++) {
+            const f16x2 h = {_Float16(acc[mb][i / 2][2 * (i % 2)] * f.y), _Float16(acc[mb][i / 2][2 * (i % 2) + 1] * f.y)};
+            v[i] = __builtin_bit_cast(uint32_t, h);
+          }
+          *reinterpret_cast<uint4*>(a.y16 + o + n) = make_uint4(v[0], v[1], v[2], v[3]);
+        } else {  // (fp32: the sums times f.x f.y, a power of two)
+          const float fs = f.x * f.y;
+#pragma unroll
+          for (int nb = 0; nb < 2; nb++)
+            *reinterpret_cast<float4*>(a.y + o + n + 4 * nb) =
+                make_float4(acc[mb][nb][0] * fs, acc[mb][nb][1] * fs, acc[mb][nb][2] * fs, acc[mb][nb][3] * fs);
         }
       }
-    } else {  // (fp32: the sums times f.x f.y, a power of two)
-      const float fs = f.x * f.y;
-#pragma unroll
-      for (int nb = 0; nb < 2; nb++) {
-        const int n = I.n0 + 32 * wv + 16 * nb + 4 * lg;
-        if (n < a.N) *reinterpret_cast<float4*>(a.y + o + n) = make_float4(acc[mb][nb][0] * fs, acc[mb][nb][1] * fs,
-                                                                            acc[mb][nb][2] * fs, acc[mb][nb][3] * fs);
-      }
     }
-  }
+    __builtin_amdgcn_sched_barrier(0);  // (a row block at a time: its factors read two ahead)
+  });
   return cslot;
 }
 
@@ -717,14 +796,22 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     pg_wait<0>();
     __syncthreads();
   }
-  // the windows of stages 0 and 1 (stages >= R + 2: prefill_supported), carrying item 1's metadata (item 0's again
-  // when there is none); the barrier that certifies stage 0; the window of stage 2, its weights now, the rest in
-  // the first step; the first step's operands
-  is.src.set(a, I, pg_tok<QT>(c, 0), c.tid);
-  is.q = 0;
-  is.st = -1;
+  // The weight stream runs a stage ahead of the A stream: weight stage 0 into slot 0; the windows of A stages 0, 1
+  // (weights 1, 2; stages >= R + 2: prefill_supported), carrying item 1's metadata (item 0's again when there is
+  // none); the barrier that certifies A stage 0 and weight stages 0, 1; the first step's operands (group 0's weights
+  // decoded, group 1's codes, the first A operands); a barrier (every wave past its reads of weight stage 0, into whose
+  // slot the first step's window loads weight stage 3).
+  is.src.set_a(a, I, pg_tok<QT>(c, 0), c.tid);
+  is.src.set_w(a, I, c.tid);
+  is.qa = is.qw = 0;
+  is.sta = -1;
+  is.stw = 0;
   is.slot = -1;
   is.mq = 0;
+  pg_wbases<QT, SWIGLU>(a, 0, is.b);
+  is.b.dstw = __builtin_amdgcn_readfirstlane(c.lbase + L::ABYTES);
+#pragma unroll
+  for (int n = 0; n < L::BI; n++) pg_dma_n<QT, SWIGLU>(n, is, c.wv);
   const int mq = c.nq > 1 ? 1 : 0;
 #pragma unroll
   for (int w = 0; w < 2; w++) {
@@ -734,9 +821,6 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   }
   pg_wait<L::LOADS>();
   pg_barrier();
-  pg_open<QT, SWIGLU>(a, c, is, mq);
-#pragma unroll
-  for (int n = 0; n < L::BI; n++) pg_dma_n<QT, SWIGLU>(n, is, c.wv);
   const PGLane<QT> ln(c.lr, c.lg, c.wv, SWIGLU);
   PGOps<QT> ops;
   u32x4 av[4];
@@ -748,6 +832,7 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 #pragma unroll
     for (int nb = 0; nb < 2; nb++) pg_decode0<QT>(ops, raw, ln, 0, nb);
   }
+  pg_barrier();
 
   int cslot = 0;
   for (int q = 0; q < c.nq; q++) {
