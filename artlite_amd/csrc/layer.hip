@@ -121,6 +121,7 @@ struct Path {
   bool split;           // bf16 hi / lo planes of fp32 x needed (the MFMA decode tiles)
   bool quant;           // XQ of x needed (made by the router's launch)
   bool small;           // top k and dispatch in one workgroup
+  bool fused_route;     // ... in the router's launch (its last expert workgroup)
 };
 
 Path path_of(const artlite_moe_layer* L, int64_t T) {
@@ -134,6 +135,7 @@ Path path_of(const artlite_moe_layer* L, int64_t T) {
   p.split = planes && (L->x_dtype == ARTLITE_X_F32 || L->d.norm_eps > 0);  // (the normalised x is fp32)
   p.quant = p.gemv_gu;
   p.small = p.gemv_gu && T * L->d.top_k <= DISPATCH_BLOCK && L->d.n_experts <= MAX_EXPERTS;
+  p.fused_route = p.small && router_route_fits(T, L->d.hidden, L->d.n_experts, L->d.top_k);
   return p;
 }
 
@@ -144,9 +146,13 @@ std::vector<std::string> kernel_list(const artlite_moe_layer* L, int64_t T) {
   if (L->d.norm_eps > 0) k.push_back("rmsnorm");
   if (p.prefill) k.push_back("prefill_x");
   if (p.split) k.push_back("split");
-  k.push_back(p.quant ? "router_quant" : "router");
+  if (p.fused_route)
+    k.push_back("router_quant_route");
+  else
+    k.push_back(p.quant ? "router_quant" : "router");
   if (L->d.shared_ffn && L->d.shared_gated) k.push_back("shared_gate");
-  if (p.small) {
+  if (p.fused_route) {
+  } else if (p.small) {
     k.push_back("route");
   } else {
     k.push_back("topk");
@@ -199,13 +205,6 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     ahi = L->xhi.as<uint16_t>();
     alo = L->xlo.as<uint16_t>();
   }
-  ART_TRY(mark());
-  ART_TRY(launch_router(xin, xdt, L->router.as<float>(), H, E, T, L->logits.as<float>(), E,
-                        path.quant ? L->xq.as<uint32_t>() : nullptr, s));
-  if (d.shared_ffn && d.shared_gated) {
-    ART_TRY(mark());
-    ART_TRY(launch_router(xin, xdt, L->sinp.as<float>(), H, 1, T, L->sg.as<float>(), 1, nullptr, s));
-  }
   const int BM = path.gemv_gu ? GEMV_BM : path.prefill ? PREFILL_BM : DECODE_BM;
   DispatchBufs db{L->ids.as<int32_t>(), P, E, k, L->table.as<int32_t>(), L->ctrl.as<int32_t>(),
                   L->counts.as<int32_t>(), L->offsets.as<int32_t>(), L->order.as<int32_t>(), L->slot.as<int32_t>(),
@@ -217,7 +216,20 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     db.row_out[0] = L->gu_row.as<float2>();
     db.row_out[1] = L->dn_row.as<float2>();
   }
-  if (path.small) {
+  ART_TRY(mark());
+  if (path.fused_route)
+    ART_TRY(launch_router_route(xin, xdt, L->router.as<float>(), H, E, T, L->logits.as<float>(),
+                                path.quant ? L->xq.as<uint32_t>() : nullptr, k, d.gating, L->ids.as<int32_t>(),
+                                L->w.as<float>(), db, s));
+  else
+    ART_TRY(launch_router(xin, xdt, L->router.as<float>(), H, E, T, L->logits.as<float>(), E,
+                          path.quant ? L->xq.as<uint32_t>() : nullptr, s));
+  if (d.shared_ffn && d.shared_gated) {
+    ART_TRY(mark());
+    ART_TRY(launch_router(xin, xdt, L->sinp.as<float>(), H, 1, T, L->sg.as<float>(), 1, nullptr, s));
+  }
+  if (path.fused_route) {
+  } else if (path.small) {
     ART_TRY(mark());
     ART_TRY(launch_route_small(L->logits.as<float>(), T, E, k, d.gating, L->ids.as<int32_t>(), L->w.as<float>(), db,
                                s));

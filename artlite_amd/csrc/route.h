@@ -24,6 +24,11 @@ __device__ __forceinline__ uint64_t logit_key(float l, int e) {
   return (uint64_t(ord) << 32) | uint32_t(~uint32_t(e));
 }
 
+// the logit of ordered bits (the high half of logit_key; -0 comes back as +0, which every use of it treats alike)
+__device__ __forceinline__ float key_logit(uint32_t ord) {
+  return __uint_as_float((ord >> 31) ? (ord & 0x7FFFFFFFu) : ~ord);
+}
+
 // numpy's pairwise sum of n <= 128 doubles (moe_host.cpp:25-39)
 __device__ __forceinline__ double row_sum(const double* a, int n) {
   if (n < 8) {
@@ -62,8 +67,8 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // ordered bits among the experts not yet taken (a 32-bit wave maximum), then the lowest id holding them (ballots: the
 // low half of logit_key decides ties), lane j keeping the j-th; then the weights. ev (64 doubles) and sum (1): the
 // wave's LDS scratch. Lane j < k writes ids[j] and the weights (w32 / w64 when given) and returns its id; other lanes
-// return -1.
-template <int R>
+// return -1. COHERENT: the logits are read at device scope (written by other workgroups of the same launch).
+template <int R, bool COHERENT = false>
 __device__ __forceinline__ int topk_wave(const float* __restrict__ p, int per_col, int64_t pitch, int E, int k,
                                          int sigmoid, double* ev, double* sum, int lane, int32_t* __restrict__ ids,
                                          float* __restrict__ w32, double* __restrict__ w64) {
@@ -72,10 +77,16 @@ __device__ __forceinline__ int topk_wave(const float* __restrict__ p, int per_co
 #pragma unroll
   for (int r = 0; r < R; r++) {
     const int e = lane + WAVE * r;
-    ord[r] = e < E ? uint32_t(logit_key(p[int64_t(e / per_col) * pitch + e % per_col], e) >> 32) : 0;
+    float l = 0.0f;
+    if (e < E) {
+      const float* q = per_col == E ? p + e : p + int64_t(e / per_col) * pitch + e % per_col;
+      l = COHERENT ? __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *q;
+    }
+    ord[r] = e < E ? uint32_t(logit_key(l, e) >> 32) : 0;
     if (e < E) live |= 1u << r;
   }
   int mine = 0;
+  uint32_t mkey = 0;  // (lane j: the ordered bits of its logit, which give the logit back)
   for (int j = 0; j < k; j++) {
     uint32_t m = 0;
 #pragma unroll
@@ -89,11 +100,11 @@ __device__ __forceinline__ int topk_wave(const float* __restrict__ p, int per_co
       if (b) wr = r, wl = __builtin_ctzll(b);
     }
     if (lane == wl) live &= ~(1u << wr);
-    if (lane == j) mine = wl + WAVE * wr;
+    if (lane == j) mine = wl + WAVE * wr, mkey = m;
   }
   const int id = mine;
   const bool on = lane < k;
-  const float l = on ? p[int64_t(id / per_col) * pitch + id % per_col] : 0.0f;
+  const float l = on ? key_logit(mkey) : 0.0f;
   const double l0 = __shfl(double(l), 0, WAVE);
   double e = 0;
   if (on) e = sigmoid ? 1.0 / (1.0 + exp(-double(l))) : exp(double(l) - l0);
@@ -143,6 +154,7 @@ enum DispatchCtrl {
   CTRL_CHUNKS = 4,    // plan chunks
   CTRL_OVER_CAP = 5,  // a column needs more than cap chunks
   CTRL_BAD_FIRST = 6, // P - (the first pair with a bad id): the reference reports the first in pair order
+  CTRL_ROUTED = 7,    // router workgroups finished (k_router_route; reset by the last)
   CTRL_WORDS = 8,
 };
 
@@ -228,5 +240,13 @@ int launch_plan(const DispatchBufs& d, const PlanBufs& p, hipStream_t s);
 // workgroup: the results of launch_topk followed by launch_dispatch.
 int launch_route_small(const float* logits, int64_t n, int E, int k, int sigmoid, int32_t* ids, float* w32,
                        const DispatchBufs& d, hipStream_t s);
+
+// Router logits (as launch_router, into logits (T, E)) and the routing of launch_route_small in one launch, for T <=
+// ROUTER_TG tokens, H a multiple of 256 (at least 2 values per wave), T k <= DISPATCH_BLOCK pairs, E <= MAX_EXPERTS
+// (router_route_fits). xq: when given, x is also quantised into XQ rows.
+bool router_route_fits(int64_t T, int H, int E, int k);
+int launch_router_route(const void* x, int x_dtype, const float* W, int H, int E, int64_t T, float* logits,
+                        uint32_t* xq, int k, int sigmoid, int32_t* ids, float* w32, const DispatchBufs& d,
+                        hipStream_t s);
 
 }  // namespace artlite

@@ -198,7 +198,7 @@ def line(name: str, shape: dict, T: int, r: dict, steps: int) -> dict:
     names = r["names"]
     # the activations as the experts' products take them: fp16 rows (prefill tiles), int8 hi + lo planes (XQ, the
     # decode GEMV), bf16 hi + lo planes (the MFMA decode tiles)
-    dtype = "f16" if "prefill_x" in names else "i8x2-xq" if "router_quant" in names else "bf16x2"
+    dtype = "f16" if "prefill_x" in names else "i8x2-xq" if any(n.startswith("router_quant") for n in names) else "bf16x2"
     return {"tokens": T, "value": T / (r["ms"] * 1e-3), "unit": "tokens/s", "ms_per_step": r["ms"],
             "ms_mean": r["ms_mean"], "steps": steps, "dtype": dtype, "experts_touched": r["U"],
             "kernel_ms": r["kernels"], "roofline": roof, "layer_roofline": lroof}
