@@ -620,13 +620,16 @@ __device__ __forceinline__ void pg_step(const PrefillArgs& a, const PGCtx& c, PG
     // stage's group 1) and group 1's (the next stage's group 0)
     pg_for<10>([&](auto tc) __attribute__((always_inline)) {
       constexpr int t = decltype(tc)::value, nb = t / 5, k = t % 5;
-      if constexpr (t * MBN / 10 == it) {
+      // (Q4_K, whose decoded operands and group-1 state take more registers than what is read: a column block's 5
+      // tasks together, at the last iterations before the operand is used)
+      constexpr int ti1 = L::K4 ? MBN - 2 + nb : t * MBN / 10, ti0 = L::K4 ? IT - 2 + nb : MBN + t * MBN / 10;
+      if constexpr (ti1 == it) {
         if constexpr (k == 0)
           p1[nb] = pg_prep1<QT>(ops, ln, nb);
         else
           b1[nb][k - 1] = pg_word<QT>(p1[nb], ln, k - 1);
       }
-      if constexpr (MBN + t * MBN / 10 == it) {
+      if constexpr (ti0 == it) {
         if constexpr (k == 0)
           p0[nb] = pg_prep0<QT>(nx, raw, ln, nqi, nb);
         else
