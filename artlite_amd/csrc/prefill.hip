@@ -64,29 +64,52 @@ struct PG {
   static constexpr int THREADS = 512;                     // 8 waves, two per SIMD
   static constexpr int ABYTES = TILE_ROWS * 128;          // a stage of A: 64 fp16 per row
   static constexpr int AI = ABYTES / 16 / THREADS;        // A DMAs (16 B) per lane per stage
-  static constexpr int BI = (WN * WDW + THREADS - 1) / THREADS;  // weight DMAs (4 B) per lane per stage
+  // Q4_0: a row's 36 stage bytes in three 12-byte DMA pieces, 12 instructions a stage: waves 0-3 issue two, waves 4-7
+  // (the younger wave of each SIMD, whose step is the longer) one. A 12-byte DMA writes each lane's piece into 16 bytes
+  // of LDS (its last dword untouched), so a row takes 48 LDS bytes, piece k at 16 k: stage byte x at x + 4 (x / 12).
+  // Else 4-byte pieces, the same count for every wave, a row's stage bytes packed.
+  static constexpr bool X3 = QT == ARTLITE_Q4_0;
+  static constexpr int BI = X3 ? 2 : (WN * WDW + THREADS - 1) / THREADS;  // weight DMAs per lane per stage (at most)
+  static constexpr int WLDS = X3 ? 48 : WROW;             // LDS bytes of a staged weight row
   static constexpr int KHDR = WN * 16;                    // Q4_K: the header region's bytes (the codes follow)
-  static constexpr int WBYTES = BI * THREADS * 4;         // (the last dwords: padding the dummies fill)
+  static constexpr int WBYTES = X3 ? WN * WLDS : BI * THREADS * 4;  // (4-byte pieces: the last dwords padding)
   static constexpr int SBYTES = ABYTES + WBYTES;
   static constexpr int MI = 2;           // item metadata DMAs (4 B) per lane per stage
   static constexpr int META = MI * THREADS * 4;  // an item's metadata: 256 row tokens (int), 256 row factors (float2),
                                                  // padding
-  static constexpr int LOADS = AI + BI + MI;
+  static constexpr int LOADS = AI + BI + MI;  // (X3: waves 4-7 issue one fewer)
   static constexpr int R = 3;
   static constexpr int MAXQ = 128;  // items of a workgroup the item table holds
   static constexpr int LDS = R * SBYTES + 2 * META + MAXQ * 16;
   static_assert(AI * 16 * THREADS == ABYTES, "whole A DMAs");
   static_assert(META >= 3 * 1024, "metadata");
   static_assert(K4 || 128 * WDW % 64 == 0, "a wave's weight DMA reads one matrix (gate or up)");
+  static_assert(!X3 || (WROW == 36 && GB == 18 && WN * 3 == 12 * 64 && 128 * 3 % 64 == 0),
+                "Q4_0: 12 DMAs of 12-byte pieces");
   static_assert(!K4 || (BI == 6 && WN * WDW == BI * THREADS), "Q4_K: two header and four code DMAs, no padding");
   static_assert(LDS <= LDS_BYTES, "LDS");
   static_assert((R - 1) * LOADS < 64, "vmcnt");
 };
 
+// the LDS row of weight row r with 48-byte rows (and back: an involution): bit 2 flipped where bit 4 is set, so that
+// the 16 rows a lane group reads at once sit in distinct banks (12-dword rows repeat their bank every 16 rows, and the
+// plain products' lanes read rows r and r + 16 together)
+__device__ __forceinline__ int pg_x3_row(int r) { return r ^ (((r >> 4) & 1) << 2); }
+
 template <int N>
 __device__ __forceinline__ void pg_wait() {
   static_assert(N >= 0 && N < 64, "vmcnt");
   asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory");
+}
+
+// until only the window just issued is in flight (wv: the wave; with 12-byte weight pieces waves 4-7 issue one load
+// fewer a window)
+template <int QT>
+__device__ __forceinline__ void pg_wait_window(int wv) {
+  if (PG<QT>::X3 && wv >= 4)
+    pg_wait<PG<QT>::LOADS - 1>();
+  else
+    pg_wait<PG<QT>::LOADS>();
 }
 
 // every wave's LDS reads done, then the workgroup barrier
@@ -103,6 +126,9 @@ template <int SIZE>
 __device__ __forceinline__ void pg_dma(const void* base, uint32_t off, uint32_t lds) {
   if constexpr (SIZE == 16)
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
+                 : "memory", "m0");
+  else if constexpr (SIZE == 12)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx3 %0, %1" ::"v"(off), "s"(base), "s"(lds)
                  : "memory", "m0");
   else
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds)
@@ -270,6 +296,10 @@ struct PGSrc {
         const int q = (j < 2 ? j : j - 2) * L::THREADS + tid;
         row = j < 2 ? q >> 2 : q >> 3;
         dw = j < 2 ? q & 3 : q & 7;
+      } else if constexpr (L::X3) {  // (piece q: LDS row q / 3, its dwords 3 (q % 3) .. + 3; waves 4-7 have no second)
+        const int q = min(j * L::THREADS + tid, L::WN * 3 - 1);
+        row = pg_x3_row(q / 3);
+        dw = 3 * (q % 3);
       } else {
         const int q = min(j * L::THREADS + tid, L::WN * L::WDW - 1);
         row = q / L::WDW;
@@ -338,15 +368,22 @@ __device__ __forceinline__ void pg_dma_n(int n, const PGIssue<QT, SWIGLU>& is, i
     const uint8_t* base;
     if constexpr (L::K4)  // (headers: instruction 1 reads up's; codes: instructions 4, 5)
       base = j < 2 ? (SWIGLU && j == 1 ? b.wb1 : b.wb0) : (SWIGLU && j >= 4 ? b.wq1 : b.wq0);
+    else if constexpr (L::X3)  // (instructions 6 .. 11: up's rows; the wave's bases)
+      base = j == 0 ? b.wb0 : b.wb1;
     else
       base = SWIGLU && (j * L::THREADS + 64 * wv) >= 128 * L::WDW ? b.wb1 : b.wb0;
-    pg_dma<4>(base, is.src.w[j], b.dstw + (8 * j + wv) * 256);
+    if constexpr (L::X3) {
+      if (j == 1 && wv >= 4) return;
+      pg_dma<12>(base, is.src.w[j], b.dstw + (8 * j + wv) * 1024);
+    } else {
+      pg_dma<4>(base, is.src.w[j], b.dstw + (8 * j + wv) * 256);
+    }
   } else if (n < L::BI + L::AI) {
     const int i = n - L::BI;
     pg_dma<16>(b.ab, is.src.a[i], b.dst + (8 * i + wv) * 1024);
   } else {
     const int j = n - L::BI - L::AI;
-    pg_dma<4>(j == 0 && wv < 4 ? b.mt : b.ms, is.meta.m[j], b.mdst + (8 * j + wv) * 256);
+    pg_dma<4>(j == 0 ? b.mt : b.ms, is.meta.m[j], b.mdst + (8 * j + wv) * 256);
   }
 }
 
@@ -368,7 +405,8 @@ struct PGLane {
 #pragma unroll
     for (int nb = 0; nb < 2; nb++) {
       const int row = swiglu ? 128 * nb + 16 * wv + lr : 32 * wv + 8 * (lr >> 2) + 4 * nb + (lr & 3);
-      bof[nb] = PG<QT>::K4 ? uint32_t(row) : uint32_t(PG<QT>::ABYTES + row * PG<QT>::WROW);
+      bof[nb] = PG<QT>::K4 ? uint32_t(row)
+                           : uint32_t(PG<QT>::ABYTES + (PG<QT>::X3 ? pg_x3_row(row) : row) * PG<QT>::WLDS);
     }
     cb = QT == ARTLITE_Q4_0 ? 8 * (lg & 1) : 8 * lg;
   }
@@ -409,6 +447,16 @@ __device__ __forceinline__ void pg_read_codes(const uint8_t* s, const PGLane<QT>
       const uint8_t* c = s + L::ABYTES + L::KHDR + ln.bof[nb] * 32 + ln.cb;
       r.d[0][nb] = dw(c);
       r.d[1][nb] = dw(c + 4);
+    } else if constexpr (L::X3) {  // (the same dwords from the 48-byte LDS rows: cb 0 or 8, cx its image 0 or 12)
+      const uint8_t* row = s + ln.bof[nb];
+      const int cx = ln.cb + (ln.cb >> 1);
+      r.d[0][nb] = dw(row + ln.cb);
+      r.d[1][nb] = dw(row + cx + 4);
+      r.d[2][nb] = dw(row + cx + 8);
+      r.sc0[nb] = dw(row);
+      o.c10[nb] = dw(row + cx + 24);
+      o.c11[nb] = dw(row + ln.cb + 32);
+      o.sc1[nb] = dw(row + 20);
     } else {
       const uint8_t* row = s + ln.bof[nb];
       r.d[0][nb] = dw(row + ln.cb);
@@ -518,9 +566,13 @@ __device__ __forceinline__ PGItem pg_table(const PGCtx& c, int q) {
 
 // the weight bases of stage sw (Q4_K: super-block sw / 4, its quarter sw % 4)
 template <int QT, bool SWIGLU>
-__device__ __forceinline__ void pg_wbases(const PrefillArgs& a, int sw, PGBases& b) {
+__device__ __forceinline__ void pg_wbases(const PrefillArgs& a, int sw, PGBases& b, int wv) {
   using L = PG<QT>;
-  if constexpr (L::K4) {
+  if constexpr (L::X3) {  // (the wave's own: instruction 0's matrix, instruction 1's)
+    b.wb0 = (SWIGLU && wv >= 6 ? a.w[1] : a.w[0]) + sw * L::WROW;
+    b.wb1 = (SWIGLU ? a.w[1] : a.w[0]) + sw * L::WROW;
+    b.wq0 = b.wq1 = nullptr;
+  } else if constexpr (L::K4) {
     b.wb0 = a.w[0] + (sw >> 2) * 144;
     b.wb1 = (SWIGLU ? a.w[1] : a.w[0]) + (sw >> 2) * 144;
     b.wq0 = b.wb0 + 16 + 32 * (sw & 3);
@@ -555,9 +607,9 @@ __device__ __forceinline__ void pg_open(const PrefillArgs& a, const PGCtx& c, PG
   const int sa = __builtin_amdgcn_readfirstlane(is.qa < c.nq ? is.sta : 0);
   PGBases& b = is.b;
   b.ab = static_cast<const uint8_t*>(static_cast<const void*>(a.a)) + 128 * sa;
-  pg_wbases<QT, SWIGLU>(a, __builtin_amdgcn_readfirstlane(is.qw < c.nq ? is.stw : 0), b);
+  pg_wbases<QT, SWIGLU>(a, __builtin_amdgcn_readfirstlane(is.qw < c.nq ? is.stw : 0), b, c.wv);
   b.ms = reinterpret_cast<const uint8_t*>(a.row_scale);
-  b.mt = a.row_a ? reinterpret_cast<const uint8_t*>(a.row_a) : b.ms;
+  b.mt = a.row_a && c.wv < 4 ? reinterpret_cast<const uint8_t*>(a.row_a) : b.ms;  // (the wave's metadata DMA 0)
   const int ws = is.slot + 1 == L::R ? 0 : is.slot + 1;
   b.dst = __builtin_amdgcn_readfirstlane(c.lbase + is.slot * L::SBYTES);
   b.dstw = __builtin_amdgcn_readfirstlane(c.lbase + ws * L::SBYTES + L::ABYTES);
@@ -601,7 +653,7 @@ __device__ __forceinline__ void pg_step(const PrefillArgs& a, const PGCtx& c, PG
     constexpr int it = decltype(itc)::value;
     if constexpr (it == 0 && HEAD > 0) pg_open<QT, SWIGLU>(a, c, is, nmq);
     if constexpr (it == HEAD) {
-      pg_wait<L::LOADS>();
+      pg_wait_window<QT>(c.wv);
       pg_barrier();
     }
 #pragma unroll
@@ -811,7 +863,7 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   is.stw = 0;
   is.slot = -1;
   is.mq = 0;
-  pg_wbases<QT, SWIGLU>(a, 0, is.b);
+  pg_wbases<QT, SWIGLU>(a, 0, is.b, c.wv);
   is.b.dstw = __builtin_amdgcn_readfirstlane(c.lbase + L::ABYTES);
 #pragma unroll
   for (int n = 0; n < L::BI; n++) pg_dma_n<QT, SWIGLU>(n, is, c.wv);
@@ -822,7 +874,7 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 #pragma unroll
     for (int n = 0; n < L::LOADS; n++) pg_dma_n<QT, SWIGLU>(n, is, c.wv);
   }
-  pg_wait<L::LOADS>();
+  pg_wait_window<QT>(c.wv);
   pg_barrier();
   const PGLane<QT> ln(c.lr, c.lg, c.wv, SWIGLU);
   PGOps<QT> ops;
