@@ -115,6 +115,31 @@ def test_layer_token_counts() -> None:
             assert rel_l2(y, layers.forward_f64(layer, x, ids, w)) < 1e-3
 
 
+def test_decode_routing_repeat() -> None:
+    """The one-launch decode routing (router workgroups, then the last to finish routes) several times in a row, token
+    counts changing between calls: its ticket counter must be back at zero after every launch. Each call's routing and
+    dispatch equal the host restatement's, and a repeated input gives bitwise the same output."""
+    spec = layers.CONFIGS["decode"]
+    layer = layers.make_layer(spec, 5)
+    outs = {}
+    with gpu_layer(layer, max_tokens=16) as g:
+        for T in (16, 1, 16, 7, 16, 7):
+            x = layers.make_x(spec, T, T)
+            y = g(gpu_input(spec, x))
+            assert "router_quant_route" in g.kernel_names(), g.kernel_names()
+            lg, ids, w = g.tap("logits"), g.tap("ids"), g.tap("weights")
+            assert ulp_diff(lg, layers.logits(layer, x)).max() <= 1
+            hids, hw = layers.route_host(layer, lg)
+            assert np.array_equal(ids, hids) and ulp_diff(w, hw).max() <= 1, T
+            dref = host_ref.dispatch(ids, spec.E)
+            for tap in ("counts", "offsets", "order", "slot"):
+                assert np.array_equal(g.tap(tap), dref[tap]), (T, tap)
+            assert rel_l2(y, moe_ref.moe_ffn(x, ids, w, layers.expert(layer))) < 1e-3, T
+            if T in outs:
+                assert np.array_equal(outs[T].view(np.uint32), y.view(np.uint32)), T
+            outs[T] = y
+
+
 def test_layer_errors() -> None:
     from artlite_amd import Error
     from artlite_amd.moe.layer import MoELayer
