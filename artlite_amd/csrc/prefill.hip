@@ -803,11 +803,16 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   c.nq = full + (rem && ((full & 1) ? j0 >= G - rem : j0 < rem));  // (at most MAXQ: the launch checks)
   if (c.nq == 0) return;
   // the ranking and the item table: every global load of the tiles and offsets, once, before any DMA is in flight
-  // (the ranking's keys and order in the ring's memory, not yet in use: n_run <= MAXQ G <= 4096)
+  // (the ranking's keys, order and the run's items in the ring's memory, not yet in use: n_run <= MAXQ G <= 4096)
   uint8_t* key = lds;
   uint16_t* order = reinterpret_cast<uint16_t*>(lds + 4096);
-  for (int i = c.tid; i < n_run; i += L::THREADS)
-    key[i] = uint8_t((pg_item<SWIGLU>(a, lo + i, nbk).m_valid + 31) / 32);  // (the K loop's even row-block count / 2)
+  int4* run = reinterpret_cast<int4*>(lds + 12288);
+  static_assert(12288 + 4096 * 16 <= L::R * L::SBYTES, "the ranking's LDS");
+  for (int i = c.tid; i < n_run; i += L::THREADS) {
+    const PGItem J = pg_item<SWIGLU>(a, lo + i, nbk);
+    key[i] = uint8_t((J.m_valid + 31) / 32);  // (the K loop's even row-block count / 2)
+    run[i] = make_int4(J.e, J.s0, J.m_valid, J.n0);
+  }
   __syncthreads();
   if (c.wv == 0) {  // (one wave: per key, ballots over runs of 64 items)
     constexpr int KM = TILE_ROWS / 32;  // (keys 1 .. KM)
@@ -834,8 +839,7 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   __syncthreads();
   if (c.tid < c.nq) {
     const int q = c.tid, pos = q * G + ((q & 1) ? G - 1 - j0 : j0);
-    const PGItem I = pg_item<SWIGLU>(a, lo + order[pos], nbk);
-    table[q] = make_int4(I.e, I.s0, I.m_valid, I.n0);
+    table[q] = run[order[pos]];
   }
   __syncthreads();
   // item 0's metadata, landed before its sources are made (buffer 0)
