@@ -529,10 +529,90 @@ __global__ __launch_bounds__(256) void k_prefill_x_rows(const void* __restrict__
   prefill_x_factors(t, threadIdx.x, xe, l1, wmax, pairs, F, gu, dn, gu2, dn2);
 }
 
+// The same, a wave per token (four tokens a workgroup): lane l holds pieces l + 64 j of the row (8 values each, H =
+// 512 NP), every load in flight at once; the row's largest magnitude and L1 norm by reductions within the wave alone
+// (no LDS, no barrier), so that a workgroup costs one round trip to memory.
+template <int XT, int NP>
+__global__ __launch_bounds__(256) void k_prefill_x_wave(const void* __restrict__ x, int64_t T, int H,
+                                                        const float* __restrict__ wmax, int pairs, int F,
+                                                        uint16_t* __restrict__ x16, float2* gu, float2* dn,
+                                                        float2* gu2, float2* dn2) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = int64_t(blockIdx.x) * 4 + threadIdx.x / 64;
+  if (t >= T) return;
+  float v[NP][8];
+  if (XT == ARTLITE_X_F32) {
+    float4 q[NP][2];
+#pragma unroll
+    for (int j = 0; j < NP; j++) {
+      const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + t * H) + 2 * (lane + 64 * j);
+      q[j][0] = p[0], q[j][1] = p[1];
+    }
+#pragma unroll
+    for (int j = 0; j < NP; j++) {
+      v[j][0] = q[j][0].x, v[j][1] = q[j][0].y, v[j][2] = q[j][0].z, v[j][3] = q[j][0].w;
+      v[j][4] = q[j][1].x, v[j][5] = q[j][1].y, v[j][6] = q[j][1].z, v[j][7] = q[j][1].w;
+    }
+  } else {
+    uint4 q[NP];
+#pragma unroll
+    for (int j = 0; j < NP; j++) q[j] = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + t * H)[lane + 64 * j];
+#pragma unroll
+    for (int j = 0; j < NP; j++) {
+      const uint32_t w[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+#pragma unroll
+      for (int c = 0; c < 4; c++) v[j][2 * c] = bf16_to_f32(w[c] & 0xFFFFu), v[j][2 * c + 1] = bf16_to_f32(w[c] >> 16);
+    }
+  }
+  float mx = 0.0f, l1 = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NP; j++)
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      mx = fmaxf(mx, fabsf(v[j][c]));
+      l1 += fabsf(v[j][c]);
+    }
+  for (int o = 32; o; o >>= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, o));
+    l1 += __shfl_xor(l1, o);
+  }
+  const int xe = (mx > 0.0f && mx <= 3.4e38f) ? ilogbf(mx) - 14 : 0;
+#pragma unroll
+  for (int j = 0; j < NP; j++) {
+    uint32_t w[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+      w[c] = uint32_t(__builtin_bit_cast(uint16_t, _Float16(__builtin_ldexpf(v[j][2 * c], -xe)))) |
+             uint32_t(__builtin_bit_cast(uint16_t, _Float16(__builtin_ldexpf(v[j][2 * c + 1], -xe)))) << 16;
+    reinterpret_cast<uint4*>(x16 + t * H)[lane + 64 * j] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  prefill_x_factors(t, lane, xe, l1, wmax, pairs, F, gu, dn, gu2, dn2);
+}
+
 int launch_prefill_x(const void* x, int x_dtype, int64_t T, int H, const float* wmax, int pairs, int F, uint16_t* x16,
                      float2* gu, float2* dn, float2* gu2, float2* dn2, hipStream_t s) {
   if (T <= 0) return ARTLITE_OK;
   if (pairs < 1 || pairs > 2 || (pairs == 2 && (!gu2 || !dn2))) return fail(ARTLITE_EINVAL, "prefill x: %d bounds", pairs);
+  if (H % 512 == 0 && (H / 512 == 1 || H / 512 == 2 || H / 512 == 4 || H / 512 == 8)) {
+    const bool f32 = x_dtype == ARTLITE_X_F32;
+    const unsigned g = unsigned((T + 3) / 4);
+#define ART_PXW(XT, NP) k_prefill_x_wave<XT, NP><<<g, 256, 0, s>>>(x, T, H, wmax, pairs, F, x16, gu, dn, gu2, dn2)
+#define ART_PXW2(NP) \
+  if (f32)           \
+    ART_PXW(ARTLITE_X_F32, NP); \
+  else               \
+    ART_PXW(ARTLITE_X_BF16, NP);
+    switch (H / 512) {
+      case 1: ART_PXW2(1) break;
+      case 2: ART_PXW2(2) break;
+      case 4: ART_PXW2(4) break;
+      default: ART_PXW2(8) break;
+    }
+#undef ART_PXW2
+#undef ART_PXW
+    ART_HIP(hipGetLastError());
+    return ARTLITE_OK;
+  }
   if (H % 8 == 0 && H <= 4 * 2048) {
     const bool f32 = x_dtype == ARTLITE_X_F32;
 #define ART_PX(XT, NP) k_prefill_x_rows<XT, NP><<<unsigned(T), 256, 0, s>>>(x, H, wmax, pairs, F, x16, gu, dn, gu2, dn2)
