@@ -231,18 +231,24 @@ __global__ __launch_bounds__(4 * WAVE) void k_router_small(const void* __restric
 // the step; result element i of lane l is row 4 i + l / 16, column l % 16. The K values of a 16-value block are dealt
 // as step s, lane group g -> k0 + 4 g + s, so each lane's four steps are one 16-byte LDS read of its x row and one of
 // its W row; step s accumulates into acc[s] (consecutive MFMAs independent), the four summed at the end. Rows past T,
-// experts past E load the last one (not stored); K past H loads zeros.
-template <int XT, int TE>
-__global__ __launch_bounds__(2 * TE / 16 * WAVE) void k_router_mfma(const void* __restrict__ xv,
-                                                                    const float* __restrict__ W, int H, int E,
-                                                                    int64_t T, float* __restrict__ out,
-                                                                    int64_t out_row) {
+// experts past E load the last one (not stored); K past H loads zeros. KP parts of K: the workgroup's waves are KP
+// sets of the above, set p taking K values [p Kp, (p + 1) Kp) through LDS buffers of its own (more waves a SIMD to
+// issue MFMAs while others wait); the sets' sums are added in set order at the end.
+template <int XT, int TE, int KP>
+__global__ __launch_bounds__(KP * 2 * TE / 16 * WAVE) void k_router_mfma(const void* __restrict__ xv,
+                                                                         const float* __restrict__ W, int H, int E,
+                                                                         int64_t T, float* __restrict__ out,
+                                                                         int64_t out_row) {
   typedef double d4 __attribute__((ext_vector_type(4)));
-  constexpr int TM = 32, KS = 64, PAD = 68, THREADS = 2 * TE / 16 * WAVE;
+  constexpr int TM = 32, KS = 64, PAD = 68, THREADS = 2 * TE / 16 * WAVE;  // (threads of one set)
   constexpr int NX = TM * 16 / THREADS, NW = TE * 16 / THREADS;  // 16-byte pieces per thread per stage
-  __shared__ __attribute__((aligned(16))) float xs[2][TM][PAD];
-  __shared__ __attribute__((aligned(16))) float ws[2][TE][PAD];
-  const int tid = threadIdx.x, lane = tid & (WAVE - 1), wv = tid / WAVE;
+  __shared__ __attribute__((aligned(16))) float xs_all[KP][2][TM][PAD];
+  __shared__ __attribute__((aligned(16))) float ws_all[KP][2][TE][PAD];
+  const int part = int(threadIdx.x) / THREADS;
+  float(&xs)[2][TM][PAD] = xs_all[part];
+  float(&ws)[2][TE][PAD] = ws_all[part];
+  const int Kp = (H / KP + KS - 1) / KS * KS, kb = part * Kp, ke = min(H, kb + Kp);
+  const int tid = threadIdx.x % THREADS, lane = tid & (WAVE - 1), wv = tid / WAVE;
   const int tb = wv & 1, eb = wv >> 1, g = lane >> 4, r = lane & 15;
   const int64_t t0 = int64_t(blockIdx.x) * TM;
   const int e0 = int(blockIdx.y) * TE;
@@ -264,7 +270,7 @@ __global__ __launch_bounds__(2 * TE / 16 * WAVE) void k_router_mfma(const void* 
   // (loads past H read the last piece again, unconditionally, so that no branch makes the compiler wait for loads in
   // flight; the store into LDS puts zeros in their place)
   auto gload = [&](int k0) -> Piece {
-    const int k = min(k0 + 4 * lq, H - 4);
+    const int k = min(kb + k0 + 4 * lq, H - 4);
     Piece p;
 #pragma unroll
     for (int i = 0; i < NX; i++) {
@@ -282,7 +288,7 @@ __global__ __launch_bounds__(2 * TE / 16 * WAVE) void k_router_mfma(const void* 
   };
   // (values, not references or lvalue selects, which the compiler turns into pointer selects over scratch copies)
   auto sstore = [&](int st, Piece p) {
-    const float m = st * KS + 4 * lq < H ? 1.0f : 0.0f;  // (x 1 exact; x 0 gives +-0, adding nothing)
+    const float m = kb + st * KS + 4 * lq < ke ? 1.0f : 0.0f;  // (x 1 exact; x 0 gives +-0, adding nothing)
 #pragma unroll
     for (int i = 0; i < NX; i++)
       *reinterpret_cast<float4*>(&xs[st & 1][(tid + i * THREADS) / 16][4 * lq]) =
@@ -295,7 +301,7 @@ __global__ __launch_bounds__(2 * TE / 16 * WAVE) void k_router_mfma(const void* 
   d4 acc[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) acc[i] = d4{0, 0, 0, 0};
-  const int S = (H + KS - 1) / KS;
+  const int S = (Kp + KS - 1) / KS;  // (the same in every set: the barriers are the workgroup's)
   // stage st: its products from buffer st & 1, then the next stage's piece (loaded two stages before) into the other
   // buffer (whose reads ended before the last barrier), then a barrier; the loop is unrolled by two so that the two
   // pieces in flight keep their registers (a copy would wait for the loads)
@@ -327,7 +333,20 @@ __global__ __launch_bounds__(2 * TE / 16 * WAVE) void k_router_mfma(const void* 
     if (st + 2 < S) sstore(st + 2, pa);
     __syncthreads();
   }
-  const d4 c = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  d4 c = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  if constexpr (KP > 1) {  // (the staging buffers are free: every read ended before the loop's last barrier)
+    double* red = reinterpret_cast<double*>(&xs_all[0][0][0][0]);
+    static_assert(sizeof(xs_all) >= size_t(KP - 1) * THREADS * 4 * sizeof(double), "the sets' sums in LDS");
+    if (part > 0)
+#pragma unroll
+      for (int i = 0; i < 4; i++) red[((part - 1) * THREADS + tid) * 4 + i] = c[i];
+    __syncthreads();
+    if (part > 0) return;
+#pragma unroll
+    for (int q = 1; q < KP; q++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) c[i] += red[((q - 1) * THREADS + tid) * 4 + i];
+  }
   const int e = e0 + 16 * eb + r;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
@@ -381,12 +400,13 @@ int launch_router(const void* x, int x_dtype, const float* W, int H, int E, int6
   if (int64_t(H) * xb > ROUTER_LDS) return fail(ARTLITE_EINVAL, "router: H %d too wide", H);
   const size_t lds = size_t(tt) * H * xb;
   if (!xq && T >= 64 && E >= 16 && H % 16 == 0) {  // (prefill-sized: the fp64 MFMA)
-    constexpr int TE = 64;  // (tiles of 32 x 64, 8 waves: measured faster than 32 x 32 with two workgroups per CU)
-    const dim3 g(unsigned((T + 31) / 32), unsigned((E + TE - 1) / TE)), b(2 * TE / 16 * WAVE);
+    // (tiles of 32 x 64, 8 waves a K part: measured faster than 32 x 32 with two workgroups per CU)
+    constexpr int TE = 64, KP = 2;
+    const dim3 g(unsigned((T + 31) / 32), unsigned((E + TE - 1) / TE)), b(KP * 2 * TE / 16 * WAVE);
     if (x_dtype == ARTLITE_X_F32)
-      k_router_mfma<ARTLITE_X_F32, TE><<<g, b, 0, s>>>(x, W, H, E, T, out, out_row);
+      k_router_mfma<ARTLITE_X_F32, TE, KP><<<g, b, 0, s>>>(x, W, H, E, T, out, out_row);
     else
-      k_router_mfma<ARTLITE_X_BF16, TE><<<g, b, 0, s>>>(x, W, H, E, T, out, out_row);
+      k_router_mfma<ARTLITE_X_BF16, TE, KP><<<g, b, 0, s>>>(x, W, H, E, T, out, out_row);
     ART_HIP(hipGetLastError());
     return ARTLITE_OK;
   }
