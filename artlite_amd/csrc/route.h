@@ -8,6 +8,7 @@ namespace artlite {
 constexpr int MAX_EXPERTS = 1024;  // (keys per lane: 16)
 constexpr int MAX_TOPK = 64;       // (one lane per chosen expert)
 constexpr int ROUTER_TG = 16;      // tokens per router block (at most)
+constexpr int ROUTER_GROUPS = 4;   // token groups of the one-launch router + routing (k_router_route), at most
 constexpr int ROUTER_EW = 8;       // experts (waves) per router block
 constexpr int ROUTER_LDS = 64 * 1024;  // bytes of staged token rows per router block
 
@@ -242,7 +243,7 @@ int launch_route_small(const float* logits, int64_t n, int E, int k, int sigmoid
                        const DispatchBufs& d, hipStream_t s);
 
 // Router logits (as launch_router, into logits (T, E)) and the routing of launch_route_small in one launch, for T <=
-// ROUTER_TG tokens, H a multiple of 256 (at least 2 values per wave), T k <= DISPATCH_BLOCK pairs, E <= MAX_EXPERTS
+// ROUTER_GROUPS ROUTER_TG tokens, H a multiple of 256 (at least 2 values per wave), T k <= DISPATCH_BLOCK pairs, E <= MAX_EXPERTS
 // (router_route_fits). xq: when given, x is also quantised into XQ rows.
 bool router_route_fits(int64_t T, int H, int E, int k);
 int launch_router_route(const void* x, int x_dtype, const float* W, int H, int E, int64_t T, float* logits,

@@ -595,12 +595,13 @@ __global__ __launch_bounds__(DISPATCH_BLOCK) void k_route_small(const float* __r
   route_block<R, false>(logits, n, E, k, sigmoid, ids, w32, d);
 }
 
-// Router logits and routing of small batches in one launch (T <= ROUTER_TG tokens, H a multiple of 256, T k <=
-// DISPATCH_BLOCK pairs). A workgroup per expert: its NW waves each take H / NW values of K (lane: values 2 lane +
-// 128 j of the wave's slice), x read straight from memory (L2), float64 products; a wave's 16 token sums by halving
-// exchanges, then the waves' sums added in wave order, rounded once to fp32. The last expert workgroup to store its
-// logits (a ticket in ctrl, reset by that workgroup) routes them (route_block). Workgroups past the experts quantise
-// x into XQ, a wave per unit.
+// Router logits and routing of small batches in one launch (T <= ROUTER_GROUPS ROUTER_TG tokens, H a multiple of
+// 256, T k <= DISPATCH_BLOCK pairs). A workgroup per expert and group of ROUTER_TG tokens (workgroup b: expert b % E,
+// tokens ROUTER_TG (b / E) ..): its NW waves each take H / NW values of K (lane: values 2 lane + 128 j of the wave's
+// slice), x read straight from memory (L2), float64 products; a wave's 16 token sums by halving exchanges, then the
+// waves' sums added in wave order, rounded once to fp32. The last of these workgroups to store its logits (a ticket
+// in ctrl, reset by that workgroup) routes them all (route_block). Workgroups past them quantise x into XQ, a wave
+// per unit.
 template <int XT, int R>
 __global__ __launch_bounds__(DISPATCH_BLOCK) void k_router_route(const void* __restrict__ xv,
                                                                  const float* __restrict__ W, int H, int E, int64_t T,
@@ -611,12 +612,13 @@ __global__ __launch_bounds__(DISPATCH_BLOCK) void k_router_route(const void* __r
   __shared__ double part[NW][ROUTER_TG];
   __shared__ int last;
   const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE;
-  if (int(blockIdx.x) >= E) {  // XQ of x
-    const int64_t w = int64_t(blockIdx.x - E) * NW + wv;
+  const int G = int((T + ROUTER_TG - 1) / ROUTER_TG);  // (token groups)
+  if (int(blockIdx.x) >= E * G) {  // XQ of x
+    const int64_t w = int64_t(blockIdx.x - E * G) * NW + wv;
     if (w < T * (H / 256)) xq_quant_unit<XT>(xv, w, H, xq, lane);
     return;
   }
-  const int e = blockIdx.x, nt = int(T);
+  const int e = int(blockIdx.x) % E, t0 = int(blockIdx.x) / E * ROUTER_TG, nt = min(ROUTER_TG, int(T) - t0);
   const int q = H / NW;
   const float* wr = W + int64_t(e) * H + wv * q;
   double acc[ROUTER_TG];
@@ -630,7 +632,7 @@ __global__ __launch_bounds__(DISPATCH_BLOCK) void k_router_route(const void* __r
     float2 xl[ROUTER_TG];
 #pragma unroll
     for (int t = 0; t < ROUTER_TG; t++) {
-      const int64_t o = int64_t(min(t, nt - 1)) * H + wv * q + i;
+      const int64_t o = int64_t(t0 + min(t, nt - 1)) * H + wv * q + i;
       if (XT == ARTLITE_X_F32) {
         xl[t] = *reinterpret_cast<const float2*>(static_cast<const float*>(xv) + o);
       } else {
@@ -662,11 +664,11 @@ __global__ __launch_bounds__(DISPATCH_BLOCK) void k_router_route(const void* __r
       double sum = part[0][lane];
 #pragma unroll
       for (int w = 1; w < NW; w++) sum += part[w][lane];
-      __hip_atomic_store(logits + int64_t(lane) * E + e, float(sum), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(logits + int64_t(t0 + lane) * E + e, float(sum), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (lane == 0)
-      last = __hip_atomic_fetch_add(d.ctrl + CTRL_ROUTED, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == E - 1;
+      last = __hip_atomic_fetch_add(d.ctrl + CTRL_ROUTED, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == E * G - 1;
   }
   lds_barrier();
   if (!last) return;
@@ -697,7 +699,7 @@ int launch_route_small(const float* logits, int64_t n, int E, int k, int sigmoid
 }
 
 bool router_route_fits(int64_t T, int H, int E, int k) {
-  return T >= 1 && T <= ROUTER_TG && H % 256 == 0 && H / (DISPATCH_BLOCK / WAVE) >= 2 && T * k <= DISPATCH_BLOCK &&
+  return T >= 1 && T <= ROUTER_GROUPS * ROUTER_TG && H % 256 == 0 && H / (DISPATCH_BLOCK / WAVE) >= 2 && T * k <= DISPATCH_BLOCK &&
          E <= MAX_EXPERTS;
 }
 
@@ -708,7 +710,7 @@ int launch_router_route(const void* x, int x_dtype, const float* W, int H, int E
     return fail(ARTLITE_EINVAL, "router_route: %lld tokens, H %d, %d experts, k %d", (long long)T, H, E, k);
   constexpr int NW = DISPATCH_BLOCK / WAVE;
   const int nq = xq ? int((T * (H / 256) + NW - 1) / NW) : 0;
-  const dim3 g(unsigned(E + nq)), b(DISPATCH_BLOCK);
+  const dim3 g(unsigned(E * ((T + ROUTER_TG - 1) / ROUTER_TG) + nq)), b(DISPATCH_BLOCK);
 #define ART_RR(XT, RR) k_router_route<XT, RR><<<g, b, 0, s>>>(x, W, H, E, T, logits, xq, k, sigmoid, ids, w32, d)
 #define ART_RR_R(XT)   \
   if (E <= 64)         \

@@ -116,14 +116,15 @@ def test_layer_token_counts() -> None:
 
 
 def test_decode_routing_repeat() -> None:
-    """The one-launch decode routing (router workgroups, then the last to finish routes) several times in a row, token
-    counts changing between calls: its ticket counter must be back at zero after every launch. Each call's routing and
-    dispatch equal the host restatement's, and a repeated input gives bitwise the same output."""
+    """The one-launch decode routing (router workgroups per expert and group of 16 tokens, then the last to finish
+    routes) several times in a row, token counts changing between calls (one to four token groups): its ticket
+    counter must be back at zero after every launch. Each call's routing and dispatch equal the host restatement's,
+    and a repeated input gives bitwise the same output."""
     spec = layers.CONFIGS["decode"]
     layer = layers.make_layer(spec, 5)
     outs = {}
-    with gpu_layer(layer, max_tokens=16) as g:
-        for T in (16, 1, 16, 7, 16, 7):
+    with gpu_layer(layer, max_tokens=64) as g:
+        for T in (16, 1, 64, 7, 40, 16, 64, 7):
             x = layers.make_x(spec, T, T)
             y = g(gpu_input(spec, x))
             assert "router_quant_route" in g.kernel_names(), g.kernel_names()
