@@ -31,6 +31,7 @@ struct artlite_moe_layer {
   DevBuf wmax;                    // max |w| of gate, up, shared gate, shared up (the bounds on |h|), down
   DevBuf logits, ids, w, sg;
   DevBuf table, ctrl, counts, offsets, order, slot, tiles;
+  DevBuf gtick;  // the one-launch routing's tickets per token group (GTICK_STRIDE ints apart)
   DevBuf hhi, hlo, ypairs, shhi, shlo, ys, y;
   DevBuf h16, sh16;  // the prefill's h (fp16, scaled per token)
   DevBuf xq, hq, shq;  // the decode path's XQ activations
@@ -216,6 +217,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     db.row_out[0] = L->gu_row.as<float2>();
     db.row_out[1] = L->dn_row.as<float2>();
   }
+  if (path.fused_route) db.gtick = L->gtick.as<int32_t>();
   ART_TRY(mark());
   if (path.fused_route)
     ART_TRY(launch_router_route(xin, xdt, L->router.as<float>(), H, E, T, L->logits.as<float>(),
@@ -559,6 +561,7 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
   res(L->order, size_t(P) * 4);
   res(L->slot, size_t(P) * 4);
   res(L->tiles, size_t(2 * tile_bound(P, int(E), 1)) * 4);
+  res(L->gtick, size_t(ROUTER_GROUPS) * GTICK_STRIDE * 4);
   res(L->hhi, size_t(P * F) * 2);
   res(L->hlo, size_t(P * F) * 2);
   res(L->ypairs, size_t(P * H) * 4);
@@ -588,7 +591,8 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
     res(L->shlo, size_t(T) * d.shared_ffn * 2);
     res(L->ys, size_t(T * H) * 4);
   }
-  if (rc == ARTLITE_OK && hipMemset(L->ctrl.p, 0, CTRL_WORDS * 4) != hipSuccess)
+  if (rc == ARTLITE_OK && (hipMemset(L->ctrl.p, 0, CTRL_WORDS * 4) != hipSuccess ||
+                           hipMemset(L->gtick.p, 0, size_t(ROUTER_GROUPS) * GTICK_STRIDE * 4) != hipSuccess))
     rc = fail(ARTLITE_EHIP, "moe layer: memset");
   if (rc != ARTLITE_OK) {
     artlite_moe_layer_destroy(L);

@@ -9,6 +9,7 @@ constexpr int MAX_EXPERTS = 1024;  // (keys per lane: 16)
 constexpr int MAX_TOPK = 64;       // (one lane per chosen expert)
 constexpr int ROUTER_TG = 16;      // tokens per router block (at most)
 constexpr int ROUTER_GROUPS = 4;   // token groups of the one-launch router + routing (k_router_route), at most
+constexpr int GTICK_STRIDE = 64;   // ints between its group tickets (each in lines of its own)
 constexpr int ROUTER_EW = 8;       // experts (waves) per router block
 constexpr int ROUTER_LDS = 64 * 1024;  // bytes of staged token rows per router block
 
@@ -68,8 +69,9 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // ordered bits among the experts not yet taken (a 32-bit wave maximum), then the lowest id holding them (ballots: the
 // low half of logit_key decides ties), lane j keeping the j-th; then the weights. ev (64 doubles) and sum (1): the
 // wave's LDS scratch. Lane j < k writes ids[j] and the weights (w32 / w64 when given) and returns its id; other lanes
-// return -1. COHERENT: the logits are read at device scope (written by other workgroups of the same launch).
-template <int R, bool COHERENT = false>
+// return -1. COHERENT: the logits are read at device scope (written by other workgroups of the same launch);
+// DEV_IDS: the ids are stored at device scope (read by other workgroups of the same launch).
+template <int R, bool COHERENT = false, bool DEV_IDS = false>
 __device__ __forceinline__ int topk_wave(const float* __restrict__ p, int per_col, int64_t pitch, int E, int k,
                                          int sigmoid, double* ev, double* sum, int lane, int32_t* __restrict__ ids,
                                          float* __restrict__ w32, double* __restrict__ w64) {
@@ -122,7 +124,10 @@ __device__ __forceinline__ int topk_wave(const float* __restrict__ p, int per_co
   const double s = *sum;
   __builtin_amdgcn_wave_barrier();  // (the scratch is free again once every lane has read the sum)
   if (!on) return -1;
-  ids[lane] = id;
+  if constexpr (DEV_IDS)
+    __hip_atomic_store(ids + lane, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    ids[lane] = id;
   const double w = e / s;
   if (w32) w32[lane] = float(w);
   if (w64) w64[lane] = w;
@@ -174,6 +179,9 @@ struct DispatchBufs {
   int32_t* cstart;   // E + 1 chunk prefix (plan only; may be null)
   int chunk;         // plan chunk size (0: no plan)
   int balanced = 0;  // 1: an expert's c rows in tiles of balanced_rows(c, BM) rows (the last one shorter)
+  // (optional, the one-launch routing of more than one token group) a ticket per group, GTICK_STRIDE ints apart,
+  // zero before the first launch (kept zero by the launches)
+  int32_t* gtick = nullptr;
   // (optional, the prefill path) per sorted row s, filled by the scatter: its token t = order[s] / k into row_a, and
   // that token's row factors row_f[0][t], row_f[1][t] into row_out[0][s], row_out[1][s]
   int32_t* row_a = nullptr;

@@ -496,7 +496,9 @@ __device__ __forceinline__ void block_scan_n(const int (&v)[S], int (&ex)[S], in
 // The routing of n tokens' (n, E) logits by one DISPATCH_BLOCK workgroup: top k (a wave per token), then the counts,
 // offsets, the tile list and each pair's sorted position. Every exchange is through LDS, so no barrier waits for the
 // global stores.
-template <int R, bool COHERENT>
+// IDS_SET: the top-k is already done (the ids at device scope in ids, written by other workgroups of the launch);
+// only the dispatch is left.
+template <int R, bool COHERENT, bool IDS_SET = false>
 __device__ __forceinline__ void route_block(const float* __restrict__ logits, int64_t n, int E, int k, int sigmoid,
                                             int32_t* __restrict__ ids, float* __restrict__ w32, const DispatchBufs& d) {
   constexpr int NW = DISPATCH_BLOCK / WAVE;
@@ -511,10 +513,14 @@ __device__ __forceinline__ void route_block(const float* __restrict__ logits, in
   static_assert(MAX_EXPERTS % 8 == 0, "wcnt rows in 16-byte pieces");
   for (int i = tid; i < NW * MAX_EXPERTS / 8; i += DISPATCH_BLOCK)
     reinterpret_cast<uint4*>(&wcnt[0][0])[i] = uint4{0, 0, 0, 0};
-  for (int64_t t = wv; t < n; t += NW) {  // (one wave per token)
-    const int id = topk_wave<R, COHERENT>(logits + t * E, E, 0, E, k, sigmoid, ev[wv], &sum[wv], lane, ids + t * k,
-                                          w32 + t * k, nullptr);
-    if (lane < k) sid[t * k + lane] = id;
+  if constexpr (IDS_SET) {
+    if (tid < n * k) sid[tid] = __hip_atomic_load(ids + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    for (int64_t t = wv; t < n; t += NW) {  // (one wave per token)
+      const int id = topk_wave<R, COHERENT>(logits + t * E, E, 0, E, k, sigmoid, ev[wv], &sum[wv], lane, ids + t * k,
+                                            w32 + t * k, nullptr);
+      if (lane < k) sid[t * k + lane] = id;
+    }
   }
   lds_barrier();
   const int P = int(n) * k, p = tid;
@@ -599,9 +605,11 @@ __global__ __launch_bounds__(DISPATCH_BLOCK) void k_route_small(const float* __r
 // 256, T k <= DISPATCH_BLOCK pairs). A workgroup per expert and group of ROUTER_TG tokens (workgroup b: expert b % E,
 // tokens ROUTER_TG (b / E) ..): its NW waves each take H / NW values of K (lane: values 2 lane + 128 j of the wave's
 // slice), x read straight from memory (L2), float64 products; a wave's 16 token sums by halving exchanges, then the
-// waves' sums added in wave order, rounded once to fp32. The last of these workgroups to store its logits (a ticket
-// in ctrl, reset by that workgroup) routes them all (route_block). Workgroups past them quantise x into XQ, a wave
-// per unit.
+// waves' sums added in wave order, rounded once to fp32. One token group: the last of these workgroups to store its
+// logits (a ticket in ctrl, reset by that workgroup) routes them all (route_block). More (d.gtick given): the last
+// workgroup of each group (a ticket per group, in lines of their own) takes the top k of the group's tokens, a wave
+// per token, and stores the ids at device scope; the last group to do so (the ticket in ctrl) dispatches all the
+// pairs. Workgroups past them quantise x into XQ, a wave per unit.
 template <int XT, int R>
 __global__ __launch_bounds__(DISPATCH_BLOCK) void k_router_route(const void* __restrict__ xv,
                                                                  const float* __restrict__ W, int H, int E, int64_t T,
@@ -618,7 +626,8 @@ __global__ __launch_bounds__(DISPATCH_BLOCK) void k_router_route(const void* __r
     if (w < T * (H / 256)) xq_quant_unit<XT>(xv, w, H, xq, lane);
     return;
   }
-  const int e = int(blockIdx.x) % E, t0 = int(blockIdx.x) / E * ROUTER_TG, nt = min(ROUTER_TG, int(T) - t0);
+  const int e = int(blockIdx.x) % E, gi = int(blockIdx.x) / E, t0 = gi * ROUTER_TG, nt = min(ROUTER_TG, int(T) - t0);
+  const bool groups = G > 1 && d.gtick;
   const int q = H / NW;
   const float* wr = W + int64_t(e) * H + wv * q;
   double acc[ROUTER_TG];
@@ -668,13 +677,38 @@ __global__ __launch_bounds__(DISPATCH_BLOCK) void k_router_route(const void* __r
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (lane == 0)
-      last = __hip_atomic_fetch_add(d.ctrl + CTRL_ROUTED, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == E * G - 1;
+      last = groups ? __hip_atomic_fetch_add(d.gtick + gi * GTICK_STRIDE, 1, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT) == E - 1
+                    : __hip_atomic_fetch_add(d.ctrl + CTRL_ROUTED, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                          E * G - 1;
   }
   lds_barrier();
   if (!last) return;
-  if (threadIdx.x == 0)  // (ready for the next launch)
-    __hip_atomic_store(d.ctrl + CTRL_ROUTED, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  route_block<R, true>(logits, T, E, k, sigmoid, ids, w32, d);
+  if (!groups) {
+    if (threadIdx.x == 0)  // (ready for the next launch)
+      __hip_atomic_store(d.ctrl + CTRL_ROUTED, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    route_block<R, true>(logits, T, E, k, sigmoid, ids, w32, d);
+    return;
+  }
+  // the group's top k (the ids at device scope, for the workgroup that dispatches), then the ticket across groups
+  if (threadIdx.x == 0) __hip_atomic_store(d.gtick + gi * GTICK_STRIDE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  {
+    __shared__ double ev[NW][WAVE];
+    __shared__ double sum[NW];
+    if (wv < nt) {
+      const int64_t t = t0 + wv;
+      topk_wave<R, true, true>(logits + t * E, E, 0, E, k, sigmoid, ev[wv], &sum[wv], lane, ids + t * k, w32 + t * k,
+                               nullptr);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  lds_barrier();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(d.ctrl + CTRL_ROUTED, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1;
+  lds_barrier();
+  if (!last) return;
+  if (threadIdx.x == 0) __hip_atomic_store(d.ctrl + CTRL_ROUTED, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  route_block<R, true, true>(logits, T, E, k, sigmoid, ids, w32, d);
 }
 
 int launch_route_small(const float* logits, int64_t n, int E, int k, int sigmoid, int32_t* ids, float* w32,
