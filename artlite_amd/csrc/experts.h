@@ -35,17 +35,19 @@ struct GemmArgs {
 constexpr int DECODE_BM = 8;
 constexpr int PREFILL_BM = 256;
 
-// One prefill launch (prefill.hip: fp16 MFMA tiles of at most PREFILL_BM rows): for each tile and each block of output
-// rows, out[s][n] = sum_k A[row_a(s)][k] W_e[n][k] with A in fp16 (its rows scaled by powers of two) and W_e's rows
-// raw GGUF blocks; row_scale[s] = (x, y) undoes the scales: plain launches write fp32 x y sum (y set) or fp16 y sum
-// (y16 set: the row's true values are x times these), SwiGLU launches (w[1] set) write h = silu(x g) (x u) y in fp16.
-struct PrefillArgs {
+// One product of a prefill launch (prefill.hip: fp16 MFMA tiles of at most PREFILL_BM rows): for each tile and each
+// block of output rows, out[s][n] = sum_k A[row_a(s)][k] W_e[n][k] over the product's K values, with A in fp16 (its
+// rows scaled by powers of two) and W_e's rows raw GGUF blocks; row_scale[s] = (x, y) undoes the scales: plain
+// products write fp32 x y sum (y set) or fp16 y sum (y16 set: the row's true values are x times these), SwiGLU
+// products (w[1] set) write h = silu(x g) (x u) y in fp16. A product may cover a range of K (a part of a split K):
+// w and a then point at its first value, lda is A's row stride and the weights' rows keep their own stride.
+struct PrefillProblem {
   const uint8_t* w[2];     // weight tensors: (gate, up) or (down, null); expert e at w + e expert_bytes
   int64_t expert_bytes;
   int row_bytes;
-  int N, K;                // output rows per expert, values per row
-  int qtype;               // ARTLITE_Q4_0 / Q8_0 / Q4_K
-  const uint16_t* a;       // A: fp16 rows of K values
+  int N, K;                // output rows per expert; the product's values of K (whole 64-value stages)
+  int lda;                 // A's row stride (values)
+  const uint16_t* a;       // A: fp16 rows
   const int32_t* row_a;    // per output row s: its A row (a token); null: A row s
   const float2* row_scale; // per output row s: (x, y) as above
   const int32_t* tiles;    // (expert, first sorted row) per tile; null: dense rows 0 .. dense_rows of expert 0
@@ -58,8 +60,20 @@ struct PrefillArgs {
   uint16_t* y16;           // or fp16 (row stride N)
 };
 
+// A prefill launch: up to PREFILL_MAXP products of one weight format and kind (all SwiGLU or all plain), their work
+// items dealt over the device together (a routed product and the shared expert's; the parts of a split K).
+constexpr int PREFILL_MAXP = 4;
+struct PrefillArgs {
+  PrefillProblem p[PREFILL_MAXP];
+  int np;
+  int qtype;               // ARTLITE_Q4_0 / Q8_0 / Q4_K
+};
+
 // whether the prefill tiling takes N rows of K values of weights of this type
 bool prefill_supported(int qtype, int K, int N);
+// whether the 32-bit offsets of the prefill tiles reach every byte: E experts of expert_bytes (their weights and the
+// zeroed tail), rows of A of K fp16 values
+bool prefill_fits(int64_t experts, int64_t expert_bytes, int64_t a_rows, int64_t K);
 
 int launch_prefill(const PrefillArgs& a, hipStream_t s);
 
@@ -84,10 +98,11 @@ int launch_expert_gemm(const GemmArgs& a, hipStream_t s);
 // res (optional; x_dtype res_dtype): added last, y[t] += res[t] (the block's residual)
 int launch_combine(const float* Y, const int32_t* slot, const float* w, int k, const float* ys, const float* ws_logit,
                    int ws_sigmoid, int64_t T, int H, const void* res, int res_dtype, float* y, hipStream_t s);
-// the same over fp16 pair outputs: Y[s] = Y16[s] yf[s].x (the down launch's row factors; H a multiple of 8)
+// the same over fp16 pair outputs: Y[s] = Y16[s] yf[s].x (the down launch's row factors; H a multiple of 8); ys in
+// ys_parts parts of T x H (a split K), added in order
 int launch_combine16(const uint16_t* Y16, const float2* yf, const int32_t* slot, const float* w, int k,
-                     const float* ys, const float* ws_logit, int ws_sigmoid, int64_t T, int H, const void* res,
-                     int res_dtype, float* y, hipStream_t s);
+                     const float* ys, int ys_parts, const float* ws_logit, int ws_sigmoid, int64_t T, int H,
+                     const void* res, int res_dtype, float* y, hipStream_t s);
 
 // fp32 activations -> bf16 hi + lo planes (x = hi + lo to 2^-16 relative)
 int launch_split(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, hipStream_t s);

@@ -736,11 +736,14 @@ int launch_combine(const float* Y, const int32_t* slot, const float* w, int k, c
 }
 
 // The same over fp16 pair outputs, 8 columns per thread (16-byte loads): Y[s] = Y16[s] yf[s].x, the factor folded
-// into the weight (a power of two: (w f) v = w (f v) exactly), so the sum is the fp32 one over those values.
+// into the weight (a power of two: (w f) v = w (f v) exactly), so the sum is the fp32 one over those values. The
+// shared expert's output may come in ys_parts parts of a split K (T x H each, one after another), added in part
+// order before its gate.
 __global__ void k_combine16(const uint16_t* __restrict__ Y16, const float2* __restrict__ yf,
                             const int32_t* __restrict__ slot, const float* __restrict__ w, int k,
-                            const float* __restrict__ ys, const float* __restrict__ ws_logit, int ws_sigmoid, int64_t T,
-                            int H, const void* __restrict__ res, int res_dtype, float* __restrict__ y) {
+                            const float* __restrict__ ys, int ys_parts, const float* __restrict__ ws_logit,
+                            int ws_sigmoid, int64_t T, int H, const void* __restrict__ res, int res_dtype,
+                            float* __restrict__ y) {
   const int64_t t = blockIdx.y;
   const int h8 = blockIdx.x * blockDim.x + threadIdx.x;
   if (h8 * 8 >= H) return;
@@ -748,10 +751,16 @@ __global__ void k_combine16(const uint16_t* __restrict__ Y16, const float2* __re
   if (ys) {
     float ws = 1.0f;
     if (ws_logit) ws = ws_sigmoid ? 1.0f / (1.0f + expf(-ws_logit[t])) : ws_logit[t];
-    const float4* p = reinterpret_cast<const float4*>(ys + t * H) + 2 * h8;
-    const float4 a = p[0], b = p[1];
-    acc[0] = ws * a.x, acc[1] = ws * a.y, acc[2] = ws * a.z, acc[3] = ws * a.w;
-    acc[4] = ws * b.x, acc[5] = ws * b.y, acc[6] = ws * b.z, acc[7] = ws * b.w;
+    float v[8];
+    for (int j = 0; j < ys_parts; j++) {
+      const float4* p = reinterpret_cast<const float4*>(ys + (j * T + t) * H) + 2 * h8;
+      const float4 a = p[0], b = p[1];
+      const float u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = j ? v[i] + u[i] : u[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc[i] = ws * v[i];
   }
   for (int i = 0; i < k; i++) {
     const int64_t r = slot[t * k + i];
@@ -785,12 +794,14 @@ __global__ void k_combine16(const uint16_t* __restrict__ Y16, const float2* __re
 }
 
 int launch_combine16(const uint16_t* Y16, const float2* yf, const int32_t* slot, const float* w, int k,
-                     const float* ys, const float* ws_logit, int ws_sigmoid, int64_t T, int H, const void* res,
-                     int res_dtype, float* y, hipStream_t s) {
+                     const float* ys, int ys_parts, const float* ws_logit, int ws_sigmoid, int64_t T, int H,
+                     const void* res, int res_dtype, float* y, hipStream_t s) {
   if (T <= 0) return ARTLITE_OK;
   if (H % 8) return fail(ARTLITE_EINVAL, "combine: H %d not a multiple of 8", H);
+  if (ys && ys_parts < 1) return fail(ARTLITE_EINVAL, "combine: %d shared parts", ys_parts);
   const dim3 grid(unsigned((H / 8 + 255) / 256), unsigned(T)), block(256);
-  k_combine16<<<grid, block, 0, s>>>(Y16, yf, slot, w, k, ys, ws_logit, ws_sigmoid, T, H, res, res_dtype, y);
+  k_combine16<<<grid, block, 0, s>>>(Y16, yf, slot, w, k, ys, ys_parts, ws_logit, ws_sigmoid, T, H, res, res_dtype,
+                                     y);
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
 }

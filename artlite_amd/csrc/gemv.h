@@ -52,8 +52,4 @@ int launch_quant(const void* x, int x_dtype, int64_t T, int K, uint32_t* xq, hip
 // one XQ row back to fp32 (host side, for inspection)
 void xq_dequant_row(const uint32_t* row, int K, float* out);
 
-// rows of XQ (K values each) -> their values s (a + b / 256) as bf16 hi + lo planes (rows x K each): the A operand of
-// the MFMA decode tiles, for a down product that the GEMV does not take after a gate / up product that it does
-int launch_xq_planes(const uint32_t* xq, int64_t rows, int K, uint16_t* hi, uint16_t* lo, hipStream_t s);
-
 }  // namespace artlite

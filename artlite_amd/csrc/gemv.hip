@@ -7,7 +7,7 @@
 // share cache lines, at about the same time), whose partial sums meet in LDS. Each wave
 // streams its own steps (16 rows x one K-unit of 8 groups of 32 values: Q4_0 / Q4_K 144 bytes a row, Q5_K 176,
 // Q8_0 272)
-// with global_load_lds_dwordx4 into D LDS slots of its own, one step ahead, across item boundaries; the XQ records
+// with global_load_lds_dwordx4 into two LDS slots of its own, one step ahead, across item boundaries; the XQ records
 // of A's rows for a K-unit come the same way. Every load is a DMA counted as it is issued, so each wait names the
 // exact count (the compiler, which cannot order DMAs against register loads, would otherwise wait for all of them).
 // Lane (p, r) -- 16-lane row p, lane r in it -- takes row r and groups 2 p, 2 p + 1 of each unit, so four lanes
@@ -471,15 +471,19 @@ struct Shape {
   static_assert(!SWIGLU || (RB % 2 == 0 && 8 * RB / 2 * GEMV_BM <= 64), "SwiGLU epilogue lanes");
 };
 
-// LDS of a workgroup: each wave's D slots of 16 rows x BYTES and its record slot (GEMV_BM chunk rows of 1 KB;
+// LDS of a workgroup: each wave's WSLOTS slots of 16 rows x BYTES and its record slot (GEMV_BM chunk rows of 1 KB;
 // one: the next K-unit's are loaded once the current ones are read, and more slots measured no faster while they
 // cost Q6_K's plain products a workgroup per CU), then (S > 1) RED_BUFS buffers of the K-ranges' partial sums and
 // their counters (then the item table, sized at launch)
 constexpr int RED_BUFS = 2;
-template <int QT, bool SWIGLU, int D>
+// Weight slots per wave: two, one step in flight behind the one being read. The stream's counts are written for this
+// depth only: each wait names at most NMAX loads issued after the one it needs, and a slot is refilled right after
+// the step that read it (deeper queues measured no faster: with the record loads they cost workgroups per CU).
+constexpr int WSLOTS = 2;
+template <int QT, bool SWIGLU>
 constexpr size_t gemv_lds() {
   using W = Shape<SWIGLU>;
-  return size_t(W::WAVES) * (D * 16 * Unit<QT>::BYTES + GEMV_BM * 1024) +
+  return size_t(W::WAVES) * (WSLOTS * 16 * Unit<QT>::BYTES + GEMV_BM * 1024) +
          (W::S > 1 ? size_t(RED_BUFS) * W::WAVES * (SWIGLU ? 2 : 1) * GEMV_BM * 16 * 4 + 32 : 0);
 }
 
@@ -548,16 +552,16 @@ __device__ __forceinline__ float row4_sum(float s) {
 }
 
 // The state of a wave's stream of steps over its items (one step: 16 rows x one K-unit of one matrix). Every load
-// of the stream is a DMA into LDS (the weights into D slots, the records of a K-unit into one slot), counted as it
+// of the stream is a DMA into LDS (the weights into WSLOTS slots, the records of a K-unit into one slot), counted as it
 // is issued (nl), so that each wait names the exact number of loads issued after the ones it needs: loads of one kind
 // return in order. (Records loaded into registers instead would make the compiler wait for all loads in flight
 // before each use: it cannot order them against the DMAs.)
-template <int QT, bool SWIGLU, int D>
+template <int QT, bool SWIGLU>
 struct Stream {
   using W = Shape<SWIGLU>;
   static constexpr int RB = W::RB, S = W::S, BY = Unit<QT>::BYTES, CH = BY / 16, LW = Unit<QT>::LW;
   static constexpr int NM = SWIGLU ? 2 : 1, WCH = 16 * CH, NI = (WCH + 63) / 64, LAST = WCH - 64 * (NI - 1);
-  static constexpr int LA = D - 1;                          // steps in flight ahead of the one being read
+  static constexpr int LA = WSLOTS - 1;                          // steps in flight ahead of the one being read
   static constexpr int XCH = GEMV_BM * 64;  // chunks of the record slot
   static constexpr int NMAX = LA * NI + (LA + 1) * GEMV_BM;  // loads issued after a step's, at most
   static_assert(NMAX < 64, "loads in flight beyond vmcnt");
@@ -568,14 +572,14 @@ struct Stream {
   uint32_t lo[NI];   // the lane's byte offset in the 16 rows of each load instruction
   int nl = 0;        // loads issued so far
   int xend = 0;       // nl after the record slot's loads
-  int wend[D] = {};  // nl after the weights of the last D steps issued (wend[0]: the latest)
+  int wend[WSLOTS] = {};  // nl after the weights of the last WSLOTS steps issued (wend[0]: the latest)
 
   __device__ __forceinline__ explicit Stream(const GemvArgs& args) : a(args) {
     extern __shared__ u32x4 slab[];
     wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     lane = threadIdx.x & 63, p = lane >> 4, r = lane & 15;
     rb = wv / S, ks = wv % S;
-    my = slab + wv * (D * WCH + XCH);
+    my = slab + wv * (WSLOTS * WCH + XCH);
     const int U = a.K / 256;
     u0 = ks;  // (the wave's K-units: ks, ks + S, ...; the pair reads neighbouring units, which share lines, together)
     NVw = (U - ks + S - 1) / S * NM;
@@ -585,7 +589,7 @@ struct Stream {
       lo[i] = uint32_t((16 * rb + row) * a.row_bytes + 16 * (q - row * CH));
     }
     wbase = lds_addr(my);
-    xbase = lds_addr(my + D * WCH) + 16 * lane;
+    xbase = lds_addr(my + WSLOTS * WCH) + 16 * lane;
     if constexpr (QT == ARTLITE_Q6_K) {  // (low bits of half p / 2, its high bits, the scales and d)
       o_w = r * BY + 64 * (p >> 1);
       o_r = r * BY + 128 + 32 * (p >> 1);
@@ -618,12 +622,12 @@ struct Stream {
       nl += NI;
     }
 #pragma unroll
-    for (int i = D - 1; i > 0; i--) wend[i] = wend[i - 1];
+    for (int i = WSLOTS - 1; i > 0; i--) wend[i] = wend[i - 1];
     wend[0] = nl;
   }
   // the records of K-unit ku of item I's rows of A into the record slot (lane l: chunk l of each row)
   __device__ __forceinline__ void load_x(const Item& I, int ku) {
-    u32x4* dst = my + D * WCH;
+    u32x4* dst = my + WSLOTS * WCH;
 #pragma unroll
     for (int t = 0; t < GEMV_BM; t++)
       if (t < I.m)
@@ -636,10 +640,10 @@ struct Stream {
 };
 
 // the wait and read of a step: vmcnt(n) (n at most NMAX), then the weights and (MX) the record chunks
-template <int QT, bool SWIGLU, int D, int MX>
-__device__ __forceinline__ void wait_read(const Stream<QT, SWIGLU, D>& st, int n, uint32_t sw, uint32_t sx,
+template <int QT, bool SWIGLU, int MX>
+__device__ __forceinline__ void wait_read(const Stream<QT, SWIGLU>& st, int n, uint32_t sw, uint32_t sx,
                                           uint32_t (&w)[Unit<QT>::LW], u32x4 (&x)[GEMV_BM]) {
-  using SS = Stream<QT, SWIGLU, D>;
+  using SS = Stream<QT, SWIGLU>;
   static_for<SS::NMAX + 1>([&](auto nc) {
     constexpr int N = decltype(nc)::value;
     if (n == N) read_unit<N, QT, MX>(w, x, sw + st.o_w, sw + st.o_r, sw + st.o_s, sx);
@@ -665,10 +669,10 @@ __device__ __forceinline__ void step_terms(const uint32_t (&w)[Unit<QT>::LW], co
 // the weights LA steps ahead, then waits for its own; at the start of each K-unit that wait also covers the
 // records, which are read into registers with the weights, and the next K-unit's are loaded into the freed slot.
 // Returns with the sums of the four lanes of a row in every lane.
-template <int QT, bool SWIGLU, int D, int M>
-__device__ __forceinline__ void run_item(Stream<QT, SWIGLU, D>& st, const Item& cur, const Item& nxt, bool has_next,
+template <int QT, bool SWIGLU, int M>
+__device__ __forceinline__ void run_item(Stream<QT, SWIGLU>& st, const Item& cur, const Item& nxt, bool has_next,
                                          int gs, float (&out)[SWIGLU ? 2 : 1][GEMV_BM]) {
-  using SS = Stream<QT, SWIGLU, D>;
+  using SS = Stream<QT, SWIGLU>;
   constexpr int NM = SS::NM, LW = SS::LW, LA = SS::LA;
   float acc[NM][M];
 #pragma unroll
@@ -685,21 +689,21 @@ __device__ __forceinline__ void run_item(Stream<QT, SWIGLU, D>& st, const Item& 
         const int vi = v + LA;
         const bool here = vi < st.NVw;
         st.template issue_w<(MX + LA) % NM>(here || has_next, here ? cur.e : nxt.e, here ? cur.n0 : nxt.n0,
-                                            here ? vi : vi - st.NVw, (gs + v + LA) % D);
+                                            here ? vi : vi - st.NVw, (gs + v + LA) % WSLOTS);
       };
       issue();
       uint32_t w[LW];
-      const uint32_t sw = st.wbase + ((gs + v) % D) * SS::WCH * 16;
+      const uint32_t sw = st.wbase + ((gs + v) % WSLOTS) * SS::WCH * 16;
       if constexpr (MX == 0) {
-        // (wend[D - 1]: this step's weights), then the next K-unit's records into the slot just read
-        const int nw = st.nl - st.wend[D - 1];
-        wait_read<QT, SWIGLU, D, M>(st, min(nw, st.nl - st.xend), sw, st.xbase, w, xc);
+        // (wend[WSLOTS - 1]: this step's weights), then the next K-unit's records into the slot just read
+        const int nw = st.nl - st.wend[WSLOTS - 1];
+        wait_read<QT, SWIGLU, M>(st, min(nw, st.nl - st.xend), sw, st.xbase, w, xc);
         if (v0 + NM < st.NVw)
           st.load_x(cur, st.u0 + SS::S * (v0 / NM + 1));
         else if (has_next)
           st.load_x(nxt, st.u0);
       } else {
-        wait_read<QT, SWIGLU, D, 0>(st, st.nl - st.wend[D - 1], sw, st.xbase, w, xc);
+        wait_read<QT, SWIGLU, 0>(st, st.nl - st.wend[WSLOTS - 1], sw, st.xbase, w, xc);
       }
       step_terms<QT, M>(w, xc, st.p, acc[MX]);
     });
@@ -717,11 +721,11 @@ __device__ __forceinline__ void run_item(Stream<QT, SWIGLU, D>& st, const Item& 
 }
 
 // A persistent workgroup: items snake_item(blockIdx.x, j, gridDim.x) of (tile, block of 16 RB rows), tile-major.
-template <int QT, bool SWIGLU, int D>
+template <int QT, bool SWIGLU>
 __global__ __launch_bounds__(Shape<SWIGLU>::THREADS) __attribute__((amdgpu_waves_per_eu(QT == ARTLITE_Q4_0 ? 4 : 2))) void k_gemv(
     const GemvArgs a) {
   using W = Shape<SWIGLU>;
-  using SS = Stream<QT, SWIGLU, D>;
+  using SS = Stream<QT, SWIGLU>;
   constexpr int RB = W::RB, S = W::S, NM = SS::NM;
   const int rows = 16 * RB, NB = (a.N + rows - 1) / rows;
   const int n_tiles = a.tiles ? *a.n_tiles : (a.dense_rows + GEMV_BM - 1) / GEMV_BM;
@@ -730,7 +734,7 @@ __global__ __launch_bounds__(Shape<SWIGLU>::THREADS) __attribute__((amdgpu_waves
   SS st(a);
   extern __shared__ u32x4 slab[];
   // [buffer][wave][matrix][row of A][row], after every wave's slots
-  float* red = reinterpret_cast<float*>(slab + W::WAVES * (D * SS::WCH + SS::XCH));
+  float* red = reinterpret_cast<float*>(slab + W::WAVES * (WSLOTS * SS::WCH + SS::XCH));
 
   const int it0 = blockIdx.x, n_my = snake_count(it0, G, n_items);
   constexpr int RED = W::WAVES * NM * GEMV_BM * 16;  // floats of one partial-sum buffer
@@ -757,10 +761,10 @@ __global__ __launch_bounds__(Shape<SWIGLU>::THREADS) __attribute__((amdgpu_waves
     if (has_next) nxt = get_item(tab, j + 1);
     float out[NM][GEMV_BM];
     switch (cur.m) {
-      case 1: run_item<QT, SWIGLU, D, 1>(st, cur, nxt, has_next, gs, out); break;
-      case 2: run_item<QT, SWIGLU, D, 2>(st, cur, nxt, has_next, gs, out); break;
-      case 3: run_item<QT, SWIGLU, D, 3>(st, cur, nxt, has_next, gs, out); break;
-      default: run_item<QT, SWIGLU, D, 4>(st, cur, nxt, has_next, gs, out); break;
+      case 1: run_item<QT, SWIGLU, 1>(st, cur, nxt, has_next, gs, out); break;
+      case 2: run_item<QT, SWIGLU, 2>(st, cur, nxt, has_next, gs, out); break;
+      case 3: run_item<QT, SWIGLU, 3>(st, cur, nxt, has_next, gs, out); break;
+      default: run_item<QT, SWIGLU, 4>(st, cur, nxt, has_next, gs, out); break;
     }
     gs += st.NVw;
     if constexpr (!SWIGLU) {
@@ -835,8 +839,8 @@ __global__ __launch_bounds__(256) void k_quant(const void* __restrict__ x, int64
   if (w < T * (K / 256)) xq_quant_unit<XT>(x, w, K, xq, threadIdx.x & 63);
 }
 
-template <int QT, bool SWIGLU, int D>
-int launch_d(const GemvArgs& a, hipStream_t s) {
+template <int QT, bool SWIGLU>
+int launch_t(const GemvArgs& a, hipStream_t s) {
   using W = Shape<SWIGLU>;
   const int64_t tiles = a.tiles ? a.max_tiles : (a.dense_rows + GEMV_BM - 1) / GEMV_BM;
   const int64_t items = tiles * ((a.N + 16 * W::RB - 1) / (16 * W::RB));
@@ -844,9 +848,9 @@ int launch_d(const GemvArgs& a, hipStream_t s) {
   if (items >= (int64_t(1) << 31)) return fail(ARTLITE_EINVAL, "expert GEMV: %lld work items", (long long)items);
   // persistent workgroups: as many as the device holds at once (queried once per kernel, with a table of 64
   // items), at most one per item; their item tables take 32 bytes an item
-  constexpr size_t lds0 = gemv_lds<QT, SWIGLU, D>(), lds_max = lds0 + 8192;
+  constexpr size_t lds0 = gemv_lds<QT, SWIGLU>(), lds_max = lds0 + 8192;
   static const int resident = [] {
-    const void* f = reinterpret_cast<const void*>(k_gemv<QT, SWIGLU, D>);
+    const void* f = reinterpret_cast<const void*>(k_gemv<QT, SWIGLU>);
     int dev = 0, cus = 0, per_cu = 0;
     if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_max)) != hipSuccess ||
         hipGetDevice(&dev) != hipSuccess ||
@@ -859,16 +863,9 @@ int launch_d(const GemvArgs& a, hipStream_t s) {
   const unsigned grid = unsigned(std::min<int64_t>(items, resident));
   const size_t lds = lds0 + size_t((items + grid - 1) / grid) * 32;
   if (lds > lds_max) return fail(ARTLITE_EINVAL, "expert GEMV: %lld work items", (long long)items);
-  k_gemv<QT, SWIGLU, D><<<grid, W::THREADS, lds, s>>>(a);
+  k_gemv<QT, SWIGLU><<<grid, W::THREADS, lds, s>>>(a);
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
-}
-
-// Weight slots per wave: two (a step in flight behind the one being read; with the record loads, deeper queues did
-// not pay for the LDS they take from the workgroups a CU holds).
-template <int QT, bool SWIGLU>
-int launch_t(const GemvArgs& a, hipStream_t s) {
-  return launch_d<QT, SWIGLU, 2>(a, s);
 }
 
 }  // namespace
@@ -916,36 +913,6 @@ int launch_quant(const void* x, int x_dtype, int64_t T, int K, uint32_t* xq, hip
     k_quant<ARTLITE_X_F32><<<blocks, 256, 0, s>>>(x, T, K, xq);
   else
     k_quant<ARTLITE_X_BF16><<<blocks, 256, 0, s>>>(x, T, K, xq);
-  ART_HIP(hipGetLastError());
-  return ARTLITE_OK;
-}
-
-// a thread per plane dword (4 values) of a group: the value s/256 (256 a + b) rounded once to fp32, then split
-__global__ void k_xq_planes(const uint32_t* __restrict__ xq, int64_t rows, int K, uint16_t* __restrict__ hi,
-                            uint16_t* __restrict__ lo) {
-  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x, per_row = K / 4;
-  if (i >= rows * per_row) return;
-  const int64_t r = i / per_row;
-  const int d = int(i - r * per_row), u = d / 64, g = (d % 64) / 8, j = d % 8;
-  const uint32_t* ub = xq + r * xq_row_dwords(K) + int64_t(u) * XQ_UNIT;
-  const uint32_t pa = ub[xq_block(g, j)], pb = ub[xq_block(g, 8 + j)];
-  const float s256 = __uint_as_float(ub[4 * (16 * (g >> 1) + 2 * (g & 1)) + 2]);
-  const int64_t o = r * K + int64_t(u) * 256 + 32 * g + 4 * j;
-#pragma unroll
-  for (int c = 0; c < 4; c++) {
-    const int qa = int8_t((pa >> (8 * c)) & 0xFFu), qb = int8_t((pb >> (8 * c)) & 0xFFu);
-    const float v = s256 * float(256 * qa + qb);
-    const uint32_t h = f32_to_bf16(v);
-    hi[o + c] = uint16_t(h);
-    lo[o + c] = uint16_t(f32_to_bf16(v - bf16_to_f32(h)));
-  }
-}
-
-int launch_xq_planes(const uint32_t* xq, int64_t rows, int K, uint16_t* hi, uint16_t* lo, hipStream_t s) {
-  if (K <= 0 || K % 256) return fail(ARTLITE_EINVAL, "XQ planes: K %d", K);
-  const int64_t n = rows * (K / 4);
-  if (n <= 0) return ARTLITE_OK;
-  k_xq_planes<<<unsigned((n + 255) / 256), 256, 0, s>>>(xq, rows, K, hi, lo);
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
 }

@@ -30,15 +30,17 @@ struct artlite_moe_layer {
   DevBuf row_a, gu_row, dn_row;   // per sorted pair row: its token and its factors
   DevBuf wmax;                    // max |w| of gate, up, shared gate, shared up (the bounds on |h|), down
   DevBuf logits, ids, w, sg;
+  DevBuf rpart;  // the router's fp64 partial sums (K split over workgroups), router_part_elems doubles
+  size_t rpart_elems = 0;
   DevBuf table, ctrl, counts, offsets, order, slot, tiles;
   DevBuf gtick;  // the one-launch routing's tickets per token group (GTICK_STRIDE ints apart)
   DevBuf hhi, hlo, ypairs, shhi, shlo, ys, y;
   DevBuf h16, sh16;  // the prefill's h (fp16, scaled per token)
   DevBuf xq, hq, shq;  // the decode path's XQ activations
   bool gemv_ok = false, shared_gemv_ok = false, prefill_ok = false, shared_prefill_ok = false;
-  bool gemv_gu_ok = false;  // the routed gate / up on the GEMV (gemv_ok: the down as well)
   int64_t last_T = -1;
   bool last_gemv = false, last_prefill = false;
+  int last_ys_parts = 1;  // (the shared expert's output of the last run: parts of its K, summed by the combine)
 };
 
 namespace {
@@ -108,14 +110,11 @@ int check_ready(const artlite_moe_layer* L) {
 }
 
 // The kernels a forward pass of T tokens takes. Decode-sized passes (at most GEMV_BM pairs per expert on
-// average) run the experts on the VALU GEMV over XQ activations; prefill-sized ones (16 pairs per expert on
-// average) on the fp16 MFMA prefill tiles; those between on the MFMA decode tiles
-// over bf16 planes. A decode-sized pass whose down format the GEMV does not take (a Q6_K down after Q4_K gate / up,
-// as mixed GGUF quantisations store them) runs gate / up on the GEMV and the down on the decode tiles, h turned from
-// XQ into bf16 planes between them.
+// average) run the experts on the VALU GEMV over XQ activations (it takes every block format); prefill-sized ones
+// (16 pairs per expert on average) on the fp16 MFMA prefill tiles; those between on the MFMA decode tiles over bf16
+// planes.
 struct Path {
-  bool gemv_gu;         // routed gate / up on the GEMV (XQ of x; tiles of GEMV_BM rows)
-  bool gemv;            // routed experts (gate / up and down) on the GEMV
+  bool gemv;            // routed experts (gate / up and down) on the GEMV (XQ of x; tiles of GEMV_BM rows)
   bool shared_gemv;     // the shared expert on the GEMV
   bool prefill;         // routed experts on the prefill tiles
   bool shared_prefill;  // the shared expert on the prefill tiles
@@ -127,18 +126,22 @@ struct Path {
 
 Path path_of(const artlite_moe_layer* L, int64_t T) {
   Path p{};
-  p.gemv_gu = L->gemv_gu_ok && T * L->d.top_k <= int64_t(GEMV_BM) * L->d.n_experts;
-  p.gemv = p.gemv_gu && L->gemv_ok;
-  p.shared_gemv = L->d.shared_ffn && p.gemv_gu && L->shared_gemv_ok;
-  p.prefill = !p.gemv_gu && L->prefill_ok && T * L->d.top_k >= int64_t(16) * L->d.n_experts;
+  p.gemv = L->gemv_ok && T * L->d.top_k <= int64_t(GEMV_BM) * L->d.n_experts;
+  p.shared_gemv = L->d.shared_ffn && p.gemv && L->shared_gemv_ok;
+  p.prefill = !p.gemv && L->prefill_ok && T * L->d.top_k >= int64_t(16) * L->d.n_experts;
   p.shared_prefill = L->d.shared_ffn && p.prefill && L->shared_prefill_ok && T >= 64;
-  const bool planes = (!p.gemv_gu && !p.prefill) || (L->d.shared_ffn && !p.shared_gemv && !p.shared_prefill);
+  const bool planes = (!p.gemv && !p.prefill) || (L->d.shared_ffn && !p.shared_gemv && !p.shared_prefill);
   p.split = planes && (L->x_dtype == ARTLITE_X_F32 || L->d.norm_eps > 0);  // (the normalised x is fp32)
-  p.quant = p.gemv_gu;
-  p.small = p.gemv_gu && T * L->d.top_k <= DISPATCH_BLOCK && L->d.n_experts <= MAX_EXPERTS;
+  p.quant = p.gemv;
+  p.small = p.gemv && T * L->d.top_k <= DISPATCH_BLOCK && L->d.n_experts <= MAX_EXPERTS;
   p.fused_route = p.small && router_route_fits(T, L->d.hidden, L->d.n_experts, L->d.top_k);
   return p;
 }
+
+// whether the shared expert's gate / up (down) products join the routed launch on the prefill tiles: the same block
+// format (the launch's kernel is instantiated per format)
+bool shared_gu_merged(const artlite_moe_layer* L) { return L->sq && L->sq->id == L->gq->id; }
+bool shared_dn_merged(const artlite_moe_layer* L) { return L->sdq && L->sdq->id == L->dq->id; }
 
 // the named kernels of a forward pass, in launch order
 std::vector<std::string> kernel_list(const artlite_moe_layer* L, int64_t T) {
@@ -160,15 +163,47 @@ std::vector<std::string> kernel_list(const artlite_moe_layer* L, int64_t T) {
     k.push_back("dispatch_count");
     k.push_back("dispatch_scatter");
   }
+  const bool sp = p.prefill && p.shared_prefill;  // (the shared expert's items in the routed launches, or beside them)
   k.push_back("gate_up");
-  if (p.gemv_gu && !p.gemv) k.push_back("h_planes");
+  if (sp && !shared_gu_merged(L)) k.push_back("shared_gate_up");
   k.push_back("down");
-  if (L->d.shared_ffn) {
+  if (sp && !shared_dn_merged(L)) k.push_back("shared_down");
+  if (L->d.shared_ffn && !sp) {
     k.push_back("shared_gate_up");
     k.push_back("shared_down");
   }
   k.push_back("combine");
   return k;
+}
+
+// The shared expert's down on the prefill tiles splits its K (the shared width) into parts, each a product of the
+// launch with a partial output of its own (T x H fp32; the combine adds them in order): whole blocks (K-quants: 256
+// values) a part, at least 5 stages (320 values) each, the first ones a block longer where they do not divide evenly.
+int shared_parts(const artlite_moe_layer* L, bool merged) {
+  const int Ks = L->d.shared_ffn, unit = L->sdq->per >= 256 ? 256 : 64, units = Ks / unit;
+  // (beside the routed down: parts about as long as its items' K; alone: as many as the launch takes)
+  int parts = merged ? std::max(1, std::min(PREFILL_MAXP - 1, (Ks + L->d.expert_ffn / 2) / L->d.expert_ffn))
+                     : PREFILL_MAXP;
+  while (parts > 1 && units / parts * unit < 320) parts--;
+  return parts;
+}
+
+// the shared down's part j of n: the product over its range of K, into ys part j
+PrefillProblem shared_down_part(const artlite_moe_layer* L, int64_t T, int j, int n) {
+  const int Ks = L->d.shared_ffn, unit = L->sdq->per >= 256 ? 256 : 64, units = Ks / unit;
+  const int u0 = j * (units / n) + std::min(j, units % n), nu = units / n + (j < units % n ? 1 : 0);
+  const int k0 = u0 * unit;
+  PrefillProblem p{};
+  p.w[0] = L->sdown.as<uint8_t>() + size_t(k0 / L->sdq->per) * L->sdq->dev;
+  p.row_bytes = int(L->sdown_row);
+  p.N = L->d.hidden;
+  p.K = nu * unit;
+  p.lda = Ks;
+  p.a = L->sh16.as<uint16_t>() + k0;
+  p.dense_rows = int(T);
+  p.row_scale = L->sdn_tok.as<float2>();
+  p.y = L->ys.as<float>() + size_t(j) * size_t(T) * L->d.hidden;
+  return p;
 }
 
 // The forward pass of the staged T tokens. ev (optional): an event recorded before each kernel and one after the
@@ -184,6 +219,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     return ARTLITE_OK;
   };
   const Path path = path_of(L, T);
+  int ys_parts = 1;  // (the shared expert's output: its parts on the prefill tiles)
   // the block's input: x as staged, or (norm_eps > 0) its RMS normalisation in fp32
   const void* xin = L->x.p;
   int xdt = L->x_dtype;
@@ -206,7 +242,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     ahi = L->xhi.as<uint16_t>();
     alo = L->xlo.as<uint16_t>();
   }
-  const int BM = path.gemv_gu ? GEMV_BM : path.prefill ? PREFILL_BM : DECODE_BM;
+  const int BM = path.gemv ? GEMV_BM : path.prefill ? PREFILL_BM : DECODE_BM;
   DispatchBufs db{L->ids.as<int32_t>(), P, E, k, L->table.as<int32_t>(), L->ctrl.as<int32_t>(),
                   L->counts.as<int32_t>(), L->offsets.as<int32_t>(), L->order.as<int32_t>(), L->slot.as<int32_t>(),
                   L->tiles.as<int32_t>(), BM, nullptr, 0, path.prefill ? 1 : 0};
@@ -225,10 +261,10 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
                                 L->w.as<float>(), db, s));
   else
     ART_TRY(launch_router(xin, xdt, L->router.as<float>(), H, E, T, L->logits.as<float>(), E,
-                          path.quant ? L->xq.as<uint32_t>() : nullptr, s));
+                          path.quant ? L->xq.as<uint32_t>() : nullptr, L->rpart.as<double>(), L->rpart_elems, s));
   if (d.shared_ffn && d.shared_gated) {
     ART_TRY(mark());
-    ART_TRY(launch_router(xin, xdt, L->sinp.as<float>(), H, 1, T, L->sg.as<float>(), 1, nullptr, s));
+    ART_TRY(launch_router(xin, xdt, L->sinp.as<float>(), H, 1, T, L->sg.as<float>(), 1, nullptr, nullptr, 0, s));
   }
   if (path.fused_route) {
   } else if (path.small) {
@@ -245,7 +281,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     ART_TRY(mark());
     ART_TRY(launch_dispatch_scatter(db, nb, s));
   }
-  if (path.gemv_gu) {
+  if (path.gemv) {
     GemvArgs g{};
     g.w[0] = L->gate.as<uint8_t>();
     g.w[1] = L->up.as<uint8_t>();
@@ -266,54 +302,35 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     g.hq = L->hq.as<uint32_t>();
     ART_TRY(mark());
     ART_TRY(launch_gemv(g, s));
-    if (path.gemv) {
-      GemvArgs dn = g;
-      dn.w[0] = L->down.as<uint8_t>();
-      dn.w[1] = nullptr;
-      dn.expert_bytes = int64_t(H) * L->down_row;
-      dn.row_bytes = int(L->down_row);
-      dn.N = H;
-      dn.K = F;
-      dn.qtype = d.down_type;
-      dn.xq = L->hq.as<uint32_t>();
-      dn.a_gather = 0;
-      dn.hq = nullptr;
-      dn.y = L->ypairs.as<float>();
-      ART_TRY(mark());
-      ART_TRY(launch_gemv(dn, s));
-    } else {  // (the down on the MFMA decode tiles, over the GEMV's tiles of GEMV_BM rows)
-      ART_TRY(mark());
-      ART_TRY(launch_xq_planes(L->hq.as<uint32_t>(), P, F, L->hhi.as<uint16_t>(), L->hlo.as<uint16_t>(), s));
-      GemmArgs dn{};
-      dn.w[0] = L->down.as<uint8_t>();
-      dn.expert_bytes = int64_t(H) * L->down_row;
-      dn.row_bytes = int(L->down_row);
-      dn.N = H;
-      dn.K = F;
-      dn.qtype = d.down_type;
-      dn.a_hi = L->hhi.as<uint16_t>();
-      dn.a_lo = L->hlo.as<uint16_t>();
-      dn.a_gather = 0;
-      dn.order = L->order.as<int32_t>();
-      dn.topk = k;
-      dn.tiles = L->tiles.as<int32_t>();
-      dn.n_tiles = L->ctrl.as<int32_t>() + CTRL_TILES;
-      dn.offsets = L->offsets.as<int32_t>();
-      dn.max_tiles = tile_bound(P, E, BM);
-      dn.bm = BM;
-      dn.y = L->ypairs.as<float>();
-      ART_TRY(mark());
-      ART_TRY(launch_expert_gemm(dn, s));
-    }
+    GemvArgs dn = g;
+    dn.w[0] = L->down.as<uint8_t>();
+    dn.w[1] = nullptr;
+    dn.expert_bytes = int64_t(H) * L->down_row;
+    dn.row_bytes = int(L->down_row);
+    dn.N = H;
+    dn.K = F;
+    dn.qtype = d.down_type;
+    dn.xq = L->hq.as<uint32_t>();
+    dn.a_gather = 0;
+    dn.hq = nullptr;
+    dn.y = L->ypairs.as<float>();
+    ART_TRY(mark());
+    ART_TRY(launch_gemv(dn, s));
   } else if (path.prefill) {
-    PrefillArgs g{};
+    // gate / up (SwiGLU), then down; the shared expert's products join them (its down in parts of its K) when their
+    // formats match, else run as launches of their own right after
+    const bool sp = d.shared_ffn && path.shared_prefill;
+    PrefillArgs gu{};
+    gu.qtype = d.gate_type;
+    gu.np = 1;
+    PrefillProblem& g = gu.p[0];
     g.w[0] = L->gate.as<uint8_t>();
     g.w[1] = L->up.as<uint8_t>();
     g.expert_bytes = int64_t(F) * L->gate_row;
     g.row_bytes = int(L->gate_row);
     g.N = F;
     g.K = H;
-    g.qtype = d.gate_type;
+    g.lda = H;
     g.a = L->x16.as<uint16_t>();
     g.row_a = L->row_a.as<int32_t>();
     g.row_scale = L->gu_row.as<float2>();
@@ -322,23 +339,60 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     g.offsets = L->offsets.as<int32_t>();
     g.max_tiles = tile_bound(P, E, BM);
     g.h = L->h16.as<uint16_t>();
+    PrefillArgs sgu{};  // (the shared gate / up: in gu, or a launch of its own)
+    if (sp) {
+      PrefillArgs& into = shared_gu_merged(L) ? gu : sgu;
+      into.qtype = L->sq->id;
+      PrefillProblem& q = into.p[into.np++];
+      q.w[0] = L->sgate.as<uint8_t>();
+      q.w[1] = L->sup.as<uint8_t>();
+      q.row_bytes = int(L->sgate_row);
+      q.N = d.shared_ffn;
+      q.K = H;
+      q.lda = H;
+      q.a = L->x16.as<uint16_t>();
+      q.dense_rows = int(T);
+      q.row_scale = L->sgu_tok.as<float2>();
+      q.h = L->sh16.as<uint16_t>();
+    }
     ART_TRY(mark());
-    ART_TRY(launch_prefill(g, s));
-    PrefillArgs dn = g;
-    dn.w[0] = L->down.as<uint8_t>();
-    dn.w[1] = nullptr;
-    dn.expert_bytes = int64_t(H) * L->down_row;
-    dn.row_bytes = int(L->down_row);
-    dn.N = H;
-    dn.K = F;
+    ART_TRY(launch_prefill(gu, s));
+    if (sgu.np) {
+      ART_TRY(mark());
+      ART_TRY(launch_prefill(sgu, s));
+    }
+    PrefillArgs dn{};
     dn.qtype = d.down_type;
-    dn.a = L->h16.as<uint16_t>();
-    dn.row_a = nullptr;
-    dn.row_scale = L->dn_row.as<float2>();
-    dn.h = nullptr;
-    dn.y16 = L->ypairs.as<uint16_t>();  // (fp16 pair outputs, their rows' true values dn_row[s].x times these)
+    dn.np = 1;
+    PrefillProblem& q = dn.p[0];
+    q = g;
+    q.w[0] = L->down.as<uint8_t>();
+    q.w[1] = nullptr;
+    q.expert_bytes = int64_t(H) * L->down_row;
+    q.row_bytes = int(L->down_row);
+    q.N = H;
+    q.K = F;
+    q.lda = F;
+    q.a = L->h16.as<uint16_t>();
+    q.row_a = nullptr;
+    q.row_scale = L->dn_row.as<float2>();
+    q.h = nullptr;
+    q.y16 = L->ypairs.as<uint16_t>();  // (fp16 pair outputs, their rows' true values dn_row[s].x times these)
+    PrefillArgs sdn{};  // (the shared down's parts: in dn, or a launch of their own)
+    if (sp) {
+      const bool merged = shared_dn_merged(L);
+      PrefillArgs& into = merged ? dn : sdn;
+      into.qtype = L->sdq->id;
+      const int n = shared_parts(L, merged);
+      for (int j = 0; j < n; j++) into.p[into.np++] = shared_down_part(L, T, j, n);
+      ys_parts = n;
+    }
     ART_TRY(mark());
     ART_TRY(launch_prefill(dn, s));
+    if (sdn.np) {
+      ART_TRY(mark());
+      ART_TRY(launch_prefill(sdn, s));
+    }
   } else {
     GemmArgs g{};
     g.w[0] = L->gate.as<uint8_t>();
@@ -404,33 +458,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     ART_TRY(mark());
     ART_TRY(launch_gemv(sd, s));
     ys = L->ys.as<float>();
-  } else if (d.shared_ffn && path.shared_prefill) {
-    PrefillArgs sg{};
-    sg.w[0] = L->sgate.as<uint8_t>();
-    sg.w[1] = L->sup.as<uint8_t>();
-    sg.row_bytes = int(L->sgate_row);
-    sg.N = d.shared_ffn;
-    sg.K = H;
-    sg.qtype = d.shared_type;
-    sg.a = L->x16.as<uint16_t>();
-    sg.dense_rows = int(T);
-    sg.row_scale = L->sgu_tok.as<float2>();
-    sg.h = L->sh16.as<uint16_t>();
-    ART_TRY(mark());
-    ART_TRY(launch_prefill(sg, s));
-    PrefillArgs sd = sg;
-    sd.w[0] = L->sdown.as<uint8_t>();
-    sd.w[1] = nullptr;
-    sd.row_bytes = int(L->sdown_row);
-    sd.N = H;
-    sd.K = d.shared_ffn;
-    sd.qtype = L->sdq->id;
-    sd.a = L->sh16.as<uint16_t>();
-    sd.row_scale = L->sdn_tok.as<float2>();
-    sd.h = nullptr;
-    sd.y = L->ys.as<float>();
-    ART_TRY(mark());
-    ART_TRY(launch_prefill(sd, s));
+  } else if (d.shared_ffn && path.shared_prefill) {  // (with the routed experts' launches)
     ys = L->ys.as<float>();
   } else if (d.shared_ffn) {
     GemmArgs sg{};
@@ -465,7 +493,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
   ART_TRY(mark());
   if (path.prefill)
     ART_TRY(launch_combine16(L->ypairs.as<uint16_t>(), L->dn_row.as<float2>(), L->slot.as<int32_t>(), L->w.as<float>(),
-                             k, ys, d.shared_gated ? L->sg.as<float>() : nullptr, 1, T, H,
+                             k, ys, ys_parts, d.shared_gated ? L->sg.as<float>() : nullptr, 1, T, H,
                              d.residual ? L->x.p : nullptr, L->x_dtype, L->y.as<float>(), s));
   else
     ART_TRY(launch_combine(L->ypairs.as<float>(), L->slot.as<int32_t>(), L->w.as<float>(), k, ys,
@@ -473,8 +501,9 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
                            L->x_dtype, L->y.as<float>(), s));
   ART_TRY(mark());
   L->last_T = T;
-  L->last_gemv = path.gemv_gu;
+  L->last_gemv = path.gemv;
   L->last_prefill = path.prefill;
+  L->last_ys_parts = ys_parts;
   return ARTLITE_OK;
 }
 
@@ -526,14 +555,20 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
     L->sgate_row = size_t(d.hidden) / sq->per * sq->dev;
     L->sdown_row = size_t(d.shared_ffn) / sdq->per * sdq->dev;
   }
-  L->gemv_gu_ok = gemv_supported(d.gate_type, d.hidden, d.expert_ffn) && d.expert_ffn % 256 == 0;
-  L->gemv_ok = L->gemv_gu_ok && gemv_supported(d.down_type, d.expert_ffn, d.hidden);
+  L->gemv_ok = gemv_supported(d.gate_type, d.hidden, d.expert_ffn) && d.expert_ffn % 256 == 0 &&
+               gemv_supported(d.down_type, d.expert_ffn, d.hidden);
+  // (the prefill tiles address weights and A rows by 32-bit offsets: every expert's bytes, every row of x16 and h16)
+  const int64_t maxP = int64_t(d.max_tokens) * d.top_k;
   L->prefill_ok = prefill_supported(d.gate_type, d.hidden, d.expert_ffn) &&
-                  prefill_supported(d.down_type, d.expert_ffn, d.hidden);
+                  prefill_supported(d.down_type, d.expert_ffn, d.hidden) &&
+                  prefill_fits(d.n_experts, int64_t(d.expert_ffn) * L->gate_row, d.max_tokens, d.hidden) &&
+                  prefill_fits(d.n_experts, int64_t(d.hidden) * L->down_row, maxP, d.expert_ffn);
   L->shared_gemv_ok = sq && gemv_supported(sq->id, d.hidden, d.shared_ffn) &&
                       gemv_supported(sdq->id, d.shared_ffn, d.hidden);
   L->shared_prefill_ok = sq && prefill_supported(sq->id, d.hidden, d.shared_ffn) &&
-                         prefill_supported(sdq->id, d.shared_ffn, d.hidden);
+                         prefill_supported(sdq->id, d.shared_ffn, d.hidden) &&
+                         prefill_fits(1, int64_t(d.shared_ffn) * L->sgate_row, d.max_tokens, d.hidden) &&
+                         prefill_fits(1, int64_t(d.hidden) * L->sdown_row, d.max_tokens, d.shared_ffn);
   hipError_t e = hipGetDevice(&L->device);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&L->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
@@ -551,6 +586,8 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
   res(L->xhi, size_t(T * H) * 2);
   res(L->xlo, size_t(T * H) * 2);
   res(L->logits, size_t(T * E) * 4);
+  L->rpart_elems = router_part_elems(T, int(E), int(H));
+  if (L->rpart_elems) res(L->rpart, L->rpart_elems * 8);
   res(L->ids, size_t(P) * 4);
   res(L->w, size_t(P) * 4);
   res(L->sg, size_t(T) * 4);
@@ -581,7 +618,7 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
       res(L->sh16, size_t(T) * d.shared_ffn * 2);
     }
   }
-  if (L->gemv_gu_ok) {
+  if (L->gemv_ok) {
     res(L->xq, size_t(T * xq_row_dwords(d.hidden)) * 4);
     res(L->hq, size_t(P * xq_row_dwords(d.expert_ffn)) * 4);
     if (L->shared_gemv_ok) res(L->shq, size_t(T * xq_row_dwords(d.shared_ffn)) * 4);
@@ -589,7 +626,7 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
   if (d.shared_ffn) {
     res(L->shhi, size_t(T) * d.shared_ffn * 2);
     res(L->shlo, size_t(T) * d.shared_ffn * 2);
-    res(L->ys, size_t(T * H) * 4);
+    res(L->ys, size_t(T * H) * 4 * (L->shared_prefill_ok ? PREFILL_MAXP : 1));  // (prefill: the down's K parts)
   }
   if (rc == ARTLITE_OK && (hipMemset(L->ctrl.p, 0, CTRL_WORDS * 4) != hipSuccess ||
                            hipMemset(L->gtick.p, 0, size_t(ROUTER_GROUPS) * GTICK_STRIDE * 4) != hipSuccess))
@@ -741,10 +778,21 @@ extern "C" int artlite_moe_layer_tap(artlite_moe_layer* L, int tap, void* out, s
       if (!(L->d.norm_eps > 0)) return fail(ARTLITE_EINVAL, "moe layer tap: no norm in this layer");
       src = L->xn.p, bytes = size_t(T) * L->d.hidden * 4;
       break;
-    case ARTLITE_TAP_YS:
+    case ARTLITE_TAP_YS: {
       if (!L->d.shared_ffn) return fail(ARTLITE_EINVAL, "moe layer tap: no shared expert in this layer");
-      src = L->ys.p, bytes = size_t(T) * L->d.hidden * 4;
-      break;
+      const size_t n = size_t(T) * L->d.hidden;
+      if (nbytes < n * 4) return fail(ARTLITE_EINVAL, "moe layer tap: %zu bytes, need %zu", nbytes, n * 4);
+      ART_HIP(hipStreamSynchronize(L->stream));
+      std::vector<float> part(n * size_t(L->last_ys_parts));
+      if (n) ART_HIP(hipMemcpy(part.data(), L->ys.p, part.size() * 4, hipMemcpyDeviceToHost));
+      float* o = static_cast<float*>(out);  // (the parts added in order, as the combine adds them)
+      for (size_t i = 0; i < n; i++) {
+        float v = part[i];
+        for (int j = 1; j < L->last_ys_parts; j++) v += part[size_t(j) * n + i];
+        o[i] = v;
+      }
+      return ARTLITE_OK;
+    }
     case ARTLITE_TAP_H: {
       const size_t n = size_t(P) * L->d.expert_ffn;
       if (nbytes < n * 4) return fail(ARTLITE_EINVAL, "moe layer tap: %zu bytes, need %zu", nbytes, n * 4);

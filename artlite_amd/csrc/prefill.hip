@@ -234,29 +234,44 @@ __device__ __forceinline__ uint32_t pg_k4_word(const PGPrep& p, int j) {
   return __builtin_bit_cast(uint32_t, h);
 }
 
-// An item: expert e, its sorted rows s0 .. s0 + m_valid, output columns n0 .. (SwiGLU: + 128 of gate and up; plain:
-// + 256)
+// An item: product p of the launch, expert e, its sorted rows s0 .. s0 + m_valid, output columns n0 .. (SwiGLU: + 128
+// of gate and up; plain: + 256), the product's K stages
 struct PGItem {
-  int e, s0, m_valid, n0;
+  int e, s0, m_valid, n0, p, stages;
 };
 
-// item w of a launch (tile w / nbk, column block w % nbk); global loads: read once per workgroup, at its start
+// the column blocks of a product, its tiles (the tile list's count, or the dense rows' tiles)
 template <bool SWIGLU>
-__device__ __forceinline__ PGItem pg_item(const PrefillArgs& a, int64_t w, int nbk) {
+__device__ __forceinline__ int pg_nbk(const PrefillProblem& P) {
   constexpr int WN = SWIGLU ? 128 : 256;
+  return (P.N + WN - 1) / WN;
+}
+__device__ __forceinline__ int64_t pg_tiles(const PrefillProblem& P) {
+  if (P.tiles) return *P.n_tiles;
+  const int rows = balanced_rows(P.dense_rows, TILE_ROWS);
+  return (P.dense_rows + rows - 1) / rows;
+}
+
+// item w of product p (tile w / nbk, column block w % nbk); global loads: read once per workgroup, at its start
+template <bool SWIGLU>
+__device__ __forceinline__ PGItem pg_item(const PrefillProblem& P, int p, int64_t w) {
+  constexpr int WN = SWIGLU ? 128 : 256;
+  const int nbk = pg_nbk<SWIGLU>(P);
   const int tl = int(w / nbk);
   PGItem I;
   I.n0 = int(w % nbk) * WN;
-  if (a.tiles) {
-    I.e = a.tiles[2 * tl];
-    I.s0 = a.tiles[2 * tl + 1];
-    const int lo = a.offsets[I.e], hi = a.offsets[I.e + 1];
+  I.p = p;
+  I.stages = P.K / 64;
+  if (P.tiles) {
+    I.e = P.tiles[2 * tl];
+    I.s0 = P.tiles[2 * tl + 1];
+    const int lo = P.offsets[I.e], hi = P.offsets[I.e + 1];
     I.m_valid = min(balanced_rows(hi - lo, TILE_ROWS), hi - I.s0);
   } else {
-    const int rows = balanced_rows(a.dense_rows, TILE_ROWS);
+    const int rows = balanced_rows(P.dense_rows, TILE_ROWS);
     I.e = 0;
     I.s0 = tl * rows;
-    I.m_valid = min(rows, a.dense_rows - I.s0);
+    I.m_valid = min(rows, P.dense_rows - I.s0);
   }
   return I;
 }
@@ -276,18 +291,18 @@ struct PGSrc {
   uint32_t w[L::BI];
   __device__ __forceinline__ static int swz(int r) { return (r >> 1) & 7; }
   // the A sources (a's row tokens from its metadata in LDS)
-  __device__ __forceinline__ void set_a(const PrefillArgs& g, const PGItem& I, const int32_t* tok, int tid) {
+  __device__ __forceinline__ void set_a(const PrefillProblem& g, const PGItem& I, const int32_t* tok, int tid) {
     tid = pg_fresh(tid);
 #pragma unroll
     for (int i = 0; i < L::AI; i++) {
       const int p = i * L::THREADS + tid, r = p >> 3, c = (p & 7) ^ swz(r);
       const int row = min(r, I.m_valid - 1);
       const int ar = g.row_a ? tok[row] : I.s0 + row;
-      a[i] = (uint32_t(ar) * uint32_t(g.K) + 8 * c) * 2;
+      a[i] = (uint32_t(ar) * uint32_t(g.lda) + 8 * c) * 2;
     }
   }
   // the weight sources
-  __device__ __forceinline__ void set_w(const PrefillArgs& g, const PGItem& I, int tid) {
+  __device__ __forceinline__ void set_w(const PrefillProblem& g, const PGItem& I, int tid) {
     tid = pg_fresh(tid);
 #pragma unroll
     for (int j = 0; j < L::BI; j++) {  // (dwords past the staged rows: padding, loading the last dword again)
@@ -317,7 +332,7 @@ struct PGSrc {
 // last. Offsets in bytes.
 struct PGMeta {
   uint32_t m[2];
-  __device__ __forceinline__ void set(const PrefillArgs& g, const PGItem& I, int tid) {
+  __device__ __forceinline__ void set(const PGItem& I, int tid) {
     tid = pg_fresh(tid);
 #pragma unroll
     for (int j = 0; j < 2; j++) {
@@ -343,24 +358,38 @@ struct PGBases {
   uint32_t dst, dstw, mdst;
 };
 
-// The issue side: the A stream (item qa, stage sta of the window last opened, its ring slot) and the weight stream one
-// stage ahead of it (item qw, stage stw: its stage index runs one ahead, and so does its slot), the item whose
-// metadata the windows carry (mq), and the open window's bases. Past the last item a stream reloads stage 0 of it
-// (dummies keep the counts fixed).
-template <int QT, bool SWIGLU>
+// The issue side: the A stream (item qa of na stages, stage sta of the window last opened, its ring slot) and the
+// weight stream one stage ahead of it (item qw of nw stages, stage stw: its stage index runs one ahead, and so does
+// its slot), the item whose metadata the windows carry (mq), their products' base pointers (A: ab0; weights: w0, w1;
+// metadata: mt0, ms0), and the open window's bases. Past the last item a stream reloads stage 0 of it (dummies keep
+// the counts fixed).
+template <int QT, bool SWIGLU, bool MP>
 struct PGIssue {
   PGSrc<QT, SWIGLU> src;
   PGMeta meta;
   PGBases b;
-  int sta, qa, stw, qw;
+  int sta, qa, na, stw, qw, nw;
   int slot;
   int mq;
+  const uint8_t *ab0, *w0, *w1, *mt0, *ms0;
+  // the base pointers of product P for the A stream, the weight stream, the metadata
+  __device__ __forceinline__ void use_a(const PrefillProblem& P) {
+    ab0 = reinterpret_cast<const uint8_t*>(P.a);
+  }
+  __device__ __forceinline__ void use_w(const PrefillProblem& P) {
+    w0 = P.w[0];
+    w1 = SWIGLU ? P.w[1] : P.w[0];
+  }
+  __device__ __forceinline__ void use_m(const PrefillProblem& P) {
+    ms0 = reinterpret_cast<const uint8_t*>(P.row_scale);
+    mt0 = P.row_a ? reinterpret_cast<const uint8_t*>(P.row_a) : ms0;
+  }
 };
 
 // One DMA of the open window: n < BI the weights' dwords (first: they come from HBM), then the A chunks, then the
 // metadata's dwords (instruction i of wave w writes the region's bytes (8 i + w) 64 + lane times the DMA's size).
-template <int QT, bool SWIGLU>
-__device__ __forceinline__ void pg_dma_n(int n, const PGIssue<QT, SWIGLU>& is, int wv) {
+template <int QT, bool SWIGLU, bool MP>
+__device__ __forceinline__ void pg_dma_n(int n, const PGIssue<QT, SWIGLU, MP>& is, int wv) {
   using L = PG<QT>;
   const PGBases& b = is.b;
   if (n < L::BI) {
@@ -544,8 +573,9 @@ struct PGCtx {
   uint8_t* lds;
   uint32_t lbase;
   int tid, wv, lane, lg, lr;
-  int stages, nq;
-  const int4* table;  // (in LDS) the items: (e, s0, m_valid, n0)
+  int nq;
+  int stages;  // (a launch of one product: its stages, those of every item)
+  const int4* table;  // (in LDS) the items: (e + 2^24 p, s0, m_valid, n0 + 2^24 stages)
 };
 
 template <int QT>
@@ -558,28 +588,35 @@ __device__ __forceinline__ const float2* pg_rowf(const PGCtx& c, int q) {  // (a
   return reinterpret_cast<const float2*>(c.lds + PG<QT>::R * PG<QT>::SBYTES + (q & 1) * PG<QT>::META + 1024);
 }
 
-__device__ __forceinline__ PGItem pg_table(const PGCtx& c, int q) {
-  const int4 v = c.table[q];
-  return PGItem{__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
-                __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w)};
+__device__ __forceinline__ int4 pg_pack(const PGItem& I) {
+  return make_int4(I.e | (I.p << 24), I.s0, I.m_valid, I.n0 | (I.stages << 24));
 }
 
-// the weight bases of stage sw (Q4_K: super-block sw / 4, its quarter sw % 4)
+// (MP: the launch holds several products; else every item is product 0's, known at compile time)
+template <bool MP>
+__device__ __forceinline__ PGItem pg_table(const PGCtx& c, int q) {
+  const int4 v = c.table[q];
+  const int x = __builtin_amdgcn_readfirstlane(v.x), w = __builtin_amdgcn_readfirstlane(v.w);
+  return PGItem{x & 0xFFFFFF, __builtin_amdgcn_readfirstlane(v.y), __builtin_amdgcn_readfirstlane(v.z),
+                w & 0xFFFFFF, MP ? x >> 24 : 0, w >> 24};
+}
+
+// the weight bases of stage sw (Q4_K: super-block sw / 4, its quarter sw % 4) from the weight stream's matrices w0, w1
 template <int QT, bool SWIGLU>
-__device__ __forceinline__ void pg_wbases(const PrefillArgs& a, int sw, PGBases& b, int wv) {
+__device__ __forceinline__ void pg_wbases(const uint8_t* w0, const uint8_t* w1, int sw, PGBases& b, int wv) {
   using L = PG<QT>;
   if constexpr (L::X3) {  // (the wave's own: instruction 0's matrix, instruction 1's)
-    b.wb0 = (SWIGLU && wv >= 6 ? a.w[1] : a.w[0]) + sw * L::WROW;
-    b.wb1 = (SWIGLU ? a.w[1] : a.w[0]) + sw * L::WROW;
+    b.wb0 = (SWIGLU && wv >= 6 ? w1 : w0) + sw * L::WROW;
+    b.wb1 = w1 + sw * L::WROW;
     b.wq0 = b.wq1 = nullptr;
   } else if constexpr (L::K4) {
-    b.wb0 = a.w[0] + (sw >> 2) * 144;
-    b.wb1 = (SWIGLU ? a.w[1] : a.w[0]) + (sw >> 2) * 144;
+    b.wb0 = w0 + (sw >> 2) * 144;
+    b.wb1 = w1 + (sw >> 2) * 144;
     b.wq0 = b.wb0 + 16 + 32 * (sw & 3);
     b.wq1 = b.wb1 + 16 + 32 * (sw & 3);
   } else {
-    b.wb0 = a.w[0] + sw * L::WROW;
-    b.wb1 = (SWIGLU ? a.w[1] : a.w[0]) + sw * L::WROW;
+    b.wb0 = w0 + sw * L::WROW;
+    b.wb1 = w1 + sw * L::WROW;
     b.wq0 = b.wq1 = nullptr;
   }
 }
@@ -588,28 +625,48 @@ __device__ __forceinline__ void pg_wbases(const PrefillArgs& a, int sw, PGBases&
 // the A sources from its metadata, which landed two windows after the first that carried it; the weight sources from
 // its table entry), into the next ring slot (weights: the slot after it), with the metadata of item mq (>= 0: a new one)
 // into its buffer.
-template <int QT, bool SWIGLU>
-__device__ __forceinline__ void pg_open(const PrefillArgs& a, const PGCtx& c, PGIssue<QT, SWIGLU>& is, int mq) {
+template <int QT, bool SWIGLU, bool MP>
+__device__ __forceinline__ void pg_open(const PrefillArgs& a, const PGCtx& c, PGIssue<QT, SWIGLU, MP>& is, int mq) {
   using L = PG<QT>;
   if (mq >= 0 && mq != is.mq) {
     is.mq = mq;
-    is.meta.set(a, pg_table(c, mq), c.tid);
+    const PGItem M = pg_table<MP>(c, mq);
+    is.meta.set(M, c.tid);
+    is.use_m(a.p[M.p]);
   }
   is.slot = is.slot + 1 == L::R ? 0 : is.slot + 1;
-  if (is.qa < c.nq && ++is.sta == c.stages) {
+  if (is.qa < c.nq && ++is.sta == (MP ? is.na : c.stages)) {
     is.sta = 0;
-    if (++is.qa < c.nq) is.src.set_a(a, pg_table(c, is.qa), pg_tok<QT>(c, is.qa), c.tid);
+    if (++is.qa < c.nq) {
+      const PGItem A = pg_table<MP>(c, is.qa);
+      is.src.set_a(a.p[A.p], A, pg_tok<QT>(c, is.qa), c.tid);
+      is.use_a(a.p[A.p]);
+      is.na = A.stages;
+    }
   }
-  if (is.qw < c.nq && ++is.stw == c.stages) {
+  if (is.qw < c.nq && ++is.stw == (MP ? is.nw : c.stages)) {
     is.stw = 0;
-    if (++is.qw < c.nq) is.src.set_w(a, pg_table(c, is.qw), c.tid);
+    if (++is.qw < c.nq) {
+      const PGItem W = pg_table<MP>(c, is.qw);
+      is.src.set_w(a.p[W.p], W, c.tid);
+      is.use_w(a.p[W.p]);
+      is.nw = W.stages;
+    }
   }
   const int sa = __builtin_amdgcn_readfirstlane(is.qa < c.nq ? is.sta : 0);
   PGBases& b = is.b;
-  b.ab = static_cast<const uint8_t*>(static_cast<const void*>(a.a)) + 128 * sa;
-  pg_wbases<QT, SWIGLU>(a, __builtin_amdgcn_readfirstlane(is.qw < c.nq ? is.stw : 0), b, c.wv);
-  b.ms = reinterpret_cast<const uint8_t*>(a.row_scale);
-  b.mt = a.row_a && c.wv < 4 ? reinterpret_cast<const uint8_t*>(a.row_a) : b.ms;  // (the wave's metadata DMA 0)
+  // (one product: its pointers read from the kernel's arguments, which the compiler may reload rather than hold)
+  PGIssue<QT, SWIGLU, MP> one;
+  if constexpr (!MP) {
+    one.use_a(a.p[0]);
+    one.use_w(a.p[0]);
+    one.use_m(a.p[0]);
+  }
+  const PGIssue<QT, SWIGLU, MP>& ptr = MP ? is : one;
+  b.ab = ptr.ab0 + 128 * sa;
+  pg_wbases<QT, SWIGLU>(ptr.w0, ptr.w1, __builtin_amdgcn_readfirstlane(is.qw < c.nq ? is.stw : 0), b, c.wv);
+  b.ms = ptr.ms0;
+  b.mt = c.wv < 4 ? ptr.mt0 : ptr.ms0;  // (the wave's metadata DMA 0)
   const int ws = is.slot + 1 == L::R ? 0 : is.slot + 1;
   b.dst = __builtin_amdgcn_readfirstlane(c.lbase + is.slot * L::SBYTES);
   b.dstw = __builtin_amdgcn_readfirstlane(c.lbase + ws * L::SBYTES + L::ABYTES);
@@ -631,8 +688,8 @@ __device__ __forceinline__ void pg_open(const PrefillArgs& a, const PGCtx& c, PG
 // only this step's window may be in flight); past it the wave reads the next step's first A operands from ns
 // (nsmall: its tile has 2 row blocks). 2 row blocks: the window, its DMAs and the codes' read come before the barrier
 // at the step's start. nmq >= 0: the item whose metadata the windows carry from now on.
-template <int QT, bool SWIGLU, int MBN>
-__device__ __forceinline__ void pg_step(const PrefillArgs& a, const PGCtx& c, PGIssue<QT, SWIGLU>& is,
+template <int QT, bool SWIGLU, bool MP, int MBN>
+__device__ __forceinline__ void pg_step(const PrefillArgs& a, const PGCtx& c, PGIssue<QT, SWIGLU, MP>& is,
                                         const PGLane<QT>& ln, PGOps<QT>& ops, u32x4 (&av)[4], const uint8_t* s,
                                         const uint8_t* ns, int nqi, bool nsmall, int nmq, f32x4 (&acc)[MBN][2]) {
   using L = PG<QT>;
@@ -643,15 +700,15 @@ __device__ __forceinline__ void pg_step(const PrefillArgs& a, const PGCtx& c, PG
   PGRaw<QT> raw;
   PGPrep p1[2], p0[2];
   if constexpr (HEAD == 0) {  // (2 row blocks: the window and the codes' read before the step's barrier)
-    pg_open<QT, SWIGLU>(a, c, is, nmq);
+    pg_open<QT, SWIGLU, MP>(a, c, is, nmq);
 #pragma unroll
-    for (int n = 0; n < L::LOADS; n++) pg_dma_n<QT, SWIGLU>(n, is, c.wv);
+    for (int n = 0; n < L::LOADS; n++) pg_dma_n<QT, SWIGLU, MP>(n, is, c.wv);
     pg_read_codes<QT>(ns, ln, nx, raw);
   }
   static_assert(HEAD == 0 || RD < HEAD, "the next stage's codes are read before the barrier that frees their slot");
   pg_for<IT>([&](auto itc) __attribute__((always_inline)) {
     constexpr int it = decltype(itc)::value;
-    if constexpr (it == 0 && HEAD > 0) pg_open<QT, SWIGLU>(a, c, is, nmq);
+    if constexpr (it == 0 && HEAD > 0) pg_open<QT, SWIGLU, MP>(a, c, is, nmq);
     if constexpr (it == HEAD) {
       pg_wait_window<QT>(c.wv);
       pg_barrier();
@@ -690,7 +747,7 @@ __device__ __forceinline__ void pg_step(const PrefillArgs& a, const PGCtx& c, PG
     });
     if constexpr (it < HEAD) {  // (the window's DMAs: weights first)
 #pragma unroll
-      for (int n = it * L::LOADS / HEAD; n < (it + 1) * L::LOADS / HEAD; n++) pg_dma_n<QT, SWIGLU>(n, is, c.wv);
+      for (int n = it * L::LOADS / HEAD; n < (it + 1) * L::LOADS / HEAD; n++) pg_dma_n<QT, SWIGLU, MP>(n, is, c.wv);
     }
     __builtin_amdgcn_sched_barrier(0);  // (nothing moves from one iteration to another)
   });
@@ -699,8 +756,8 @@ __device__ __forceinline__ void pg_step(const PrefillArgs& a, const PGCtx& c, PG
 
 // One item: its K loop (stage by stage through the ring; cslot: the slot of its stage 0) and its epilogue. Its first
 // step's operands are read already (ops, av), and its last step reads those of the next item's first.
-template <int QT, bool SWIGLU, int MBN>
-__device__ __forceinline__ int pg_run(const PrefillArgs& a, const PGCtx& c, PGIssue<QT, SWIGLU>& is,
+template <int QT, bool SWIGLU, bool MP, int MBN>
+__device__ __forceinline__ int pg_run(const PrefillArgs& a, const PGCtx& c, PGIssue<QT, SWIGLU, MP>& is,
                                       const PGLane<QT>& ln, PGOps<QT>& ops, u32x4 (&av)[4], const PGItem& I, int q,
                                       int cslot) {
   using L = PG<QT>;
@@ -713,18 +770,20 @@ __device__ __forceinline__ int pg_run(const PrefillArgs& a, const PGCtx& c, PGIs
   // for the next item.
   const int nmq = q + 1 < c.nq ? q + 1 : q;
   bool nsmall = false;
-  if (q + 1 < c.nq) nsmall = pg_table(c, q + 1).m_valid <= 32;
+  if (q + 1 < c.nq) nsmall = pg_table<MP>(c, q + 1).m_valid <= 32;
+  const int stages = MP ? I.stages : c.stages;
 #pragma clang loop unroll(disable)  // (one copy of the step: none peeled for the first)
-  for (int st = 0; st < c.stages; st++) {
+  for (int st = 0; st < stages; st++) {
     const int ns = cslot + 1 == L::R ? 0 : cslot + 1;
-    pg_step<QT, SWIGLU, MBN>(a, c, is, ln, ops, av, c.lds + cslot * L::SBYTES, c.lds + ns * L::SBYTES, (st + 1) & 3,
-                             st + 1 < c.stages ? MBN == 2 : nsmall, st == 1 ? nmq : -1, acc);
+    pg_step<QT, SWIGLU, MP, MBN>(a, c, is, ln, ops, av, c.lds + cslot * L::SBYTES, c.lds + ns * L::SBYTES, (st + 1) & 3,
+                                 st + 1 < stages ? MBN == 2 : nsmall, st == 1 ? nmq : -1, acc);
     cslot = __builtin_amdgcn_readfirstlane(ns);
   }
   // epilogue: lane output i of block (mb, nb): row 16 mb + lr of the tile; column (SwiGLU) n0 + 16 wv + 4 lg + i, gate
   // in nb 0 and up in nb 1; (plain) n0 + 32 wv + 8 lg + 4 nb + i. A lane stores its row's 4 (8) columns at once.
   const float2* rf = pg_rowf<QT>(c, q);
   const int lr = pg_fresh(c.lr), lg = pg_fresh(c.lg);
+  const PrefillProblem& P = a.p[I.p];
   float2 fr[3];  // (the row factors, read two row blocks ahead; rows past the valid ones hold the last one's)
   fr[0] = rf[lr];
   fr[1] = rf[16 + lr];
@@ -733,10 +792,10 @@ __device__ __forceinline__ int pg_run(const PrefillArgs& a, const PGCtx& c, PGIs
     if constexpr (mb + 2 < MBN) fr[(mb + 2) % 3] = rf[16 * (mb + 2) + lr];
     const int m = 16 * mb + lr;
     const float2 f = fr[mb % 3];
-    const int64_t o = int64_t(I.s0 + m) * a.N;
+    const int64_t o = int64_t(I.s0 + m) * P.N;
     if constexpr (SWIGLU) {
       const int n = I.n0 + 16 * wv + 4 * lg;
-      if (m < I.m_valid && n < a.N) {
+      if (m < I.m_valid && n < P.N) {
         uint32_t v[2];
 #pragma unroll
         for (int i = 0; i < 2; i++) {
@@ -744,24 +803,24 @@ __device__ __forceinline__ int pg_run(const PrefillArgs& a, const PGCtx& c, PGIs
                            _Float16(pg_swiglu(acc[mb][0][2 * i + 1] * f.x, acc[mb][1][2 * i + 1] * f.x) * f.y)};
           v[i] = __builtin_bit_cast(uint32_t, h);
         }
-        *reinterpret_cast<uint2*>(a.h + o + n) = make_uint2(v[0], v[1]);
+        *reinterpret_cast<uint2*>(P.h + o + n) = make_uint2(v[0], v[1]);
       }
     } else {
       const int n = I.n0 + 32 * wv + 8 * lg;  // (the lane's 8 columns: 4 of each column block)
-      if (m < I.m_valid && n < a.N) {
-        if (a.y16) {  // (fp16: the sums times f.y)
+      if (m < I.m_valid && n < P.N) {
+        if (P.y16) {  // (fp16: the sums times f.y)
           uint32_t v[4];
 #pragma unroll
           for (int i = 0; i < 4; i++) {
             const f16x2 h = {_Float16(acc[mb][i / 2][2 * (i % 2)] * f.y), _Float16(acc[mb][i / 2][2 * (i % 2) + 1] * f.y)};
             v[i] = __builtin_bit_cast(uint32_t, h);
           }
-          *reinterpret_cast<uint4*>(a.y16 + o + n) = make_uint4(v[0], v[1], v[2], v[3]);
+          *reinterpret_cast<uint4*>(P.y16 + o + n) = make_uint4(v[0], v[1], v[2], v[3]);
         } else {  // (fp32: the sums times f.x f.y, a power of two)
           const float fs = f.x * f.y;
 #pragma unroll
           for (int nb = 0; nb < 2; nb++)
-            *reinterpret_cast<float4*>(a.y + o + n + 4 * nb) =
+            *reinterpret_cast<float4*>(P.y + o + n + 4 * nb) =
                 make_float4(acc[mb][nb][0] * fs, acc[mb][nb][1] * fs, acc[mb][nb][2] * fs, acc[mb][nb][3] * fs);
         }
       }
@@ -771,10 +830,9 @@ __device__ __forceinline__ int pg_run(const PrefillArgs& a, const PGCtx& c, PGIs
   return cslot;
 }
 
-template <int QT, bool SWIGLU>
+template <int QT, bool SWIGLU, bool MP>
 __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_pgemm(const PrefillArgs a) {
   using L = PG<QT>;
-  constexpr int WN = SWIGLU ? 128 : 256;  // output columns per item
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   PGCtx c;
   c.lds = lds;
@@ -784,38 +842,55 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   c.wv = __builtin_amdgcn_readfirstlane(c.tid / WAVE);
   c.lg = c.lane >> 4;
   c.lr = c.lane & 15;
-  c.stages = a.K / 64;
+  c.stages = a.p[0].K / 64;
   int4* table = reinterpret_cast<int4*>(lds + L::R * L::SBYTES + 2 * L::META);
   c.table = table;
-  const int nbk = (a.N + WN - 1) / WN;
-  const int drows = a.tiles ? 0 : balanced_rows(a.dense_rows, TILE_ROWS);
-  const int64_t ntl = a.tiles ? int64_t(*a.n_tiles) : (a.dense_rows + drows - 1) / drows;
-  const int64_t items = ntl * nbk, per = (items + 7) / 8;
-  // Items are dealt to the 8 XCDs in contiguous runs (workgroup b runs on XCD b % 8): the column blocks of a tile, and
-  // an expert's tiles, run close in time on one XCD and share its L2 (the tile's A rows, the expert's weights). Within
-  // a run, an item costs about its tile's row blocks, so the XCD's G workgroups take the run's items ranked by row
-  // blocks (most first, then by index), dealt back and forth: position q G + j0 in even rounds, q G + G - 1 - j0 in
-  // odd ones. Every workgroup of the XCD ranks the same way, so each item is taken once (any assignment gives the
+  // Each product's items are dealt to the 8 XCDs in contiguous runs (workgroup b runs on XCD b % 8): the column blocks
+  // of a tile, and an expert's tiles, run close in time on one XCD and share its L2 (the tile's A rows, the expert's
+  // weights); an XCD's run holds its share of every product. Within a run, an item costs about its stages times its
+  // tile's row blocks (plus a step's fixed part), so the XCD's G workgroups take the run's items ranked by that cost
+  // (most first, then by place in the run), dealt back and forth: position q G + j0 in even rounds, q G + G - 1 - j0
+  // in odd ones. Every workgroup of the XCD ranks the same way, so each item is taken once (any assignment gives the
   // same results: each item writes its own outputs).
   const int G = gridDim.x / 8, x = blockIdx.x % 8, j0 = blockIdx.x / 8;
-  const int64_t lo = x * per, hi = min(items, (x + 1) * per);
-  const int n_run = hi > lo ? int(hi - lo) : 0, full = n_run / G, rem = n_run - full * G;
+  int64_t lo[PREFILL_MAXP];
+  int cnt[PREFILL_MAXP + 1];
+  cnt[0] = 0;
+  int most = 1;  // (the largest item cost of the launch: the cost unit)
+  for (int p = 0; p < PREFILL_MAXP; p++) {
+    int n = 0;
+    lo[p] = 0;
+    if (p < (MP ? a.np : 1)) {
+      const int64_t items = pg_tiles(a.p[p]) * pg_nbk<SWIGLU>(a.p[p]), per = (items + 7) / 8;
+      lo[p] = x * per;
+      const int64_t hi = min(items, (x + 1) * per);
+      n = hi > lo[p] ? int(hi - lo[p]) : 0;
+      most = max(most, a.p[p].K / 64 * (TILE_ROWS / 32 + 1));
+    }
+    cnt[p + 1] = cnt[p] + n;
+  }
+  const int n_run = cnt[PREFILL_MAXP], full = n_run / G, rem = n_run - full * G;
   c.nq = full + (rem && ((full & 1) ? j0 >= G - rem : j0 < rem));  // (at most MAXQ: the launch checks)
   if (c.nq == 0) return;
   // the ranking and the item table: every global load of the tiles and offsets, once, before any DMA is in flight
   // (the ranking's keys, order and the run's items in the ring's memory, not yet in use: n_run <= MAXQ G <= 4096)
+  constexpr int KM = 16;  // (cost keys 1 .. KM)
+  const int unit = (most + KM - 1) / KM;
   uint8_t* key = lds;
   uint16_t* order = reinterpret_cast<uint16_t*>(lds + 4096);
   int4* run = reinterpret_cast<int4*>(lds + 12288);
   static_assert(12288 + 4096 * 16 <= L::R * L::SBYTES, "the ranking's LDS");
   for (int i = c.tid; i < n_run; i += L::THREADS) {
-    const PGItem J = pg_item<SWIGLU>(a, lo + i, nbk);
-    key[i] = uint8_t((J.m_valid + 31) / 32);  // (the K loop's even row-block count / 2)
-    run[i] = make_int4(J.e, J.s0, J.m_valid, J.n0);
+    int p = 0;
+#pragma unroll
+    for (int q = 1; q < PREFILL_MAXP; q++) p += i >= cnt[q] ? 1 : 0;
+    const PGItem J = pg_item<SWIGLU>(a.p[p], p, lo[p] + (i - cnt[p]));
+    const int cost = J.stages * ((J.m_valid + 31) / 32 + 1);
+    key[i] = uint8_t(min(KM, max(1, (cost + unit - 1) / unit)));
+    run[i] = pg_pack(J);
   }
   __syncthreads();
   if (c.wv == 0) {  // (one wave: per key, ballots over runs of 64 items)
-    constexpr int KM = TILE_ROWS / 32;  // (keys 1 .. KM)
     int tot[KM + 1] = {}, start[KM + 1];
     for (int i0 = 0; i0 < n_run; i0 += WAVE) {
       const int k = i0 + c.lane < n_run ? key[i0 + c.lane] : 0;
@@ -843,15 +918,15 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   }
   __syncthreads();
   // item 0's metadata, landed before its sources are made (buffer 0)
-  PGIssue<QT, SWIGLU> is;
-  PGItem I = pg_table(c, 0);
-  is.meta.set(a, I, c.tid);
+  PGIssue<QT, SWIGLU, MP> is;
+  PGItem I = pg_table<MP>(c, 0);
+  is.meta.set(I, c.tid);
+  is.use_m(a.p[I.p]);
   {
-    const uint8_t* ms = reinterpret_cast<const uint8_t*>(a.row_scale);
-    const uint8_t* mt = a.row_a ? reinterpret_cast<const uint8_t*>(a.row_a) : ms;
     const uint32_t mdst = __builtin_amdgcn_readfirstlane(c.lbase + L::R * L::SBYTES);
 #pragma unroll
-    for (int j = 0; j < L::MI; j++) pg_dma<4>(j == 0 && c.wv < 4 ? mt : ms, is.meta.m[j], mdst + (8 * j + c.wv) * 256);
+    for (int j = 0; j < L::MI; j++)
+      pg_dma<4>(j == 0 && c.wv < 4 ? is.mt0 : is.ms0, is.meta.m[j], mdst + (8 * j + c.wv) * 256);
     pg_wait<0>();
     __syncthreads();
   }
@@ -860,23 +935,26 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   // none); the barrier that certifies A stage 0 and weight stages 0, 1; the first step's operands (group 0's weights
   // decoded, group 1's codes, the first A operands); a barrier (every wave past its reads of weight stage 0, into whose
   // slot the first step's window loads weight stage 3).
-  is.src.set_a(a, I, pg_tok<QT>(c, 0), c.tid);
-  is.src.set_w(a, I, c.tid);
+  is.src.set_a(a.p[I.p], I, pg_tok<QT>(c, 0), c.tid);
+  is.src.set_w(a.p[I.p], I, c.tid);
+  is.use_a(a.p[I.p]);
+  is.use_w(a.p[I.p]);
   is.qa = is.qw = 0;
+  is.na = is.nw = I.stages;
   is.sta = -1;
   is.stw = 0;
   is.slot = -1;
   is.mq = 0;
-  pg_wbases<QT, SWIGLU>(a, 0, is.b, c.wv);
+  pg_wbases<QT, SWIGLU>(is.w0, is.w1, 0, is.b, c.wv);
   is.b.dstw = __builtin_amdgcn_readfirstlane(c.lbase + L::ABYTES);
 #pragma unroll
-  for (int n = 0; n < L::BI; n++) pg_dma_n<QT, SWIGLU>(n, is, c.wv);
+  for (int n = 0; n < L::BI; n++) pg_dma_n<QT, SWIGLU, MP>(n, is, c.wv);
   const int mq = c.nq > 1 ? 1 : 0;
 #pragma unroll
   for (int w = 0; w < 2; w++) {
-    pg_open<QT, SWIGLU>(a, c, is, mq);
+    pg_open<QT, SWIGLU, MP>(a, c, is, mq);
 #pragma unroll
-    for (int n = 0; n < L::LOADS; n++) pg_dma_n<QT, SWIGLU>(n, is, c.wv);
+    for (int n = 0; n < L::LOADS; n++) pg_dma_n<QT, SWIGLU, MP>(n, is, c.wv);
   }
   pg_wait_window<QT>(c.wv);
   pg_barrier();
@@ -895,32 +973,43 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 
   int cslot = 0;
   for (int q = 0; q < c.nq; q++) {
-    I = pg_table(c, q);
+    I = pg_table<MP>(c, q);
     // the tile's row blocks, rounded up to an even count (an instance of the K loop per count)
     switch ((I.m_valid + 31) / 32) {
-      case 1: cslot = pg_run<QT, SWIGLU, 2>(a, c, is, ln, ops, av, I, q, cslot); break;
-      case 2: cslot = pg_run<QT, SWIGLU, 4>(a, c, is, ln, ops, av, I, q, cslot); break;
-      case 3: cslot = pg_run<QT, SWIGLU, 6>(a, c, is, ln, ops, av, I, q, cslot); break;
-      case 4: cslot = pg_run<QT, SWIGLU, 8>(a, c, is, ln, ops, av, I, q, cslot); break;
-      case 5: cslot = pg_run<QT, SWIGLU, 10>(a, c, is, ln, ops, av, I, q, cslot); break;
-      case 6: cslot = pg_run<QT, SWIGLU, 12>(a, c, is, ln, ops, av, I, q, cslot); break;
-      case 7: cslot = pg_run<QT, SWIGLU, 14>(a, c, is, ln, ops, av, I, q, cslot); break;
-      default: cslot = pg_run<QT, SWIGLU, 16>(a, c, is, ln, ops, av, I, q, cslot); break;
+      case 1: cslot = pg_run<QT, SWIGLU, MP, 2>(a, c, is, ln, ops, av, I, q, cslot); break;
+      case 2: cslot = pg_run<QT, SWIGLU, MP, 4>(a, c, is, ln, ops, av, I, q, cslot); break;
+      case 3: cslot = pg_run<QT, SWIGLU, MP, 6>(a, c, is, ln, ops, av, I, q, cslot); break;
+      case 4: cslot = pg_run<QT, SWIGLU, MP, 8>(a, c, is, ln, ops, av, I, q, cslot); break;
+      case 5: cslot = pg_run<QT, SWIGLU, MP, 10>(a, c, is, ln, ops, av, I, q, cslot); break;
+      case 6: cslot = pg_run<QT, SWIGLU, MP, 12>(a, c, is, ln, ops, av, I, q, cslot); break;
+      case 7: cslot = pg_run<QT, SWIGLU, MP, 14>(a, c, is, ln, ops, av, I, q, cslot); break;
+      default: cslot = pg_run<QT, SWIGLU, MP, 16>(a, c, is, ln, ops, av, I, q, cslot); break;
     }
   }
   pg_wait<0>();  // (the dummy loads past the last stage land before the workgroup's LDS is released)
 }
 
-template <int QT, bool SWIGLU>
+// a product's work items at most (its tile bound times its column blocks)
+int64_t pg_items_bound(const PrefillProblem& P, bool swiglu) {
+  const int64_t tiles = P.tiles ? P.max_tiles
+                                : (P.dense_rows + balanced_rows(P.dense_rows, TILE_ROWS) - 1) /
+                                      balanced_rows(P.dense_rows, TILE_ROWS);
+  return tiles * ((P.N + (swiglu ? 127 : 255)) / (swiglu ? 128 : 256));
+}
+
+template <int QT, bool SWIGLU, bool MP>
 int launch_pgemm(const PrefillArgs& a, hipStream_t s) {
   using L = PG<QT>;
-  const int rows = a.tiles ? TILE_ROWS : balanced_rows(a.dense_rows, TILE_ROWS);
-  const int64_t tiles = a.tiles ? a.max_tiles : (a.dense_rows + rows - 1) / rows;
-  const int64_t items = tiles * ((a.N + (SWIGLU ? 127 : 255)) / (SWIGLU ? 128 : 256));
+  int64_t items = 0, run = 0;
+  for (int p = 0; p < a.np; p++) {
+    const int64_t n = pg_items_bound(a.p[p], SWIGLU);
+    items += n;
+    run += (n + 7) / 8;  // (an XCD's run: its share of each product)
+  }
   if (items <= 0) return ARTLITE_OK;
   // persistent workgroups: as many as the device holds at once (a multiple of 8, the XCDs), at most the items
   static const int resident = [] {
-    const void* f = reinterpret_cast<const void*>(k_pgemm<QT, SWIGLU>);
+    const void* f = reinterpret_cast<const void*>(k_pgemm<QT, SWIGLU, MP>);
     int dev = 0, cus = 0, per_cu = 0;
     if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, L::LDS) != hipSuccess ||
         hipGetDevice(&dev) != hipSuccess ||
@@ -930,12 +1019,12 @@ int launch_pgemm(const PrefillArgs& a, hipStream_t s) {
     return cus * std::max(1, per_cu);
   }();
   if (resident < 8) return fail(ARTLITE_EHIP, "prefill GEMM: kernel set-up failed");
-  const int64_t grid = std::min<int64_t>((items + 7) / 8 * 8, resident / 8 * 8);
-  // a workgroup's items (an XCD's run of ceil(items / 8), dealt over its grid / 8 workgroups) fit its item table
-  // (and an XCD's run fits the ranking's 4096 entries)
-  if (((items + 7) / 8 + grid / 8 - 1) / (grid / 8) > L::MAXQ || (items + 7) / 8 > 4096)
+  const int64_t grid = std::min<int64_t>(run * 8, resident / 8 * 8);
+  // a workgroup's items (an XCD's run, dealt over its grid / 8 workgroups) fit its item table (and an XCD's run fits
+  // the ranking's 4096 entries)
+  if ((run + grid / 8 - 1) / (grid / 8) > L::MAXQ || run > 4096)
     return fail(ARTLITE_EINVAL, "prefill GEMM: %lld work items, more than %d per workgroup", (long long)items, L::MAXQ);
-  k_pgemm<QT, SWIGLU><<<unsigned(grid), L::THREADS, L::LDS, s>>>(a);
+  k_pgemm<QT, SWIGLU, MP><<<unsigned(grid), L::THREADS, L::LDS, s>>>(a);
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
 }
@@ -948,20 +1037,37 @@ bool prefill_supported(int qtype, int K, int N) {
   // the next item's metadata: stages - R >= 2)
   // (Q4_K: whole super-blocks)
   return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0 || qtype == ARTLITE_Q4_K) &&
-         K >= 64 * (PG<ARTLITE_Q4_0>::R + 2) && K % (qtype == ARTLITE_Q4_K ? 256 : 64) == 0 && N > 0 && N % 16 == 0;
+         K >= 64 * (PG<ARTLITE_Q4_0>::R + 2) && K % (qtype == ARTLITE_Q4_K ? 256 : 64) == 0 && K / 64 < 256 && N > 0 &&
+         N % 16 == 0;
+}
+
+bool prefill_fits(int64_t experts, int64_t expert_bytes, int64_t a_rows, int64_t K) {
+  // (the lane offsets of the weight DMAs reach e expert_bytes + the row's bytes, those of A rows row K 2 bytes)
+  return experts > 0 && experts * expert_bytes + WEIGHT_TAIL < (int64_t(1) << 32) && a_rows * K * 2 < (int64_t(1) << 32);
 }
 
 int launch_prefill(const PrefillArgs& a, hipStream_t s) {
-  if (!prefill_supported(a.qtype, a.K, a.N))
-    return fail(ARTLITE_EINVAL, "prefill GEMM: weight type %d, K %d, N %d", a.qtype, a.K, a.N);
-  if (!a.a || !a.row_scale || (a.w[1] ? !a.h : !a.y && !a.y16) || (a.tiles && (!a.n_tiles || !a.offsets)))
-    return fail(ARTLITE_EINVAL, "prefill GEMM: null argument");
-  const bool swiglu = a.w[1] != nullptr;
-  if (a.qtype == ARTLITE_Q4_0)
-    return swiglu ? launch_pgemm<ARTLITE_Q4_0, true>(a, s) : launch_pgemm<ARTLITE_Q4_0, false>(a, s);
-  if (a.qtype == ARTLITE_Q4_K)
-    return swiglu ? launch_pgemm<ARTLITE_Q4_K, true>(a, s) : launch_pgemm<ARTLITE_Q4_K, false>(a, s);
-  return swiglu ? launch_pgemm<ARTLITE_Q8_0, true>(a, s) : launch_pgemm<ARTLITE_Q8_0, false>(a, s);
+  if (a.np < 1 || a.np > PREFILL_MAXP) return fail(ARTLITE_EINVAL, "prefill GEMM: %d products", a.np);
+  const bool swiglu = a.p[0].w[1] != nullptr;
+  for (int p = 0; p < a.np; p++) {
+    const PrefillProblem& P = a.p[p];
+    if (!prefill_supported(a.qtype, P.K, P.N))
+      return fail(ARTLITE_EINVAL, "prefill GEMM: weight type %d, K %d, N %d", a.qtype, P.K, P.N);
+    if (!P.a || !P.row_scale || !P.w[0] || (P.w[1] != nullptr) != swiglu || (swiglu ? !P.h : !P.y && !P.y16) ||
+        (P.tiles && (!P.n_tiles || !P.offsets)) || P.lda < P.K)
+      return fail(ARTLITE_EINVAL, "prefill GEMM: product %d: null or mismatched argument", p);
+    if (P.expert_bytes >= (int64_t(1) << 32) || int64_t(P.N) * P.row_bytes >= (int64_t(1) << 32) ||
+        (!P.tiles && P.dense_rows > (1 << 24)))
+      return fail(ARTLITE_EINVAL, "prefill GEMM: product %d beyond the tiles' 32-bit offsets", p);
+  }
+  // (one product: the kernel with product 0 known at compile time)
+#define ART_PG(QT) \
+  return swiglu ? (a.np > 1 ? launch_pgemm<QT, true, true>(a, s) : launch_pgemm<QT, true, false>(a, s)) \
+                : (a.np > 1 ? launch_pgemm<QT, false, true>(a, s) : launch_pgemm<QT, false, false>(a, s))
+  if (a.qtype == ARTLITE_Q4_0) ART_PG(ARTLITE_Q4_0);
+  if (a.qtype == ARTLITE_Q4_K) ART_PG(ARTLITE_Q4_K);
+  ART_PG(ARTLITE_Q8_0);
+#undef ART_PG
 }
 
 }  // namespace artlite

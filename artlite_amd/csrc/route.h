@@ -140,9 +140,12 @@ int launch_topk(const float* logits, int64_t n, int64_t row, int per_col, int64_
                 int32_t* ids, float* w32, double* w64, hipStream_t s);
 
 // Router logits out[t out_row + e] = x[t] . W[e] (float64 accumulation, rounded once). xq: when given, x is also
-// quantised into XQ rows (gemv.h) by extra workgroups of the same launch (H a multiple of 256).
+// quantised into XQ rows (gemv.h) by extra workgroups of the same launch (H a multiple of 256). part (part_elems
+// doubles, router_part_elems for the most tokens of a layer; may be null): the fp64 partial sums of prefill-sized
+// batches whose tiles are too few for the device, K split over workgroups and the parts added in a fixed order.
 int launch_router(const void* x, int x_dtype, const float* W, int H, int E, int64_t T, float* out, int64_t out_row,
-                  uint32_t* xq, hipStream_t s);
+                  uint32_t* xq, double* part, size_t part_elems, hipStream_t s);
+size_t router_part_elems(int64_t max_T, int E, int H);
 
 // out (T x H fp32) = x / sqrt(mean(x^2) + eps) * w per row (float64 mean and quotient, rounded once, then fp32 w)
 int launch_rmsnorm(const void* x, int x_dtype, const float* w, float eps, int64_t T, int H, float* out,

@@ -232,13 +232,16 @@ __global__ __launch_bounds__(4 * WAVE) void k_router_small(const void* __restric
 // as step s, lane group g -> k0 + 4 g + s, so each lane's four steps are one 16-byte LDS read of its x row and one of
 // its W row; step s accumulates into acc[s] (consecutive MFMAs independent), the four summed at the end. Rows past T,
 // experts past E load the last one (not stored); K past H loads zeros. KP parts of K: the workgroup's waves are KP
-// sets of the above, set p taking K values [p Kp, (p + 1) Kp) through LDS buffers of its own (more waves a SIMD to
-// issue MFMAs while others wait); the sets' sums are added in set order at the end.
+// sets of the above, set p taking K values [p Kp, (p + 1) Kp) of the workgroup's range through LDS buffers of its
+// own (more waves a SIMD to issue MFMAs while others wait); the sets' sums are added in set order at the end.
+// Split K (part set): workgroup z of the grid takes K values [z kchunk, (z + 1) kchunk) and stores its fp64 sums as
+// part[(z T + t) E + e]; launch_router adds the parts in z order and rounds once. Else (kchunk >= H) the fp32 logits.
 template <int XT, int TE, int KP>
 __global__ __launch_bounds__(KP * 2 * TE / 16 * WAVE) void k_router_mfma(const void* __restrict__ xv,
                                                                          const float* __restrict__ W, int H, int E,
                                                                          int64_t T, float* __restrict__ out,
-                                                                         int64_t out_row) {
+                                                                         int64_t out_row, int kchunk,
+                                                                         double* __restrict__ part_out) {
   typedef double d4 __attribute__((ext_vector_type(4)));
   constexpr int TM = 32, KS = 64, PAD = 68, THREADS = 2 * TE / 16 * WAVE;  // (threads of one set)
   constexpr int NX = TM * 16 / THREADS, NW = TE * 16 / THREADS;  // 16-byte pieces per thread per stage
@@ -247,7 +250,8 @@ __global__ __launch_bounds__(KP * 2 * TE / 16 * WAVE) void k_router_mfma(const v
   const int part = int(threadIdx.x) / THREADS;
   float(&xs)[2][TM][PAD] = xs_all[part];
   float(&ws)[2][TE][PAD] = ws_all[part];
-  const int Kp = (H / KP + KS - 1) / KS * KS, kb = part * Kp, ke = min(H, kb + Kp);
+  const int kz = int(blockIdx.z) * kchunk, kze = min(H, kz + kchunk);
+  const int Kp = (kchunk / KP + KS - 1) / KS * KS, kb = kz + part * Kp, ke = min(kze, kb + Kp);
   const int tid = threadIdx.x % THREADS, lane = tid & (WAVE - 1), wv = tid / WAVE;
   const int tb = wv & 1, eb = wv >> 1, g = lane >> 4, r = lane & 15;
   const int64_t t0 = int64_t(blockIdx.x) * TM;
@@ -351,8 +355,23 @@ __global__ __launch_bounds__(KP * 2 * TE / 16 * WAVE) void k_router_mfma(const v
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int64_t tt = t0 + 16 * tb + 4 * i + g;
-    if (tt < T && e < E) out[tt * out_row + e] = float(c[i]);
+    if (tt < T && e < E) {
+      if (part_out)
+        part_out[(int64_t(blockIdx.z) * T + tt) * E + e] = c[i];
+      else
+        out[tt * out_row + e] = float(c[i]);
+    }
   }
+}
+
+// the split router's parts added in part order, rounded once: a thread per logit
+__global__ __launch_bounds__(256) void k_router_parts(const double* __restrict__ part, int parts, int64_t T, int E,
+                                                     float* __restrict__ out, int64_t out_row) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x, n = T * E;
+  if (i >= n) return;
+  double c = part[i];
+  for (int z = 1; z < parts; z++) c += part[int64_t(z) * n + i];
+  out[(i / E) * out_row + i % E] = float(c);
 }
 
 // ---- RMSNorm of the block's input (the reference's rms_norm, tests/np_ops.py:27-32): the mean of x^2 in float64
@@ -390,8 +409,41 @@ int launch_rmsnorm(const void* x, int x_dtype, const float* w, float eps, int64_
   return ARTLITE_OK;
 }
 
+namespace {
+
+// the fp64 MFMA router's tile (TE experts) and its K parts across workgroups for T tokens: enough workgroups for the
+// device (about 256; one a CU, the kernel's LDS), each part at least 128 values of K (whole stages of each wave set)
+struct RouterSplit {
+  int te, parts, kchunk;
+};
+RouterSplit router_split(int64_t T, int E, int H) {
+  RouterSplit r;
+  r.te = E <= 32 ? 32 : 64;
+  const int64_t tiles = (T + 31) / 32 * ((E + r.te - 1) / r.te);
+  int parts = int(std::min<int64_t>(16, std::max<int64_t>(1, 256 / std::max<int64_t>(1, tiles))));
+  parts = std::min(parts, std::max(1, H / 128));
+  r.kchunk = (H + parts - 1) / parts;
+  r.kchunk = (r.kchunk + 127) / 128 * 128;
+  r.parts = (H + r.kchunk - 1) / r.kchunk;
+  return r;
+}
+
+bool router_mfma_path(int64_t T, int E, int H, bool xq) { return !xq && T >= 64 && E >= 16 && H % 16 == 0; }
+
+}  // namespace
+
+size_t router_part_elems(int64_t max_T, int E, int H) {
+  size_t most = 0;
+  for (int64_t T = 64; T <= max_T; T++) {
+    const RouterSplit r = router_split(T, E, H);
+    if (r.parts > 1) most = std::max(most, size_t(r.parts) * size_t(T) * size_t(E));
+    if (r.parts == 1) break;  // (fewer parts for more tokens)
+  }
+  return most;
+}
+
 int launch_router(const void* x, int x_dtype, const float* W, int H, int E, int64_t T, float* out, int64_t out_row,
-                  uint32_t* xq, hipStream_t s) {
+                  uint32_t* xq, double* part, size_t part_elems, hipStream_t s) {
   if (T <= 0) return ARTLITE_OK;
   if (H % 8) return fail(ARTLITE_EINVAL, "router: H %d not a multiple of 8", H);
   if (xq && H % 256) return fail(ARTLITE_EINVAL, "router: XQ of H %d (not a multiple of 256)", H);
@@ -399,15 +451,33 @@ int launch_router(const void* x, int x_dtype, const float* W, int H, int E, int6
   const int tt = int(std::min<int64_t>(ROUTER_TG, std::max<int64_t>(1, ROUTER_LDS / (int64_t(H) * xb))));
   if (int64_t(H) * xb > ROUTER_LDS) return fail(ARTLITE_EINVAL, "router: H %d too wide", H);
   const size_t lds = size_t(tt) * H * xb;
-  if (!xq && T >= 64 && E >= 16 && H % 16 == 0) {  // (prefill-sized: the fp64 MFMA)
-    // (tiles of 32 x 64, 8 waves a K part: measured faster than 32 x 32 with two workgroups per CU)
-    constexpr int TE = 64, KP = 2;
-    const dim3 g(unsigned((T + 31) / 32), unsigned((E + TE - 1) / TE)), b(KP * 2 * TE / 16 * WAVE);
-    if (x_dtype == ARTLITE_X_F32)
-      k_router_mfma<ARTLITE_X_F32, TE, KP><<<g, b, 0, s>>>(x, W, H, E, T, out, out_row);
-    else
-      k_router_mfma<ARTLITE_X_BF16, TE, KP><<<g, b, 0, s>>>(x, W, H, E, T, out, out_row);
+  if (router_mfma_path(T, E, H, xq)) {  // (prefill-sized: the fp64 MFMA)
+    // (tiles of 32 x 64, 8 waves a K part: measured faster than 32 x 32 with two workgroups per CU; 32 x 32 for at
+    // most 32 experts; K split over workgroups when the tiles are fewer than the device's CUs)
+    constexpr int KP = 2;
+    RouterSplit r = router_split(T, E, H);
+    if (r.parts > 1 && (!part || size_t(r.parts) * size_t(T) * size_t(E) > part_elems)) r = RouterSplit{r.te, 1, H};
+    double* po = r.parts > 1 ? part : nullptr;
+    const dim3 g(unsigned((T + 31) / 32), unsigned((E + r.te - 1) / r.te), unsigned(r.parts));
+    if (r.te == 32) {
+      const dim3 b(KP * 2 * 32 / 16 * WAVE);
+      if (x_dtype == ARTLITE_X_F32)
+        k_router_mfma<ARTLITE_X_F32, 32, KP><<<g, b, 0, s>>>(x, W, H, E, T, out, out_row, r.kchunk, po);
+      else
+        k_router_mfma<ARTLITE_X_BF16, 32, KP><<<g, b, 0, s>>>(x, W, H, E, T, out, out_row, r.kchunk, po);
+    } else {
+      const dim3 b(KP * 2 * 64 / 16 * WAVE);
+      if (x_dtype == ARTLITE_X_F32)
+        k_router_mfma<ARTLITE_X_F32, 64, KP><<<g, b, 0, s>>>(x, W, H, E, T, out, out_row, r.kchunk, po);
+      else
+        k_router_mfma<ARTLITE_X_BF16, 64, KP><<<g, b, 0, s>>>(x, W, H, E, T, out, out_row, r.kchunk, po);
+    }
     ART_HIP(hipGetLastError());
+    if (po) {
+      const int64_t n = T * E;
+      k_router_parts<<<unsigned((n + 255) / 256), 256, 0, s>>>(po, r.parts, T, E, out, out_row);
+      ART_HIP(hipGetLastError());
+    }
     return ARTLITE_OK;
   }
   if (T <= ROUTER_TG && H % 1024 == 0) {  // (a workgroup per expert)

@@ -128,10 +128,12 @@ def time_T(gls: list, shape: dict, T: int, steps: int, warmup: int) -> dict:
             "names": list(kernels)}
 
 
-def work(shape: dict, T: int, U: float, pair_bytes: int) -> dict:
+def work(shape: dict, T: int, U: float, pair_bytes: int, names: list) -> dict:
     """Algorithmic bytes and flops of the layer and of its gate / up and down launches (U experts touched): the
     weights of the touched experts once, the activations in bf16, h in fp16, the pair outputs in ``pair_bytes`` per
-    value (the path's format: fp16 on the prefill tiles, fp32 elsewhere), the layer's output in fp32."""
+    value (the path's format: fp16 on the prefill tiles, fp32 elsewhere), the layer's output in fp32. On the prefill
+    tiles the shared expert's products join the routed launches of their format (``names`` then lacks
+    ``shared_gate_up`` / ``shared_down``), and their work counts in those launches'."""
     H, E, k, F = shape["H"], shape["E"], shape["k"], shape["F"]
     P = T * k
     Fs = shape.get("shared_F", 0)
@@ -141,7 +143,14 @@ def work(shape: dict, T: int, U: float, pair_bytes: int) -> dict:
     layer_b = gu_b + dn_b + sh_b + E * H * 4 + T * H * 4
     gu_f = 2.0 * P * 2 * H * F
     dn_f = 2.0 * P * H * F
-    layer_f = gu_f + dn_f + 2.0 * T * 3 * H * Fs + 2.0 * T * H * E
+    if Fs and "prefill_x" in names:
+        if "shared_gate_up" not in names:
+            gu_b += 2 * H * Fs * bpw(shape["shared"]) + T * Fs * 2
+            gu_f += 2.0 * T * 2 * H * Fs
+        if "shared_down" not in names:
+            dn_b += H * Fs * bpw(shape["shared"]) + T * Fs * 2 + T * H * 4
+            dn_f += 2.0 * T * H * Fs
+    layer_f = 2.0 * P * 3 * H * F + 2.0 * T * 3 * H * Fs + 2.0 * T * H * E
     return {"gate_up": (gu_b, gu_f), "down": (dn_b, dn_f), "layer": (layer_b, layer_f)}
 
 
@@ -172,7 +181,7 @@ TRAFFIC = {("decode", "gate_up"): ROOT / "profiles" / "gemv_gate_up_decode_b16_t
 def line(name: str, shape: dict, T: int, r: dict, steps: int) -> dict:
     """One workload's object: tokens/s, median / mean step, per-kernel ms, the roofline of its dominant kernel (of
     gate_up and down, the longer), the layer's."""
-    w = work(shape, T, r["U"], 2 if "prefill_x" in r["names"] else 4)
+    w = work(shape, T, r["U"], 2 if "prefill_x" in r["names"] else 4, r["names"])
     lb, lf = w["layer"]
     mfma = lf / (MFMA_F16_PEAK_TFLOPS * 1e12) > lb / (HBM_PEAK_GBS * 1e9)  # (the layer's binding roof)
     kern = max(("gate_up", "down"), key=lambda n: r["kernels"].get(n, 0.0))

@@ -64,6 +64,11 @@ CONFIGS = {
     # the prefill tiles)
     "mix_pf": Spec("mix_pf", H=1024, E=16, k=2, F=512, gate_type="Q8_0", down_type="Q4_0", scale=0.01,
                    x_dtype="f32", shared_F=512, shared_type="Q8_0", shared_gated=True, tokens=(256,)),
+    # test-only prefill-sized Q4_0 layer with a Q4_0 shared expert twice as wide as the routed ones: on the prefill
+    # tiles the shared gate / up joins the routed gate / up launch and the shared down, in two parts of its K, the
+    # routed down launch
+    "shared_pf": Spec("shared_pf", H=1024, E=16, k=2, F=512, gate_type="Q4_0", down_type="Q4_0", scale=0.02,
+                      shared_F=1024, shared_type="Q4_0", tokens=(256,)),
     # test-only: Q4_0 with about 128 pairs per expert (T = 512), so the prefill tiles' 8-row-block form runs
     "q4_rows": Spec("q4_rows", H=1024, E=8, k=2, F=512, gate_type="Q4_0", down_type="Q4_0", scale=0.02,
                     router="uniform", tokens=(512,)),

@@ -52,6 +52,9 @@ def test_full_deepseek_cfg4() -> None:
     tokens, 64 experts top 6."""
     r = run_full("deepseek", 512)
     assert r["counts"].sum() == 512 * 6 and (r["counts"] > 0).sum() == 64
+    # (the shared gate / up's items in the routed gate / up launch; its Q4_K down, unlike the routed Q8_0 one, in a
+    # launch of its own over four parts of its K)
+    assert "shared_gate_up" not in r["kernels"] and "shared_down" in r["kernels"], r["kernels"]
 
 
 def test_full_skewed_cfg5() -> None:

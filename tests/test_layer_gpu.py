@@ -14,6 +14,7 @@ Config sizes are reduced here; test_layer_full_gpu.py runs configs 3, 4 and 5 at
 import numpy as np
 import pytest
 
+from artlite_amd.moe.layer import MoELayer
 from oracle import gguf_ref, host_ref, layers, moe_ref
 
 from .helpers import check_against_oracle, gpu_input, gpu_layer, near_tie, rel_l2, ulp_diff
@@ -21,7 +22,8 @@ from .helpers import check_against_oracle, gpu_input, gpu_layer, near_tie, rel_l
 pytestmark = pytest.mark.gpu
 
 CASES = [("cpu", 16), ("decode", 1), ("decode", 4), ("decode", 16), ("decode", 64), ("prefill", 256),
-         ("deepseek", 64), ("skewed", 192), ("mix_q8k", 16), ("mix_k8", 24), ("mix_pf", 256), ("kquants", 32),
+         ("deepseek", 64), ("skewed", 192), ("mix_q8k", 16), ("mix_k8", 24), ("mix_pf", 256), ("shared_pf", 256),
+         ("kquants", 32),
          ("kquants", 160), ("iq4", 24), ("iq4", 96), ("kmix", 16), ("kmix", 64),
          ("q5km", 16), ("q5k", 24), ("q6k", 24), ("mixtile", 16), ("iq4", 16), ("q41", 16), ("q3k", 16)]
 
@@ -42,9 +44,11 @@ def check_layer(name: str, T: int, seed: int = 0) -> None:
     with gpu_layer(layer, max_tokens=T) as g:
         y = g(gpu_input(spec, x))
         gemv = any(n.startswith("router_quant") for n in g.kernel_names())
-        assert "h_planes" not in g.kernel_names(), name  # (every format's down on the GEMV when its gate / up is)
         prefill = "prefill_x" in g.kernel_names()
         assert gemv == ((name, T) in GEMV_CASES), (name, T, g.kernel_names())
+        if name in ("shared_pf", "mix_pf"):  # (the shared gate / up in the routed launch; the down too when alike)
+            assert "shared_gate_up" not in g.kernel_names(), g.kernel_names()
+            assert ("shared_down" in g.kernel_names()) == (name == "mix_pf"), g.kernel_names()
         tol = 1e-4 if gemv else 1e-3 if prefill else 1e-5
         lg = g.tap("logits")
         ids, w = g.tap("ids"), g.tap("weights")
@@ -173,3 +177,17 @@ def test_layer_sigmoid_gating(name: str, T: int) -> None:
     assert np.array_equal(taps["ids"][~near], want["ids"][~near])
     s = 1 / (1 + np.exp(-np.take_along_axis(lg, taps["ids"], 1).astype(np.float64)))
     np.testing.assert_allclose(taps["weights"], s / np.maximum(s.sum(1, keepdims=True), 2.0 ** -14), rtol=3e-7)
+
+
+def test_prefill_offset_guard() -> None:
+    """The prefill tiles address an expert tensor and the rows of A with 32-bit offsets: a layer whose Q8_0 gate tensor
+    passes 4 GiB (256 experts of 4096 x 4096) takes the MFMA decode tiles at prefill sizes instead, while the same layer
+    with 128 experts (2.1 GiB) takes the prefill tiles. (No weights are uploaded: the path is chosen at creation.)"""
+    H = F = 4096
+    T = 4096
+    x = np.zeros((T, H), np.uint16)
+    for E, prefill in ((128, True), (256, False)):
+        with MoELayer(hidden=H, n_experts=E, top_k=8, expert_ffn=F, gate_type="Q8_0", down_type="Q8_0",
+                      max_tokens=T) as g:
+            g.stage(x)
+            assert ("prefill_x" in g.kernel_names()) == prefill, (E, g.kernel_names())
