@@ -98,6 +98,34 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ raw
   }
 }
 
+// the largest L1 norm of the rows (sum |w| of the values as dequantized, in fp32, rounded up by 2^-10 relative: the
+// fp32 sum of at most 2^13 terms is within 2^-11 of the exact one), a wave per row, by an atomic max on the float's
+// bits (non-negative floats order as their bits). BYTES: the block's stride (the layer's padded Q6_K / Q3_K blocks
+// keep the file's bytes first)
+template <int QT, int PER, int BYTES>
+__global__ __launch_bounds__(256) void k_row_l1(const uint8_t* __restrict__ raw, int64_t rows, size_t row_bytes,
+                                                int cols, uint32_t* __restrict__ out) {
+  const int64_t r = (int64_t(blockIdx.x) * 256 + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  float s = 0.0f;
+  if (r < rows) {
+    const uint8_t* row = raw + r * row_bytes;
+    for (int c = lane; c < cols; c += 64) s += fabsf(value<QT>(row + (c / PER) * BYTES, c % PER));
+  }
+  for (int o = 32; o; o >>= 1) s += __shfl_xor(s, o);
+  if (lane == 0 && r < rows) atomicMax(out, __float_as_uint(s * (1.0f + 0x1p-10f)));
+}
+
+template <int QT, int PER, int BYTES>
+int launch_l1(const uint8_t* raw, int64_t rows, size_t row_bytes, int cols, float* out, hipStream_t s) {
+  ART_HIP(hipMemsetAsync(out, 0, 4, s));
+  if (rows <= 0) return ARTLITE_OK;
+  k_row_l1<QT, PER, BYTES><<<unsigned((rows + 3) / 4), 256, 0, s>>>(raw, rows, row_bytes, cols,
+                                                                    reinterpret_cast<uint32_t*>(out));
+  ART_HIP(hipGetLastError());
+  return ARTLITE_OK;
+}
+
 template <int QT, int PER, int BYTES>
 int launch_t(const uint8_t* raw, size_t n, size_t row_bytes, size_t cols, float* out, hipStream_t s) {
   const size_t passes = n * ((cols + CHUNK - 1) / CHUNK);
@@ -126,6 +154,21 @@ int launch_dequant(const QType* t, const uint8_t* raw, size_t n, size_t row_byte
     case ARTLITE_IQ4_NL: return launch_t<ARTLITE_IQ4_NL, 32, 18>(raw, n, row_bytes, cols, out, s);
     case ARTLITE_IQ4_XS: return launch_t<ARTLITE_IQ4_XS, 256, 136>(raw, n, row_bytes, cols, out, s);
     default: return fail(ARTLITE_EINVAL, "dequant: type %d", t->id);
+  }
+}
+
+int launch_weight_l1(const uint8_t* w, int qtype, int64_t rows, size_t row_bytes, int cols, float* out, hipStream_t s) {
+  if (cols <= 0 || cols > 8192) return fail(ARTLITE_EINVAL, "weight L1: %d columns", cols);
+  switch (qtype) {  // (block strides as the layer stores them: Q6_K padded to 224 bytes, Q3_K to 112)
+    case ARTLITE_Q4_0: return launch_l1<ARTLITE_Q4_0, 32, 18>(w, rows, row_bytes, cols, out, s);
+    case ARTLITE_Q4_1: return launch_l1<ARTLITE_Q4_1, 32, 20>(w, rows, row_bytes, cols, out, s);
+    case ARTLITE_Q8_0: return launch_l1<ARTLITE_Q8_0, 32, 34>(w, rows, row_bytes, cols, out, s);
+    case ARTLITE_Q3_K: return launch_l1<ARTLITE_Q3_K, 256, 112>(w, rows, row_bytes, cols, out, s);
+    case ARTLITE_Q4_K: return launch_l1<ARTLITE_Q4_K, 256, 144>(w, rows, row_bytes, cols, out, s);
+    case ARTLITE_Q5_K: return launch_l1<ARTLITE_Q5_K, 256, 176>(w, rows, row_bytes, cols, out, s);
+    case ARTLITE_Q6_K: return launch_l1<ARTLITE_Q6_K, 256, 224>(w, rows, row_bytes, cols, out, s);
+    case ARTLITE_IQ4_NL: return launch_l1<ARTLITE_IQ4_NL, 32, 18>(w, rows, row_bytes, cols, out, s);
+    default: return fail(ARTLITE_EINVAL, "weight L1: type %d", qtype);
   }
 }
 

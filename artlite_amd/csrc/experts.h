@@ -79,16 +79,20 @@ int launch_prefill(const PrefillArgs& a, hipStream_t s);
 
 // x (T rows of H fp32 / bf16 values) -> the prefill's fp16 rows x16 = x 2^-xe[t] (each token's largest |x| into
 // [2^14, 2^15)), and per token the row factors of the expert products: gu[t] = (2^xe, 2^-he) for the gate / up
-// launch (he: the exponent of h's scale, from the bound on |h| that wmax[0], wmax[1] give: max |w| of the gate and up
-// matrices) and dn[t] = (2^(he + ye), 2^-ye) for the down launch's fp16 output (ye from the bound on its sums that F
-// and wmax[4], max |w| of the down matrix, give: |sum| 2^-ye < 2^15); pairs 2: the same for a second (shared)
-// expert's matrices wmax[2], wmax[3] into gu2, and dn2 = (2^he, 1) for its fp32 down output
+// launch (he: the exponent of h's scale, from the bound on |h| that the gate and up matrices' max |w| (wmax[0],
+// wmax[1]) and largest row L1 norms (wmax[5], wmax[6]) give) and dn[t] = (2^(he + ye), 2^-ye) for the down launch's
+// fp16 output (ye from the bound on its sums that the down matrix's largest row L1 norm wmax[9] gives:
+// |sum| 2^-ye < 2^15); pairs 2: the same for a second (shared) expert's matrices (wmax[2], wmax[3]; wmax[7], wmax[8])
+// into gu2, and dn2 = (2^he, 1) for its fp32 down output
 int launch_prefill_x(const void* x, int x_dtype, int64_t T, int H, const float* wmax, int pairs, int F, uint16_t* x16,
                      float2* gu, float2* dn, float2* gu2, float2* dn2, hipStream_t s);
 
 // *out = a bound on max |w| over a tensor's nblocks GGUF blocks (Q4_0, Q8_0: exact; Q4_K: from d, dmin and the
 // largest 6-bit scale and min)
 int launch_weight_max(const uint8_t* w, int qtype, int64_t nblocks, float* out, hipStream_t s);
+// *out = a bound on the largest L1 norm (sum |w|) of a tensor's rows of cols values as the layer stores them
+// (dequant.hip)
+int launch_weight_l1(const uint8_t* w, int qtype, int64_t rows, size_t row_bytes, int cols, float* out, hipStream_t s);
 // the most 32-value groups of a row (K <= 32 MAX_GROUPS)
 constexpr int MAX_GROUPS = 128;
 

@@ -417,24 +417,28 @@ int launch_decode(const GemmArgs& a, hipStream_t s) {
 
 // ---- the prefill's activations: per token t, x's row in fp16 scaled by 2^-xe (its largest |x| into [2^14, 2^15);
 // exact for bf16 x unless below 2^-14 of that), and the factors of the expert products' rows: gu[t] = (2^xe, 2^-he),
-// he the exponent of h's scale from the bound B = 2 (sum |x|)^2 (max |w_gate|) (max |w_up|) >= |silu(g) u| >= |h|
-// (|g| <= sum |x| max |w_gate|, |silu(g)| <= |g|): he = ilogb(B) - 14, so |h| 2^-he < 2^15 (fp16 holds it). wmax[j]:
-// max |w| of the bound's two matrices (pair j: wmax[2 j], wmax[2 j + 1]). The down launch's sums over F fp16 values
-// of h 2^-he (below 2^15) times weights (below max |w_down| = wmax[4], up to fp16 rounding) stay below
-// 2^15 F wmax[4] (1 + 2^-11): with ye = ilogb(F wmax[4]) + 1 they stay below 2^15 (1 + 2^-11) < 65504 after the
-// factor 2^-ye, so the expert launch writes fp16 sums times 2^-ye and the true output is that times 2^(he + ye):
+// he the exponent of h's scale from a bound B >= 2 |g| |u| >= |silu(g) u| = |h| (|silu(g)| <= |g|), where each of
+// |g|, |u| is at most the smaller of (sum |x|) (max |w|) and (max |x|) (the matrix's largest row L1 norm):
+// he = ilogb(B) - 14, so |h| 2^-he < 2^15 (fp16 holds it). wmax[2 j], wmax[2 j + 1]: max |w| of pair j's matrices,
+// wmax[5 + 2 j], wmax[6 + 2 j] their largest row L1 norms (a block with an outlier scale raises its row's L1 norm by
+// its 32 values' share, not every row's bound by the outlier's factor). The down launch's sums over F fp16 values of
+// h 2^-he (below 2^15) times a row of weights (of L1 norm at most L1d = wmax[9], up to fp16 rounding) stay below
+// 2^15 L1d (1 + 2^-11): with ye = ilogb(L1d) + 1 they stay below 2^15 (1 + 2^-11) < 65504 after the factor 2^-ye,
+// so the expert launch writes fp16 sums times 2^-ye and the true output is that times 2^(he + ye):
 // dn[t] = (2^(he + ye), 2^-ye). The shared expert's down writes fp32: dn2[t] = (2^he, 1). One workgroup per token.
-__device__ __forceinline__ void prefill_x_factors(int64_t t, int tid, int xe, float l1, const float* wmax, int pairs,
-                                                  int F, float2* gu, float2* dn, float2* gu2, float2* dn2) {
+__device__ __forceinline__ void prefill_x_factors(int64_t t, int tid, int xe, float mx, float l1, const float* wmax,
+                                                  int pairs, int F, float2* gu, float2* dn, float2* gu2, float2* dn2) {
   if (tid < pairs) {
-    // (in double: the square of a large sum stays finite)
-    const double b = 2.0 * double(l1) * double(l1) * double(wmax[2 * tid]) * double(wmax[2 * tid + 1]);
+    // (in double: the product of two large bounds stays finite)
+    const double bg = fmin(double(l1) * double(wmax[2 * tid]), double(mx) * double(wmax[5 + 2 * tid]));
+    const double bu = fmin(double(l1) * double(wmax[2 * tid + 1]), double(mx) * double(wmax[6 + 2 * tid]));
+    const double b = 2.0 * bg * bu;
     const int he = max(-126, min(126, (b > 0.0 && b < 1e300) ? ilogb(b) - 14 : 0));
     (tid ? gu2 : gu)[t] = make_float2(__builtin_ldexpf(1.0f, xe), __builtin_ldexpf(1.0f, -he));
     if (tid) {
       dn2[t] = make_float2(__builtin_ldexpf(1.0f, he), 1.0f);
     } else {
-      const double bd = double(F) * double(wmax[4]);
+      const double bd = fmin(double(F) * double(wmax[4]), double(wmax[9]));
       const int ye = (bd > 0.0 && bd < 1e300) ? min(min(126, 126 - he), max(max(-126, -126 - he), ilogb(bd) + 1)) : 0;
       dn[t] = make_float2(__builtin_ldexpf(1.0f, he + ye), __builtin_ldexpf(1.0f, -ye));
     }
@@ -468,7 +472,7 @@ __global__ __launch_bounds__(256) void k_prefill_x(const void* __restrict__ x, i
   const int xe = (mx > 0.0f && mx <= 3.4e38f) ? ilogbf(mx) - 14 : 0;
   for (int i = threadIdx.x; i < H; i += 256)
     x16[t * H + i] = __builtin_bit_cast(uint16_t, _Float16(__builtin_ldexpf(at(i), -xe)));
-  prefill_x_factors(t, threadIdx.x, xe, l1, wmax, pairs, F, gu, dn, gu2, dn2);
+  prefill_x_factors(t, threadIdx.x, xe, mx, l1, wmax, pairs, F, gu, dn, gu2, dn2);
 }
 
 // The same for H a multiple of 8 up to 2048 NP: the row read once, 8 values per thread per piece (one 16-byte load for
@@ -526,7 +530,7 @@ __global__ __launch_bounds__(256) void k_prefill_x_rows(const void* __restrict__
       reinterpret_cast<uint4*>(x16 + t * H)[i] = make_uint4(w[0], w[1], w[2], w[3]);
     }
   }
-  prefill_x_factors(t, threadIdx.x, xe, l1, wmax, pairs, F, gu, dn, gu2, dn2);
+  prefill_x_factors(t, threadIdx.x, xe, mx, l1, wmax, pairs, F, gu, dn, gu2, dn2);
 }
 
 // The same, a wave per token (four tokens a workgroup): lane l holds pieces l + 64 j of the row (8 values each, H =
@@ -586,7 +590,7 @@ __global__ __launch_bounds__(256) void k_prefill_x_wave(const void* __restrict__
              uint32_t(__builtin_bit_cast(uint16_t, _Float16(__builtin_ldexpf(v[j][2 * c + 1], -xe)))) << 16;
     reinterpret_cast<uint4*>(x16 + t * H)[lane + 64 * j] = make_uint4(w[0], w[1], w[2], w[3]);
   }
-  prefill_x_factors(t, lane, xe, l1, wmax, pairs, F, gu, dn, gu2, dn2);
+  prefill_x_factors(t, lane, xe, mx, l1, wmax, pairs, F, gu, dn, gu2, dn2);
 }
 
 int launch_prefill_x(const void* x, int x_dtype, int64_t T, int H, const float* wmax, int pairs, int F, uint16_t* x16,

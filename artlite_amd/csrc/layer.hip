@@ -28,7 +28,8 @@ struct artlite_moe_layer {
   DevBuf x16;                     // the prefill's fp16 activations (each token's row scaled by a power of two)
   DevBuf gu_tok, dn_tok, sgu_tok, sdn_tok;  // per token, the row factors of the prefill's products (float2)
   DevBuf row_a, gu_row, dn_row;   // per sorted pair row: its token and its factors
-  DevBuf wmax;                    // max |w| of gate, up, shared gate, shared up (the bounds on |h|), down
+  DevBuf wmax;  // max |w| of gate, up, shared gate, shared up (the bounds on |h|), down; then the largest row L1 norm
+                // of each
   DevBuf logits, ids, w, sg;
   DevBuf rpart;  // the router's fp64 partial sums (K split over workgroups), router_part_elems doubles
   size_t rpart_elems = 0;
@@ -603,7 +604,7 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
   res(L->hlo, size_t(P * F) * 2);
   res(L->ypairs, size_t(P * H) * 4);
   res(L->y, size_t(T * H) * 4);
-  res(L->wmax, 5 * 4);
+  res(L->wmax, 10 * 4);
   if (L->prefill_ok) {
     res(L->x16, size_t(T * H) * 2);
     res(L->gu_tok, size_t(T) * 8);
@@ -684,6 +685,13 @@ extern "C" int artlite_moe_layer_upload(artlite_moe_layer* L, int t, const void*
     const QType* q = wm < 2 ? L->gq : wm == 4 ? L->dq : L->sq;
     ART_TRY(launch_weight_max(static_cast<const uint8_t*>(b->p), q->id, int64_t(want / q->bytes),
                               L->wmax.as<float>() + wm, L->stream));
+    const artlite_moe_desc& d = L->d;
+    const int cols = wm == 4 ? d.expert_ffn : d.hidden;
+    const size_t row = wm < 2 ? L->gate_row : wm == 4 ? L->down_row : L->sgate_row;
+    const int64_t rows = wm < 2 ? int64_t(d.n_experts) * d.expert_ffn : wm == 4 ? int64_t(d.n_experts) * d.hidden
+                                                                                 : int64_t(d.shared_ffn);
+    ART_TRY(launch_weight_l1(static_cast<const uint8_t*>(b->p), q->id, rows, row, cols, L->wmax.as<float>() + 5 + wm,
+                             L->stream));
   }
   ART_HIP(hipStreamSynchronize(L->stream));
   L->have[t] = true;

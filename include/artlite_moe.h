@@ -60,12 +60,13 @@ int artlite_moe_plan(const int32_t* ids, int64_t n, int k, int E, int cols, int 
                      int32_t* counts, int32_t* sizes, int32_t* rows, int64_t* pos);
 
 /* ---- the chunk plan without allocating: no counterpart in the reference. For callers that cannot allocate device
- * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): artlite_moe_plan's
+ * memory (tight serving loops, harnesses that forbid hipMalloc): artlite_moe_plan's
  * arguments and results, with every device buffer it needs (the staged ids, the per-block histograms, counters,
  * the results before their copy back) carved from one static 8 MiB array per GPU, held until the process ends, and
  * the null stream. It calls no hipMalloc / hipFree. A call needing more than that array returns ARTLITE_EINVAL
  * (about 250000 pairs at E = 128). Calls share the GPU's array: calls that overlap on one GPU (other threads) race;
- * each call clears the counters it needs. */
+ * each call clears the counters it needs. Its host copies and synchronization make it unsuitable under HIP graph
+ * capture. */
 int artlite_moe_plan_static(const int32_t* ids, int64_t n, int k, int E, int cols, int cap, int chunk,
                             int32_t* experts, int32_t* counts, int32_t* sizes, int32_t* rows, int64_t* pos);
 

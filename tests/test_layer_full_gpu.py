@@ -21,10 +21,12 @@ from .helpers import check_against_oracle, check_pairs_f64, gpu_input, gpu_layer
 pytestmark = pytest.mark.gpu
 
 
-def run_full(name: str, T: int, seed: int = 0) -> dict:
+def run_full(name: str, T: int, seed: int = 0, plant=None) -> dict:
     spec = layers.CONFIGS[name]
-    print(f"full-size layer {name} T={T} seed={seed}", flush=True)
+    print(f"full-size layer {name} T={T} seed={seed}{' planted' if plant else ''}", flush=True)
     layer = layers.make_layer(spec, seed)
+    if plant:
+        plant(layer)
     x = layers.make_x(spec, T, seed)
     with gpu_layer(layer, max_tokens=T) as g:
         y = g(gpu_input(spec, x))
@@ -64,6 +66,25 @@ def test_full_skewed_cfg5() -> None:
     c = r["counts"]
     assert (c == 0).sum() == 6 and np.array_equal(np.flatnonzero(c == 0), r["layer"].meta["cold"])
     assert 0.4 < np.sort(c)[::-1][:4].sum() / c.sum() < 0.6
+    assert "prefill_x" in r["kernels"]
+
+
+def plant_q8_outliers(layer: layers.Layer, factor: float = 32.0) -> None:
+    """Multiply the fp16 scale of one Q8_0 block by ``factor`` in a row of the gate, the up and the down matrix of
+    one routed expert that receives tokens (an outlier block, as real GGUF tensors hold them)."""
+    spec = layer.spec
+    e = next(i for i in range(spec.E) if i not in set(layer.meta.get("cold", [])))
+    for m, row, blk in ((layer.gate, e * spec.F + 5, 3), (layer.up, e * spec.F + 9, 1), (layer.down, e * spec.H + 7, 2)):
+        d = m[row, 34 * blk:34 * blk + 2].view(np.float16)
+        m[row, 34 * blk:34 * blk + 2] = (d.astype(np.float32) * factor).astype(np.float16).view(np.uint8)
+
+
+def test_full_skewed_outlier_scales() -> None:
+    """Config 5 with one block of 32x the usual scale in a gate, an up and a down row of one routed expert: the prefill
+    tiles' fp16 h and pair outputs take their scales from the matrices' largest row L1 norms (an outlier block raises
+    one row's norm by its 32 values' share), so the layer stays within 1e-3 of the fp32 oracle and h and the pair
+    outputs within 1e-3 of float64 math."""
+    r = run_full("skewed", 2048, plant=plant_q8_outliers)
     assert "prefill_x" in r["kernels"]
 
 

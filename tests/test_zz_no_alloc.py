@@ -55,3 +55,31 @@ def test_plan_static_errors() -> None:
     big = np.zeros((400_000, 1), np.int32)
     rc, _ = _plan("artlite_moe_plan_static", big, 8, 2200)
     assert rc == _hip.EINVAL and "bytes of device scratch" in _hip.last_error()
+
+
+def _free_bytes() -> int:
+    """The device's free memory (hipMemGetInfo of the HIP runtime this process has loaded)."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
+
+
+def test_plan_static_allocates_nothing() -> None:
+    """After a first call (the array's address resolved), calls of growing size within the limit leave the device's
+    free memory as it was; artlite_moe_plan on a larger batch than it has seen grows its buffers (the contrast)."""
+    E, k = 128, 8
+    ids0 = _ids(64, k, E, 1)
+    cap0 = -(-(E + -(-64 * k // CHUNK)) // COLS)
+    assert _plan("artlite_moe_plan_static", ids0, E, cap0)[0] == _hip.OK
+    before = _free_bytes()
+    for T in (256, 1024, 8192, 20000):
+        ids = _ids(T, k, E, T)
+        cap = -(-(E + -(-T * k // CHUNK)) // COLS)
+        assert _plan("artlite_moe_plan_static", ids, E, cap)[0] == _hip.OK, _hip.last_error()
+        assert _free_bytes() == before, T
+    T = 1 << 20  # (8 M pairs: tens of MB of staged ids, histograms and results)
+    ids = np.random.default_rng(0).integers(0, E, (T, k), dtype=np.int32)
+    cap = -(-(E + -(-T * k // CHUNK)) // COLS)
+    assert _plan("artlite_moe_plan", ids, E, cap)[0] == _hip.OK, _hip.last_error()
+    assert _free_bytes() < before
