@@ -6,6 +6,7 @@
 // this file is compiled with -ffp-contract=off); the writes are coalesced rows of fp32. The C entry points
 // artlite_dequant_supported / artlite_dequant_rows.
 #include "common.h"
+#include "experts.h"
 
 namespace artlite {
 
@@ -33,8 +34,9 @@ __device__ __forceinline__ void k_scale_min(const uint8_t* s, int g, int& sc, in
   }
 }
 
-// value j of the block at b, as the reference computes it (dequant.cpp line ranges per format)
-template <int QT>
+// value j of the block at b, as the reference computes it (dequant.cpp line ranges per format); XS: where IQ4_XS's
+// codes start (8 in the file, 16 in the layer's padded block)
+template <int QT, int XS = 8>
 __device__ __forceinline__ float value(const uint8_t* b, int j) {
   if constexpr (QT == ARTLITE_Q4_0) {  // (q - 8) d (:41-48)
     return __fmul_rn(float(nibble32(b + 2, j)) - 8.0f, f16_to_f32(ld_u16(b)));
@@ -72,7 +74,7 @@ __device__ __forceinline__ float value(const uint8_t* b, int j) {
     const int g = j >> 5;
     const int ls = ((b[4 + g / 2] >> (4 * (g & 1))) & 15) | (((int(ld_u16(b + 2)) >> (2 * g)) & 3) << 4);
     const float dl = __fmul_rn(f16_to_f32(ld_u16(b)), float(ls - 32));
-    return __fmul_rn(dl, float(IQ4_VALUES[nibble32(b + 8 + 16 * g, j & 31)]));
+    return __fmul_rn(dl, float(IQ4_VALUES[nibble32(b + XS + 16 * g, j & 31)]));
   } else if constexpr (QT == ARTLITE_F32) {
     return __uint_as_float(uint32_t(b[0]) | uint32_t(b[1]) << 8 | uint32_t(b[2]) << 16 | uint32_t(b[3]) << 24);
   } else if constexpr (QT == ARTLITE_F16) {
@@ -110,7 +112,7 @@ __global__ __launch_bounds__(256) void k_row_l1(const uint8_t* __restrict__ raw,
   float s = 0.0f;
   if (r < rows) {
     const uint8_t* row = raw + r * row_bytes;
-    for (int c = lane; c < cols; c += 64) s += fabsf(value<QT>(row + (c / PER) * BYTES, c % PER));
+    for (int c = lane; c < cols; c += 64) s += fabsf(value<QT, 16>(row + (c / PER) * BYTES, c % PER));
   }
   for (int o = 32; o; o >>= 1) s += __shfl_xor(s, o);
   if (lane == 0 && r < rows) atomicMax(out, __float_as_uint(s * (1.0f + 0x1p-10f)));
@@ -135,7 +137,163 @@ int launch_t(const uint8_t* raw, size_t n, size_t row_bytes, size_t cols, float*
   return ARTLITE_OK;
 }
 
+// ---- the prefill layout (experts.h, PREFILL_PQ6): per 64 values of a row, their codes (6 bits: a nibble plane and a
+// crumb plane) and the fp32 scales of their sub-blocks, made from a block of the layer's uploaded tensor. The code,
+// scale and min of value w of a block, as the file's fields hold them (dequant.cpp lines as in value<>).
+template <int QT>
+struct Pq6;
+template <>
+struct Pq6<ARTLITE_Q6_K> {  // (layer block: 224 bytes, the file's 210 first) q = 6 bits, (q - 32) (d sc_16)
+  static constexpr int PER = 256, DEV = 224, MODE = 0;
+  static __device__ uint32_t code(const uint8_t* b, int w) {
+    const int h = w >> 7, jj = (w >> 5) & 3, l = w & 31;
+    const uint32_t c = b[64 * h + 32 * (jj & 1) + l], e = b[128 + 32 * h + l];
+    return ((c >> (jj < 2 ? 0 : 4)) & 15u) | (((e >> (2 * jj)) & 3u) << 4);
+  }
+  static __device__ float2 scale(const uint8_t* b, int w) {
+    return make_float2(__fmul_rn(float(int8_t(b[192 + (w >> 4)])), f16_to_f32(ld_u16(b + 208))), 0.0f);
+  }
+};
+template <>
+struct Pq6<ARTLITE_Q3_K> {  // (layer block: 112 bytes, the file's 110 first) q = 3 bits, (d (sc_16 - 32)) (q - 4)
+  static constexpr int PER = 256, DEV = 112, MODE = 0;
+  static __device__ uint32_t code(const uint8_t* b, int w) {
+    const int n = w >> 7, jj = (w >> 5) & 3, hl = w & 31;
+    return uint32_t(((b[32 + 32 * n + hl] >> (2 * jj)) & 3) | (((b[hl] >> (4 * n + jj)) & 1) << 2));
+  }
+  static __device__ float2 scale(const uint8_t* b, int w) {
+    const int sb = w >> 4;
+    const uint8_t* s = b + 96;
+    const int lo = sb < 8 ? s[sb] & 15 : s[sb - 8] >> 4, hi = (s[8 + (sb & 3)] >> (2 * (sb >> 2))) & 3;
+    return make_float2(__fmul_rn(f16_to_f32(ld_u16(b + 108)), float((lo | (hi << 4)) - 32)), 0.0f);
+  }
+};
+template <>
+struct Pq6<ARTLITE_Q5_K> {  // q = 5 bits, q (d sc_32) - dmin m_32
+  static constexpr int PER = 256, DEV = 176, MODE = 1;
+  static __device__ uint32_t code(const uint8_t* b, int w) {
+    const int g = w >> 5, l = w & 31;
+    const uint32_t c = b[48 + 32 * (g >> 1) + l];
+    return ((g & 1) ? c >> 4 : c & 15u) | (((uint32_t(b[16 + l]) >> g) & 1u) << 4);
+  }
+  static __device__ float2 scale(const uint8_t* b, int w) {
+    int sc, mn;
+    k_scale_min(b + 4, w >> 5, sc, mn);
+    return make_float2(__fmul_rn(f16_to_f32(ld_u16(b)), float(sc)), __fmul_rn(f16_to_f32(ld_u16(b + 2)), float(mn)));
+  }
+};
+template <>
+struct Pq6<ARTLITE_Q4_1> {  // q = 4 bits, d q + m
+  static constexpr int PER = 32, DEV = 20, MODE = 1;
+  static __device__ uint32_t code(const uint8_t* b, int w) { return nibble32(b + 4, w); }
+  static __device__ float2 scale(const uint8_t* b, int) {
+    return make_float2(f16_to_f32(ld_u16(b)), -f16_to_f32(ld_u16(b + 2)));
+  }
+};
+template <>
+struct Pq6<ARTLITE_IQ4_NL> {  // the index of IQ4's value, d IQ4[q]
+  static constexpr int PER = 32, DEV = 18, MODE = 2;
+  static __device__ uint32_t code(const uint8_t* b, int w) { return nibble32(b + 2, w); }
+  static __device__ float2 scale(const uint8_t* b, int) { return make_float2(f16_to_f32(ld_u16(b)), 0.0f); }
+};
+template <>
+struct Pq6<ARTLITE_IQ4_XS> {  // (layer block: 144 bytes, the 8-byte header padded to 16) (d (ls_32 - 32)) IQ4[q]
+  static constexpr int PER = 256, DEV = 144, MODE = 2;
+  static __device__ uint32_t code(const uint8_t* b, int w) { return nibble32(b + 16 + 16 * (w >> 5), w & 31); }
+  static __device__ float2 scale(const uint8_t* b, int w) {
+    const int g = w >> 5;
+    const int ls = ((b[4 + g / 2] >> (4 * (g & 1))) & 15) | (((int(ld_u16(b + 2)) >> (2 * g)) & 3) << 4);
+    return make_float2(__fmul_rn(f16_to_f32(ld_u16(b)), float(ls - 32)), 0.0f);
+  }
+};
+
+// a thread per (row, 64-value stage): its 64 bytes of the prefill layout
+template <int QT>
+__global__ __launch_bounds__(256) void k_pq6_pack(const uint8_t* __restrict__ src, int64_t rows, int K,
+                                                  size_t row_bytes, uint8_t* __restrict__ dst) {
+  using F = Pq6<QT>;
+  const int stages = K / 64;
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= rows * stages) return;
+  const int64_t r = i / stages;
+  const int st = int(i % stages);
+  const uint8_t* row = src + r * row_bytes;
+  auto at = [&](int v) { const int a = 64 * st + v; return row + (a / F::PER) * F::DEV; };
+  auto in = [&](int v) { return (64 * st + v) % F::PER; };
+  float hdr[4];
+  if (F::MODE == 1) {  // (scale and min of each 32 values)
+    for (int g = 0; g < 2; g++) {
+      const float2 so = F::scale(at(32 * g), in(32 * g));
+      hdr[2 * g] = so.x;
+      hdr[2 * g + 1] = so.y;
+    }
+  } else {  // (the scale of each 16 values)
+    for (int h = 0; h < 4; h++) hdr[h] = F::scale(at(16 * h), in(16 * h)).x;
+  }
+  uint32_t nib[8], cr[4];
+  for (int d = 0; d < 8; d++) {  // (nibble dword 4 g + l: byte k = value 32 g + 8 l + k | value + 4 in the high nibble)
+    nib[d] = 0;
+    for (int k = 0; k < 4; k++) {
+      const int v = 8 * d + k;
+      nib[d] |= ((F::code(at(v), in(v)) & 15u) | ((F::code(at(v + 4), in(v + 4)) & 15u) << 4)) << (8 * k);
+    }
+  }
+  for (int d = 0; d < 4; d++) {  // (crumb dword 2 g + m: lane groups 2 m + 1 (bits 0-3), 2 m (bits 4-7) of group g)
+    cr[d] = 0;
+    const int g = d >> 1, m = d & 1;
+    for (int k = 0; k < 4; k++) {
+      uint32_t byte = 0;
+      for (int par = 0; par < 2; par++) {
+        const int v = 32 * g + 8 * (2 * m + 1 - par) + k;
+        byte |= ((F::code(at(v), in(v)) >> 4) | ((F::code(at(v + 4), in(v + 4)) >> 4) << 2)) << (4 * par);
+      }
+      cr[d] |= byte << (8 * k);
+    }
+  }
+  uint4* o = reinterpret_cast<uint4*>(dst + r * int64_t(K) + 64 * st);
+  o[0] = make_uint4(__float_as_uint(hdr[0]), __float_as_uint(hdr[1]), __float_as_uint(hdr[2]), __float_as_uint(hdr[3]));
+  o[1] = make_uint4(nib[0], nib[1], nib[2], nib[3]);
+  o[2] = make_uint4(nib[4], nib[5], nib[6], nib[7]);
+  o[3] = make_uint4(cr[0], cr[1], cr[2], cr[3]);
+}
+
+template <int QT>
+int launch_pack(const uint8_t* src, int64_t rows, int K, size_t row_bytes, uint8_t* dst, hipStream_t s) {
+  if (K % Pq6<QT>::PER) return fail(ARTLITE_EINVAL, "prefill layout: K %d is not a multiple of the block", K);
+  const int64_t n = rows * (K / 64);
+  if (n <= 0) return ARTLITE_OK;
+  k_pq6_pack<QT><<<unsigned((n + 255) / 256), 256, 0, s>>>(src, rows, K, row_bytes, dst);
+  ART_HIP(hipGetLastError());
+  return ARTLITE_OK;
+}
+
 }  // namespace
+
+bool pq6_mode(int qtype, int& mode, float& off) {
+  switch (qtype) {
+    case ARTLITE_Q6_K: mode = 0, off = 32.0f; return true;
+    case ARTLITE_Q3_K: mode = 0, off = 4.0f; return true;
+    case ARTLITE_Q5_K:
+    case ARTLITE_Q4_1: mode = 1, off = 0.0f; return true;
+    case ARTLITE_IQ4_NL:
+    case ARTLITE_IQ4_XS: mode = 2, off = 128.0f; return true;
+    default: return false;
+  }
+}
+
+int launch_pq6_pack(const uint8_t* src, int qtype, int64_t rows, int K, size_t row_bytes, uint8_t* dst,
+                    hipStream_t s) {
+  if (K <= 0 || K % 64) return fail(ARTLITE_EINVAL, "prefill layout: K %d is not a multiple of 64", K);
+  switch (qtype) {
+    case ARTLITE_Q6_K: return launch_pack<ARTLITE_Q6_K>(src, rows, K, row_bytes, dst, s);
+    case ARTLITE_Q3_K: return launch_pack<ARTLITE_Q3_K>(src, rows, K, row_bytes, dst, s);
+    case ARTLITE_Q5_K: return launch_pack<ARTLITE_Q5_K>(src, rows, K, row_bytes, dst, s);
+    case ARTLITE_Q4_1: return launch_pack<ARTLITE_Q4_1>(src, rows, K, row_bytes, dst, s);
+    case ARTLITE_IQ4_NL: return launch_pack<ARTLITE_IQ4_NL>(src, rows, K, row_bytes, dst, s);
+    case ARTLITE_IQ4_XS: return launch_pack<ARTLITE_IQ4_XS>(src, rows, K, row_bytes, dst, s);
+    default: return fail(ARTLITE_EINVAL, "prefill layout: type %d", qtype);
+  }
+}
 
 int launch_dequant(const QType* t, const uint8_t* raw, size_t n, size_t row_bytes, size_t cols, float* out,
                    hipStream_t s) {
@@ -159,7 +317,7 @@ int launch_dequant(const QType* t, const uint8_t* raw, size_t n, size_t row_byte
 
 int launch_weight_l1(const uint8_t* w, int qtype, int64_t rows, size_t row_bytes, int cols, float* out, hipStream_t s) {
   if (cols <= 0 || cols > 8192) return fail(ARTLITE_EINVAL, "weight L1: %d columns", cols);
-  switch (qtype) {  // (block strides as the layer stores them: Q6_K padded to 224 bytes, Q3_K to 112)
+  switch (qtype) {  // (block strides as the layer stores them: Q6_K padded to 224 bytes, Q3_K to 112, IQ4_XS to 144)
     case ARTLITE_Q4_0: return launch_l1<ARTLITE_Q4_0, 32, 18>(w, rows, row_bytes, cols, out, s);
     case ARTLITE_Q4_1: return launch_l1<ARTLITE_Q4_1, 32, 20>(w, rows, row_bytes, cols, out, s);
     case ARTLITE_Q8_0: return launch_l1<ARTLITE_Q8_0, 32, 34>(w, rows, row_bytes, cols, out, s);
@@ -168,6 +326,7 @@ int launch_weight_l1(const uint8_t* w, int qtype, int64_t rows, size_t row_bytes
     case ARTLITE_Q5_K: return launch_l1<ARTLITE_Q5_K, 256, 176>(w, rows, row_bytes, cols, out, s);
     case ARTLITE_Q6_K: return launch_l1<ARTLITE_Q6_K, 256, 224>(w, rows, row_bytes, cols, out, s);
     case ARTLITE_IQ4_NL: return launch_l1<ARTLITE_IQ4_NL, 32, 18>(w, rows, row_bytes, cols, out, s);
+    case ARTLITE_IQ4_XS: return launch_l1<ARTLITE_IQ4_XS, 256, 144>(w, rows, row_bytes, cols, out, s);
     default: return fail(ARTLITE_EINVAL, "weight L1: type %d", qtype);
   }
 }

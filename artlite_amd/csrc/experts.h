@@ -60,13 +60,31 @@ struct PrefillProblem {
   uint16_t* y16;           // or fp16 (row stride N)
 };
 
+// The prefill layout of the block formats the prefill tiles do not read from the file's bytes (Q3_K, Q5_K, Q6_K, Q4_1,
+// IQ4_NL, IQ4_XS): made at upload (launch_pq6_pack), 64 bytes per 64 values of a row (a stage of the tiles), four
+// 16-byte chunks: the scales (4 fp32), two of nibbles, one of crumbs. Value 32 g + 8 l + i (g < 2, l < 4, i < 8) has
+// code c (6 bits): its low 4 bits are nibble (i / 4) of byte i % 4 of dword 4 g + l (bytes 16 ..), its high 2 bits
+// bits 2 (i / 4) + 4 (1 - l % 2) of byte i % 4 of dword 2 g + l / 2 of the crumbs (bytes 48 ..). Its weight is
+// w = s c - o, in one of three modes: 0 (Q3_K, Q6_K) s the fp32 scale of its 16 values (scale 4 g + 2 l / 2 ... of
+// the stage: s[2 g + l / 2]), o = off s (off: 4, 32); 1 (Q4_1, Q5_K) (s, o) = the fp32 scale and min of its 32 values
+// (scales 2 g, 2 g + 1); 2 (IQ4_NL, IQ4_XS) as mode 0 with off 128, c = IQ4[nibble] + 128. Every s and o is the block's
+// own product of fp16 and integer fields, exact in fp32, so w is the file's value.
+constexpr int PREFILL_PQ6 = 0x106;  // (a prefill launch's qtype: weights in the prefill layout)
+// the mode and offset of a block format's prefill layout; false: the format has none
+bool pq6_mode(int qtype, int& mode, float& off);
+// rows of K values (K a multiple of 64 and of the format's block) of a tensor as the layer stores it (row_bytes apart)
+// -> the prefill layout (K bytes a row)
+int launch_pq6_pack(const uint8_t* src, int qtype, int64_t rows, int K, size_t row_bytes, uint8_t* dst, hipStream_t s);
+
 // A prefill launch: up to PREFILL_MAXP products of one weight format and kind (all SwiGLU or all plain), their work
 // items dealt over the device together (a routed product and the shared expert's; the parts of a split K).
 constexpr int PREFILL_MAXP = 4;
 struct PrefillArgs {
   PrefillProblem p[PREFILL_MAXP];
   int np;
-  int qtype;               // ARTLITE_Q4_0 / Q8_0 / Q4_K
+  int qtype;               // ARTLITE_Q4_0 / Q8_0 / Q4_K, or PREFILL_PQ6 (every product's weights in the prefill layout)
+  int pq_mode;             // PREFILL_PQ6: the products' mode and offset (pq6_mode)
+  float pq_off;
 };
 
 // whether the prefill tiling takes N rows of K values of weights of this type
@@ -88,7 +106,7 @@ int launch_prefill_x(const void* x, int x_dtype, int64_t T, int H, const float* 
                      float2* gu, float2* dn, float2* gu2, float2* dn2, hipStream_t s);
 
 // *out = a bound on max |w| over a tensor's nblocks GGUF blocks (Q4_0, Q8_0: exact; Q4_K: from d, dmin and the
-// largest 6-bit scale and min)
+// largest 6-bit scale and min; other formats: the largest fp32 value, no bound, so that the L1 norms govern)
 int launch_weight_max(const uint8_t* w, int qtype, int64_t nblocks, float* out, hipStream_t s);
 // *out = a bound on the largest L1 norm (sum |w|) of a tensor's rows of cols values as the layer stores them
 // (dequant.hip)

@@ -653,8 +653,11 @@ __global__ void k_weight_max(const uint8_t* __restrict__ w, int block_bytes, flo
 }
 
 int launch_weight_max(const uint8_t* w, int qtype, int64_t nblocks, float* out, hipStream_t s) {
-  if (qtype != ARTLITE_Q4_0 && qtype != ARTLITE_Q8_0 && qtype != ARTLITE_Q4_K)
-    return fail(ARTLITE_EINVAL, "weight max: type %d", qtype);
+  if (qtype != ARTLITE_Q4_0 && qtype != ARTLITE_Q8_0 && qtype != ARTLITE_Q4_K) {
+    // (no bound of this form: the largest fp32 value, so that the rows' L1 norms bound the products alone)
+    ART_HIP(hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(out), 0x7F7FFFFF, 1, s));
+    return ARTLITE_OK;
+  }
   ART_HIP(hipMemsetAsync(out, 0, 4, s));
   if (nblocks <= 0) return ARTLITE_OK;
   const int bb = qtype == ARTLITE_Q4_0 ? 18 : qtype == ARTLITE_Q8_0 ? 34 : 144;

@@ -37,6 +37,10 @@ struct artlite_moe_layer {
   DevBuf gtick;  // the one-launch routing's tickets per token group (GTICK_STRIDE ints apart)
   DevBuf hhi, hlo, ypairs, shhi, shlo, ys, y;
   DevBuf h16, sh16;  // the prefill's h (fp16, scaled per token)
+  // the prefill tiles' weights of the formats they do not read from the file's bytes: the prefill layout (experts.h,
+  // PREFILL_PQ6) of gate, up, down, shared gate, shared up, shared down, made at upload
+  DevBuf pq_gate, pq_up, pq_down, pq_sgate, pq_sup, pq_sdown;
+  int pre_g = 0, pre_d = 0, pre_sg = 0, pre_sd = 0;  // the prefill launches' weight format of each product (0: none)
   DevBuf xq, hq, shq;  // the decode path's XQ activations
   bool gemv_ok = false, shared_gemv_ok = false, prefill_ok = false, shared_prefill_ok = false;
   int64_t last_T = -1;
@@ -96,6 +100,30 @@ DevBuf* tensor_buf(artlite_moe_layer* L, int t) {
 
 // the block formats of the experts' kernels (every quantized type the dequantizer reads)
 bool is_expert_type(const QType* q) { return q && q->per >= 32; }
+
+// the prefill tiles' weight format of a block format: its own (Q4_0, Q8_0, Q4_K: read from the file's bytes) or the
+// prefill layout (the others)
+int prefill_type(const QType* q) {
+  int mode;
+  float off;
+  if (!q) return 0;
+  if (q->id == ARTLITE_Q4_0 || q->id == ARTLITE_Q8_0 || q->id == ARTLITE_Q4_K) return q->id;
+  return pq6_mode(q->id, mode, off) ? PREFILL_PQ6 : 0;
+}
+
+// a prefill launch's weight format (and the prefill layout's mode) for products of block format q
+void prefill_format(const QType* q, PrefillArgs& a) {
+  a.qtype = prefill_type(q);
+  a.pq_mode = 0;
+  a.pq_off = 0.0f;
+  if (a.qtype == PREFILL_PQ6) pq6_mode(q->id, a.pq_mode, a.pq_off);
+}
+
+// a product's weights and row bytes as the prefill tiles read them (the prefill layout: one byte a value)
+const uint8_t* prefill_w(const DevBuf& raw, const DevBuf& pq, int pre) {
+  return pre == PREFILL_PQ6 ? pq.as<uint8_t>() : raw.as<uint8_t>();
+}
+size_t prefill_row(size_t raw_row, int K, int pre) { return pre == PREFILL_PQ6 ? size_t(K) : raw_row; }
 
 int check_ready(const artlite_moe_layer* L) {
   for (int t = ARTLITE_ROUTER; t <= ARTLITE_DOWN_EXPS; t++)
@@ -195,8 +223,9 @@ PrefillProblem shared_down_part(const artlite_moe_layer* L, int64_t T, int j, in
   const int u0 = j * (units / n) + std::min(j, units % n), nu = units / n + (j < units % n ? 1 : 0);
   const int k0 = u0 * unit;
   PrefillProblem p{};
-  p.w[0] = L->sdown.as<uint8_t>() + size_t(k0 / L->sdq->per) * L->sdq->dev;
-  p.row_bytes = int(L->sdown_row);
+  const bool pq = L->pre_sd == PREFILL_PQ6;  // (the prefill layout: a byte a value)
+  p.w[0] = pq ? L->pq_sdown.as<uint8_t>() + k0 : L->sdown.as<uint8_t>() + size_t(k0 / L->sdq->per) * L->sdq->dev;
+  p.row_bytes = int(prefill_row(L->sdown_row, Ks, L->pre_sd));
   p.N = L->d.hidden;
   p.K = nu * unit;
   p.lda = Ks;
@@ -322,13 +351,13 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     // formats match, else run as launches of their own right after
     const bool sp = d.shared_ffn && path.shared_prefill;
     PrefillArgs gu{};
-    gu.qtype = d.gate_type;
+    prefill_format(L->gq, gu);
     gu.np = 1;
     PrefillProblem& g = gu.p[0];
-    g.w[0] = L->gate.as<uint8_t>();
-    g.w[1] = L->up.as<uint8_t>();
-    g.expert_bytes = int64_t(F) * L->gate_row;
-    g.row_bytes = int(L->gate_row);
+    g.w[0] = prefill_w(L->gate, L->pq_gate, L->pre_g);
+    g.w[1] = prefill_w(L->up, L->pq_up, L->pre_g);
+    g.row_bytes = int(prefill_row(L->gate_row, H, L->pre_g));
+    g.expert_bytes = int64_t(F) * g.row_bytes;
     g.N = F;
     g.K = H;
     g.lda = H;
@@ -343,11 +372,11 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     PrefillArgs sgu{};  // (the shared gate / up: in gu, or a launch of its own)
     if (sp) {
       PrefillArgs& into = shared_gu_merged(L) ? gu : sgu;
-      into.qtype = L->sq->id;
+      prefill_format(L->sq, into);
       PrefillProblem& q = into.p[into.np++];
-      q.w[0] = L->sgate.as<uint8_t>();
-      q.w[1] = L->sup.as<uint8_t>();
-      q.row_bytes = int(L->sgate_row);
+      q.w[0] = prefill_w(L->sgate, L->pq_sgate, L->pre_sg);
+      q.w[1] = prefill_w(L->sup, L->pq_sup, L->pre_sg);
+      q.row_bytes = int(prefill_row(L->sgate_row, H, L->pre_sg));
       q.N = d.shared_ffn;
       q.K = H;
       q.lda = H;
@@ -363,14 +392,14 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
       ART_TRY(launch_prefill(sgu, s));
     }
     PrefillArgs dn{};
-    dn.qtype = d.down_type;
+    prefill_format(L->dq, dn);
     dn.np = 1;
     PrefillProblem& q = dn.p[0];
     q = g;
-    q.w[0] = L->down.as<uint8_t>();
+    q.w[0] = prefill_w(L->down, L->pq_down, L->pre_d);
     q.w[1] = nullptr;
-    q.expert_bytes = int64_t(H) * L->down_row;
-    q.row_bytes = int(L->down_row);
+    q.row_bytes = int(prefill_row(L->down_row, F, L->pre_d));
+    q.expert_bytes = int64_t(H) * q.row_bytes;
     q.N = H;
     q.K = F;
     q.lda = F;
@@ -383,7 +412,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     if (sp) {
       const bool merged = shared_dn_merged(L);
       PrefillArgs& into = merged ? dn : sdn;
-      into.qtype = L->sdq->id;
+      prefill_format(L->sdq, into);
       const int n = shared_parts(L, merged);
       for (int j = 0; j < n; j++) into.p[into.np++] = shared_down_part(L, T, j, n);
       ys_parts = n;
@@ -560,16 +589,24 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
                gemv_supported(d.down_type, d.expert_ffn, d.hidden);
   // (the prefill tiles address weights and A rows by 32-bit offsets: every expert's bytes, every row of x16 and h16)
   const int64_t maxP = int64_t(d.max_tokens) * d.top_k;
-  L->prefill_ok = prefill_supported(d.gate_type, d.hidden, d.expert_ffn) &&
-                  prefill_supported(d.down_type, d.expert_ffn, d.hidden) &&
-                  prefill_fits(d.n_experts, int64_t(d.expert_ffn) * L->gate_row, d.max_tokens, d.hidden) &&
-                  prefill_fits(d.n_experts, int64_t(d.hidden) * L->down_row, maxP, d.expert_ffn);
+  L->pre_g = prefill_type(gq);
+  L->pre_d = prefill_type(dq);
+  L->prefill_ok = L->pre_g && L->pre_d && prefill_supported(L->pre_g, d.hidden, d.expert_ffn) &&
+                  prefill_supported(L->pre_d, d.expert_ffn, d.hidden) &&
+                  prefill_fits(d.n_experts, int64_t(d.expert_ffn) * prefill_row(L->gate_row, d.hidden, L->pre_g),
+                               d.max_tokens, d.hidden) &&
+                  prefill_fits(d.n_experts, int64_t(d.hidden) * prefill_row(L->down_row, d.expert_ffn, L->pre_d), maxP,
+                               d.expert_ffn);
   L->shared_gemv_ok = sq && gemv_supported(sq->id, d.hidden, d.shared_ffn) &&
                       gemv_supported(sdq->id, d.shared_ffn, d.hidden);
-  L->shared_prefill_ok = sq && prefill_supported(sq->id, d.hidden, d.shared_ffn) &&
-                         prefill_supported(sdq->id, d.shared_ffn, d.hidden) &&
-                         prefill_fits(1, int64_t(d.shared_ffn) * L->sgate_row, d.max_tokens, d.hidden) &&
-                         prefill_fits(1, int64_t(d.hidden) * L->sdown_row, d.max_tokens, d.shared_ffn);
+  L->pre_sg = prefill_type(sq);
+  L->pre_sd = prefill_type(sdq);
+  L->shared_prefill_ok = sq && L->pre_sg && L->pre_sd && prefill_supported(L->pre_sg, d.hidden, d.shared_ffn) &&
+                         prefill_supported(L->pre_sd, d.shared_ffn, d.hidden) &&
+                         prefill_fits(1, int64_t(d.shared_ffn) * prefill_row(L->sgate_row, d.hidden, L->pre_sg),
+                                      d.max_tokens, d.hidden) &&
+                         prefill_fits(1, int64_t(d.hidden) * prefill_row(L->sdown_row, d.shared_ffn, L->pre_sd),
+                                      d.max_tokens, d.shared_ffn);
   hipError_t e = hipGetDevice(&L->device);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&L->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
@@ -692,6 +729,37 @@ extern "C" int artlite_moe_layer_upload(artlite_moe_layer* L, int t, const void*
                                                                                  : int64_t(d.shared_ffn);
     ART_TRY(launch_weight_l1(static_cast<const uint8_t*>(b->p), q->id, rows, row, cols, L->wmax.as<float>() + 5 + wm,
                              L->stream));
+  }
+  // the prefill layout of a product the prefill tiles take in it (from the uploaded blocks)
+  {
+    const artlite_moe_desc& d = L->d;
+    DevBuf* pq = nullptr;
+    int pre = 0, K = 0;
+    int64_t rows = 0;
+    size_t row = 0;
+    switch (t) {
+      case ARTLITE_GATE_EXPS: pq = &L->pq_gate, pre = L->prefill_ok ? L->pre_g : 0; break;
+      case ARTLITE_UP_EXPS: pq = &L->pq_up, pre = L->prefill_ok ? L->pre_g : 0; break;
+      case ARTLITE_DOWN_EXPS: pq = &L->pq_down, pre = L->prefill_ok ? L->pre_d : 0; break;
+      case ARTLITE_GATE_SHEXP: pq = &L->pq_sgate, pre = L->shared_prefill_ok ? L->pre_sg : 0; break;
+      case ARTLITE_UP_SHEXP: pq = &L->pq_sup, pre = L->shared_prefill_ok ? L->pre_sg : 0; break;
+      case ARTLITE_DOWN_SHEXP: pq = &L->pq_sdown, pre = L->shared_prefill_ok ? L->pre_sd : 0; break;
+      default: break;
+    }
+    if (pre == PREFILL_PQ6) {
+      switch (t) {
+        case ARTLITE_GATE_EXPS:
+        case ARTLITE_UP_EXPS: rows = int64_t(d.n_experts) * d.expert_ffn, K = d.hidden, row = L->gate_row; break;
+        case ARTLITE_DOWN_EXPS: rows = int64_t(d.n_experts) * d.hidden, K = d.expert_ffn, row = L->down_row; break;
+        case ARTLITE_GATE_SHEXP:
+        case ARTLITE_UP_SHEXP: rows = d.shared_ffn, K = d.hidden, row = L->sgate_row; break;
+        default: rows = d.hidden, K = d.shared_ffn, row = L->sdown_row; break;
+      }
+      const size_t bytes = size_t(rows) * size_t(K);
+      ART_TRY(pq->reserve(bytes + WEIGHT_TAIL));
+      ART_HIP(hipMemsetAsync(pq->as<uint8_t>() + bytes, 0, WEIGHT_TAIL, L->stream));
+      ART_TRY(launch_pq6_pack(static_cast<const uint8_t*>(b->p), tq->id, rows, K, row, pq->as<uint8_t>(), L->stream));
+    }
   }
   ART_HIP(hipStreamSynchronize(L->stream));
   L->have[t] = true;

@@ -55,12 +55,16 @@ template <int QT>
 struct PG {
   // Q4_K: a stage is a quarter of a 256-value super-block (144 B: d, dmin, 12 bytes of 6-bit scales and mins, 128
   // code bytes); a row's stage bytes are its super-block's 16-byte header and the quarter's 32 code bytes, staged in
-  // two regions (the headers of the item's 256 rows, then their codes), each DMA instruction reading one of them
+  // two regions (the headers of the item's 256 rows, then their codes), each DMA instruction reading one of them.
+  // PQ6 (the prefill layout of the other block formats, PREFILL_PQ6): a stage is 64 bytes of a row, four 16-byte
+  // chunks (the scales, two of nibbles, one of crumbs), staged whole, each row's chunks swizzled by pq6_swz.
   static constexpr bool K4 = QT == ARTLITE_Q4_K;
+  static constexpr bool P6 = QT == PREFILL_PQ6;
+  static constexpr bool F32D = K4 || P6;                  // (weights decoded in fp32: pg_k4_word)
   static constexpr int GB = QT == ARTLITE_Q4_0 ? 18 : 34;  // bytes of a 32-value block (Q4_0, Q8_0)
   static constexpr int WN = 256;                          // weight rows staged per item
-  static constexpr int WROW = K4 ? 48 : 2 * GB;           // stage bytes of a staged weight row (two blocks)
-  static constexpr int WDW = WROW / 4;                    // its dwords (9 / 17 / 12)
+  static constexpr int WROW = K4 ? 48 : P6 ? 64 : 2 * GB;  // stage bytes of a staged weight row (two blocks)
+  static constexpr int WDW = WROW / 4;                    // its dwords (9 / 17 / 12 / 16)
   static constexpr int THREADS = 512;                     // 8 waves, two per SIMD
   static constexpr int ABYTES = TILE_ROWS * 128;          // a stage of A: 64 fp16 per row
   static constexpr int AI = ABYTES / 16 / THREADS;        // A DMAs (16 B) per lane per stage
@@ -69,10 +73,11 @@ struct PG {
   // of LDS (its last dword untouched), so a row takes 48 LDS bytes, piece k at 16 k: stage byte x at x + 4 (x / 12).
   // Else 4-byte pieces, the same count for every wave, a row's stage bytes packed.
   static constexpr bool X3 = QT == ARTLITE_Q4_0;
-  static constexpr int BI = X3 ? 2 : (WN * WDW + THREADS - 1) / THREADS;  // weight DMAs per lane per stage (at most)
+  // weight DMAs per lane per stage (at most; PQ6: 16-byte pieces, 4 a row, 2 per lane)
+  static constexpr int BI = X3 ? 2 : P6 ? WN * 4 / THREADS : (WN * WDW + THREADS - 1) / THREADS;
   static constexpr int WLDS = X3 ? 48 : WROW;             // LDS bytes of a staged weight row
   static constexpr int KHDR = WN * 16;                    // Q4_K: the header region's bytes (the codes follow)
-  static constexpr int WBYTES = X3 ? WN * WLDS : BI * THREADS * 4;  // (4-byte pieces: the last dwords padding)
+  static constexpr int WBYTES = X3 || P6 ? WN * WLDS : BI * THREADS * 4;  // (4-byte pieces: the last dwords padding)
   static constexpr int SBYTES = ABYTES + WBYTES;
   static constexpr int MI = 2;           // item metadata DMAs (4 B) per lane per stage
   static constexpr int META = MI * THREADS * 4;  // an item's metadata: 256 row tokens (int), 256 row factors (float2),
@@ -87,6 +92,7 @@ struct PG {
   static_assert(!X3 || (WROW == 36 && GB == 18 && WN * 3 == 12 * 64 && 128 * 3 % 64 == 0),
                 "Q4_0: 12 DMAs of 12-byte pieces");
   static_assert(!K4 || (BI == 6 && WN * WDW == BI * THREADS), "Q4_K: two header and four code DMAs, no padding");
+  static_assert(!P6 || (BI == 2 && WBYTES == WN * 64 && 128 * 4 == THREADS), "PQ6: a DMA of gate rows, one of up's");
   static_assert(LDS <= LDS_BYTES, "LDS");
   static_assert((R - 1) * LOADS < 64, "vmcnt");
 };
@@ -95,6 +101,11 @@ struct PG {
 // the 16 rows a lane group reads at once sit in distinct banks (12-dword rows repeat their bank every 16 rows, and the
 // plain products' lanes read rows r and r + 16 together)
 __device__ __forceinline__ int pg_x3_row(int r) { return r ^ (((r >> 4) & 1) << 2); }
+
+// PQ6: the LDS chunk of a staged row r's chunk c is c ^ pq6_swz(r) (rows 64 bytes apart repeat their banks every 4 rows:
+// the 16 rows a lane group reads, SwiGLU's consecutive ones or the plain products' runs of 4 rows 8 apart, take 4
+// different chunk orders within each set of rows that share banks)
+__device__ __forceinline__ int pq6_swz(int r) { return ((r >> 2) ^ (r >> 3)) & 3; }
 
 template <int N>
 __device__ __forceinline__ void pg_wait() {
@@ -311,6 +322,10 @@ struct PGSrc {
         const int q = (j < 2 ? j : j - 2) * L::THREADS + tid;
         row = j < 2 ? q >> 2 : q >> 3;
         dw = j < 2 ? q & 3 : q & 7;
+      } else if constexpr (L::P6) {  // (piece q: LDS row q / 4, LDS chunk q % 4, which holds the row's chunk q % 4 ^ swz)
+        const int q = j * L::THREADS + tid;
+        row = q >> 2;
+        dw = 4 * ((q & 3) ^ pq6_swz(row));
       } else if constexpr (L::X3) {  // (piece q: LDS row q / 3, its dwords 3 (q % 3) .. + 3; waves 4-7 have no second)
         const int q = min(j * L::THREADS + tid, L::WN * 3 - 1);
         row = pg_x3_row(q / 3);
@@ -397,13 +412,15 @@ __device__ __forceinline__ void pg_dma_n(int n, const PGIssue<QT, SWIGLU, MP>& i
     const uint8_t* base;
     if constexpr (L::K4)  // (headers: instruction 1 reads up's; codes: instructions 4, 5)
       base = j < 2 ? (SWIGLU && j == 1 ? b.wb1 : b.wb0) : (SWIGLU && j >= 4 ? b.wq1 : b.wq0);
-    else if constexpr (L::X3)  // (instructions 6 .. 11: up's rows; the wave's bases)
+    else if constexpr (L::X3 || L::P6)  // (X3: instructions 6 .. 11: up's rows, the wave's bases; P6: instruction 1)
       base = j == 0 ? b.wb0 : b.wb1;
     else
       base = SWIGLU && (j * L::THREADS + 64 * wv) >= 128 * L::WDW ? b.wb1 : b.wb0;
     if constexpr (L::X3) {
       if (j == 1 && wv >= 4) return;
       pg_dma<12>(base, is.src.w[j], b.dstw + (8 * j + wv) * 1024);
+    } else if constexpr (L::P6) {
+      pg_dma<16>(base, is.src.w[j], b.dstw + (8 * j + wv) * 1024);
     } else {
       pg_dma<4>(base, is.src.w[j], b.dstw + (8 * j + wv) * 256);
     }
@@ -421,23 +438,34 @@ __device__ __forceinline__ void pg_dma_n(int n, const PGIssue<QT, SWIGLU, MP>& i
 // their regions): SwiGLU gate rows 16 wv .. + 16 (column block 0) and the same rows of up (staged
 // at + 128); plain: of rows 32 wv .. + 32, MFMA row i of block nb is row 32 wv + 8 (i / 4) + 4 nb + i % 4, so that a
 // lane's outputs of the two blocks are 8 consecutive columns; cb its code bytes' offset in a block (Q4_K: in the
-// quarter's 32 bytes, 8 lg).
+// quarter's 32 bytes, 8 lg). PQ6: bof is the row's scale chunk (its chunk c at bof ^ 16 c: rows are 64-byte aligned),
+// and the launch's decode mode (pmode, poff: PrefillArgs) with the lane's half of a 32-value group (hi16).
 template <int QT>
 struct PGLane {
   uint32_t aof0, aof1, bof[2];
   int cb;
+  int pmode;
+  float poff;
+  bool hi16;
   PGDecode<QT> dec;
-  __device__ __forceinline__ PGLane(int lr, int lg, int wv, bool swiglu) : dec(lg) {
+  __device__ __forceinline__ PGLane(int lr, int lg, int wv, bool swiglu, int mode = 0, float off = 0.0f) : dec(lg) {
     const int sz = (lr >> 1) & 7;  // (the A rows' chunk swizzle, PGSrc::swz)
     aof0 = uint32_t(lr * 128 + ((0 + lg) ^ sz) * 16);
     aof1 = uint32_t(lr * 128 + ((4 + lg) ^ sz) * 16);
 #pragma unroll
     for (int nb = 0; nb < 2; nb++) {
       const int row = swiglu ? 128 * nb + 16 * wv + lr : 32 * wv + 8 * (lr >> 2) + 4 * nb + (lr & 3);
-      bof[nb] = PG<QT>::K4 ? uint32_t(row)
-                           : uint32_t(PG<QT>::ABYTES + (PG<QT>::X3 ? pg_x3_row(row) : row) * PG<QT>::WLDS);
+      if constexpr (PG<QT>::K4)
+        bof[nb] = uint32_t(row);
+      else if constexpr (PG<QT>::P6)
+        bof[nb] = uint32_t(PG<QT>::ABYTES + row * PG<QT>::WLDS + 16 * pq6_swz(row));
+      else
+        bof[nb] = uint32_t(PG<QT>::ABYTES + (PG<QT>::X3 ? pg_x3_row(row) : row) * PG<QT>::WLDS);
     }
     cb = QT == ARTLITE_Q4_0 ? 8 * (lg & 1) : 8 * lg;
+    pmode = mode;
+    poff = off;
+    hi16 = (lg & 2) != 0;
   }
 };
 
@@ -464,14 +492,23 @@ struct PGRaw {
 // The LDS reads of a step's weight codes from its slot s, all aligned dwords: per column block, group 0's from the lane
 // group's code byte offset cb (Q4_0: 8 (lg & 1), both nibbles of those 8 bytes; Q8_0: 8 lg) two bytes past the
 // block's scale (the row's first dword: the scale in its low half); group 1's from GB + 2 + cb (20 or 36), its scale
-// the high half of the dword at GB - 2. Q4_K: the header, the code dwords 2 lg, 2 lg + 1.
+// the high half of the dword at GB - 2. Q4_K: the header, the code dwords 2 lg, 2 lg + 1. PQ6: the scale chunk, each
+// group's nibble and crumb dwords.
 template <int QT>
 __device__ __forceinline__ void pg_read_codes(const uint8_t* s, const PGLane<QT>& ln, PGOps<QT>& o, PGRaw<QT>& r) {
   using L = PG<QT>;
   auto dw = [](const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); };
 #pragma unroll
   for (int nb = 0; nb < 2; nb++) {
-    if constexpr (L::K4) {
+    if constexpr (L::P6) {  // (the scales; group g's nibble dword: chunk 1 + g, dword lg; its crumbs: chunk 3, dword
+                            // 2 g + lg / 2)
+      const uint32_t hd = ln.bof[nb], nbx = hd + 4 * uint32_t(ln.cb >> 3), cr = hd + 4 * uint32_t(ln.cb >> 4);
+      r.h[nb] = *reinterpret_cast<const u32x4*>(s + hd);
+      r.d[0][nb] = dw(s + (nbx ^ 16u));
+      r.d[1][nb] = dw(s + (cr ^ 48u));
+      r.d[2][nb] = dw(s + (nbx ^ 32u));
+      r.sc0[nb] = dw(s + (cr ^ 48u) + 8);
+    } else if constexpr (L::K4) {
       r.h[nb] = *reinterpret_cast<const u32x4*>(s + L::ABYTES + ln.bof[nb] * 16);
       const uint8_t* c = s + L::ABYTES + L::KHDR + ln.bof[nb] * 32 + ln.cb;
       r.d[0][nb] = dw(c);
@@ -507,11 +544,50 @@ __device__ __forceinline__ u32x4 pg_read_a0(const uint8_t* s, const PGLane<QT>& 
   return *reinterpret_cast<const u32x4*>(s + o);
 }
 
+// PQ6: the lane's 8 codes of a group (values 8 lg .. + 8 of its 32) as two dwords of bytes, from its nibble dword n
+// (byte k: value k's low 4 bits, value k + 4's in the high nibble) and its crumb dword x (byte k: the high 2 bits of
+// lane group 2 m + 1's values k and k + 4 in bits 0-3, lane group 2 m's in bits 4-7); mode 2 (IQ4): the nibble is an
+// index of IQ4's table, whose value + 128 is the code (the offset 128 comes off in the decode)
+__device__ __forceinline__ void pq6_codes(uint32_t n, uint32_t x, bool odd, int mode, uint32_t& v0, uint32_t& v1) {
+  const uint32_t lo0 = n & 0x0F0F0F0Fu, lo1 = (n >> 4) & 0x0F0F0F0Fu;
+  if (mode == 2) {
+    v0 = iq4_int8(lo0) ^ 0x80808080u;
+    v1 = iq4_int8(lo1) ^ 0x80808080u;
+  } else {
+    const uint32_t y = odd ? x << 4 : x;
+    v0 = lo0 | (y & 0x30303030u);
+    v1 = lo1 | ((y >> 2) & 0x30303030u);
+  }
+}
+
+// PQ6: the scale s and the offset o of the lane's 8 values of group g (w = s c - o) from the row's scale chunk h: modes
+// 0, 2: per 16 values s = h[2 g + hi16], o = off s (exact: off a power of two); mode 1: per 32, (s, o) = (h[2 g],
+// h[2 g + 1])
+template <int QT>
+__device__ __forceinline__ void pq6_scale(const u32x4& h, int g, const PGLane<QT>& ln, float& s, float& o) {
+  const float a = __uint_as_float(h[2 * g]), b = __uint_as_float(h[2 * g + 1]);
+  if (ln.pmode == 1) {
+    s = a;
+    o = b;
+  } else {
+    s = ln.hi16 ? b : a;
+    o = s * ln.poff;
+  }
+}
+
 // The preparation of group 0's operand of column block nb from what was read (Q4_K: also group 1's codes, scale and
 // min into o; qi the stage's quarter of its super-block), and a word of an operand.
 template <int QT>
 __device__ __forceinline__ PGPrep pg_prep0(PGOps<QT>& o, const PGRaw<QT>& r, const PGLane<QT>& ln, int qi, int nb) {
-  if constexpr (PG<QT>::K4) {
+  if constexpr (PG<QT>::P6) {  // (group 1's codes, scale and offset into o)
+    const bool odd = (ln.cb >> 3) & 1;
+    pq6_codes(r.d[2][nb], r.sc0[nb], odd, ln.pmode, o.c10[nb], o.c11[nb]);
+    pq6_scale<QT>(r.h[nb], 1, ln, o.ks1[nb], o.ko1[nb]);
+    PGPrep p;
+    pq6_codes(r.d[0][nb], r.d[1][nb], odd, ln.pmode, p.v0, p.v1);
+    pq6_scale<QT>(r.h[nb], 0, ln, p.s, p.o);
+    return p;
+  } else if constexpr (PG<QT>::K4) {
     float ks[2], ko[2];
     pg_k4_scales(r.h[nb], qi, ks, ko);
     o.ks1[nb] = ks[1];
@@ -533,7 +609,7 @@ __device__ __forceinline__ PGPrep pg_prep0(PGOps<QT>& o, const PGRaw<QT>& r, con
 // the preparation of group 1's operand of column block nb (its codes read a step before)
 template <int QT>
 __device__ __forceinline__ PGPrep pg_prep1(const PGOps<QT>& o, const PGLane<QT>& ln, int nb) {
-  if constexpr (PG<QT>::K4) {
+  if constexpr (PG<QT>::F32D) {
     PGPrep p;
     p.v0 = o.c10[nb];
     p.v1 = o.c11[nb];
@@ -547,7 +623,7 @@ __device__ __forceinline__ PGPrep pg_prep1(const PGOps<QT>& o, const PGLane<QT>&
 
 template <int QT>
 __device__ __forceinline__ uint32_t pg_word(const PGPrep& p, const PGLane<QT>& ln, int j) {
-  if constexpr (PG<QT>::K4)
+  if constexpr (PG<QT>::F32D)
     return pg_k4_word(p, j);
   else
     return ln.dec.word(p, j);
@@ -607,6 +683,10 @@ __device__ __forceinline__ void pg_wbases(const uint8_t* w0, const uint8_t* w1, 
   using L = PG<QT>;
   if constexpr (L::X3) {  // (the wave's own: instruction 0's matrix, instruction 1's)
     b.wb0 = (SWIGLU && wv >= 6 ? w1 : w0) + sw * L::WROW;
+    b.wb1 = w1 + sw * L::WROW;
+    b.wq0 = b.wq1 = nullptr;
+  } else if constexpr (L::P6) {  // (instruction 0: rows 0 .. 127, gate's; 1: up's)
+    b.wb0 = w0 + sw * L::WROW;
     b.wb1 = w1 + sw * L::WROW;
     b.wq0 = b.wq1 = nullptr;
   } else if constexpr (L::K4) {
@@ -729,9 +809,9 @@ __device__ __forceinline__ void pg_step(const PrefillArgs& a, const PGCtx& c, PG
     // stage's group 1) and group 1's (the next stage's group 0)
     pg_for<10>([&](auto tc) __attribute__((always_inline)) {
       constexpr int t = decltype(tc)::value, nb = t / 5, k = t % 5;
-      // (Q4_K, whose decoded operands and group-1 state take more registers than what is read: a column block's 5
-      // tasks together, at the last iterations before the operand is used)
-      constexpr int ti1 = L::K4 ? MBN - 2 + nb : t * MBN / 10, ti0 = L::K4 ? IT - 2 + nb : MBN + t * MBN / 10;
+      // (Q4_K and PQ6, whose decoded operands and group-1 state take more registers than what is read: a column
+      // block's 5 tasks together, at the last iterations before the operand is used)
+      constexpr int ti1 = L::F32D ? MBN - 2 + nb : t * MBN / 10, ti0 = L::F32D ? IT - 2 + nb : MBN + t * MBN / 10;
       if constexpr (ti1 == it) {
         if constexpr (k == 0)
           p1[nb] = pg_prep1<QT>(ops, ln, nb);
@@ -958,7 +1038,7 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   }
   pg_wait_window<QT>(c.wv);
   pg_barrier();
-  const PGLane<QT> ln(c.lr, c.lg, c.wv, SWIGLU);
+  const PGLane<QT> ln(c.lr, c.lg, c.wv, SWIGLU, a.pq_mode, a.pq_off);
   PGOps<QT> ops;
   u32x4 av[4];
   {
@@ -1036,7 +1116,7 @@ bool prefill_supported(int qtype, int K, int N) {
   // stages - R, which must come at least two windows after that item's first step opened the first window carrying
   // the next item's metadata: stages - R >= 2)
   // (Q4_K: whole super-blocks)
-  return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0 || qtype == ARTLITE_Q4_K) &&
+  return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0 || qtype == ARTLITE_Q4_K || qtype == PREFILL_PQ6) &&
          K >= 64 * (PG<ARTLITE_Q4_0>::R + 2) && K % (qtype == ARTLITE_Q4_K ? 256 : 64) == 0 && K / 64 < 256 && N > 0 &&
          N % 16 == 0;
 }
@@ -1066,6 +1146,10 @@ int launch_prefill(const PrefillArgs& a, hipStream_t s) {
                 : (a.np > 1 ? launch_pgemm<QT, false, true>(a, s) : launch_pgemm<QT, false, false>(a, s))
   if (a.qtype == ARTLITE_Q4_0) ART_PG(ARTLITE_Q4_0);
   if (a.qtype == ARTLITE_Q4_K) ART_PG(ARTLITE_Q4_K);
+  if (a.qtype == PREFILL_PQ6) {
+    if (a.pq_mode < 0 || a.pq_mode > 2) return fail(ARTLITE_EINVAL, "prefill GEMM: PQ6 mode %d", a.pq_mode);
+    ART_PG(PREFILL_PQ6);
+  }
   ART_PG(ARTLITE_Q8_0);
 #undef ART_PG
 }

@@ -1,8 +1,9 @@
 """The headline benchmark: MoE-layer tokens/s of a Qwen3-30B-A3B-shaped Q4_0 layer (H 2048, 128 experts, top 8,
 SwiGLU F 768) on one MI355X, at decode (16 tokens: ``value``) and at a 4096-token prefill (``prefill``), plus the
-other BASELINE workloads (decode at 1, 4 and 64 tokens; the DeepSeek-V2-Lite-shaped Q4_K layer at 512 tokens; the
-Zipf-skewed Q8_0 layer at 2048 tokens), each with its dominant kernel's roofline fraction and the numpy CPU oracle
-timed on the host beside it.
+other BASELINE workloads (decode at 1, 4 and 64 tokens, and at 128, between decode and prefill sizes; the
+DeepSeek-V2-Lite-shaped Q4_K layer at 512 tokens; the Zipf-skewed Q8_0 layer at 2048 tokens) and the prefill shape
+with Q4_K gate / up and a Q6_K down (``q4km``, as Q4_K_M files hold it), each with its dominant kernel's roofline
+fraction and the numpy CPU oracle timed on the host beside it.
 
 One step = one layer forward (router, routing, dispatch, experts, combine) over one batch already resident in HBM.
 Decode steps cycle through ``--weight-sets`` distinct weight sets so the working set (~220 MB per call) streams from
@@ -34,6 +35,8 @@ SHAPES = {
     "deepseek": dict(H=2048, E=64, k=6, F=1408, gate="Q4_K", down="Q8_0", scale=2e-4, dmin=1.5e-3, shared_F=2816,
                      shared="Q4_K", router="normal"),
     "skewed": dict(H=2880, E=32, k=4, F=2880, gate="Q8_0", down="Q8_0", scale=0.01, router="zipf"),
+    # config 3's shape as Q4_K_M files quantise it (Q4_K gate / up, Q6_K down: the down through the prefill layout)
+    "q4km": dict(H=2048, E=128, k=8, F=768, gate="Q4_K", down="Q6_K", scale=2e-4, dmin=1.5e-3, router="uniform"),
 }
 ZIPF_S, ZIPF_ACTIVE, ZIPF_BETA = 1.2, 26, 0.7  # config 5: 26 experts ranked by Zipf s = 1.2, 6 never chosen
 
@@ -43,7 +46,7 @@ def log(msg: str) -> None:
 
 
 # (values per block, bytes per block, offsets of the fp16 fields: scale, then Q4_K's dmin)
-BLOCK = {"Q4_0": (32, 18, (0,)), "Q8_0": (32, 34, (0,)), "Q4_K": (256, 144, (0, 2))}
+BLOCK = {"Q4_0": (32, 18, (0,)), "Q8_0": (32, 34, (0,)), "Q4_K": (256, 144, (0, 2)), "Q6_K": (256, 210, (208,))}
 
 
 def bpw(qtype: str) -> float:
@@ -274,7 +277,7 @@ def main() -> None:
     assert device_count() > 0, "no GPU visible"
     shape = SHAPES["decode"]
     T = args.tokens
-    batches = [T] if args.no_extra else sorted({1, 4, T, 64})
+    batches = [T] if args.no_extra else sorted({1, 4, T, 64, 128})
     log(f"decode: T in {batches}, {args.weight_sets} weight sets")
     gls = build_layers(shape, args.weight_sets, max(batches))
     dec = {b: time_T(gls, shape, b, args.steps, args.warmup) for b in batches}
@@ -306,7 +309,7 @@ def main() -> None:
         g[0].close()
     extra = {}
     if not args.no_extra:
-        for name, Tx, sets in (("deepseek", 512, 2), ("skewed", 2048, 1)):
+        for name, Tx, sets in (("deepseek", 512, 2), ("skewed", 2048, 1), ("q4km", 4096, 1)):
             log(f"{name}: T={Tx}")
             sx = SHAPES[name]
             g = build_layers(sx, sets, Tx)

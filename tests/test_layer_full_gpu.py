@@ -102,6 +102,14 @@ def test_full_k4_rows() -> None:
     assert "prefill_x" in r["kernels"] and r["counts"].min() > 64
 
 
+def test_full_q4km_prefill() -> None:
+    """The Qwen3-30B-A3B shape as Q4_K_M files quantise it (Q4_K gate / up, Q6_K down) at 4096 tokens: gate / up on
+    the prefill tiles from the file's Q4_K bytes, the down on the prefill tiles through the prefill layout of its Q6_K
+    blocks (made at upload); every expert over 64 rows."""
+    r = run_full("q4km", 4096)
+    assert "prefill_x" in r["kernels"] and r["counts"].min() > 64 and r["counts"].sum() == 4096 * 8
+
+
 def test_full_decode_cfg2_t64() -> None:
     """Config 2 at its largest decode batch (64 tokens) with a second seed."""
     r = run_full("decode", 64, seed=7)

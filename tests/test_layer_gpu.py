@@ -25,7 +25,9 @@ CASES = [("cpu", 16), ("decode", 1), ("decode", 4), ("decode", 16), ("decode", 6
          ("deepseek", 64), ("skewed", 192), ("mix_q8k", 16), ("mix_k8", 24), ("mix_pf", 256), ("shared_pf", 256),
          ("kquants", 32),
          ("kquants", 160), ("iq4", 24), ("iq4", 96), ("kmix", 16), ("kmix", 64),
-         ("q5km", 16), ("q5k", 24), ("q6k", 24), ("mixtile", 16), ("iq4", 16), ("q41", 16), ("q3k", 16)]
+         ("q5km", 16), ("q5k", 24), ("q6k", 24), ("mixtile", 16), ("iq4", 16), ("q41", 16), ("q3k", 16),
+         # prefill-sized passes of the formats the prefill tiles read through the prefill layout
+         ("kmix", 160), ("q5km", 160), ("q5k", 160), ("q6k", 192), ("mixtile", 160), ("q3k", 160), ("q41", 160)]
 
 # Decode-sized passes (at most 4 pairs per expert on average, K a multiple of 256) take the GEMV over XQ activations:
 # int8 hi / lo planes per 32 values, |x - xq| <= max|x| / 65024 per group, so h (itself held in XQ) and the pair
@@ -49,6 +51,8 @@ def check_layer(name: str, T: int, seed: int = 0) -> None:
         if name in ("shared_pf", "mix_pf"):  # (the shared gate / up in the routed launch; the down too when alike)
             assert "shared_gate_up" not in g.kernel_names(), g.kernel_names()
             assert ("shared_down" in g.kernel_names()) == (name == "mix_pf"), g.kernel_names()
+        # (every block format has prefill tiles: a pass of 16 pairs per expert or more takes them)
+        assert prefill == (not gemv and T * spec.k >= 16 * spec.E), (name, T, g.kernel_names())
         tol = 1e-4 if gemv else 1e-3 if prefill else 1e-5
         lg = g.tap("logits")
         ids, w = g.tap("ids"), g.tap("weights")
