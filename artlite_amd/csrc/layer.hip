@@ -139,9 +139,11 @@ int check_ready(const artlite_moe_layer* L) {
 }
 
 // The kernels a forward pass of T tokens takes. Decode-sized passes (at most GEMV_BM pairs per expert on
-// average) run the experts on the VALU GEMV over XQ activations (it takes every block format); prefill-sized ones
-// (16 pairs per expert on average) on the fp16 MFMA prefill tiles; those between on the MFMA decode tiles over bf16
-// planes.
+// average) run the experts on the VALU GEMV over XQ activations (it takes every block format); larger ones on the
+// fp16 MFMA prefill tiles (every block format: Q4_0, Q8_0, Q4_K from the file's bytes, the others through the prefill
+// layout), and where those do not take a product's shape (K below 320 or not a multiple of 64) on the MFMA decode
+// tiles over bf16 planes. (At 128 tokens of config 2, 8 pairs per expert, the prefill tiles' tiles of 32 rows took
+// 208 us against 323 on the MFMA decode tiles: the decode tiles do twice the MFMA work on bf16 hi / lo planes.)
 struct Path {
   bool gemv;            // routed experts (gate / up and down) on the GEMV (XQ of x; tiles of GEMV_BM rows)
   bool shared_gemv;     // the shared expert on the GEMV
@@ -157,7 +159,7 @@ Path path_of(const artlite_moe_layer* L, int64_t T) {
   Path p{};
   p.gemv = L->gemv_ok && T * L->d.top_k <= int64_t(GEMV_BM) * L->d.n_experts;
   p.shared_gemv = L->d.shared_ffn && p.gemv && L->shared_gemv_ok;
-  p.prefill = !p.gemv && L->prefill_ok && T * L->d.top_k >= int64_t(16) * L->d.n_experts;
+  p.prefill = !p.gemv && L->prefill_ok;
   p.shared_prefill = L->d.shared_ffn && p.prefill && L->shared_prefill_ok && T >= 64;
   const bool planes = (!p.gemv && !p.prefill) || (L->d.shared_ffn && !p.shared_gemv && !p.shared_prefill);
   p.split = planes && (L->x_dtype == ARTLITE_X_F32 || L->d.norm_eps > 0);  // (the normalised x is fp32)

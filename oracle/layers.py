@@ -102,6 +102,10 @@ CONFIGS = {
     # test-only: Q4_1 throughout (d q + m blocks: the min term) with an IQ4_XS / IQ4_NL shared expert
     "q41": Spec("q41", H=1024, E=16, k=2, F=512, gate_type="Q4_1", down_type="Q4_1", scale=4e-3, shared_F=256,
                 shared_type="IQ4_XS", shared_down_type="IQ4_NL", shared_scale=5e-5, tokens=(16,)),
+    # test-only: an expert width of 256 (the down's K below the prefill tiles' 320), so that passes past the GEMV's
+    # sizes take the MFMA decode tiles
+    "dtiles": Spec("dtiles", H=1024, E=16, k=2, F=256, gate_type="Q4_K", down_type="Q6_K", scale=2e-4,
+                   dmin_scale=1.5e-3, tokens=(96,)),
     # the Qwen3-30B-A3B shape as Q4_K_M files quantise it (Q4_K gate / up, Q6_K down) at a 4096-token prefill: the
     # down on the prefill tiles through the prefill layout
     "q4km": Spec("q4km", H=2048, E=128, k=8, F=768, gate_type="Q4_K", down_type="Q6_K", scale=2e-4, dmin_scale=1.5e-3,

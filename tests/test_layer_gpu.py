@@ -27,13 +27,17 @@ CASES = [("cpu", 16), ("decode", 1), ("decode", 4), ("decode", 16), ("decode", 6
          ("kquants", 160), ("iq4", 24), ("iq4", 96), ("kmix", 16), ("kmix", 64),
          ("q5km", 16), ("q5k", 24), ("q6k", 24), ("mixtile", 16), ("iq4", 16), ("q41", 16), ("q3k", 16),
          # prefill-sized passes of the formats the prefill tiles read through the prefill layout
-         ("kmix", 160), ("q5km", 160), ("q5k", 160), ("q6k", 192), ("mixtile", 160), ("q3k", 160), ("q41", 160)]
+         ("kmix", 160), ("q5km", 160), ("q5k", 160), ("q6k", 192), ("mixtile", 160), ("q3k", 160), ("q41", 160),
+         # past the GEMV's sizes with a down the prefill tiles do not take (K = 256): the MFMA decode tiles
+         ("dtiles", 96)]
+# (passes on the MFMA decode tiles)
+DTILE_CASES = {("dtiles", 96)}
 
 # Decode-sized passes (at most 4 pairs per expert on average, K a multiple of 256) take the GEMV over XQ activations:
 # int8 hi / lo planes per 32 values, |x - xq| <= max|x| / 65024 per group, so h (itself held in XQ) and the pair
-# outputs carry a few 1e-5 of relative error; the MFMA decode tiles' bf16 hi / lo planes, about 2^-17. Prefill-sized
-# passes (16 pairs per expert on average) take fp16 products: weights d (q - 8) and h rounded once to fp16 (2^-11
-# relative at most), a few 1e-4 of relative error in h and the pair outputs.
+# outputs carry a few 1e-5 of relative error; the MFMA decode tiles' bf16 hi / lo planes, about 2^-17. Larger passes
+# take the prefill tiles' fp16 products: weights d (q - 8) and h rounded once to fp16 (2^-11 relative at most), a few
+# 1e-4 of relative error in h and the pair outputs.
 GEMV_CASES = {("cpu", 16), ("decode", 1), ("decode", 4), ("decode", 16), ("decode", 64), ("mix_q8k", 16), ("mix_k8", 24),
               ("kmix", 16), ("q5km", 16), ("q5k", 24), ("kquants", 32), ("q6k", 24), ("mixtile", 16), ("iq4", 16),
               ("q41", 16), ("q3k", 16)}
@@ -51,8 +55,8 @@ def check_layer(name: str, T: int, seed: int = 0) -> None:
         if name in ("shared_pf", "mix_pf"):  # (the shared gate / up in the routed launch; the down too when alike)
             assert "shared_gate_up" not in g.kernel_names(), g.kernel_names()
             assert ("shared_down" in g.kernel_names()) == (name == "mix_pf"), g.kernel_names()
-        # (every block format has prefill tiles: a pass of 16 pairs per expert or more takes them)
-        assert prefill == (not gemv and T * spec.k >= 16 * spec.E), (name, T, g.kernel_names())
+        # (every block format has prefill tiles: every pass past the GEMV's sizes takes them where they take its shapes)
+        assert prefill == (not gemv and (name, T) not in DTILE_CASES), (name, T, g.kernel_names())
         tol = 1e-4 if gemv else 1e-3 if prefill else 1e-5
         lg = g.tap("logits")
         ids, w = g.tap("ids"), g.tap("weights")
@@ -165,7 +169,7 @@ def test_layer_errors() -> None:
     g.close()
 
 
-@pytest.mark.parametrize(("name", "T"), [("decode", 16), ("mix_pf", 256), ("kquants", 32), ("q4_rows", 512)])
+@pytest.mark.parametrize(("name", "T"), [("decode", 16), ("mix_pf", 256), ("dtiles", 96), ("q4_rows", 512)])
 def test_layer_sigmoid_gating(name: str, T: int) -> None:
     """Sigmoid gating over the whole layer (the GEMV, the prefill tiles, the MFMA decode tiles) against the oracle's
     ``moe_route(gating="sigmoid")`` and the C++ host routing's sigmoid mode."""
