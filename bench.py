@@ -157,9 +157,10 @@ def work(shape: dict, T: int, U: float, pair_bytes: int, names: list) -> dict:
     return {"gate_up": (gu_b, gu_f), "down": (dn_b, dn_f), "layer": (layer_b, layer_f)}
 
 
-def traffic(path: Path) -> tuple[float | None, str | None]:
-    """(HBM bytes per launch, where from) of a counter summary under profiles/: its line ``traffic_bytes_per_launch:
-    N`` (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the copy calibration) and its ``commit:`` line."""
+def traffic(path: Path, kernel: str) -> tuple[float | None, str | None]:
+    """(HBM bytes per launch, where from) of a kernel in a counter summary under profiles/: its line
+    ``traffic_bytes_per_launch[kernel]: N`` (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the copy
+    calibration) and the summary's ``commit:`` line."""
     try:
         lines = path.read_text().splitlines()
     except OSError:
@@ -167,7 +168,7 @@ def traffic(path: Path) -> tuple[float | None, str | None]:
     val, commit = None, "?"
     for line in lines:
         s = line.strip().lstrip("-* ")
-        if s.startswith("traffic_bytes_per_launch:"):
+        if s.startswith(f"traffic_bytes_per_launch[{kernel}]:"):
             val = float(s.split(":", 1)[1])
         elif s.startswith("commit:"):
             commit = s.split(":", 1)[1].strip()
@@ -177,8 +178,13 @@ def traffic(path: Path) -> tuple[float | None, str | None]:
                  f"at commit {commit})")
 
 
-TRAFFIC = {("decode", "gate_up"): ROOT / "profiles" / "gemv_gate_up_decode_b16_traffic.md",
-           ("prefill", "gate_up"): ROOT / "profiles" / "prefill_gate_up_t4096_traffic.md"}
+# the counter summaries of the workloads profiled on their own (bench.py --only), by (workload, tokens)
+TRAFFIC = {("decode", 16): ROOT / "profiles" / "gemv_decode_b16_traffic.md",
+           ("decode", 128): ROOT / "profiles" / "pgemm_decode_t128_traffic.md",
+           ("prefill", 4096): ROOT / "profiles" / "pgemm_prefill_t4096_traffic.md",
+           ("deepseek", 512): ROOT / "profiles" / "pgemm_deepseek_t512_traffic.md",
+           ("skewed", 2048): ROOT / "profiles" / "pgemm_skewed_t2048_traffic.md",
+           ("q4km", 4096): ROOT / "profiles" / "pgemm_q4km_t4096_traffic.md"}
 
 
 def line(name: str, shape: dict, T: int, r: dict, steps: int) -> dict:
@@ -190,7 +196,7 @@ def line(name: str, shape: dict, T: int, r: dict, steps: int) -> dict:
     kern = max(("gate_up", "down"), key=lambda n: r["kernels"].get(n, 0.0))
     kms = r["kernels"].get(kern, float("nan"))
     kb, kf = w[kern]
-    tb, src = traffic(TRAFFIC[(name, kern)]) if (name, kern) in TRAFFIC else (None, None)
+    tb, src = traffic(TRAFFIC[(name, T)], kern) if (name, T) in TRAFFIC else (None, None)
     if mfma:
         ach = kf / (kms * 1e-3) / 1e12
         roof = {"bound": "mfma", "kernel": kern, "achieved": ach, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
@@ -266,6 +272,8 @@ def main() -> None:
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of each headline CPU baseline (0: none)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB (the calibration kernel of counter profiles)")
+    ap.add_argument("--only", choices=["decode", "prefill", "deepseek", "skewed", "q4km"],
+                    help="run one workload alone (decode at --tokens), for profiling; prints its line object")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU (asked for {args.gpus}); the path is single-GPU by design",
@@ -275,6 +283,24 @@ def main() -> None:
     from artlite_amd import device_count
 
     assert device_count() > 0, "no GPU visible"
+    if args.copy_probe:
+        from artlite_amd.moe.layer import hbm_copy_ms
+
+        log(f"copy probe: {args.copy_probe} MiB, {hbm_copy_ms(args.copy_probe << 20, 1):.3f} ms")
+    if args.only:
+        name = args.only
+        sx = SHAPES[name]
+        Tx = {"decode": args.tokens, "prefill": args.prefill_tokens, "deepseek": 512, "skewed": 2048,
+              "q4km": 4096}[name]
+        sets = args.weight_sets if name == "decode" else 2 if name == "deepseek" else 1
+        steps = args.steps if name == "decode" else args.prefill_steps
+        log(f"{name}: T={Tx}, {sets} weight set(s)")
+        g = build_layers(sx, sets, Tx)
+        obj = line(name, sx, Tx, time_T(g, sx, Tx, steps, args.warmup if name == "decode" else 2), steps)
+        for y in g:
+            y.close()
+        print(json.dumps({"workload": name, **obj}), flush=True)
+        return
     shape = SHAPES["decode"]
     T = args.tokens
     batches = [T] if args.no_extra else sorted({1, 4, T, 64, 128})
@@ -283,10 +309,6 @@ def main() -> None:
     dec = {b: time_T(gls, shape, b, args.steps, args.warmup) for b in batches}
     for g in gls:
         g.close()
-    if args.copy_probe:
-        from artlite_amd.moe.layer import hbm_copy_ms
-
-        log(f"copy probe: {args.copy_probe} MiB, {hbm_copy_ms(args.copy_probe << 20, 1):.3f} ms")
     head = line("decode", shape, T, dec[T], args.steps)
     out = {
         "metric": METRIC, "value": head["value"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
