@@ -639,11 +639,14 @@ struct Stream {
   }
 };
 
-// the wait and read of a step: vmcnt(n) (n at most NMAX), then the weights and (MX) the record chunks
+// the wait and read of a step: vmcnt(n), then the weights and (MX) the record chunks. n is at most NMAX (the stream's
+// counts: after a step's weights come the next step's (NI) and at most one K-unit's records); a larger n, which the
+// two-slot stream does not produce, would wait for every load (vmcnt(0)), never for fewer than needed
 template <int QT, bool SWIGLU, int MX>
 __device__ __forceinline__ void wait_read(const Stream<QT, SWIGLU>& st, int n, uint32_t sw, uint32_t sx,
                                           uint32_t (&w)[Unit<QT>::LW], u32x4 (&x)[GEMV_BM]) {
   using SS = Stream<QT, SWIGLU>;
+  if (n > SS::NMAX) n = 0;
   static_for<SS::NMAX + 1>([&](auto nc) {
     constexpr int N = decltype(nc)::value;
     if (n == N) read_unit<N, QT, MX>(w, x, sw + st.o_w, sw + st.o_r, sw + st.o_s, sx);
