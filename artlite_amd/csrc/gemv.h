@@ -3,6 +3,7 @@
 #pragma once
 
 #include "common.h"
+#include "route.h"
 
 namespace artlite {
 
@@ -39,7 +40,21 @@ struct GemvArgs {
   int64_t max_tiles;       // grid bound
   uint32_t* hq;            // SwiGLU: h = silu(gate) up as XQ rows (by sorted row)
   float* y;                // plain: fp32 rows (by sorted row), stride N
+  // (SwiGLU, optional) the routing done by the launch itself: when logits is given, every workgroup routes the T
+  // tokens' (T, E) logits in its LDS (gemv_route_fits) and takes its items from that; workgroup 0 also stores ids,
+  // weights and the dispatch (d: counts, offsets, order, slot, tiles, ctrl[CTRL_TILES]) for the launches after it.
+  // tiles, n_tiles, offsets and order above are then not read.
+  struct Route {
+    const float* logits = nullptr;
+    int T = 0, E = 0, k = 0, sigmoid = 0;
+    int32_t* ids = nullptr;
+    float* w32 = nullptr;
+    DispatchBufs d{};
+  } route;
 };
+
+// whether a SwiGLU GEMV launch can route T tokens of E experts, top k, itself (GemvArgs::route)
+bool gemv_route_fits(int64_t T, int E, int k);
 
 // whether the GEMV takes N rows of K values of weights of this type
 bool gemv_supported(int qtype, int K, int N);

@@ -505,24 +505,42 @@ __device__ __forceinline__ int snake_count(int w, int G, int n_items) {
   return full + (r && ((full & 1) ? w >= G - r : w < r));
 }
 
-// wave 0: items snake_item(it0, 0, G), ... (n of them) into tab, 64 at a time, lane j one item
+// A tile-list entry (tiles[2 t], tiles[2 t + 1]): the expert, with (lists in the GEMV's order, made by route_core)
+// the tile's rows above bit 24 (0: not given, then from the expert's end in offsets), and the first sorted row.
+__device__ __forceinline__ int tile_rows(int2 te, const int32_t* offsets) {
+  const int m = te.x >> 24;
+  return m ? m : min(GEMV_BM, offsets[(te.x & 0xFFFFFF) + 1] - te.y);
+}
+
+// (wave 0) the tile entry of item j of this workgroup (lane j), clamped into the list's bounds: loaded before the
+// tile count is known, so that both are one memory round trip (an entry past the count is not used)
+__device__ __forceinline__ int2 item_tile(const GemvArgs& a, const int32_t* tiles, int it0, int G, int NB, int j) {
+  if (!tiles) return make_int2(0, 0);
+  const int tile = min(snake_item(it0, j, G) / NB, int(a.max_tiles) - 1);
+  return make_int2(tiles[2 * tile], tiles[2 * tile + 1]);
+}
+
+// wave 0: items snake_item(it0, 0, G), ... (n of them) into tab, 64 at a time, lane j one item; the tile list,
+// offsets and order from tiles, offsets and order (the launch's arrays, or the workgroup's own routing in LDS); pre:
+// the entry of item lane of the first 64, already loaded (item_tile)
 __device__ __forceinline__ void fill_items(const GemvArgs& a, int it0, int G, int n, int NB, int rows, int4* tab,
-                                           int lane) {
+                                           int lane, const int32_t* tiles, const int32_t* offsets,
+                                           const int32_t* order, int2 pre) {
   for (int j0 = 0; j0 < n; j0 += 64) {
     const int j = j0 + lane;
     if (j < n) {
       const int it = snake_item(it0, j, G), tile = it / NB;
-      int e = 0, s0 = tile * GEMV_BM, end = a.dense_rows;
-      if (a.tiles) {
-        e = a.tiles[2 * tile];
-        s0 = a.tiles[2 * tile + 1];
-        end = a.offsets[e + 1];
+      int e = 0, s0 = tile * GEMV_BM, m = min(GEMV_BM, a.dense_rows - s0);
+      if (tiles) {
+        const int2 te = j0 ? make_int2(tiles[2 * tile], tiles[2 * tile + 1]) : pre;
+        e = te.x & 0xFFFFFF;
+        s0 = te.y;
+        m = tile_rows(te, offsets);
       }
-      const int m = min(GEMV_BM, end - s0);
       int ar[GEMV_BM];
 #pragma unroll
       for (int t = 0; t < GEMV_BM; t++)
-        ar[t] = a.a_gather ? a.order[min(s0 + min(t, m - 1), a.rows_total - 1)] / a.topk : s0 + min(t, m - 1);
+        ar[t] = a.a_gather ? order[min(s0 + min(t, m - 1), a.rows_total - 1)] / a.topk : s0 + min(t, m - 1);
       tab[2 * j] = make_int4(e, s0, m, (it - tile * NB) * rows);
       tab[2 * j + 1] = make_int4(ar[0], ar[1], ar[2], ar[3]);
     }
@@ -731,32 +749,78 @@ __global__ __launch_bounds__(Shape<SWIGLU>::THREADS) __attribute__((amdgpu_waves
   using SS = Stream<QT, SWIGLU>;
   constexpr int RB = W::RB, S = W::S, NM = SS::NM;
   const int rows = 16 * RB, NB = (a.N + rows - 1) / rows;
-  const int n_tiles = a.tiles ? *a.n_tiles : (a.dense_rows + GEMV_BM - 1) / GEMV_BM;
-  const int n_items = n_tiles * NB, G = gridDim.x;
-  if (int(blockIdx.x) >= n_items) return;
-  SS st(a);
   extern __shared__ u32x4 slab[];
+  int n_tiles;
+  bool routed = false;
+  if constexpr (SWIGLU) {
+    if (a.route.logits) {
+      // the routing in this workgroup's LDS, over the weight and record slots (no load into them is issued before
+      // the barrier after the item table); workgroup 0 also stores it for the launches after this one
+      const GemvArgs::Route& r = a.route;
+      auto& rl = *reinterpret_cast<RouteLds<W::THREADS>*>(slab);
+      int* ro = reinterpret_cast<int*>(&rl + 1);
+      RouteOut o;
+      o.tiles = ro;
+      o.order = ro + 2 * a.max_tiles;
+      o.offsets = o.order + r.T * r.k;
+      o.n_tiles = o.offsets + r.E + 1;
+      o.stage = reinterpret_cast<float*>(ro + (2 * a.max_tiles + r.T * r.k + r.E + 2 + 3) / 4 * 4);
+      const bool w0 = blockIdx.x == 0;
+      int32_t* ids = w0 ? r.ids : nullptr;
+      float* w32 = w0 ? r.w32 : nullptr;
+      if (r.E <= 64)
+        route_core<W::THREADS, 1, true>(r.logits, r.T, r.E, r.k, r.sigmoid, GEMV_BM, 0, ids, w32, r.d, w0, rl, o);
+      else if (r.E <= 128)
+        route_core<W::THREADS, 2, true>(r.logits, r.T, r.E, r.k, r.sigmoid, GEMV_BM, 0, ids, w32, r.d, w0, rl, o);
+      else if (r.E <= 256)
+        route_core<W::THREADS, 4, true>(r.logits, r.T, r.E, r.k, r.sigmoid, GEMV_BM, 0, ids, w32, r.d, w0, rl, o);
+      else
+        route_core<W::THREADS, 8, true>(r.logits, r.T, r.E, r.k, r.sigmoid, GEMV_BM, 0, ids, w32, r.d, w0, rl, o);
+      __syncthreads();
+      n_tiles = __builtin_amdgcn_readfirstlane(lds_read_i32(o.n_tiles));
+      routed = true;
+    }
+  }
+  const int G = gridDim.x, it0 = blockIdx.x;
+  // (not routed here: the workgroup's first 64 tile entries in flight with the tile count, in every wave: lane 0's
+  // gives each wave its first steps, wave 0's the table)
+  const int2 pre = routed ? make_int2(0, 0) : item_tile(a, a.tiles, it0, G, NB, threadIdx.x & 63);
+  if (!routed) n_tiles = a.tiles ? *a.n_tiles : (a.dense_rows + GEMV_BM - 1) / GEMV_BM;
+  const int n_items = n_tiles * NB;
+  if (it0 >= n_items) return;
+  SS st(a);
   // [buffer][wave][matrix][row of A][row], after every wave's slots
   float* red = reinterpret_cast<float*>(slab + W::WAVES * (WSLOTS * SS::WCH + SS::XCH));
 
-  const int it0 = blockIdx.x, n_my = snake_count(it0, G, n_items);
+  const int n_my = snake_count(it0, G, n_items);
   constexpr int RED = W::WAVES * NM * GEMV_BM * 16;  // floats of one partial-sum buffer
   int* ctr = reinterpret_cast<int*>(red + (S > 1 ? RED_BUFS * RED : 0));  // [b]: arrivals, [4 + b]: epilogues done
   int4* tab = reinterpret_cast<int4*>(ctr + (S > 1 ? 8 : 0));
-  // the first item's first LA steps, its expert from a scalar load, ahead of the table
-  if (st.NVw > 0) {
-    const int e0 = a.tiles ? a.tiles[2 * (it0 / NB)] : 0, n00 = (it0 % NB) * rows;
+  // the first item's first LA steps (its expert from a scalar load) ahead of the table; routed here: after it
+  auto first_steps = [&](int e0) {
+    const int n00 = (it0 % NB) * rows;
     for (int v = 0; v < SS::LA; v++) {
       if (NM == 1 || v % NM == 0)
         st.template issue_w<0>(true, e0, n00, v, v);
       else
         st.template issue_w<NM - 1>(true, e0, n00, v, v);
     }
+  };
+  if (!routed && st.NVw > 0) first_steps(__builtin_amdgcn_readfirstlane(pre.x) & 0xFFFFFF);
+  if (st.wv == 0) {
+    if (routed) {  // (the workgroup's own copies, from the LDS address itself: read as LDS)
+      const int* ro = reinterpret_cast<const int*>(slab) + sizeof(RouteLds<W::THREADS>) / 4;
+      const int* ord = ro + 2 * a.max_tiles;
+      fill_items(a, it0, G, n_my, NB, rows, tab, st.lane, ro, ord + a.rows_total, ord,
+                 item_tile(a, ro, it0, G, NB, st.lane));
+    } else {
+      fill_items(a, it0, G, n_my, NB, rows, tab, st.lane, a.tiles, a.offsets, a.order, pre);
+    }
   }
-  if (st.wv == 0) fill_items(a, it0, G, n_my, NB, rows, tab, st.lane);
   if (S > 1 && threadIdx.x < 8) ctr[threadIdx.x] = 0;
   __syncthreads();
   Item cur = get_item(tab, 0), nxt = cur;
+  if (routed && st.NVw > 0) first_steps(cur.e);
   if (st.NVw > 0) st.load_x(cur, st.u0);
   int gs = 0;
   for (int j = 0; j < n_my; j++) {
@@ -866,12 +930,30 @@ int launch_t(const GemvArgs& a, hipStream_t s) {
   const unsigned grid = unsigned(std::min<int64_t>(items, resident));
   const size_t lds = lds0 + size_t((items + grid - 1) / grid) * 32;
   if (lds > lds_max) return fail(ARTLITE_EINVAL, "expert GEMV: %lld work items", (long long)items);
+  if (SWIGLU && a.route.logits) {
+    // the routing's LDS (scratch, then the tile list, order, offsets and tile count) within the slots
+    const GemvArgs::Route& r = a.route;
+    const size_t need = sizeof(RouteLds<W::THREADS>) + 4 * (size_t(2 * a.max_tiles + r.T * r.k + r.E + 2 + 3) / 4 * 4) +
+                        4 * size_t(r.T) * r.E;
+    const size_t slots = size_t(W::WAVES) * (WSLOTS * 16 * Unit<QT>::BYTES + GEMV_BM * 1024);
+    if (!gemv_route_fits(r.T, r.E, r.k) || need > slots || a.rows_total != r.T * r.k || a.topk != r.k ||
+        a.max_tiles != tile_bound(int64_t(r.T) * r.k, r.E, GEMV_BM))
+      return fail(ARTLITE_EINVAL, "expert GEMV: routing of %d tokens, %d experts, top %d in the launch", r.T, r.E,
+                  r.k);
+  }
   k_gemv<QT, SWIGLU><<<grid, W::THREADS, lds, s>>>(a);
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
 }
 
 }  // namespace
+
+// (the LDS it takes, at the most these allow: RouteLds<512>, 9.2 KB of tile list, order and offsets, 32 KB of staged
+// logits; within the weight and record slots of every format, Q3_K's 61.4 KB the least)
+bool gemv_route_fits(int64_t T, int E, int k) {
+  return T >= 1 && k >= 1 && k <= MAX_TOPK && k <= E && E <= Shape<true>::THREADS && E % 4 == 0 &&
+         T * k <= Shape<true>::THREADS && T * E <= 8192;
+}
 
 bool gemv_supported(int qtype, int K, int N) {
   return (qtype == ARTLITE_Q4_0 || qtype == ARTLITE_Q8_0 || qtype == ARTLITE_Q4_K || qtype == ARTLITE_Q5_K ||

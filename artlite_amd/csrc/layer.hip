@@ -34,7 +34,6 @@ struct artlite_moe_layer {
   DevBuf rpart;  // the router's fp64 partial sums (K split over workgroups), router_part_elems doubles
   size_t rpart_elems = 0;
   DevBuf table, ctrl, counts, offsets, order, slot, tiles;
-  DevBuf gtick;  // the one-launch routing's tickets per token group (GTICK_STRIDE ints apart)
   DevBuf hhi, hlo, ypairs, shhi, shlo, ys, y;
   DevBuf h16, sh16;  // the prefill's h (fp16, scaled per token)
   // the prefill tiles' weights of the formats they do not read from the file's bytes: the prefill layout (experts.h,
@@ -151,8 +150,9 @@ struct Path {
   bool shared_prefill;  // the shared expert on the prefill tiles
   bool split;           // bf16 hi / lo planes of fp32 x needed (the MFMA decode tiles)
   bool quant;           // XQ of x needed (made by the router's launch)
-  bool small;           // top k and dispatch in one workgroup
-  bool fused_route;     // ... in the router's launch (its last expert workgroup)
+  bool few_router;      // the router's launch of few tokens: a workgroup per expert and 16 tokens (and XQ of x)
+  bool gemv_route;      // top k and dispatch in the gate / up GEMV's launch (each workgroup in its LDS)
+  bool small;           // ... else in one workgroup of a launch of their own
 };
 
 Path path_of(const artlite_moe_layer* L, int64_t T) {
@@ -164,8 +164,9 @@ Path path_of(const artlite_moe_layer* L, int64_t T) {
   const bool planes = (!p.gemv && !p.prefill) || (L->d.shared_ffn && !p.shared_gemv && !p.shared_prefill);
   p.split = planes && (L->x_dtype == ARTLITE_X_F32 || L->d.norm_eps > 0);  // (the normalised x is fp32)
   p.quant = p.gemv;
-  p.small = p.gemv && T * L->d.top_k <= DISPATCH_BLOCK && L->d.n_experts <= MAX_EXPERTS;
-  p.fused_route = p.small && router_route_fits(T, L->d.hidden, L->d.n_experts, L->d.top_k);
+  p.few_router = p.gemv && router_few_fits(T, L->d.hidden, L->d.n_experts);
+  p.gemv_route = p.few_router && gemv_route_fits(T, L->d.n_experts, L->d.top_k);
+  p.small = p.gemv && !p.gemv_route && T * L->d.top_k <= DISPATCH_BLOCK && L->d.n_experts <= MAX_EXPERTS;
   return p;
 }
 
@@ -181,12 +182,9 @@ std::vector<std::string> kernel_list(const artlite_moe_layer* L, int64_t T) {
   if (L->d.norm_eps > 0) k.push_back("rmsnorm");
   if (p.prefill) k.push_back("prefill_x");
   if (p.split) k.push_back("split");
-  if (p.fused_route)
-    k.push_back("router_quant_route");
-  else
-    k.push_back(p.quant ? "router_quant" : "router");
+  k.push_back(p.quant ? "router_quant" : "router");
   if (L->d.shared_ffn && L->d.shared_gated) k.push_back("shared_gate");
-  if (p.fused_route) {
+  if (p.gemv_route) {
   } else if (p.small) {
     k.push_back("route");
   } else {
@@ -285,12 +283,10 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     db.row_out[0] = L->gu_row.as<float2>();
     db.row_out[1] = L->dn_row.as<float2>();
   }
-  if (path.fused_route) db.gtick = L->gtick.as<int32_t>();
   ART_TRY(mark());
-  if (path.fused_route)
-    ART_TRY(launch_router_route(xin, xdt, L->router.as<float>(), H, E, T, L->logits.as<float>(),
-                                path.quant ? L->xq.as<uint32_t>() : nullptr, k, d.gating, L->ids.as<int32_t>(),
-                                L->w.as<float>(), db, s));
+  if (path.few_router)
+    ART_TRY(launch_router_few(xin, xdt, L->router.as<float>(), H, E, T, L->logits.as<float>(),
+                                path.quant ? L->xq.as<uint32_t>() : nullptr, s));
   else
     ART_TRY(launch_router(xin, xdt, L->router.as<float>(), H, E, T, L->logits.as<float>(), E,
                           path.quant ? L->xq.as<uint32_t>() : nullptr, L->rpart.as<double>(), L->rpart_elems, s));
@@ -298,7 +294,7 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     ART_TRY(mark());
     ART_TRY(launch_router(xin, xdt, L->sinp.as<float>(), H, 1, T, L->sg.as<float>(), 1, nullptr, nullptr, 0, s));
   }
-  if (path.fused_route) {
+  if (path.gemv_route) {
   } else if (path.small) {
     ART_TRY(mark());
     ART_TRY(launch_route_small(L->logits.as<float>(), T, E, k, d.gating, L->ids.as<int32_t>(), L->w.as<float>(), db,
@@ -332,9 +328,20 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     g.offsets = L->offsets.as<int32_t>();
     g.max_tiles = tile_bound(P, E, BM);
     g.hq = L->hq.as<uint32_t>();
+    if (path.gemv_route) {
+      g.route.logits = L->logits.as<float>();
+      g.route.T = int(T);
+      g.route.E = E;
+      g.route.k = k;
+      g.route.sigmoid = d.gating;
+      g.route.ids = L->ids.as<int32_t>();
+      g.route.w32 = L->w.as<float>();
+      g.route.d = db;
+    }
     ART_TRY(mark());
     ART_TRY(launch_gemv(g, s));
     GemvArgs dn = g;
+    dn.route = GemvArgs::Route{};
     dn.w[0] = L->down.as<uint8_t>();
     dn.w[1] = nullptr;
     dn.expert_bytes = int64_t(H) * L->down_row;
@@ -638,7 +645,6 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
   res(L->order, size_t(P) * 4);
   res(L->slot, size_t(P) * 4);
   res(L->tiles, size_t(2 * tile_bound(P, int(E), 1)) * 4);
-  res(L->gtick, size_t(ROUTER_GROUPS) * GTICK_STRIDE * 4);
   res(L->hhi, size_t(P * F) * 2);
   res(L->hlo, size_t(P * F) * 2);
   res(L->ypairs, size_t(P * H) * 4);
@@ -668,8 +674,7 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
     res(L->shlo, size_t(T) * d.shared_ffn * 2);
     res(L->ys, size_t(T * H) * 4 * (L->shared_prefill_ok ? PREFILL_MAXP : 1));  // (prefill: the down's K parts)
   }
-  if (rc == ARTLITE_OK && (hipMemset(L->ctrl.p, 0, CTRL_WORDS * 4) != hipSuccess ||
-                           hipMemset(L->gtick.p, 0, size_t(ROUTER_GROUPS) * GTICK_STRIDE * 4) != hipSuccess))
+  if (rc == ARTLITE_OK && hipMemset(L->ctrl.p, 0, CTRL_WORDS * 4) != hipSuccess)
     rc = fail(ARTLITE_EHIP, "moe layer: memset");
   if (rc != ARTLITE_OK) {
     artlite_moe_layer_destroy(L);

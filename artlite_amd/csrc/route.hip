@@ -516,179 +516,27 @@ int launch_router(const void* x, int x_dtype, const float* W, int H, int E, int6
 // ---- small batches: the top k of every token, then the stable counting sort of the pairs, in one workgroup
 // (the results of k_topk, k_count and k_scatter for a single block of pairs)
 
-// a workgroup barrier over LDS alone: global stores issued before it are not waited for (nothing in the workgroup
-// reads them back)
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-// a wave's inclusive prefix sum by DPP (row shifts within 16-lane rows, then the row broadcasts of lanes 15 and 31):
-// x + the values of 1, 2, 3 lanes back, then 4 back in lanes 4..15 of a row, 8 back in lanes 8..15, lane 15's in
-// rows 1 and 3, lane 31's in rows 2 and 3 (a disabled or out-of-row source adds 0)
-__device__ __forceinline__ int wave_scan_dpp(int a) {
-  int x = a + __builtin_amdgcn_update_dpp(0, a, 0x111, 0xF, 0xF, false);  // row_shr:1
-  x += __builtin_amdgcn_update_dpp(0, a, 0x112, 0xF, 0xF, false);         // row_shr:2
-  x += __builtin_amdgcn_update_dpp(0, a, 0x113, 0xF, 0xF, false);         // row_shr:3
-  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xE, false);         // row_shr:4, banks 1-3
-  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xC, false);         // row_shr:8, banks 2-3
-  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);         // row_bcast:15, rows 1 and 3
-  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);         // row_bcast:31, rows 2 and 3
-  return x;
-}
-
-// exclusive prefixes of S values per thread of a DISPATCH_BLOCK workgroup (ex), and their sums (tot, every thread):
-// wave scans, the waves' sums scanned by wave 0; two LDS barriers (ws: S x NW ints of LDS, free again only after a
-// further barrier)
-template <int S>
-__device__ __forceinline__ void block_scan_n(const int (&v)[S], int (&ex)[S], int (&tot)[S], int (*ws)[DISPATCH_BLOCK / WAVE]) {
-  constexpr int NW = DISPATCH_BLOCK / WAVE;
-  const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE;
-  int x[S];
-#pragma unroll
-  for (int j = 0; j < S; j++) x[j] = wave_scan_dpp(v[j]);
-  if (lane == WAVE - 1)
-#pragma unroll
-    for (int j = 0; j < S; j++) ws[j][wv] = x[j];
-  lds_barrier();
-  if (wv == 0) {
-#pragma unroll
-    for (int j = 0; j < S; j++) {
-      const int y = wave_scan_dpp(lane < NW ? ws[j][lane] : 0);
-      if (lane < NW) ws[j][lane] = y;  // (inclusive over waves)
-    }
-  }
-  lds_barrier();
-#pragma unroll
-  for (int j = 0; j < S; j++) {
-    ex[j] = (wv ? ws[j][wv - 1] : 0) + x[j] - v[j];
-    tot[j] = ws[j][NW - 1];
-  }
-}
-
-// The routing of n tokens' (n, E) logits by one DISPATCH_BLOCK workgroup: top k (a wave per token), then the counts,
-// offsets, the tile list and each pair's sorted position. Every exchange is through LDS, so no barrier waits for the
-// global stores.
-// IDS_SET: the top-k is already done (the ids at device scope in ids, written by other workgroups of the launch);
-// only the dispatch is left.
-template <int R, bool COHERENT, bool IDS_SET = false>
-__device__ __forceinline__ void route_block(const float* __restrict__ logits, int64_t n, int E, int k, int sigmoid,
-                                            int32_t* __restrict__ ids, float* __restrict__ w32, const DispatchBufs& d) {
-  constexpr int NW = DISPATCH_BLOCK / WAVE;
-  __shared__ double ev[NW][WAVE];
-  __shared__ double sum[NW];
-  __shared__ int sid[DISPATCH_BLOCK];
-  __shared__ int base[MAX_EXPERTS];
-  __shared__ __align__(16) uint16_t wcnt[NW][MAX_EXPERTS];
-  __shared__ int ws[3][NW];
-  const int tid = threadIdx.x, lane = tid & (WAVE - 1), wv = tid / WAVE;
-  for (int e = tid; e < E; e += DISPATCH_BLOCK) base[e] = 0;
-  static_assert(MAX_EXPERTS % 8 == 0, "wcnt rows in 16-byte pieces");
-  for (int i = tid; i < NW * MAX_EXPERTS / 8; i += DISPATCH_BLOCK)
-    reinterpret_cast<uint4*>(&wcnt[0][0])[i] = uint4{0, 0, 0, 0};
-  if constexpr (IDS_SET) {
-    if (tid < n * k) sid[tid] = __hip_atomic_load(ids + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  } else {
-    for (int64_t t = wv; t < n; t += NW) {  // (one wave per token)
-      const int id = topk_wave<R, COHERENT>(logits + t * E, E, 0, E, k, sigmoid, ev[wv], &sum[wv], lane, ids + t * k,
-                                            w32 + t * k, nullptr);
-      if (lane < k) sid[t * k + lane] = id;
-    }
-  }
-  lds_barrier();
-  const int P = int(n) * k, p = tid;
-  const bool valid = p < P;
-  const int id = valid ? sid[p] : -1;
-  if (valid) atomicAdd(&base[id], 1);  // (counts: order-free)
-  // each pair's rank among the earlier pairs of its expert: the lanes of its wave with the same expert (ballots over
-  // the id bits), then the earlier waves' counts (read once every wave has written its own)
-  uint64_t peers = __ballot(valid);
-  for (int bit = 0; (1 << bit) < E; bit++) {
-    const bool set = (id >> bit) & 1;
-    const uint64_t b = __ballot(set);
-    peers &= set ? b : ~b;
-  }
-  const uint64_t below = (uint64_t(1) << lane) - 1;
-  int rank = __popcll(peers & below);
-  if (valid && !(peers & below)) wcnt[wv][id] = uint16_t(__popcll(peers));
-  lds_barrier();
-  // the prefixes: the expert's count (low 16 bits) and its tiles of the expert GEMMs (high 16 bits; both sums stay
-  // below 2^16: at most DISPATCH_BLOCK pairs); for the GEMV's tile order, its full tiles and its last tile's class
-  const int e = tid;
-  const int c = e < E ? base[e] : 0;
-  const int rows = d.balanced ? balanced_rows(c, d.BM) : d.BM;
-  const int nt = e < E && d.BM > 0 ? (c + rows - 1) / rows : 0;
-  const bool gemv_order = d.BM > 0 && !d.balanced && d.BM <= 4;
-  const int full = gemv_order && e < E ? c / rows : 0, rem = gemv_order && e < E ? c % rows : 0;
-  // (11-bit class fields: a class holds at most MAX_EXPERTS tiles; the last field's prefix stays below 2^10 and its
-  // total, which may reach 2^10 and carry out of the word, is not read)
-  const int v[3] = {c | (nt << 16), full, (rem == 3) | (rem == 2) << 11 | (rem == 1) << 22};
-  int ex[3], tot[3];
-  block_scan_n<3>(v, ex, tot, ws);
-  const int packed = ex[0], packed_total = tot[0];
-  const int start = packed & 0xFFFF, total = packed_total & 0xFFFF;
-  if (e < E) {
-    d.counts[e] = c;
-    d.offsets[e] = start;
-    base[e] = start;
-  }
-  if (e == 0) d.offsets[E] = total;
-  if (d.BM > 0 && !gemv_order) {  // the expert GEMMs' tiles: experts ascending, BM sorted rows each
-    const int t0 = packed >> 16;
-    for (int m = 0; m < nt; m++) {
-      d.tiles[2 * (t0 + m)] = e;
-      d.tiles[2 * (t0 + m) + 1] = start + m * rows;
-    }
-  } else if (gemv_order) {
-    // the GEMV's tiles by rows, most first: every expert's full tiles of BM rows, then the last tiles of BM - 1
-    // rows, ..., of 1 row (experts ascending within each class), so that a persistent launch dealing its items back
-    // and forth hands each workgroup items of about equal total rows
-    const int pf = ex[1], nfull = tot[1];
-    for (int m = 0; m < full; m++) {
-      d.tiles[2 * (pf + m)] = e;
-      d.tiles[2 * (pf + m) + 1] = start + m * rows;
-    }
-    if (rem) {  // (class base: the full tiles, then the classes of more rows)
-      const uint32_t up = uint32_t(ex[2]), ut = uint32_t(tot[2]);
-      const int n3 = int(ut & 0x7FF), n2 = int((ut >> 11) & 0x7FF);
-      const int t = nfull + (rem == 3 ? int(up & 0x7FF) : rem == 2 ? n3 + int((up >> 11) & 0x7FF) : n3 + n2 + int(up >> 22));
-      d.tiles[2 * t] = e;
-      d.tiles[2 * t + 1] = start + full * rows;
-    }
-  }
-  if (d.BM > 0 && e == 0) d.ctrl[CTRL_TILES] = packed_total >> 16;
-  lds_barrier();  // (base now holds each expert's start)
-  if (!valid) return;
-#pragma unroll
-  for (int w = 0; w < NW; w++)  // (all the reads in flight at once)
-    if (w < wv) rank += wcnt[w][id];
-  const int dest = base[id] + rank;
-  d.order[dest] = p;
-  d.slot[p] = dest;
-}
-
 template <int R>
 __global__ __launch_bounds__(DISPATCH_BLOCK) void k_route_small(const float* __restrict__ logits, int64_t n, int E,
                                                                 int k, int sigmoid, int32_t* __restrict__ ids,
                                                                 float* __restrict__ w32, DispatchBufs d) {
-  route_block<R, false>(logits, n, E, k, sigmoid, ids, w32, d);
+  __shared__ RouteLds<DISPATCH_BLOCK> lds;
+  route_core<DISPATCH_BLOCK, R>(logits, int(n), E, k, sigmoid, d.BM, d.balanced, ids, w32, d, true, lds, RouteOut{});
 }
 
-// Router logits and routing of small batches in one launch (T <= ROUTER_GROUPS ROUTER_TG tokens, H a multiple of
-// 256, T k <= DISPATCH_BLOCK pairs). A workgroup per expert and group of ROUTER_TG tokens (workgroup b: expert b % E,
-// tokens ROUTER_TG (b / E) ..): its NW waves each take H / NW values of K (lane: values 2 lane + 128 j of the wave's
-// slice), x read straight from memory (L2), float64 products; a wave's 16 token sums by halving exchanges, then the
-// waves' sums added in wave order, rounded once to fp32. One token group: the last of these workgroups to store its
-// logits (a ticket in ctrl, reset by that workgroup) routes them all (route_block). More (d.gtick given): the last
-// workgroup of each group (a ticket per group, in lines of their own) takes the top k of the group's tokens, a wave
-// per token, and stores the ids at device scope; the last group to do so (the ticket in ctrl) dispatches all the
-// pairs. Workgroups past them quantise x into XQ, a wave per unit.
-template <int XT, int R>
-__global__ __launch_bounds__(DISPATCH_BLOCK) void k_router_route(const void* __restrict__ xv,
+// Router logits of small batches (T <= ROUTER_GROUPS ROUTER_TG tokens, H a multiple of 256, at least 2 values a
+// wave). A workgroup per expert and group of ROUTER_TG tokens (workgroup b: expert b % E, tokens ROUTER_TG (b / E)
+// ..): its NW waves each take H / NW values of K (lane: values 2 lane + 128 j of the wave's slice), x read straight
+// from memory (L2), float64 products; a wave's 16 token sums by halving exchanges, then the waves' sums added in wave
+// order, rounded once to fp32. Workgroups past them quantise x into XQ, a wave per unit. (Whatever reads the logits
+// runs in a later launch: the launch boundary publishes them.)
+template <int XT>
+__global__ __launch_bounds__(DISPATCH_BLOCK) void k_router_few(const void* __restrict__ xv,
                                                                  const float* __restrict__ W, int H, int E, int64_t T,
-                                                                 float* __restrict__ logits, uint32_t* __restrict__ xq,
-                                                                 int k, int sigmoid, int32_t* __restrict__ ids,
-                                                                 float* __restrict__ w32, DispatchBufs d) {
+                                                                 float* __restrict__ logits,
+                                                                 uint32_t* __restrict__ xq) {
   constexpr int NW = DISPATCH_BLOCK / WAVE;
   __shared__ double part[NW][ROUTER_TG];
-  __shared__ int last;
   const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE;
   const int G = int((T + ROUTER_TG - 1) / ROUTER_TG);  // (token groups)
   if (int(blockIdx.x) >= E * G) {  // XQ of x
@@ -697,7 +545,6 @@ __global__ __launch_bounds__(DISPATCH_BLOCK) void k_router_route(const void* __r
     return;
   }
   const int e = int(blockIdx.x) % E, gi = int(blockIdx.x) / E, t0 = gi * ROUTER_TG, nt = min(ROUTER_TG, int(T) - t0);
-  const bool groups = G > 1 && d.gtick;
   const int q = H / NW;
   const float* wr = W + int64_t(e) * H + wv * q;
   double acc[ROUTER_TG];
@@ -735,50 +582,12 @@ __global__ __launch_bounds__(DISPATCH_BLOCK) void k_router_route(const void* __r
   const double v = token_sums(acc, lane);
   if ((lane & 3) == 0) part[wv][sum_token(lane)] = v;
   lds_barrier();
-  // wave 0 stores the expert's logits at device scope (past the workgroup's L2, which other chiplets' workgroups do
-  // not read), waits until they are acknowledged, then takes a ticket; the workgroup holding the last one reads the
-  // logits at device scope too, so no fence has to write back or drop a whole L2
-  if (wv == 0) {
-    if (lane < nt) {
-      double sum = part[0][lane];
+  if (wv == 0 && lane < nt) {
+    double sum = part[0][lane];
 #pragma unroll
-      for (int w = 1; w < NW; w++) sum += part[w][lane];
-      __hip_atomic_store(logits + int64_t(t0 + lane) * E + e, float(sum), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (lane == 0)
-      last = groups ? __hip_atomic_fetch_add(d.gtick + gi * GTICK_STRIDE, 1, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT) == E - 1
-                    : __hip_atomic_fetch_add(d.ctrl + CTRL_ROUTED, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                          E * G - 1;
+    for (int w = 1; w < NW; w++) sum += part[w][lane];
+    logits[int64_t(t0 + lane) * E + e] = float(sum);
   }
-  lds_barrier();
-  if (!last) return;
-  if (!groups) {
-    if (threadIdx.x == 0)  // (ready for the next launch)
-      __hip_atomic_store(d.ctrl + CTRL_ROUTED, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    route_block<R, true>(logits, T, E, k, sigmoid, ids, w32, d);
-    return;
-  }
-  // the group's top k (the ids at device scope, for the workgroup that dispatches), then the ticket across groups
-  if (threadIdx.x == 0) __hip_atomic_store(d.gtick + gi * GTICK_STRIDE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  {
-    __shared__ double ev[NW][WAVE];
-    __shared__ double sum[NW];
-    if (wv < nt) {
-      const int64_t t = t0 + wv;
-      topk_wave<R, true, true>(logits + t * E, E, 0, E, k, sigmoid, ev[wv], &sum[wv], lane, ids + t * k, w32 + t * k,
-                               nullptr);
-    }
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  lds_barrier();
-  if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(d.ctrl + CTRL_ROUTED, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1;
-  lds_barrier();
-  if (!last) return;
-  if (threadIdx.x == 0) __hip_atomic_store(d.ctrl + CTRL_ROUTED, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  route_block<R, true, true>(logits, T, E, k, sigmoid, ids, w32, d);
 }
 
 int launch_route_small(const float* logits, int64_t n, int E, int k, int sigmoid, int32_t* ids, float* w32,
@@ -802,38 +611,22 @@ int launch_route_small(const float* logits, int64_t n, int E, int k, int sigmoid
   return ARTLITE_OK;
 }
 
-bool router_route_fits(int64_t T, int H, int E, int k) {
-  return T >= 1 && T <= ROUTER_GROUPS * ROUTER_TG && H % 256 == 0 && H / (DISPATCH_BLOCK / WAVE) >= 2 && T * k <= DISPATCH_BLOCK &&
+bool router_few_fits(int64_t T, int H, int E) {
+  return T >= 1 && T <= ROUTER_GROUPS * ROUTER_TG && H % 256 == 0 && H / (DISPATCH_BLOCK / WAVE) >= 2 &&
          E <= MAX_EXPERTS;
 }
 
-int launch_router_route(const void* x, int x_dtype, const float* W, int H, int E, int64_t T, float* logits,
-                        uint32_t* xq, int k, int sigmoid, int32_t* ids, float* w32, const DispatchBufs& d,
-                        hipStream_t s) {
-  if (!router_route_fits(T, H, E, k))
-    return fail(ARTLITE_EINVAL, "router_route: %lld tokens, H %d, %d experts, k %d", (long long)T, H, E, k);
+int launch_router_few(const void* x, int x_dtype, const float* W, int H, int E, int64_t T, float* logits,
+                        uint32_t* xq, hipStream_t s) {
+  if (!router_few_fits(T, H, E))
+    return fail(ARTLITE_EINVAL, "router_few: %lld tokens, H %d, %d experts", (long long)T, H, E);
   constexpr int NW = DISPATCH_BLOCK / WAVE;
   const int nq = xq ? int((T * (H / 256) + NW - 1) / NW) : 0;
   const dim3 g(unsigned(E * ((T + ROUTER_TG - 1) / ROUTER_TG) + nq)), b(DISPATCH_BLOCK);
-#define ART_RR(XT, RR) k_router_route<XT, RR><<<g, b, 0, s>>>(x, W, H, E, T, logits, xq, k, sigmoid, ids, w32, d)
-#define ART_RR_R(XT)   \
-  if (E <= 64)         \
-    ART_RR(XT, 1);     \
-  else if (E <= 128)   \
-    ART_RR(XT, 2);     \
-  else if (E <= 256)   \
-    ART_RR(XT, 4);     \
-  else if (E <= 512)   \
-    ART_RR(XT, 8);     \
-  else                 \
-    ART_RR(XT, 16);
-  if (x_dtype == ARTLITE_X_F32) {
-    ART_RR_R(ARTLITE_X_F32)
-  } else {
-    ART_RR_R(ARTLITE_X_BF16)
-  }
-#undef ART_RR_R
-#undef ART_RR
+  if (x_dtype == ARTLITE_X_F32)
+    k_router_few<ARTLITE_X_F32><<<g, b, 0, s>>>(x, W, H, E, T, logits, xq);
+  else
+    k_router_few<ARTLITE_X_BF16><<<g, b, 0, s>>>(x, W, H, E, T, logits, xq);
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
 }

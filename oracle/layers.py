@@ -106,6 +106,10 @@ CONFIGS = {
     # sizes take the MFMA decode tiles
     "dtiles": Spec("dtiles", H=1024, E=16, k=2, F=256, gate_type="Q4_K", down_type="Q6_K", scale=2e-4,
                    dmin_scale=1.5e-3, tokens=(96,)),
+    # test-only: top 16 of 160 experts, so that 33 to 40 decode tokens (more pairs than a GEMV workgroup routes) take
+    # the routing launch of their own
+    "widek": Spec("widek", H=512, E=160, k=16, F=256, gate_type="Q4_0", down_type="Q4_0", scale=0.02,
+                  tokens=(16, 40)),
     # the Qwen3-30B-A3B shape as Q4_K_M files quantise it (Q4_K gate / up, Q6_K down) at a 4096-token prefill: the
     # down on the prefill tiles through the prefill layout
     "q4km": Spec("q4km", H=2048, E=128, k=8, F=768, gate_type="Q4_K", down_type="Q6_K", scale=2e-4, dmin_scale=1.5e-3,

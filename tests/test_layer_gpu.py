@@ -29,7 +29,9 @@ CASES = [("cpu", 16), ("decode", 1), ("decode", 4), ("decode", 16), ("decode", 6
          # prefill-sized passes of the formats the prefill tiles read through the prefill layout
          ("kmix", 160), ("q5km", 160), ("q5k", 160), ("q6k", 192), ("mixtile", 160), ("q3k", 160), ("q41", 160),
          # past the GEMV's sizes with a down the prefill tiles do not take (K = 256): the MFMA decode tiles
-         ("dtiles", 96)]
+         ("dtiles", 96),
+         # the decode routing in a launch of its own (more pairs than a GEMV workgroup routes), and in the GEMV's
+         ("widek", 40), ("widek", 16)]
 # (passes on the MFMA decode tiles)
 DTILE_CASES = {("dtiles", 96)}
 
@@ -40,7 +42,7 @@ DTILE_CASES = {("dtiles", 96)}
 # 1e-4 of relative error in h and the pair outputs.
 GEMV_CASES = {("cpu", 16), ("decode", 1), ("decode", 4), ("decode", 16), ("decode", 64), ("mix_q8k", 16), ("mix_k8", 24),
               ("kmix", 16), ("q5km", 16), ("q5k", 24), ("kquants", 32), ("q6k", 24), ("mixtile", 16), ("iq4", 16),
-              ("q41", 16), ("q3k", 16)}
+              ("q41", 16), ("q3k", 16), ("widek", 40), ("widek", 16)}
 
 
 def check_layer(name: str, T: int, seed: int = 0) -> None:
@@ -127,19 +129,24 @@ def test_layer_token_counts() -> None:
             assert rel_l2(y, layers.forward_f64(layer, x, ids, w)) < 1e-3
 
 
-def test_decode_routing_repeat() -> None:
-    """The one-launch decode routing (router workgroups per expert and group of 16 tokens, then the last to finish
-    routes) several times in a row, token counts changing between calls (one to four token groups): its ticket
-    counter must be back at zero after every launch. Each call's routing and dispatch equal the host restatement's,
-    and a repeated input gives bitwise the same output."""
-    spec = layers.CONFIGS["decode"]
+@pytest.mark.parametrize(("name", "counts", "in_gemv"), [("decode", (16, 1, 64, 7, 40, 16, 64, 7), True),
+                                                         ("widek", (40, 16, 33, 40), None)])
+def test_decode_routing_repeat(name: str, counts: tuple, in_gemv: bool | None) -> None:
+    """The decode routing several times in a row, token counts changing between calls (one to four router token
+    groups): the few-token router's logits, then the top k and dispatch in every workgroup of the gate / up GEMV's
+    launch (workgroup 0 storing them), or, past the pairs a GEMV workgroup routes (``widek``: top 16 of 160 experts,
+    more than 512 pairs at 40 tokens), in a one-workgroup launch of their own. Each call's routing and dispatch equal
+    the host restatement's, and a repeated input gives bitwise the same output."""
+    spec = layers.CONFIGS[name]
     layer = layers.make_layer(spec, 5)
     outs = {}
-    with gpu_layer(layer, max_tokens=64) as g:
-        for T in (16, 1, 64, 7, 40, 16, 64, 7):
+    with gpu_layer(layer, max_tokens=max(counts)) as g:
+        for T in counts:
             x = layers.make_x(spec, T, T)
             y = g(gpu_input(spec, x))
-            assert "router_quant_route" in g.kernel_names(), g.kernel_names()
+            names = g.kernel_names()
+            assert "router_quant" in names, names
+            assert ("route" not in names) == (in_gemv if in_gemv is not None else T * spec.k <= 512), (T, names)
             lg, ids, w = g.tap("logits"), g.tap("ids"), g.tap("weights")
             assert ulp_diff(lg, layers.logits(layer, x)).max() <= 1
             hids, hw = layers.route_host(layer, lg)
