@@ -521,8 +521,9 @@ __device__ __forceinline__ int2 item_tile(const GemvArgs& a, const int32_t* tile
 }
 
 // wave 0: items snake_item(it0, 0, G), ... (n of them) into tab, 64 at a time, lane j one item; the tile list,
-// offsets and order from tiles, offsets and order (the launch's arrays, or the workgroup's own routing in LDS); pre:
-// the entry of item lane of the first 64, already loaded (item_tile)
+// offsets and order from tiles, offsets and order (the launch's arrays, or the workgroup's own routing in LDS, whose
+// order holds the pairs' tokens: TOK); pre: the entry of item lane of the first 64, already loaded (item_tile)
+template <bool TOK = false>
 __device__ __forceinline__ void fill_items(const GemvArgs& a, int it0, int G, int n, int NB, int rows, int4* tab,
                                            int lane, const int32_t* tiles, const int32_t* offsets,
                                            const int32_t* order, int2 pre) {
@@ -540,7 +541,12 @@ __device__ __forceinline__ void fill_items(const GemvArgs& a, int it0, int G, in
       int ar[GEMV_BM];
 #pragma unroll
       for (int t = 0; t < GEMV_BM; t++)
-        ar[t] = a.a_gather ? order[min(s0 + min(t, m - 1), a.rows_total - 1)] / a.topk : s0 + min(t, m - 1);
+        if (a.a_gather) {
+          const int o = order[min(s0 + min(t, m - 1), a.rows_total - 1)];
+          ar[t] = TOK ? o : o / a.topk;
+        } else {
+          ar[t] = s0 + min(t, m - 1);
+        }
       tab[2 * j] = make_int4(e, s0, m, (it - tile * NB) * rows);
       tab[2 * j + 1] = make_int4(ar[0], ar[1], ar[2], ar[3]);
     }
@@ -811,8 +817,8 @@ __global__ __launch_bounds__(Shape<SWIGLU>::THREADS) __attribute__((amdgpu_waves
     if (routed) {  // (the workgroup's own copies, from the LDS address itself: read as LDS)
       const int* ro = reinterpret_cast<const int*>(slab) + sizeof(RouteLds<W::THREADS>) / 4;
       const int* ord = ro + 2 * a.max_tiles;
-      fill_items(a, it0, G, n_my, NB, rows, tab, st.lane, ro, ord + a.rows_total, ord,
-                 item_tile(a, ro, it0, G, NB, st.lane));
+      fill_items<true>(a, it0, G, n_my, NB, rows, tab, st.lane, ro, ord + a.rows_total, ord,
+                       item_tile(a, ro, it0, G, NB, st.lane));
     } else {
       fill_items(a, it0, G, n_my, NB, rows, tab, st.lane, a.tiles, a.offsets, a.order, pre);
     }

@@ -359,7 +359,8 @@ struct RouteLds {
 };
 
 // route_core's outputs into memory of the workgroup's own (LDS), each optional: the tile list (2 ints a tile), the
-// sorted order (P), the expert offsets (E + 1) and the tile count (1); and (route_core's STAGE) room for the n E
+// sorted pairs' tokens (P: order / k, the rows of A a gate / up tile reads), the expert offsets (E + 1) and the tile
+// count (1); and (route_core's STAGE) room for the n E
 // logits, which are then copied there first, all loads in flight at once, rather than read a token at a time by its
 // wave
 struct RouteOut {
@@ -531,7 +532,7 @@ __device__ __forceinline__ void route_core(const float* __restrict__ logits, int
       g.order[dest] = p;
       g.slot[p] = dest;
     }
-    if (o.order) o.order[dest] = p;
+    if (o.order) o.order[dest] = p / k;
   }
 }
 
