@@ -164,42 +164,60 @@ __device__ __forceinline__ uint32_t group_min_u32(uint32_t v) {
   return v;
 }
 
+// A lane's RR keys sorted in descending order in place, by a sorting network (RR = 1, 2, 4, 8; 8: Batcher's odd-even
+// merge sort, 19 compare-exchanges)
+template <int RR>
+__device__ __forceinline__ void sort_desc(uint64_t (&k)[RR]) {
+  auto cx = [&](int i, int j) {
+    const uint64_t a = k[i], b = k[j];
+    k[i] = b > a ? b : a;
+    k[j] = b > a ? a : b;
+  };
+  if constexpr (RR == 2) {
+    cx(0, 1);
+  } else if constexpr (RR == 4) {
+    cx(0, 1), cx(2, 3), cx(0, 2), cx(1, 3), cx(1, 2);
+  } else if constexpr (RR == 8) {
+    cx(0, 1), cx(2, 3), cx(4, 5), cx(6, 7), cx(0, 2), cx(1, 3), cx(4, 6), cx(5, 7), cx(1, 2), cx(5, 6);
+    cx(0, 4), cx(1, 5), cx(2, 6), cx(3, 7), cx(2, 4), cx(3, 5), cx(1, 2), cx(3, 4), cx(5, 6);
+  } else {
+    static_assert(RR == 1, "keys per lane: 1, 2, 4 or 8");
+  }
+}
+
 // The top k of 64 / W tokens' logits at once, one group of W lanes each (E <= W RR experts, k <= W): lane c of a
-// group holds experts W r + c (r < RR) of its token's logits p as their ordered bits (0 once taken), then k rounds
-// of: the group's largest ordered bits among the experts not yet taken (a group maximum), the lowest id holding them
-// (a group minimum of each lane's first such id), the lane holding it dropping it, lane j of the group keeping the
-// j-th. The same choice, in the same order, as topk_wave (larger logits first, equal logits to the lower id), with
-// the groups' rounds side by side. on: the group has a token. Lane j < k of a group gets its id (the return value)
-// and the logit's ordered bits (key); other lanes get -1.
+// group holds experts W r + c (r < RR) of its token's logits p as logit_key's keys (ordered bits above ~id; 0 for
+// none), sorted in descending order within the lane, then k rounds of: the group's largest ordered bits among the
+// lanes' first keys (a group maximum), the largest ~id among the first keys holding them (a second group maximum:
+// the lowest id), the lane holding that key dropping it from its list, lane j of the group keeping the j-th. A lane's
+// first key is its best one left, so the round takes the best key left in the group: the same choice, in the same
+// order, as topk_wave (larger logits first, equal logits to the lower id), with the groups' rounds side by side. on:
+// the group has a token. Lane j < k of a group gets its id (the return value) and the logit's ordered bits (key);
+// other lanes get -1.
 template <int W, int RR>
 __device__ __forceinline__ int topk_rows(const float* __restrict__ p, int E, int k, bool on, int c, uint32_t& key) {
-  static_assert(RR <= 8, "keys per lane");
   float l[RR];
 #pragma unroll
   for (int r = 0; r < RR; r++) l[r] = p[min(W * r + c, E - 1)];  // (every load issued before any is used)
-  uint32_t ordl[RR];  // (the ordered bits while live, else 0)
-  bool live[RR];
+  uint64_t kk[RR];
 #pragma unroll
   for (int r = 0; r < RR; r++) {
     const int e = W * r + c;
-    live[r] = on && e < E;
-    ordl[r] = live[r] ? uint32_t(logit_key(l[r], e) >> 32) : 0;
+    kk[r] = on && e < E ? logit_key(l[r], e) : 0;  // (a real key's low half, ~id, is never 0)
   }
+  sort_desc<RR>(kk);
   int mine = -1;
   uint32_t mkey = 0;
   for (int j = 0; j < k; j++) {
-    uint32_t m = ordl[0];
+    const uint32_t hi = uint32_t(kk[0] >> 32), lo = uint32_t(kk[0]);
+    const uint32_t m = group_max_u32<W>(hi);
+    const uint32_t cl = group_max_u32<W>(hi == m ? lo : 0u);
+    if (hi == m && lo == cl) {  // (the one lane holding the round's key: the ids, hence ~ids, are distinct)
 #pragma unroll
-    for (int r = 1; r < RR; r++) m = max(m, ordl[r]);
-    m = group_max_u32<W>(m);
-    uint32_t cand = 0xFFFFFFFFu;  // (the lane's lowest live expert holding m: the first r)
-#pragma unroll
-    for (int r = RR - 1; r >= 0; r--) cand = live[r] && ordl[r] == m ? uint32_t(W * r + c) : cand;
-    cand = group_min_u32<W>(cand);
-#pragma unroll
-    for (int r = 0; r < RR; r++)
-      if (uint32_t(W * r + c) == cand) live[r] = false, ordl[r] = 0;
-    if (c == j) mine = int(cand), mkey = m;
+      for (int r = 0; r + 1 < RR; r++) kk[r] = kk[r + 1];
+      kk[RR - 1] = 0;
+    }
+    if (c == j) mine = int(~cl), mkey = m;
   }
   key = mkey;
   return on && c < k ? mine : -1;
