@@ -127,10 +127,11 @@ __device__ __forceinline__ float4 lds_read_f4(const void* p) {
   return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
 }
 
-// After vmcnt(N), the lane's dwords of a unit (at pw; Q4_K / Q5_K: header, Q5_K high bits, at pw, its run at pr) and (MX > 0) its record
-// chunk of each of MX rows of A (at px, 1024 bytes apart), and their completion, in one asm block: the compiler
-// would otherwise wait for every load in flight before reading LDS (it takes the slots' global_load_lds writes for
-// possible producers), and it must not touch the outputs before the final wait.
+// The lane's dwords of a unit (at pw; Q4_K / Q5_K: header, Q5_K high bits, at pw, its run at pr) and (MX > 0) its
+// record chunk of each of MX rows of A (at px, 1024 bytes apart), and their completion, in one asm block, after the
+// step's wait (wait_vm, an asm block of its own just before it): the compiler would otherwise wait for every load in
+// flight before reading LDS (it takes the slots' global_load_lds writes for possible producers), and it must not
+// touch the outputs before the final wait.
 #define ART_R2(I, J) "ds_read2_b32 %[w" #I "], %[pw] offset0:" #J " offset1:" #J "+1\n\t"
 #define ART_R1(I, J) "ds_read_b32 %[w" #I "], %[pw] offset:" #J "*4\n\t"
 #define ART_OW2(I) [w##I] "=&v"(w2[I])
@@ -185,20 +186,25 @@ __device__ __forceinline__ float4 lds_read_f4(const void* p) {
 #define ART_OX2 ART_OX1, [x1] "=&v"(x[1])
 #define ART_OX3 ART_OX2, [x2] "=&v"(x[2])
 #define ART_OX4 ART_OX3, [x3] "=&v"(x[3])
-#define ART_READ(WN, MN)                                                                       \
-  asm volatile("s_waitcnt vmcnt(%[n])\n\t" ART_W##WN ART_X##MN "s_waitcnt lgkmcnt(0)"       \
-               : ART_OW##WN ART_OX##MN                                                          \
-               : [pw] "v"(pw), [pr] "v"(pr), [ps] "v"(ps), [px] "v"(px), [n] "i"(N))
+#define ART_READ(WN, MN)                                                 \
+  asm volatile(ART_W##WN ART_X##MN "s_waitcnt lgkmcnt(0)"                \
+               : ART_OW##WN ART_OX##MN                                    \
+               : [pw] "v"(pw), [pr] "v"(pr), [ps] "v"(ps), [px] "v"(px) \
+               : "memory")
 #define ART_READ_M(WN)                   \
   if constexpr (MX == 0) ART_READ(WN, 0); \
   if constexpr (MX == 1) ART_READ(WN, 1); \
   if constexpr (MX == 2) ART_READ(WN, 2); \
   if constexpr (MX == 3) ART_READ(WN, 3); \
   if constexpr (MX == 4) ART_READ(WN, 4);
-template <int N, int QT, int MX>
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "i"(N) : "memory");
+}
+template <int QT, int MX>
 __device__ __forceinline__ void read_unit(uint32_t (&w)[Unit<QT>::LW], u32x4 (&x)[GEMV_BM], uint32_t pw, uint32_t pr,
                                           uint32_t ps, uint32_t px) {
-  static_assert(N >= 0 && N < 64, "vmcnt");
   constexpr int LW = Unit<QT>::LW;
   if constexpr (LW == 12) {
     u32x4 w4[3];
@@ -471,19 +477,20 @@ struct Shape {
   static_assert(!SWIGLU || (RB % 2 == 0 && 8 * RB / 2 * GEMV_BM <= 64), "SwiGLU epilogue lanes");
 };
 
-// LDS of a workgroup: each wave's WSLOTS slots of 16 rows x BYTES and its record slot (GEMV_BM chunk rows of 1 KB;
+// LDS of a workgroup: each wave's D slots of 16 rows x BYTES and its record slot (GEMV_BM chunk rows of 1 KB;
 // one: the next K-unit's are loaded once the current ones are read, and more slots measured no faster while they
 // cost Q6_K's plain products a workgroup per CU), then (S > 1) RED_BUFS buffers of the K-ranges' partial sums and
 // their counters (then the item table, sized at launch)
 constexpr int RED_BUFS = 2;
-// Weight slots per wave: two, one step in flight behind the one being read. The stream's counts are written for this
-// depth only: each wait names at most NMAX loads issued after the one it needs, and a slot is refilled right after
-// the step that read it (deeper queues measured no faster: with the record loads they cost workgroups per CU).
+// Weight slots per wave (the streams' D): two, one step in flight behind the one being read. Each wait names the
+// loads issued after the one it needs (at most NMAX: LA = D - 1 steps' weights and LA + 1 K-units' records), and a
+// slot is refilled right after the step that read it. Deeper queues measured no faster: with many items they cost
+// workgroups per CU, and with one item per workgroup (4 slots, one token) gate / up took 17.9 µs against 15.1.
 constexpr int WSLOTS = 2;
-template <int QT, bool SWIGLU>
+template <int QT, bool SWIGLU, int D>
 constexpr size_t gemv_lds() {
   using W = Shape<SWIGLU>;
-  return size_t(W::WAVES) * (WSLOTS * 16 * Unit<QT>::BYTES + GEMV_BM * 1024) +
+  return size_t(W::WAVES) * (D * 16 * Unit<QT>::BYTES + GEMV_BM * 1024) +
          (W::S > 1 ? size_t(RED_BUFS) * W::WAVES * (SWIGLU ? 2 : 1) * GEMV_BM * 16 * 4 + 32 : 0);
 }
 
@@ -576,16 +583,16 @@ __device__ __forceinline__ float row4_sum(float s) {
 }
 
 // The state of a wave's stream of steps over its items (one step: 16 rows x one K-unit of one matrix). Every load
-// of the stream is a DMA into LDS (the weights into WSLOTS slots, the records of a K-unit into one slot), counted as it
+// of the stream is a DMA into LDS (the weights into D slots, the records of a K-unit into one slot), counted as it
 // is issued (nl), so that each wait names the exact number of loads issued after the ones it needs: loads of one kind
 // return in order. (Records loaded into registers instead would make the compiler wait for all loads in flight
 // before each use: it cannot order them against the DMAs.)
-template <int QT, bool SWIGLU>
+template <int QT, bool SWIGLU, int D>
 struct Stream {
   using W = Shape<SWIGLU>;
   static constexpr int RB = W::RB, S = W::S, BY = Unit<QT>::BYTES, CH = BY / 16, LW = Unit<QT>::LW;
   static constexpr int NM = SWIGLU ? 2 : 1, WCH = 16 * CH, NI = (WCH + 63) / 64, LAST = WCH - 64 * (NI - 1);
-  static constexpr int LA = WSLOTS - 1;                          // steps in flight ahead of the one being read
+  static constexpr int LA = D - 1;                          // steps in flight ahead of the one being read
   static constexpr int XCH = GEMV_BM * 64;  // chunks of the record slot
   static constexpr int NMAX = LA * NI + (LA + 1) * GEMV_BM;  // loads issued after a step's, at most
   static_assert(NMAX < 64, "loads in flight beyond vmcnt");
@@ -596,14 +603,14 @@ struct Stream {
   uint32_t lo[NI];   // the lane's byte offset in the 16 rows of each load instruction
   int nl = 0;        // loads issued so far
   int xend = 0;       // nl after the record slot's loads
-  int wend[WSLOTS] = {};  // nl after the weights of the last WSLOTS steps issued (wend[0]: the latest)
+  int wend[D] = {};  // nl after the weights of the last D steps issued (wend[0]: the latest)
 
   __device__ __forceinline__ explicit Stream(const GemvArgs& args) : a(args) {
     extern __shared__ u32x4 slab[];
     wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     lane = threadIdx.x & 63, p = lane >> 4, r = lane & 15;
     rb = wv / S, ks = wv % S;
-    my = slab + wv * (WSLOTS * WCH + XCH);
+    my = slab + wv * (D * WCH + XCH);
     const int U = a.K / 256;
     u0 = ks;  // (the wave's K-units: ks, ks + S, ...; the pair reads neighbouring units, which share lines, together)
     NVw = (U - ks + S - 1) / S * NM;
@@ -613,7 +620,7 @@ struct Stream {
       lo[i] = uint32_t((16 * rb + row) * a.row_bytes + 16 * (q - row * CH));
     }
     wbase = lds_addr(my);
-    xbase = lds_addr(my + WSLOTS * WCH) + 16 * lane;
+    xbase = lds_addr(my + D * WCH) + 16 * lane;
     if constexpr (QT == ARTLITE_Q6_K) {  // (low bits of half p / 2, its high bits, the scales and d)
       o_w = r * BY + 64 * (p >> 1);
       o_r = r * BY + 128 + 32 * (p >> 1);
@@ -646,12 +653,12 @@ struct Stream {
       nl += NI;
     }
 #pragma unroll
-    for (int i = WSLOTS - 1; i > 0; i--) wend[i] = wend[i - 1];
+    for (int i = D - 1; i > 0; i--) wend[i] = wend[i - 1];
     wend[0] = nl;
   }
   // the records of K-unit ku of item I's rows of A into the record slot (lane l: chunk l of each row)
   __device__ __forceinline__ void load_x(const Item& I, int ku) {
-    u32x4* dst = my + WSLOTS * WCH;
+    u32x4* dst = my + D * WCH;
 #pragma unroll
     for (int t = 0; t < GEMV_BM; t++)
       if (t < I.m)
@@ -664,17 +671,18 @@ struct Stream {
 };
 
 // the wait and read of a step: vmcnt(n), then the weights and (MX) the record chunks. n is at most NMAX (the stream's
-// counts: after a step's weights come the next step's (NI) and at most one K-unit's records); a larger n, which the
-// two-slot stream does not produce, would wait for every load (vmcnt(0)), never for fewer than needed
-template <int QT, bool SWIGLU, int MX>
-__device__ __forceinline__ void wait_read(const Stream<QT, SWIGLU>& st, int n, uint32_t sw, uint32_t sx,
+// counts: after a step's weights come the LA steps' issued ahead (NI each) and at most LA + 1 K-units' records); a
+// larger n, which the stream does not produce, would wait for every load (vmcnt(0)), never for fewer than needed
+template <int QT, bool SWIGLU, int MX, int D>
+__device__ __forceinline__ void wait_read(const Stream<QT, SWIGLU, D>& st, int n, uint32_t sw, uint32_t sx,
                                           uint32_t (&w)[Unit<QT>::LW], u32x4 (&x)[GEMV_BM]) {
-  using SS = Stream<QT, SWIGLU>;
+  using SS = Stream<QT, SWIGLU, D>;
   if (n > SS::NMAX) n = 0;
   static_for<SS::NMAX + 1>([&](auto nc) {
     constexpr int N = decltype(nc)::value;
-    if (n == N) read_unit<N, QT, MX>(w, x, sw + st.o_w, sw + st.o_r, sw + st.o_s, sx);
+    if (n == N) wait_vm<N>();
   });
+  read_unit<QT, MX>(w, x, sw + st.o_w, sw + st.o_r, sw + st.o_s, sx);
 }
 
 // The dot products of one step: the lane's two groups of the unit w against the M rows of A's records x.
@@ -696,10 +704,10 @@ __device__ __forceinline__ void step_terms(const uint32_t (&w)[Unit<QT>::LW], co
 // the weights LA steps ahead, then waits for its own; at the start of each K-unit that wait also covers the
 // records, which are read into registers with the weights, and the next K-unit's are loaded into the freed slot.
 // Returns with the sums of the four lanes of a row in every lane.
-template <int QT, bool SWIGLU, int M>
-__device__ __forceinline__ void run_item(Stream<QT, SWIGLU>& st, const Item& cur, const Item& nxt, bool has_next,
+template <int QT, bool SWIGLU, int M, int D>
+__device__ __forceinline__ void run_item(Stream<QT, SWIGLU, D>& st, const Item& cur, const Item& nxt, bool has_next,
                                          int gs, float (&out)[SWIGLU ? 2 : 1][GEMV_BM]) {
-  using SS = Stream<QT, SWIGLU>;
+  using SS = Stream<QT, SWIGLU, D>;
   constexpr int NM = SS::NM, LW = SS::LW, LA = SS::LA;
   float acc[NM][M];
 #pragma unroll
@@ -716,21 +724,21 @@ __device__ __forceinline__ void run_item(Stream<QT, SWIGLU>& st, const Item& cur
         const int vi = v + LA;
         const bool here = vi < st.NVw;
         st.template issue_w<(MX + LA) % NM>(here || has_next, here ? cur.e : nxt.e, here ? cur.n0 : nxt.n0,
-                                            here ? vi : vi - st.NVw, (gs + v + LA) % WSLOTS);
+                                            here ? vi : vi - st.NVw, (gs + v + LA) % D);
       };
       issue();
       uint32_t w[LW];
-      const uint32_t sw = st.wbase + ((gs + v) % WSLOTS) * SS::WCH * 16;
+      const uint32_t sw = st.wbase + ((gs + v) % D) * SS::WCH * 16;
       if constexpr (MX == 0) {
-        // (wend[WSLOTS - 1]: this step's weights), then the next K-unit's records into the slot just read
-        const int nw = st.nl - st.wend[WSLOTS - 1];
-        wait_read<QT, SWIGLU, M>(st, min(nw, st.nl - st.xend), sw, st.xbase, w, xc);
+        // (wend[D - 1]: this step's weights), then the next K-unit's records into the slot just read
+        const int nw = st.nl - st.wend[D - 1];
+        wait_read<QT, SWIGLU, M, D>(st, min(nw, st.nl - st.xend), sw, st.xbase, w, xc);
         if (v0 + NM < st.NVw)
           st.load_x(cur, st.u0 + SS::S * (v0 / NM + 1));
         else if (has_next)
           st.load_x(nxt, st.u0);
       } else {
-        wait_read<QT, SWIGLU, 0>(st, st.nl - st.wend[WSLOTS - 1], sw, st.xbase, w, xc);
+        wait_read<QT, SWIGLU, 0, D>(st, st.nl - st.wend[D - 1], sw, st.xbase, w, xc);
       }
       step_terms<QT, M>(w, xc, st.p, acc[MX]);
     });
@@ -748,11 +756,11 @@ __device__ __forceinline__ void run_item(Stream<QT, SWIGLU>& st, const Item& cur
 }
 
 // A persistent workgroup: items snake_item(blockIdx.x, j, gridDim.x) of (tile, block of 16 RB rows), tile-major.
-template <int QT, bool SWIGLU>
+template <int QT, bool SWIGLU, int D>
 __global__ __launch_bounds__(Shape<SWIGLU>::THREADS) __attribute__((amdgpu_waves_per_eu(QT == ARTLITE_Q4_0 ? 4 : 2))) void k_gemv(
     const GemvArgs a) {
   using W = Shape<SWIGLU>;
-  using SS = Stream<QT, SWIGLU>;
+  using SS = Stream<QT, SWIGLU, D>;
   constexpr int RB = W::RB, S = W::S, NM = SS::NM;
   const int rows = 16 * RB, NB = (a.N + rows - 1) / rows;
   extern __shared__ u32x4 slab[];
@@ -796,7 +804,7 @@ __global__ __launch_bounds__(Shape<SWIGLU>::THREADS) __attribute__((amdgpu_waves
   if (it0 >= n_items) return;
   SS st(a);
   // [buffer][wave][matrix][row of A][row], after every wave's slots
-  float* red = reinterpret_cast<float*>(slab + W::WAVES * (WSLOTS * SS::WCH + SS::XCH));
+  float* red = reinterpret_cast<float*>(slab + W::WAVES * (D * SS::WCH + SS::XCH));
 
   const int n_my = snake_count(it0, G, n_items);
   constexpr int RED = W::WAVES * NM * GEMV_BM * 16;  // floats of one partial-sum buffer
@@ -834,10 +842,10 @@ __global__ __launch_bounds__(Shape<SWIGLU>::THREADS) __attribute__((amdgpu_waves
     if (has_next) nxt = get_item(tab, j + 1);
     float out[NM][GEMV_BM];
     switch (cur.m) {
-      case 1: run_item<QT, SWIGLU, 1>(st, cur, nxt, has_next, gs, out); break;
-      case 2: run_item<QT, SWIGLU, 2>(st, cur, nxt, has_next, gs, out); break;
-      case 3: run_item<QT, SWIGLU, 3>(st, cur, nxt, has_next, gs, out); break;
-      default: run_item<QT, SWIGLU, 4>(st, cur, nxt, has_next, gs, out); break;
+      case 1: run_item<QT, SWIGLU, 1, D>(st, cur, nxt, has_next, gs, out); break;
+      case 2: run_item<QT, SWIGLU, 2, D>(st, cur, nxt, has_next, gs, out); break;
+      case 3: run_item<QT, SWIGLU, 3, D>(st, cur, nxt, has_next, gs, out); break;
+      default: run_item<QT, SWIGLU, 4, D>(st, cur, nxt, has_next, gs, out); break;
     }
     gs += st.NVw;
     if constexpr (!SWIGLU) {
@@ -912,18 +920,22 @@ __global__ __launch_bounds__(256) void k_quant(const void* __restrict__ x, int64
   if (w < T * (K / 256)) xq_quant_unit<XT>(x, w, K, xq, threadIdx.x & 63);
 }
 
-template <int QT, bool SWIGLU>
-int launch_t(const GemvArgs& a, hipStream_t s) {
+// work items of a launch (the tile bound times the blocks of 16 RB rows)
+template <bool SWIGLU>
+int64_t gemv_items(const GemvArgs& a) {
   using W = Shape<SWIGLU>;
   const int64_t tiles = a.tiles ? a.max_tiles : (a.dense_rows + GEMV_BM - 1) / GEMV_BM;
-  const int64_t items = tiles * ((a.N + 16 * W::RB - 1) / (16 * W::RB));
-  if (items <= 0) return ARTLITE_OK;
-  if (items >= (int64_t(1) << 31)) return fail(ARTLITE_EINVAL, "expert GEMV: %lld work items", (long long)items);
-  // persistent workgroups: as many as the device holds at once (queried once per kernel, with a table of 64
-  // items), at most one per item; their item tables take 32 bytes an item
-  constexpr size_t lds0 = gemv_lds<QT, SWIGLU>(), lds_max = lds0 + 8192;
+  return tiles * ((a.N + 16 * W::RB - 1) / (16 * W::RB));
+}
+
+// persistent workgroups of k_gemv<QT, SWIGLU, D>: as many as the device holds at once (queried once per kernel, with
+// a table of 64 items; 0: set-up failed); their item tables take 32 bytes an item, at most lds_max in all
+template <int QT, bool SWIGLU, int D>
+int gemv_resident() {
+  using W = Shape<SWIGLU>;
+  constexpr size_t lds0 = gemv_lds<QT, SWIGLU, D>(), lds_max = lds0 + 8192;
   static const int resident = [] {
-    const void* f = reinterpret_cast<const void*>(k_gemv<QT, SWIGLU>);
+    const void* f = reinterpret_cast<const void*>(k_gemv<QT, SWIGLU, D>);
     int dev = 0, cus = 0, per_cu = 0;
     if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_max)) != hipSuccess ||
         hipGetDevice(&dev) != hipSuccess ||
@@ -932,6 +944,17 @@ int launch_t(const GemvArgs& a, hipStream_t s) {
       return 0;
     return cus * std::max(1, per_cu);
   }();
+  return resident;
+}
+
+template <int QT, bool SWIGLU, int D>
+int launch_t(const GemvArgs& a, hipStream_t s) {
+  using W = Shape<SWIGLU>;
+  const int64_t items = gemv_items<SWIGLU>(a);
+  if (items <= 0) return ARTLITE_OK;
+  if (items >= (int64_t(1) << 31)) return fail(ARTLITE_EINVAL, "expert GEMV: %lld work items", (long long)items);
+  constexpr size_t lds0 = gemv_lds<QT, SWIGLU, D>(), lds_max = lds0 + 8192;
+  const int resident = gemv_resident<QT, SWIGLU, D>();
   if (resident <= 0) return fail(ARTLITE_EHIP, "expert GEMV: kernel set-up failed");
   const unsigned grid = unsigned(std::min<int64_t>(items, resident));
   const size_t lds = lds0 + size_t((items + grid - 1) / grid) * 32;
@@ -941,13 +964,13 @@ int launch_t(const GemvArgs& a, hipStream_t s) {
     const GemvArgs::Route& r = a.route;
     const size_t need = sizeof(RouteLds<W::THREADS>) + 4 * (size_t(2 * a.max_tiles + r.T * r.k + r.E + 2 + 3) / 4 * 4) +
                         4 * size_t(r.T) * r.E;
-    const size_t slots = size_t(W::WAVES) * (WSLOTS * 16 * Unit<QT>::BYTES + GEMV_BM * 1024);
+    const size_t slots = size_t(W::WAVES) * (D * 16 * Unit<QT>::BYTES + GEMV_BM * 1024);
     if (!gemv_route_fits(r.T, r.E, r.k) || need > slots || a.rows_total != r.T * r.k || a.topk != r.k ||
         a.max_tiles != tile_bound(int64_t(r.T) * r.k, r.E, GEMV_BM))
       return fail(ARTLITE_EINVAL, "expert GEMV: routing of %d tokens, %d experts, top %d in the launch", r.T, r.E,
                   r.k);
   }
-  k_gemv<QT, SWIGLU><<<grid, W::THREADS, lds, s>>>(a);
+  k_gemv<QT, SWIGLU, D><<<grid, W::THREADS, lds, s>>>(a);
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
 }
@@ -980,7 +1003,7 @@ int launch_gemv(const GemvArgs& a, hipStream_t s) {
   if (swiglu && (a.N % 256 || !a.hq))
     return fail(ARTLITE_EINVAL, "expert GEMV: SwiGLU width %d is not a multiple of 256", a.N);
   if (!swiglu && !a.y) return fail(ARTLITE_EINVAL, "expert GEMV: no output");
-#define ART_DISPATCH(QT) return swiglu ? launch_t<QT, true>(a, s) : launch_t<QT, false>(a, s)
+#define ART_DISPATCH(QT) return swiglu ? launch_t<QT, true, WSLOTS>(a, s) : launch_t<QT, false, WSLOTS>(a, s)
   switch (a.qtype) {
     case ARTLITE_Q4_0: ART_DISPATCH(ARTLITE_Q4_0);
     case ARTLITE_Q8_0: ART_DISPATCH(ARTLITE_Q8_0);
