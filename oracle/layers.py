@@ -114,6 +114,9 @@ CONFIGS = {
     # the top k a wave per token
     "topk20": Spec("topk20", H=512, E=64, k=20, F=256, gate_type="Q4_0", down_type="Q4_0", scale=0.02,
                    tokens=(12,)),
+    # test-only: 320 experts (eight logits a lane in the gate / up launch's top k)
+    "wide_e": Spec("wide_e", H=256, E=320, k=4, F=256, gate_type="Q4_0", down_type="Q4_0", scale=0.02,
+                   tokens=(16,)),
     # the Qwen3-30B-A3B shape as Q4_K_M files quantise it (Q4_K gate / up, Q6_K down) at a 4096-token prefill: the
     # down on the prefill tiles through the prefill layout
     "q4km": Spec("q4km", H=2048, E=128, k=8, F=768, gate_type="Q4_K", down_type="Q6_K", scale=2e-4, dmin_scale=1.5e-3,

@@ -33,7 +33,7 @@ CASES = [("cpu", 16), ("decode", 1), ("decode", 4), ("decode", 16), ("decode", 6
          # the decode routing in a launch of its own (more pairs than a GEMV workgroup routes), and in the GEMV's
          ("widek", 40), ("widek", 16),
          # the routing in the gate / up launch with a wave per token (top 20: more than a lane group takes)
-         ("topk20", 12)]
+         ("topk20", 12), ("wide_e", 16)]
 # (passes on the MFMA decode tiles)
 DTILE_CASES = {("dtiles", 96)}
 
@@ -44,7 +44,7 @@ DTILE_CASES = {("dtiles", 96)}
 # 1e-4 of relative error in h and the pair outputs.
 GEMV_CASES = {("cpu", 16), ("decode", 1), ("decode", 4), ("decode", 16), ("decode", 64), ("mix_q8k", 16), ("mix_k8", 24),
               ("kmix", 16), ("q5km", 16), ("q5k", 24), ("kquants", 32), ("q6k", 24), ("mixtile", 16), ("iq4", 16),
-              ("q41", 16), ("q3k", 16), ("widek", 40), ("widek", 16), ("topk20", 12)}
+              ("q41", 16), ("q3k", 16), ("widek", 40), ("widek", 16), ("topk20", 12), ("wide_e", 16)}
 
 
 def check_layer(name: str, T: int, seed: int = 0) -> None:
