@@ -54,6 +54,7 @@ struct PrefillProblem {
   const int32_t* n_tiles;  // the tile count (device)
   const int32_t* offsets;  // E + 1 expert offsets in the sorted order
   int dense_rows;
+  int dense_tile;          // dense rows: a tile's rows, at most 256 (0: balanced_rows(dense_rows, 256))
   int64_t max_tiles;       // grid bound
   uint16_t* h;             // SwiGLU output: fp16 (row stride N)
   float* y;                // plain output: fp32 (row stride N)

@@ -14,7 +14,7 @@ using namespace artlite;
 
 struct artlite_moe_layer {
   artlite_moe_desc d{};
-  int device = 0;
+  int device = 0, cus = 0;  // (the device's compute units)
   hipStream_t stream = nullptr;
   const QType *gq = nullptr, *dq = nullptr, *sq = nullptr, *sdq = nullptr;  // (sdq: the shared down's)
   size_t gate_row = 0, down_row = 0, sgate_row = 0, sdown_row = 0;  // row bytes in the layer (QType::dev blocks)
@@ -423,7 +423,13 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
       PrefillArgs& into = merged ? dn : sdn;
       prefill_format(L->sdq, into);
       const int n = shared_parts(L, merged);
-      for (int j = 0; j < n; j++) into.p[into.np++] = shared_down_part(L, T, j, n);
+      // (a launch of its own: tiles of fewer rows where 256-row tiles would leave compute units without an item)
+      int tile = 256;
+      while (!merged && tile > 64 && (T + tile - 1) / tile * ((H + 255) / 256) * n < L->cus) tile /= 2;
+      for (int j = 0; j < n; j++) {
+        into.p[into.np] = shared_down_part(L, T, j, n);
+        into.p[into.np++].dense_tile = balanced_rows(int(T), tile);
+      }
       ys_parts = n;
     }
     ART_TRY(mark());
@@ -617,6 +623,7 @@ extern "C" int artlite_moe_layer_create(const artlite_moe_desc* desc, artlite_mo
                          prefill_fits(1, int64_t(d.hidden) * prefill_row(L->sdown_row, d.shared_ffn, L->pre_sd),
                                       d.max_tokens, d.shared_ffn);
   hipError_t e = hipGetDevice(&L->device);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&L->cus, hipDeviceAttributeMultiprocessorCount, L->device);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&L->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete L;

@@ -257,9 +257,13 @@ __device__ __forceinline__ int pg_nbk(const PrefillProblem& P) {
   constexpr int WN = SWIGLU ? 128 : 256;
   return (P.N + WN - 1) / WN;
 }
+// dense rows: the rows of a tile
+__host__ __device__ __forceinline__ int pg_dense_rows(const PrefillProblem& P) {
+  return P.dense_tile > 0 ? P.dense_tile : balanced_rows(P.dense_rows, TILE_ROWS);
+}
 __device__ __forceinline__ int64_t pg_tiles(const PrefillProblem& P) {
   if (P.tiles) return *P.n_tiles;
-  const int rows = balanced_rows(P.dense_rows, TILE_ROWS);
+  const int rows = pg_dense_rows(P);
   return (P.dense_rows + rows - 1) / rows;
 }
 
@@ -279,7 +283,7 @@ __device__ __forceinline__ PGItem pg_item(const PrefillProblem& P, int p, int64_
     const int lo = P.offsets[I.e], hi = P.offsets[I.e + 1];
     I.m_valid = min(balanced_rows(hi - lo, TILE_ROWS), hi - I.s0);
   } else {
-    const int rows = balanced_rows(P.dense_rows, TILE_ROWS);
+    const int rows = pg_dense_rows(P);
     I.e = 0;
     I.s0 = tl * rows;
     I.m_valid = min(rows, P.dense_rows - I.s0);
@@ -1071,9 +1075,7 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 
 // a product's work items at most (its tile bound times its column blocks)
 int64_t pg_items_bound(const PrefillProblem& P, bool swiglu) {
-  const int64_t tiles = P.tiles ? P.max_tiles
-                                : (P.dense_rows + balanced_rows(P.dense_rows, TILE_ROWS) - 1) /
-                                      balanced_rows(P.dense_rows, TILE_ROWS);
+  const int64_t tiles = P.tiles ? P.max_tiles : (P.dense_rows + pg_dense_rows(P) - 1) / pg_dense_rows(P);
   return tiles * ((P.N + (swiglu ? 127 : 255)) / (swiglu ? 128 : 256));
 }
 
@@ -1134,7 +1136,8 @@ int launch_prefill(const PrefillArgs& a, hipStream_t s) {
     if (!prefill_supported(a.qtype, P.K, P.N))
       return fail(ARTLITE_EINVAL, "prefill GEMM: weight type %d, K %d, N %d", a.qtype, P.K, P.N);
     if (!P.a || !P.row_scale || !P.w[0] || (P.w[1] != nullptr) != swiglu || (swiglu ? !P.h : !P.y && !P.y16) ||
-        (P.tiles && (!P.n_tiles || !P.offsets)) || P.lda < P.K)
+        (P.tiles && (!P.n_tiles || !P.offsets)) || P.lda < P.K ||
+        P.dense_tile < 0 || P.dense_tile > TILE_ROWS)
       return fail(ARTLITE_EINVAL, "prefill GEMM: product %d: null or mismatched argument", p);
     if (P.expert_bytes >= (int64_t(1) << 32) || int64_t(P.N) * P.row_bytes >= (int64_t(1) << 32) ||
         (!P.tiles && P.dense_rows > (1 << 24)))
