@@ -284,12 +284,16 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
     db.row_out[1] = L->dn_row.as<float2>();
   }
   ART_TRY(mark());
+  // (a split router's parts, when the top k follows as a launch of its own: added by the top k)
+  int parts = 0;
+  const bool topk_launch = !path.gemv_route && !path.small;
   if (path.few_router)
     ART_TRY(launch_router_few(xin, xdt, L->router.as<float>(), H, E, T, L->logits.as<float>(),
                                 path.quant ? L->xq.as<uint32_t>() : nullptr, s));
   else
     ART_TRY(launch_router(xin, xdt, L->router.as<float>(), H, E, T, L->logits.as<float>(), E,
-                          path.quant ? L->xq.as<uint32_t>() : nullptr, L->rpart.as<double>(), L->rpart_elems, s));
+                          path.quant ? L->xq.as<uint32_t>() : nullptr, L->rpart.as<double>(), L->rpart_elems, s,
+                          topk_launch ? &parts : nullptr));
   if (d.shared_ffn && d.shared_gated) {
     ART_TRY(mark());
     ART_TRY(launch_router(xin, xdt, L->sinp.as<float>(), H, 1, T, L->sg.as<float>(), 1, nullptr, nullptr, 0, s));
@@ -301,8 +305,12 @@ int run(artlite_moe_layer* L, int64_t T, hipEvent_t* ev) {
                                s));
   } else {
     ART_TRY(mark());
-    ART_TRY(launch_topk(L->logits.as<float>(), T, E, E, 0, E, k, d.gating, L->ids.as<int32_t>(), L->w.as<float>(),
-                        nullptr, s));
+    if (parts)
+      ART_TRY(launch_topk_parts(L->rpart.as<double>(), parts, T, E, L->logits.as<float>(), E, k, d.gating,
+                                L->ids.as<int32_t>(), L->w.as<float>(), s));
+    else
+      ART_TRY(launch_topk(L->logits.as<float>(), T, E, E, 0, E, k, d.gating, L->ids.as<int32_t>(), L->w.as<float>(),
+                          nullptr, s));
     const int64_t nb = dispatch_blocks(P);
     ART_TRY(mark());
     ART_TRY(launch_dispatch_count(db, nb, s));

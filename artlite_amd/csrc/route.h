@@ -71,20 +71,18 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // low half of logit_key decides ties), lane j keeping the j-th; then the weights. ev (64 doubles) and sum (1): the
 // wave's LDS scratch. Lane j < k writes ids[j] and the weights (w32 / w64 when given) and returns its id; other lanes
 // return -1 (ids null: none written; w32 and w64 null: no weights computed).
-template <int R>
-__device__ __forceinline__ int topk_wave(const float* __restrict__ p, int per_col, int64_t pitch, int E, int k,
-                                         int sigmoid, double* ev, double* sum, int lane, int32_t* __restrict__ ids,
-                                         float* __restrict__ w32, double* __restrict__ w64) {
+// (topk_wave_by: the logit of expert e < E from load(e), called by the lane that ranks it)
+template <int R, typename LOAD>
+__device__ __forceinline__ int topk_wave_by(LOAD load, int E, int k, int sigmoid, double* ev, double* sum, int lane,
+                                            int32_t* __restrict__ ids, float* __restrict__ w32,
+                                            double* __restrict__ w64) {
   static_assert(R <= 32, "keys per lane");
   uint32_t ord[R], live = 0;
 #pragma unroll
   for (int r = 0; r < R; r++) {
     const int e = lane + WAVE * r;
     float l = 0.0f;
-    if (e < E) {
-      const float* q = per_col == E ? p + e : p + int64_t(e / per_col) * pitch + e % per_col;
-      l = *q;
-    }
+    if (e < E) l = load(e);
     ord[r] = e < E ? uint32_t(logit_key(l, e) >> 32) : 0;
     if (e < E) live |= 1u << r;
   }
@@ -133,6 +131,14 @@ __device__ __forceinline__ int topk_wave(const float* __restrict__ p, int per_co
   if (w32) w32[lane] = float(w);
   if (w64) w64[lane] = w;
   return id;
+}
+template <int R>
+__device__ __forceinline__ int topk_wave(const float* __restrict__ p, int per_col, int64_t pitch, int E, int k,
+                                         int sigmoid, double* ev, double* sum, int lane, int32_t* __restrict__ ids,
+                                         float* __restrict__ w32, double* __restrict__ w64) {
+  return topk_wave_by<R>(
+      [&](int e) { return per_col == E ? p[e] : p[int64_t(e / per_col) * pitch + e % per_col]; }, E, k, sigmoid, ev,
+      sum, lane, ids, w32, w64);
 }
 
 // the 32-bit maximum / minimum over each group of W lanes (16: a DPP row; 32: two rows, then the permlane16 swap
@@ -255,13 +261,19 @@ int check_route_args(int64_t n, int per_col, int E, int k);
 
 int launch_topk(const float* logits, int64_t n, int64_t row, int per_col, int64_t pitch, int E, int k, int sigmoid,
                 int32_t* ids, float* w32, double* w64, hipStream_t s);
+// the same over a split router's fp64 parts (launch_router with parts_left): each logit is the sum of its parts in
+// part order, rounded once, and is also stored to out[t out_row + e]
+int launch_topk_parts(const double* part, int parts, int64_t n, int E, float* out, int64_t out_row, int k, int sigmoid,
+                      int32_t* ids, float* w32, hipStream_t s);
 
 // Router logits out[t out_row + e] = x[t] . W[e] (float64 accumulation, rounded once). xq: when given, x is also
 // quantised into XQ rows (gemv.h) by extra workgroups of the same launch (H a multiple of 256). part (part_elems
 // doubles, router_part_elems for the most tokens of a layer; may be null): the fp64 partial sums of prefill-sized
 // batches whose tiles are too few for the device, K split over workgroups and the parts added in a fixed order.
+// parts_left (optional): the parts are then not added here: *parts_left = their count (for launch_topk_parts), or 0
+// when the logits are in out.
 int launch_router(const void* x, int x_dtype, const float* W, int H, int E, int64_t T, float* out, int64_t out_row,
-                  uint32_t* xq, double* part, size_t part_elems, hipStream_t s);
+                  uint32_t* xq, double* part, size_t part_elems, hipStream_t s, int* parts_left = nullptr);
 size_t router_part_elems(int64_t max_T, int E, int H);
 
 // out (T x H fp32) = x / sqrt(mean(x^2) + eps) * w per row (float64 mean and quotient, rounded once, then fp32 w)

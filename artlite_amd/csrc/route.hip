@@ -30,6 +30,59 @@ __global__ __launch_bounds__(TOPK_WAVES * WAVE) void k_topk(const float* __restr
   (void)id;
 }
 
+constexpr int TOPK_MAXPARTS = 16;  // (router_split's parts at most)
+
+// one wave per token over a split router's parts: lane e's logit the sum of its parts in part order (as
+// k_router_parts adds them), rounded once and stored
+template <int R>
+__global__ __launch_bounds__(TOPK_WAVES * WAVE) void k_topk_parts(const double* __restrict__ part, int parts,
+                                                                  int64_t n, int E, float* __restrict__ out,
+                                                                  int64_t out_row, int k, int sigmoid,
+                                                                  int32_t* __restrict__ ids, float* __restrict__ w32) {
+  __shared__ double ev[TOPK_WAVES][WAVE];
+  __shared__ double sum[TOPK_WAVES];
+  const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE;
+  const int64_t t = int64_t(blockIdx.x) * TOPK_WAVES + wv, pn = n * E;
+  if (t >= n) return;  // (uniform per wave)
+  auto load = [&](int e) {
+    const double* q = part + t * E + e;
+    double v[TOPK_MAXPARTS];  // (every part's load in flight together)
+#pragma unroll
+    for (int z = 0; z < TOPK_MAXPARTS; z++) v[z] = z < parts ? q[int64_t(z) * pn] : 0.0;
+    double c = v[0];
+#pragma unroll
+    for (int z = 1; z < TOPK_MAXPARTS; z++)
+      if (z < parts) c += v[z];
+    const float l = float(c);
+    out[t * out_row + e] = l;
+    return l;
+  };
+  topk_wave_by<R>(load, E, k, sigmoid, ev[wv], &sum[wv], lane, ids + t * k, w32 ? w32 + t * k : nullptr, nullptr);
+}
+
+int launch_topk_parts(const double* part, int parts, int64_t n, int E, float* out, int64_t out_row, int k, int sigmoid,
+                      int32_t* ids, float* w32, hipStream_t s) {
+  if (n <= 0) return ARTLITE_OK;
+  if (parts < 1 || parts > TOPK_MAXPARTS || E < 1 || E > MAX_EXPERTS || k < 1 || k > E || k > MAX_TOPK)
+    return fail(ARTLITE_EINVAL, "top-k over router parts: %d parts, E %d, k %d", parts, E, k);
+  const dim3 grid(unsigned((n + TOPK_WAVES - 1) / TOPK_WAVES)), block(TOPK_WAVES * WAVE);
+#define ART_TOPK(RR) \
+  k_topk_parts<RR><<<grid, block, 0, s>>>(part, parts, n, E, out, out_row, k, sigmoid, ids, w32)
+  if (E <= 64)
+    ART_TOPK(1);
+  else if (E <= 128)
+    ART_TOPK(2);
+  else if (E <= 256)
+    ART_TOPK(4);
+  else if (E <= 512)
+    ART_TOPK(8);
+  else
+    ART_TOPK(16);
+#undef ART_TOPK
+  ART_HIP(hipGetLastError());
+  return ARTLITE_OK;
+}
+
 int launch_topk(const float* logits, int64_t n, int64_t row, int per_col, int64_t pitch, int E, int k, int sigmoid,
                 int32_t* ids, float* w32, double* w64, hipStream_t s) {
   if (n <= 0) return ARTLITE_OK;
@@ -420,7 +473,7 @@ RouterSplit router_split(int64_t T, int E, int H) {
   RouterSplit r;
   r.te = E <= 32 ? 32 : 64;
   const int64_t tiles = (T + 31) / 32 * ((E + r.te - 1) / r.te);
-  int parts = int(std::min<int64_t>(16, std::max<int64_t>(1, 256 / std::max<int64_t>(1, tiles))));
+  int parts = int(std::min<int64_t>(TOPK_MAXPARTS, std::max<int64_t>(1, 256 / std::max<int64_t>(1, tiles))));
   parts = std::min(parts, std::max(1, H / 128));
   r.kchunk = (H + parts - 1) / parts;
   r.kchunk = (r.kchunk + 127) / 128 * 128;
@@ -443,7 +496,8 @@ size_t router_part_elems(int64_t max_T, int E, int H) {
 }
 
 int launch_router(const void* x, int x_dtype, const float* W, int H, int E, int64_t T, float* out, int64_t out_row,
-                  uint32_t* xq, double* part, size_t part_elems, hipStream_t s) {
+                  uint32_t* xq, double* part, size_t part_elems, hipStream_t s, int* parts_left) {
+  if (parts_left) *parts_left = 0;
   if (T <= 0) return ARTLITE_OK;
   if (H % 8) return fail(ARTLITE_EINVAL, "router: H %d not a multiple of 8", H);
   if (xq && H % 256) return fail(ARTLITE_EINVAL, "router: XQ of H %d (not a multiple of 256)", H);
@@ -473,7 +527,9 @@ int launch_router(const void* x, int x_dtype, const float* W, int H, int E, int6
         k_router_mfma<ARTLITE_X_BF16, 64, KP><<<g, b, 0, s>>>(x, W, H, E, T, out, out_row, r.kchunk, po);
     }
     ART_HIP(hipGetLastError());
-    if (po) {
+    if (po && parts_left) {
+      *parts_left = r.parts;
+    } else if (po) {
       const int64_t n = T * E;
       k_router_parts<<<unsigned((n + 255) / 256), 256, 0, s>>>(po, r.parts, T, E, out, out_row);
       ART_HIP(hipGetLastError());
