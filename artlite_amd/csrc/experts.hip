@@ -769,15 +769,32 @@ __global__ void k_combine16(const uint16_t* __restrict__ Y16, const float2* __re
 #pragma unroll
     for (int i = 0; i < 8; i++) acc[i] = ws * v[i];
   }
-  for (int i = 0; i < k; i++) {
-    const int64_t r = slot[t * k + i];
-    const float wi = w[t * k + i] * yf[r].x;
-    const uint4 v = reinterpret_cast<const uint4*>(Y16 + r * H)[h8];
-    const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+  // (KC pairs at a time: their slots and weights, then their factors and rows, all in flight before the sums, which
+  // go in pair order)
+  constexpr int KC = 8;
+  for (int i0 = 0; i0 < k; i0 += KC) {
+    int64_t r[KC];
+    float wi[KC];
+    u32x4 v[KC];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      acc[2 * j] = __builtin_fmaf(wi, h2f(q[j] & 0xFFFFu), acc[2 * j]);
-      acc[2 * j + 1] = __builtin_fmaf(wi, h2f(q[j] >> 16), acc[2 * j + 1]);
+    for (int i = 0; i < KC; i++) {  // (pairs past k load pair k - 1 again, unused: no branch between the loads)
+      const int64_t pi = t * k + min(i0 + i, k - 1);
+      r[i] = slot[pi], wi[i] = w[pi];
+    }
+#pragma unroll
+    for (int i = 0; i < KC; i++) wi[i] *= yf[r[i]].x, v[i] = reinterpret_cast<const u32x4*>(Y16 + r[i] * H)[h8];
+    // (every row in registers before the first sum: else the compiler moves each load into the branch that uses it,
+    // one round trip a pair)
+    asm volatile("" : : "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]));
+#pragma unroll
+    for (int i = 0; i < KC; i++) {
+      if (i0 + i >= k) break;
+      const uint32_t q[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        acc[2 * j] = __builtin_fmaf(wi[i], h2f(q[j] & 0xFFFFu), acc[2 * j]);
+        acc[2 * j + 1] = __builtin_fmaf(wi[i], h2f(q[j] >> 16), acc[2 * j + 1]);
+      }
     }
   }
   if (res) {
