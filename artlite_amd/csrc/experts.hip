@@ -710,13 +710,33 @@ __global__ void k_combine(const float* __restrict__ Y, const int32_t* __restrict
     const float4 v = reinterpret_cast<const float4*>(ys + t * H)[h4];
     acc.x = ws * v.x, acc.y = ws * v.y, acc.z = ws * v.z, acc.w = ws * v.w;
   }
-  for (int i = 0; i < k; i++) {
-    const float wi = w[t * k + i];
-    const float4 v = reinterpret_cast<const float4*>(Y + int64_t(slot[t * k + i]) * H)[h4];
-    acc.x = __builtin_fmaf(wi, v.x, acc.x);
-    acc.y = __builtin_fmaf(wi, v.y, acc.y);
-    acc.z = __builtin_fmaf(wi, v.z, acc.z);
-    acc.w = __builtin_fmaf(wi, v.w, acc.w);
+  // (KC pairs at a time: their slots and weights, then their rows, all in flight before the sums, which go in pair
+  // order; pairs past k load pair k - 1 again, unused, so that no branch separates the loads)
+  constexpr int KC = 8;
+  for (int i0 = 0; i0 < k; i0 += KC) {
+    int r[KC];
+    float wi[KC];
+    f32x4 v[KC];
+#pragma unroll
+    for (int i = 0; i < KC; i++) {
+      const int64_t pi = t * k + min(i0 + i, k - 1);
+      r[i] = slot[pi], wi[i] = w[pi];
+    }
+    // (the slots as outputs of an empty asm: every slot load issued before any row's address is formed from one)
+    asm volatile("" : "+s"(r[0]), "+s"(r[1]), "+s"(r[2]), "+s"(r[3]), "+s"(r[4]), "+s"(r[5]), "+s"(r[6]), "+s"(r[7]));
+#pragma unroll
+    for (int i = 0; i < KC; i++) v[i] = reinterpret_cast<const f32x4*>(Y + int64_t(r[i]) * H)[h4];
+    // (every row in registers before the first sum: else the compiler moves each load into the branch that uses it)
+    asm volatile("" : : "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]));
+    asm volatile("" : : "s"(wi[0]), "s"(wi[1]), "s"(wi[2]), "s"(wi[3]), "s"(wi[4]), "s"(wi[5]), "s"(wi[6]), "s"(wi[7]));
+#pragma unroll
+    for (int i = 0; i < KC; i++) {
+      if (i0 + i >= k) break;
+      acc.x = __builtin_fmaf(wi[i], v[i].x, acc.x);
+      acc.y = __builtin_fmaf(wi[i], v[i].y, acc.y);
+      acc.z = __builtin_fmaf(wi[i], v[i].z, acc.z);
+      acc.w = __builtin_fmaf(wi[i], v[i].w, acc.w);
+    }
   }
   if (res) {  // (the residual add after the block: y = moe + x)
     float4 r;
@@ -770,22 +790,24 @@ __global__ void k_combine16(const uint16_t* __restrict__ Y16, const float2* __re
     for (int i = 0; i < 8; i++) acc[i] = ws * v[i];
   }
   // (KC pairs at a time: their slots and weights, then their factors and rows, all in flight before the sums, which
-  // go in pair order)
+  // go in pair order; pairs past k load pair k - 1 again, unused, so that no branch separates the loads)
   constexpr int KC = 8;
   for (int i0 = 0; i0 < k; i0 += KC) {
-    int64_t r[KC];
+    int r[KC];
     float wi[KC];
     u32x4 v[KC];
 #pragma unroll
-    for (int i = 0; i < KC; i++) {  // (pairs past k load pair k - 1 again, unused: no branch between the loads)
+    for (int i = 0; i < KC; i++) {
       const int64_t pi = t * k + min(i0 + i, k - 1);
       r[i] = slot[pi], wi[i] = w[pi];
     }
+    // (the slots as outputs of an empty asm: every slot load issued before any row's address is formed from one)
+    asm volatile("" : "+s"(r[0]), "+s"(r[1]), "+s"(r[2]), "+s"(r[3]), "+s"(r[4]), "+s"(r[5]), "+s"(r[6]), "+s"(r[7]));
 #pragma unroll
-    for (int i = 0; i < KC; i++) wi[i] *= yf[r[i]].x, v[i] = reinterpret_cast<const u32x4*>(Y16 + r[i] * H)[h8];
-    // (every row in registers before the first sum: else the compiler moves each load into the branch that uses it,
-    // one round trip a pair)
+    for (int i = 0; i < KC; i++) wi[i] *= yf[r[i]].x, v[i] = reinterpret_cast<const u32x4*>(Y16 + int64_t(r[i]) * H)[h8];
+    // (every row in registers before the first sum: else the compiler moves each load into the branch that uses it)
     asm volatile("" : : "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]));
+    asm volatile("" : : "s"(wi[0]), "s"(wi[1]), "s"(wi[2]), "s"(wi[3]), "s"(wi[4]), "s"(wi[5]), "s"(wi[6]), "s"(wi[7]));
 #pragma unroll
     for (int i = 0; i < KC; i++) {
       if (i0 + i >= k) break;
