@@ -266,7 +266,7 @@ def main() -> None:
     ap.add_argument("--tokens", type=int, default=16)
     ap.add_argument("--weight-sets", type=int, default=4)
     ap.add_argument("--prefill-tokens", type=int, default=4096)
-    ap.add_argument("--prefill-steps", type=int, default=10)
+    ap.add_argument("--prefill-steps", type=int, default=20)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="only the headline decode and prefill lines")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of each headline CPU baseline (0: none)")
@@ -296,7 +296,7 @@ def main() -> None:
         steps = args.steps if name == "decode" else args.prefill_steps
         log(f"{name}: T={Tx}, {sets} weight set(s)")
         g = build_layers(sx, sets, Tx)
-        obj = line(name, sx, Tx, time_T(g, sx, Tx, steps, args.warmup if name == "decode" else 2), steps)
+        obj = line(name, sx, Tx, time_T(g, sx, Tx, steps, args.warmup), steps)
         for y in g:
             y.close()
         print(json.dumps({"workload": name, **obj}), flush=True)
@@ -327,7 +327,8 @@ def main() -> None:
         log(f"prefill: T={Tp}")
         ps = SHAPES["prefill"]
         g = build_layers(ps, 1, Tp)
-        out["prefill"] = line("prefill", ps, Tp, time_T(g, ps, Tp, args.prefill_steps, 2), args.prefill_steps)
+        out["prefill"] = line("prefill", ps, Tp, time_T(g, ps, Tp, args.prefill_steps, args.warmup),
+                              args.prefill_steps)
         g[0].close()
     extra = {}
     if not args.no_extra:
@@ -335,7 +336,7 @@ def main() -> None:
             log(f"{name}: T={Tx}")
             sx = SHAPES[name]
             g = build_layers(sx, sets, Tx)
-            extra[name] = line(name, sx, Tx, time_T(g, sx, Tx, args.prefill_steps, 2), args.prefill_steps)
+            extra[name] = line(name, sx, Tx, time_T(g, sx, Tx, args.prefill_steps, args.warmup), args.prefill_steps)
             for y in g:
                 y.close()
         out["configs"] = extra
