@@ -193,9 +193,9 @@ class MoELayer:
 
 def time_layers(layers: list[MoELayer], *, warmup: int, iters: int, per_kernel: bool = True
                 ) -> tuple[float, list[float], dict[str, float]]:
-    """(ms per run over ``iters`` runs cycling through ``layers`` after ``warmup``; each run's ms, from an event
-    before each run of that region; per kernel average ms, from a second timed region with an event before each
-    kernel) with HIP events on the layers' stream."""
+    """(ms per run over ``iters`` back-to-back runs cycling through ``layers`` after ``warmup``; each run's ms, from
+    an event before each run of a second region; per kernel average ms, from a third timed region with an event before
+    each kernel) with HIP events on the layers' stream."""
     T = layers[0].T
     hs = (ctypes.c_void_p * len(layers))(*[ly.handle.value for ly in layers])
     ms = ctypes.c_double(0)

@@ -8,8 +8,9 @@ fraction and the numpy CPU oracle timed on the host beside it.
 One step = one layer forward (router, routing, dispatch, experts, combine) over one batch already resident in HBM.
 Decode steps cycle through ``--weight-sets`` distinct weight sets so the working set (~220 MB per call) streams from
 HBM rather than the 256 MB Infinity Cache. Timing uses HIP events on the layer's stream (``artlite_moe_layer_time``):
-``ms_per_step`` is the median of the per-step times (an event before each step), ``ms_mean`` the timed region over the
-step count. Prints ONE JSON line."""
+``ms_per_step`` is a timed region of back-to-back steps over the step count (events only at its ends, a
+synchronization before it), ``ms_median_evented`` the median step of a second region with an event before each step
+(each such event holds the step after it back by a few microseconds). Prints ONE JSON line."""
 
 import argparse
 import json
@@ -127,7 +128,7 @@ def time_T(gls: list, shape: dict, T: int, steps: int, warmup: int) -> dict:
         U.append(int((g.tap("counts") > 0).sum()))
         g.stage(x)
     mean, runs, kernels = time_layers(gls, warmup=warmup, iters=steps)
-    return {"ms": float(np.median(runs)), "ms_mean": mean, "kernels": kernels, "U": float(np.mean(U)),
+    return {"ms": mean, "ms_median_evented": float(np.median(runs)), "kernels": kernels, "U": float(np.mean(U)),
             "names": list(kernels)}
 
 
@@ -218,7 +219,7 @@ def line(name: str, shape: dict, T: int, r: dict, steps: int) -> dict:
     # decode GEMV), bf16 hi + lo planes (the MFMA decode tiles)
     dtype = "f16" if "prefill_x" in names else "i8x2-xq" if any(n.startswith("router_quant") for n in names) else "bf16x2"
     return {"tokens": T, "value": T / (r["ms"] * 1e-3), "unit": "tokens/s", "ms_per_step": r["ms"],
-            "ms_mean": r["ms_mean"], "steps": steps, "dtype": dtype, "experts_touched": r["U"],
+            "ms_median_evented": r["ms_median_evented"], "steps": steps, "dtype": dtype, "experts_touched": r["U"],
             "kernel_ms": r["kernels"], "roofline": roof, "layer_roofline": lroof}
 
 
@@ -318,7 +319,8 @@ def main() -> None:
                    "tokens": T, "hidden": shape["H"], "experts": shape["E"], "top_k": shape["k"],
                    "expert_ffn": shape["F"], "weights": shape["gate"], "activations": "bf16",
                    "weight_sets": args.weight_sets, "experts_touched": head["experts_touched"]},
-        "ms_mean": head["ms_mean"], "roofline": head["roofline"], "layer_roofline": head["layer_roofline"],
+        "ms_median_evented": head["ms_median_evented"], "roofline": head["roofline"],
+        "layer_roofline": head["layer_roofline"],
         "kernel_ms": head["kernel_ms"], "commit": commit(),
         "decode_batches": {str(b): line("decode", shape, b, dec[b], args.steps) for b in batches if b != T},
     }

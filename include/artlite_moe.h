@@ -151,9 +151,10 @@ int artlite_moe_layer_tap(artlite_moe_layer* layer, int tap, void* out, size_t n
 
 /* Timing on the layers' stream with HIP events: warmup then iters runs of T tokens, cycling through the n layers
  * (distinct weight sets, so a working set larger than the GPU's caches is streamed from HBM). ms_per_run: the
- * average over the timed region. run_ms (may be NULL; iters entries): each run's duration, from an event recorded
- * before each run of that region. kernel_ms (may be NULL): with per-kernel events in a second timed region, each
- * kernel's average duration (artlite_moe_kernel_names order), kernel_cap entries at most; *n_kernels the count. */
+ * average over a timed region of back-to-back runs (events only at its ends). run_ms (may be NULL; iters entries):
+ * each run's duration, from an event recorded before each run of a second region (those events hold each run back
+ * by a few microseconds). kernel_ms (may be NULL): with per-kernel events in a further timed region, each kernel's
+ * average duration (artlite_moe_kernel_names order), kernel_cap entries at most; *n_kernels the count. */
 int artlite_moe_layer_time(artlite_moe_layer** layers, int n, int64_t T, int warmup, int iters, double* ms_per_run,
                            double* run_ms, double* kernel_ms, int kernel_cap, int* n_kernels);
 /* The names of the kernels of a run of T tokens on this layer, ';'-separated, into buf. */
