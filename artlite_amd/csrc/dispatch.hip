@@ -165,11 +165,18 @@ __global__ __launch_bounds__(DISPATCH_BLOCK) void k_count(DispatchBufs d) {
 __global__ __launch_bounds__(DISPATCH_BLOCK) void k_scatter(DispatchBufs d, PlanBufs pl) {
   __shared__ uint16_t wcnt[DISPATCH_BLOCK / WAVE][MAX_EXPERTS];
   const int tid = threadIdx.x, lane = tid & (WAVE - 1), wv = tid / WAVE;
-  for (int i = tid; i < (DISPATCH_BLOCK / WAVE) * d.E; i += DISPATCH_BLOCK) wcnt[i / d.E][i % d.E] = 0;
-  __syncthreads();
   const int64_t p = int64_t(blockIdx.x) * DISPATCH_BLOCK + tid;
   const int id = p < d.P ? d.ids[p] : -1;
+  for (int i = tid; i < (DISPATCH_BLOCK / WAVE) * d.E; i += DISPATCH_BLOCK) wcnt[i / d.E][i % d.E] = 0;
+  __syncthreads();
   const bool valid = id >= 0 && id < d.E;
+  // (the block's base of this expert and the pair's token factors, which need the id alone, loaded together now;
+  // the empty asm statement keeps the compiler from moving each load to its use, one round trip after another)
+  const int t = int((p < d.P ? p : d.P - 1) / d.k);  // (pairs past P: the last pair's token, unused)
+  const int base = d.table[int64_t(blockIdx.x) * d.E + (valid ? id : 0)];
+  float2 f0 = {0.0f, 0.0f}, f1 = f0;
+  if (d.row_a) f0 = d.row_f[0][t], f1 = d.row_f[1][t];
+  asm volatile("" : : "v"(base), "v"(f0.x), "v"(f0.y), "v"(f1.x), "v"(f1.y));
   // the lanes of this wave with the same expert (ballots over the id bits)
   uint64_t peers = __ballot(valid);
   for (int bit = 0; (1 << bit) < d.E; bit++) {
@@ -183,14 +190,13 @@ __global__ __launch_bounds__(DISPATCH_BLOCK) void k_scatter(DispatchBufs d, Plan
   __syncthreads();
   if (!valid) return;
   for (int w = 0; w < wv; w++) rank += wcnt[w][id];
-  const int dest = d.table[int64_t(blockIdx.x) * d.E + id] + rank;
+  const int dest = base + rank;
   d.order[dest] = int32_t(p);
   d.slot[p] = dest;
   if (d.row_a) {  // (the prefill's per-row token and factors, gathered here rather than by a launch of their own)
-    const int t = int(p / d.k);
     d.row_a[dest] = t;
-    d.row_out[0][dest] = d.row_f[0][t];
-    d.row_out[1][dest] = d.row_f[1][t];
+    d.row_out[0][dest] = f0;
+    d.row_out[1][dest] = f1;
   }
   if (pl.pos) {  // the plan's row of this pair
     const int o = dest - d.offsets[id];
