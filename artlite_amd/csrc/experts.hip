@@ -426,19 +426,31 @@ int launch_decode(const GemmArgs& a, hipStream_t s) {
 // 2^15 L1d (1 + 2^-11): with ye = ilogb(L1d) + 1 they stay below 2^15 (1 + 2^-11) < 65504 after the factor 2^-ye,
 // so the expert launch writes fp16 sums times 2^-ye and the true output is that times 2^(he + ye):
 // dn[t] = (2^(he + ye), 2^-ye). The shared expert's down writes fp32: dn2[t] = (2^he, 1). One workgroup per token.
-__device__ __forceinline__ void prefill_x_factors(int64_t t, int tid, int xe, float mx, float l1, const float* wmax,
+// the bounds prefill_x_factors reads for pair min(tid, pairs - 1), loaded at a kernel's start: wmax[2 q], wmax[2 q + 1],
+// wmax[5 + 2 q], wmax[6 + 2 q], wmax[4], wmax[9] (an empty asm statement takes them, so that the compiler does not
+// move the loads to their use after the row's own round trips)
+struct PXBounds {
+  float g, u, gl, ul, d, dl;
+};
+__device__ __forceinline__ PXBounds px_bounds(const float* wmax, int tid, int pairs) {
+  const int q = min(tid, pairs - 1);
+  PXBounds b{wmax[2 * q], wmax[2 * q + 1], wmax[5 + 2 * q], wmax[6 + 2 * q], wmax[4], wmax[9]};
+  asm volatile("" : : "v"(b.g), "v"(b.u), "v"(b.gl), "v"(b.ul), "v"(b.d), "v"(b.dl));
+  return b;
+}
+__device__ __forceinline__ void prefill_x_factors(int64_t t, int tid, int xe, float mx, float l1, const PXBounds& w,
                                                   int pairs, int F, float2* gu, float2* dn, float2* gu2, float2* dn2) {
   if (tid < pairs) {
     // (in double: the product of two large bounds stays finite)
-    const double bg = fmin(double(l1) * double(wmax[2 * tid]), double(mx) * double(wmax[5 + 2 * tid]));
-    const double bu = fmin(double(l1) * double(wmax[2 * tid + 1]), double(mx) * double(wmax[6 + 2 * tid]));
+    const double bg = fmin(double(l1) * double(w.g), double(mx) * double(w.gl));
+    const double bu = fmin(double(l1) * double(w.u), double(mx) * double(w.ul));
     const double b = 2.0 * bg * bu;
     const int he = max(-126, min(126, (b > 0.0 && b < 1e300) ? ilogb(b) - 14 : 0));
     (tid ? gu2 : gu)[t] = make_float2(__builtin_ldexpf(1.0f, xe), __builtin_ldexpf(1.0f, -he));
     if (tid) {
       dn2[t] = make_float2(__builtin_ldexpf(1.0f, he), 1.0f);
     } else {
-      const double bd = fmin(double(F) * double(wmax[4]), double(wmax[9]));
+      const double bd = fmin(double(F) * double(w.d), double(w.dl));
       const int ye = (bd > 0.0 && bd < 1e300) ? min(min(126, 126 - he), max(max(-126, -126 - he), ilogb(bd) + 1)) : 0;
       dn[t] = make_float2(__builtin_ldexpf(1.0f, he + ye), __builtin_ldexpf(1.0f, -ye));
     }
@@ -451,6 +463,7 @@ __global__ __launch_bounds__(256) void k_prefill_x(const void* __restrict__ x, i
                                                    float2* dn2) {
   __shared__ float red[2][8];
   const int64_t t = blockIdx.x;
+  const PXBounds wb = px_bounds(wmax, threadIdx.x, pairs);
   auto at = [&](int i) -> float {
     return x_dtype == ARTLITE_X_F32 ? static_cast<const float*>(x)[t * H + i]
                                     : bf16_to_f32(static_cast<const uint16_t*>(x)[t * H + i]);
@@ -472,7 +485,7 @@ __global__ __launch_bounds__(256) void k_prefill_x(const void* __restrict__ x, i
   const int xe = (mx > 0.0f && mx <= 3.4e38f) ? ilogbf(mx) - 14 : 0;
   for (int i = threadIdx.x; i < H; i += 256)
     x16[t * H + i] = __builtin_bit_cast(uint16_t, _Float16(__builtin_ldexpf(at(i), -xe)));
-  prefill_x_factors(t, threadIdx.x, xe, mx, l1, wmax, pairs, F, gu, dn, gu2, dn2);
+  prefill_x_factors(t, threadIdx.x, xe, mx, l1, wb, pairs, F, gu, dn, gu2, dn2);
 }
 
 // The same for H a multiple of 8 up to 2048 NP: the row read once, 8 values per thread per piece (one 16-byte load for
@@ -509,6 +522,7 @@ __global__ __launch_bounds__(256) void k_prefill_x_rows(const void* __restrict__
       }
     }
   }
+  const PXBounds wb = px_bounds(wmax, threadIdx.x, pairs);
   for (int o = 32; o; o >>= 1) {
     mx = fmaxf(mx, __shfl_xor(mx, o));
     l1 += __shfl_xor(l1, o);
@@ -530,7 +544,7 @@ __global__ __launch_bounds__(256) void k_prefill_x_rows(const void* __restrict__
       reinterpret_cast<uint4*>(x16 + t * H)[i] = make_uint4(w[0], w[1], w[2], w[3]);
     }
   }
-  prefill_x_factors(t, threadIdx.x, xe, mx, l1, wmax, pairs, F, gu, dn, gu2, dn2);
+  prefill_x_factors(t, threadIdx.x, xe, mx, l1, wb, pairs, F, gu, dn, gu2, dn2);
 }
 
 // The same, a wave per token (four tokens a workgroup): lane l holds pieces l + 64 j of the row (8 values each, H =
@@ -568,6 +582,7 @@ __global__ __launch_bounds__(256) void k_prefill_x_wave(const void* __restrict__
       for (int c = 0; c < 4; c++) v[j][2 * c] = bf16_to_f32(w[c] & 0xFFFFu), v[j][2 * c + 1] = bf16_to_f32(w[c] >> 16);
     }
   }
+  const PXBounds wb = px_bounds(wmax, lane, pairs);
   float mx = 0.0f, l1 = 0.0f;
 #pragma unroll
   for (int j = 0; j < NP; j++)
@@ -590,7 +605,7 @@ __global__ __launch_bounds__(256) void k_prefill_x_wave(const void* __restrict__
              uint32_t(__builtin_bit_cast(uint16_t, _Float16(__builtin_ldexpf(v[j][2 * c + 1], -xe)))) << 16;
     reinterpret_cast<uint4*>(x16 + t * H)[lane + 64 * j] = make_uint4(w[0], w[1], w[2], w[3]);
   }
-  prefill_x_factors(t, lane, xe, mx, l1, wmax, pairs, F, gu, dn, gu2, dn2);
+  prefill_x_factors(t, lane, xe, mx, l1, wb, pairs, F, gu, dn, gu2, dn2);
 }
 
 int launch_prefill_x(const void* x, int x_dtype, int64_t T, int H, const float* wmax, int pairs, int F, uint16_t* x16,
