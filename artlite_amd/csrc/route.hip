@@ -581,67 +581,75 @@ __global__ __launch_bounds__(DISPATCH_BLOCK) void k_route_small(const float* __r
 }
 
 // Router logits of small batches (T <= ROUTER_GROUPS ROUTER_TG tokens, H a multiple of 256, at least 2 values a
-// wave). A workgroup per expert and group of ROUTER_TG tokens (workgroup b: expert b % E, tokens ROUTER_TG (b / E)
-// ..): its NW waves each take H / NW values of K (lane: values 2 lane + 128 j of the wave's slice), x read straight
-// from memory (L2), float64 products; a wave's 16 token sums by halving exchanges, then the waves' sums added in wave
-// order, rounded once to fp32. Workgroups past them quantise x into XQ, a wave per unit. (Whatever reads the logits
+// wave). A workgroup per EPW experts and group of ROUTER_TG tokens (workgroup b: experts EPW (b % (E / EPW)) .., tokens
+// ROUTER_TG (b / (E / EPW)) ..): each expert's NW / EPW waves each take a slice of H / (NW / EPW) values of K (lane:
+// values 2 lane + 128 j of the wave's slice), x read straight from memory (L2), float64 products; a wave's 16 token
+// sums by halving exchanges, then the expert's slices' sums added in slice order, rounded once to fp32. Workgroups past them quantise x into XQ, a wave per unit. (Whatever reads the logits
 // runs in a later launch: the launch boundary publishes them.)
-template <int XT>
+template <int XT, int EPW>
 __global__ __launch_bounds__(DISPATCH_BLOCK) void k_router_few(const void* __restrict__ xv,
                                                                  const float* __restrict__ W, int H, int E, int64_t T,
                                                                  float* __restrict__ logits,
                                                                  uint32_t* __restrict__ xq) {
-  constexpr int NW = DISPATCH_BLOCK / WAVE;
+  constexpr int NW = DISPATCH_BLOCK / WAVE, WE = NW / EPW;  // (waves a workgroup, waves an expert)
   __shared__ double part[NW][ROUTER_TG];
   const int lane = threadIdx.x & (WAVE - 1), wv = threadIdx.x / WAVE;
-  const int G = int((T + ROUTER_TG - 1) / ROUTER_TG);  // (token groups)
-  if (int(blockIdx.x) >= E * G) {  // XQ of x
-    const int64_t w = int64_t(blockIdx.x - E * G) * NW + wv;
+  const int G = int((T + ROUTER_TG - 1) / ROUTER_TG), EB = E / EPW;  // (token groups, expert blocks)
+  if (int(blockIdx.x) >= EB * G) {  // XQ of x
+    const int64_t w = int64_t(blockIdx.x - EB * G) * NW + wv;
     if (w < T * (H / 256)) xq_quant_unit<XT>(xv, w, H, xq, lane);
     return;
   }
-  const int e = int(blockIdx.x) % E, gi = int(blockIdx.x) / E, t0 = gi * ROUTER_TG, nt = min(ROUTER_TG, int(T) - t0);
-  const int q = H / NW;
-  const float* wr = W + int64_t(e) * H + wv * q;
+  const int eb = int(blockIdx.x) % EB, gi = int(blockIdx.x) / EB, t0 = gi * ROUTER_TG, nt = min(ROUTER_TG, int(T) - t0);
+  const int e = eb * EPW + wv / WE, ew = wv % WE;  // (this wave's expert, its slice of H)
+  const int q = H / WE;
+  const float* wr = W + int64_t(e) * H + ew * q;
   double acc[ROUTER_TG];
 #pragma unroll
   for (int t = 0; t < ROUTER_TG; t++) acc[t] = 0.0;
-  for (int j = 0; j < (q + 2 * WAVE - 1) / (2 * WAVE); j++) {
-    const int i = min(2 * (lane + WAVE * j), q - 2);  // (lanes past the slice load its last pair, unused)
-    const bool on = 2 * (lane + WAVE * j) < q;
-    // every load of the step issued before any is used (one memory round trip, not one per token)
-    const float2 wl = *reinterpret_cast<const float2*>(wr + i);
-    float2 xl[ROUTER_TG];
+  // (EPW steps of 128 values at a time: every load of them issued before any is used, one memory round trip, not
+  // one per token or per step)
+  const int J = (q + 2 * WAVE - 1) / (2 * WAVE);
+  for (int j0 = 0; j0 < J; j0 += EPW) {
+    float2 wl[EPW], xl[EPW][ROUTER_TG];
 #pragma unroll
-    for (int t = 0; t < ROUTER_TG; t++) {
-      const int64_t o = int64_t(t0 + min(t, nt - 1)) * H + wv * q + i;
-      if (XT == ARTLITE_X_F32) {
-        xl[t] = *reinterpret_cast<const float2*>(static_cast<const float*>(xv) + o);
-      } else {
-        const uint32_t v = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(xv) + o);
-        xl[t] = make_float2(__uint_as_float(v << 16), __uint_as_float(v & 0xFFFF0000u));
+    for (int u = 0; u < EPW; u++) {
+      const int i = min(2 * (lane + WAVE * (j0 + u)), q - 2);  // (lanes past the slice load its last pair, unused)
+      wl[u] = *reinterpret_cast<const float2*>(wr + i);
+#pragma unroll
+      for (int t = 0; t < ROUTER_TG; t++) {
+        const int64_t o = int64_t(t0 + min(t, nt - 1)) * H + ew * q + i;
+        if (XT == ARTLITE_X_F32) {
+          xl[u][t] = *reinterpret_cast<const float2*>(static_cast<const float*>(xv) + o);
+        } else {
+          const uint32_t v = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(xv) + o);
+          xl[u][t] = make_float2(__uint_as_float(v << 16), __uint_as_float(v & 0xFFFF0000u));
+        }
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-    float xf[ROUTER_TG][2];
 #pragma unroll
-    for (int t = 0; t < ROUTER_TG; t++) xf[t][0] = xl[t].x, xf[t][1] = xl[t].y;
-    const double w0 = wl.x, w1 = wl.y;
-    if (on) {
+    for (int u = 0; u < EPW; u++) {
+      float xf[ROUTER_TG][2];
 #pragma unroll
-      for (int t = 0; t < ROUTER_TG; t++) {
-        acc[t] += double(xf[t][0]) * w0;
-        acc[t] += double(xf[t][1]) * w1;
+      for (int t = 0; t < ROUTER_TG; t++) xf[t][0] = xl[u][t].x, xf[t][1] = xl[u][t].y;
+      const double w0 = wl[u].x, w1 = wl[u].y;
+      if (j0 + u < J && 2 * (lane + WAVE * (j0 + u)) < q) {
+#pragma unroll
+        for (int t = 0; t < ROUTER_TG; t++) {
+          acc[t] += double(xf[t][0]) * w0;
+          acc[t] += double(xf[t][1]) * w1;
+        }
       }
     }
   }
   const double v = token_sums(acc, lane);
   if ((lane & 3) == 0) part[wv][sum_token(lane)] = v;
   lds_barrier();
-  if (wv == 0 && lane < nt) {
-    double sum = part[0][lane];
+  if (ew == 0 && lane < nt) {  // (the expert's first wave: its slices' sums in slice order)
+    double sum = part[wv][lane];
 #pragma unroll
-    for (int w = 1; w < NW; w++) sum += part[w][lane];
+    for (int w = 1; w < WE; w++) sum += part[wv + w][lane];
     logits[int64_t(t0 + lane) * E + e] = float(sum);
   }
 }
@@ -678,11 +686,20 @@ int launch_router_few(const void* x, int x_dtype, const float* W, int H, int E, 
     return fail(ARTLITE_EINVAL, "router_few: %lld tokens, H %d, %d experts", (long long)T, H, E);
   constexpr int NW = DISPATCH_BLOCK / WAVE;
   const int nq = xq ? int((T * (H / 256) + NW - 1) / NW) : 0;
-  const dim3 g(unsigned(E * ((T + ROUTER_TG - 1) / ROUTER_TG) + nq)), b(DISPATCH_BLOCK);
-  if (x_dtype == ARTLITE_X_F32)
-    k_router_few<ARTLITE_X_F32><<<g, b, 0, s>>>(x, W, H, E, T, logits, xq);
-  else
-    k_router_few<ARTLITE_X_BF16><<<g, b, 0, s>>>(x, W, H, E, T, logits, xq);
+  // (past two token groups, two experts a workgroup: fewer, longer workgroups, which the device holds in one round)
+  const int epw = T > 2 * ROUTER_TG && E % 2 == 0 ? 2 : 1;
+  const dim3 g(unsigned(E / epw * ((T + ROUTER_TG - 1) / ROUTER_TG) + nq)), b(DISPATCH_BLOCK);
+  if (epw == 2) {
+    if (x_dtype == ARTLITE_X_F32)
+      k_router_few<ARTLITE_X_F32, 2><<<g, b, 0, s>>>(x, W, H, E, T, logits, xq);
+    else
+      k_router_few<ARTLITE_X_BF16, 2><<<g, b, 0, s>>>(x, W, H, E, T, logits, xq);
+  } else {
+    if (x_dtype == ARTLITE_X_F32)
+      k_router_few<ARTLITE_X_F32, 1><<<g, b, 0, s>>>(x, W, H, E, T, logits, xq);
+    else
+      k_router_few<ARTLITE_X_BF16, 1><<<g, b, 0, s>>>(x, W, H, E, T, logits, xq);
+  }
   ART_HIP(hipGetLastError());
   return ARTLITE_OK;
 }
