@@ -175,7 +175,8 @@ def traffic(path: Path, kernel: str) -> tuple[float | None, str | None]:
             commit = s.split(":", 1)[1].strip()
     if val is None:
         return None, None
-    return val, (f"{path.relative_to(ROOT)} (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, copy-calibrated, "
+    where = path.relative_to(ROOT) if path.is_relative_to(ROOT) else path
+    return val, (f"{where} (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, copy-calibrated, "
                  f"at commit {commit})")
 
 
