@@ -181,7 +181,10 @@ def traffic(path: Path, kernel: str) -> tuple[float | None, str | None]:
 
 
 # the counter summaries of the workloads profiled on their own (bench.py --only), by (workload, tokens)
-TRAFFIC = {("decode", 16): ROOT / "profiles" / "gemv_decode_b16_traffic.md",
+TRAFFIC = {("decode", 1): ROOT / "profiles" / "gemv_decode_b1_traffic.md",
+           ("decode", 4): ROOT / "profiles" / "gemv_decode_b4_traffic.md",
+           ("decode", 16): ROOT / "profiles" / "gemv_decode_b16_traffic.md",
+           ("decode", 64): ROOT / "profiles" / "gemv_decode_b64_traffic.md",
            ("decode", 128): ROOT / "profiles" / "pgemm_decode_t128_traffic.md",
            ("prefill", 4096): ROOT / "profiles" / "pgemm_prefill_t4096_traffic.md",
            ("deepseek", 512): ROOT / "profiles" / "pgemm_deepseek_t512_traffic.md",
