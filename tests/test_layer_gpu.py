@@ -34,11 +34,11 @@ CASES = [("cpu", 16), ("decode", 1), ("decode", 4), ("decode", 16), ("decode", 6
          ("widek", 40), ("widek", 16),
          # the routing in the gate / up launch with a wave per token (top 20: more than a lane group takes)
          ("topk20", 12), ("wide_e", 16),
-         # 320 experts past the GEMV's sizes (H 256: the MFMA decode tiles): the router's K in parts that the top-k
-         # launch adds, eight logits a lane
-         ("wide_e", 384)]
+         # 320 and 160 experts past the GEMV's sizes (the MFMA decode tiles): the router's K in parts that the top-k
+         # launch adds, eight and four logits a lane
+         ("wide_e", 384), ("widek", 256)]
 # (passes on the MFMA decode tiles)
-DTILE_CASES = {("dtiles", 96), ("wide_e", 384)}
+DTILE_CASES = {("dtiles", 96), ("wide_e", 384), ("widek", 256)}
 
 # Decode-sized passes (at most 4 pairs per expert on average, K a multiple of 256) take the GEMV over XQ activations:
 # int8 hi / lo planes per 32 values, |x - xq| <= max|x| / 65024 per group, so h (itself held in XQ) and the pair
